@@ -1,0 +1,120 @@
+/* C ABI of the MI355X (gfx950) Qwen3.5-0.8B decode engine: libqwen35.so.
+ *
+ * Plain pointers and sizes only; every entry point returns 0 on success or a negative
+ * q35_status, and q35_last_error() describes the last failure of the calling thread.
+ * One engine owns one HIP stream, its device weights and its scratch; it is not
+ * thread-safe. Host pointers are host memory unless a name says "_dev".
+ *
+ * Lanes are independent sequences (requests). A state holds `lanes` copies of the
+ * reference's per-request tuple (engine/state.h:83-116): GDN S f32 [18][16][128][128],
+ * conv window f32 [18][3][6144], K and V caches bf16 [6][2][cap][256], prefix_len, plus
+ * the MTP block's own K/V [2][mtp_cap][256] and its length.
+ */
+#ifndef Q35_H
+#define Q35_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct q35_engine q35_engine;
+typedef struct q35_state q35_state;
+
+enum q35_status {
+    Q35_OK = 0,
+    Q35_ERR_ARG = -1,      /* bad argument: token out of range, lane out of range, NULL, ... */
+    Q35_ERR_CAP = -2,      /* context capacity or row capacity exceeded */
+    Q35_ERR_HIP = -3,      /* a HIP call failed */
+    Q35_ERR_STATE = -4     /* call order violated (no weights, no MTP slots, ...) */
+};
+
+typedef struct q35_config {
+    int device;            /* HIP device ordinal */
+    int max_rows;          /* rows (lanes x tokens) one body pass may carry */
+    int max_ctx;           /* largest cache capacity any state will use (sizes attention scratch) */
+    int use_graph;         /* capture decode bodies in hipGraphs (1) or launch eagerly (0) */
+} q35_config;
+
+/* Engine lifetime.  Replaces WeightStore + allocate_scratch + prepare_weight_adapters
+ * (engine/loader.cpp:478, engine/decode_step.h:479,595). */
+int q35_create(const q35_config* cfg, q35_engine** out);
+int q35_destroy(q35_engine* e);
+const char* q35_last_error(void);
+
+/* Synthetic weights of the benchmark workload: matrices N(0,0.02), RMSNorm weights 1.0,
+ * A_log = log U(1,16), dt_bias ~ U(-1,1), from the portable seeded stream. */
+int q35_init_random(q35_engine* e, uint64_t seed);
+/* Load one tensor given in checkpoint layout and dtype bf16 (row-major, the reference's
+ * names, e.g. "model.language_model.layers.0.mlp.gate_proj.weight"); engine/loader.cpp:478. */
+int q35_load_tensor(q35_engine* e, const char* name, const uint16_t* host_bf16, size_t n_elems);
+/* Read a tensor back in checkpoint layout (tests). */
+int q35_read_tensor(q35_engine* e, const char* name, uint16_t* host_bf16, size_t n_elems);
+
+/* Request state.  allocate_state / free_state / reset (engine/state.h:101,115-116). */
+int q35_state_alloc(q35_engine* e, int lanes, int cap, int mtp_k, int mtp_cap, q35_state** out);
+int q35_state_free(q35_engine* e, q35_state* s);
+int q35_state_reset(q35_engine* e, q35_state* s, const int32_t* lanes, int n);
+/* Seeded state of the batched benchmark: S ~ N(0,0.1) f32, K/V ~ N(0,1) bf16 (slots
+ * [0, prefix_len)), window zero, prefix_len as given, for every lane. */
+int q35_state_seed(q35_engine* e, q35_state* s, uint64_t seed, int prefix_len);
+int q35_state_prefix_len(q35_engine* e, q35_state* s, int lane, int32_t* out);
+/* Copy one lane's tensors to host: which = 0 S [18][16][128][128] f32, 1 window
+ * [18][3][6144] f32, 2 keys [6][2][n][256] bf16 (first n slots), 3 values, 4 MTP keys
+ * [2][n][256], 5 MTP values. */
+int q35_state_read(q35_engine* e, q35_state* s, int lane, int which, int n_slots, void* host, size_t bytes);
+int q35_state_write(q35_engine* e, q35_state* s, int lane, int which, int n_slots, const void* host, size_t bytes);
+
+/* Prompt of one lane (prefill_wave, engine/prefill.cpp:63 / specimpl.py:457-464): the
+ * tokens are consumed in waves of at most max_rows rows; *y0 = greedy id after the last
+ * prompt token; logits (nullable) receives that row's 248320 bf16-valued logits. */
+int q35_prefill(q35_engine* e, q35_state* s, int lane, const int32_t* ids, int n, int32_t* y0,
+                float* logits);
+
+/* One greedy decode step for n lanes (decode_step, engine/decode_step.h:582): lane
+ * lanes[i] (or i when lanes is NULL) consumes tokens[i]; out_tok[i] = argmax (lowest id on
+ * ties) of the bf16 logits; out_logits (nullable) is [n][248320]. */
+int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n,
+                    const int32_t* tokens, int32_t* out_tok, float* out_logits);
+
+/* MTP draft (mtpdraft::draft_round, engine/mtp_draft.h:233 / speccheck/mtp.py:57-83):
+ * for each lane i, draft the token at position pos[i] from token y[i] and hidden h
+ * (h_dev == NULL: the post-final-norm row the last body left for that lane). Appends one
+ * entry to the lane's MTP K/V.  out_xd (nullable, host [n][1024] bf16) receives x_d. */
+int q35_mtp_draft(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* y,
+                  const int32_t* pos, int step, int32_t* out_tok, uint16_t* out_xd,
+                  float* out_logits);
+
+/* One speculative round (greedy_mtp body, speccheck/mtp.py:150-177 with k drafts): per
+ * lane, k drafts from (cur, h), a (k+1)-row verify body over [cur, d1..dk] writing the GDN
+ * state after every row to spare slots, greedy accept of the longest matching prefix a,
+ * rollback (state slot after row a, prefix_len = p + a + 1, MTP K/V truncated when a < k).
+ * emit[i][0..n_emit[i]) = accepted drafts + bonus token; stats (nullable, [4]) accumulates
+ * drafted, accepted, bonus, target rows. */
+int q35_mtp_round(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* cur,
+                  int k, int32_t* emit, int32_t* n_emit, int64_t* stats);
+
+/* Per-op entry points on caller device buffers (benchmark and parity harness). */
+/* Y[M][N] = X[M][K] . W^T with W in checkpoint row-major layout, tiled into scratch first
+ * by q35_op_tile_weight. */
+int q35_op_tile_weight(q35_engine* e, const uint16_t* w_rowmajor_dev, int N, int K, uint16_t* w_tiled_dev);
+int q35_op_gemm(q35_engine* e, const uint16_t* w_tiled_dev, int N, int K, const uint16_t* x_dev,
+                int M, uint16_t* y_dev);
+int q35_op_lm_head_argmax(q35_engine* e, const uint16_t* x_dev, int M, int32_t* tok_dev, float* logits_dev);
+int q35_sync(q35_engine* e);
+/* Options: "layers" (diagnostic: bodies run only the first n of the 24 layers, the final
+ * norm then applies to that layer's output), "graph" (0/1). */
+int q35_set_option(q35_engine* e, const char* name, int value);
+/* Copy the current content of a named scratch buffer ("x", "h", "nrm", "delta", "proj",
+ * "o", "gu", "aout", "q") to host, after the stream drains (diagnostics and tests). */
+int q35_read_scratch(q35_engine* e, const char* name, void* host, size_t bytes);
+/* Timing of the engine stream with HIP events: begin/end bracket; elapsed in ms. */
+int q35_timer_begin(q35_engine* e);
+int q35_timer_end(q35_engine* e, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

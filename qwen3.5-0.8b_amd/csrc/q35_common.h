@@ -1,0 +1,88 @@
+// Shared device/host definitions of the Qwen3.5-0.8B MI355X (gfx950) decode engine.
+//
+// Model constants follow speccheck/specimpl.py:26-58 and engine/state.h:41-67 of the
+// reference. Storage is IEEE bfloat16 bits in uint16_t; all accumulation is f32.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q35 {
+
+constexpr int kHidden = 1024;
+constexpr int kLayers = 24;
+constexpr int kGdnLayers = 18;
+constexpr int kAttnLayers = 6;
+constexpr int kFF = 3584;
+constexpr int kVocab = 248320;
+constexpr int kHv = 16;            // GDN value heads (= key heads)
+constexpr int kDk = 128;
+constexpr int kDv = 128;
+constexpr int kConvCh = 6144;      // q 2048 | k 2048 | v 2048
+constexpr int kConvK = 4;
+constexpr long long kSLayer = (long long)kHv * kDk * kDv;   // one GDN layer's state, 262144 f32
+constexpr long long kWLayer = 3LL * kConvCh;                // one layer's conv window, 18432 f32
+constexpr int kNq = 8;
+constexpr int kNkv = 2;
+constexpr int kHeadDim = 256;
+constexpr int kRotDim = 64;
+constexpr float kEps = 1e-6f;
+constexpr float kRopeTheta = 1e7f;
+
+// Fused input projection widths (rows of the concatenated weight matrix).
+constexpr int kGdnInRows = kConvCh + 2048 + 16 + 16;   // qkv | z | b | a  = 8224
+constexpr int kGdnZOff = kConvCh;                      // 6144
+constexpr int kGdnBOff = kConvCh + 2048;               // 8192
+constexpr int kGdnAOff = kConvCh + 2048 + 16;          // 8208
+constexpr int kAttnInRows = 2 * kNq * kHeadDim + 2 * kNkv * kHeadDim;   // q|gate 4096, k 512, v 512
+constexpr int kAttnKOff = 2 * kNq * kHeadDim;          // 4096
+constexpr int kAttnVOff = kAttnKOff + kNkv * kHeadDim; // 4608
+constexpr int kGuRows = 2 * kFF;                       // gate 3584 | up 3584
+
+constexpr bool is_attn_layer(int l) { return (l % 4) == 3; }
+constexpr int gdn_slot(int l) { return l - (l + 1) / 4; }
+constexpr int attn_slot(int l) { return l / 4; }
+
+// GEMM weight tiling: 16 output rows x 256 k per tile, 8 KiB contiguous, laid out so a
+// wave's 8 dwordx4 loads (step s = 0..7, lane = g*16 + n%16) are each 1 KiB contiguous.
+// Element (n, k): tile (n/16, k/256); g = (k%256)/64; s = (k%64)/8; e = k%8.
+constexpr int kTileN = 16;
+constexpr int kTileK = 256;
+__host__ __device__ inline size_t tiled_offset(int n, int k, int K) {
+    int nt = n >> 4, kb = k >> 8, kk = k & 255;
+    int g = kk >> 6, s = (kk >> 3) & 7, e = kk & 7;
+    int lane = g * 16 + (n & 15);
+    return ((((size_t)nt * (K >> 8) + kb) * 8 + s) * 64 + lane) * 8 + e;
+}
+
+}  // namespace q35
+
+// ---------------------------------------------------------------- device helpers
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 q35_bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float q35_f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t q35_u32x4;
+
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// Round-to-nearest-even f32 -> bf16 bits (NaN stays a quiet NaN).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffffu) ? 0x40u : 0u));
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}

@@ -1,0 +1,904 @@
+// Engine host side and C ABI (include/q35.h).
+//
+// Follows the reference's decode order (engine/decode_step.cpp:448-1354, specification
+// 07-decode-step.md:6-20): embed -> input norm -> 24 blocks (GDN or gated attention, then
+// the MLP, with the residual add fused into the next norm) -> final norm -> tied lm_head ->
+// greedy argmax. Every pass is a "body" over R rows = nlanes x T tokens; decode is T = 1,
+// a prompt wave is one lane with T tokens, an MTP verify is T = k + 1.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/q35.h"
+#include "q35_common.h"
+#include "q35_kernels.h"
+
+using namespace q35;
+
+namespace {
+
+thread_local std::string g_err;
+
+struct Q35Error : std::runtime_error {
+    int code;
+    Q35Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+#define HCK(x)                                                                              \
+    do {                                                                                    \
+        hipError_t _e = (x);                                                                \
+        if (_e != hipSuccess)                                                               \
+            throw Q35Error(Q35_ERR_HIP, std::string(#x) + ": " + hipGetErrorString(_e));   \
+    } while (0)
+#define REQ(cond, code, msg)                                  \
+    do {                                                      \
+        if (!(cond)) throw Q35Error((code), (msg));           \
+    } while (0)
+
+uint64_t hmix(uint64_t x) {
+    uint64_t z = x + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+uint64_t fnv1a64(const std::string& s) {
+    uint64_t h = 0xCBF29CE484222325ull;
+    for (unsigned char c : s) { h ^= c; h *= 0x100000001B3ull; }
+    return h;
+}
+uint64_t stream_key(uint64_t seed, const std::string& name) { return hmix(hmix(seed) + fnv1a64(name)); }
+uint16_t h_f2bf(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffff) ? 0x40 : 0));
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+enum Kind { kNormal, kOne, kAlog, kDtBias };
+
+// Where a checkpoint tensor lives on the device.
+struct Placement {
+    uint16_t* base = nullptr;  // plain: the tensor; tiled: the combined matrix
+    int rows = 0, cols = 0;    // logical shape (cols = K for matrices; 1-D: rows = n, cols = 1)
+    bool tiled = false;
+    int row_off = 0;           // tiled: first row inside the combined matrix
+    Kind kind = kNormal;
+};
+
+struct LayerW {
+    uint16_t *norm_in, *norm_post, *W_in, *W_out, *W_gu, *W_down;
+    uint16_t *conv_w, *A_log, *dt_bias, *gnorm;   // GDN
+    uint16_t *q_norm, *k_norm;                     // attention
+};
+
+}  // namespace
+
+struct q35_state {
+    int lanes = 0, cap = 0, mtp_cap = 0, nslots = 2, mtp_k = 0;
+    float* S = nullptr;      // [lanes][nslots][18][16][128][128]
+    float* win = nullptr;    // [lanes][nslots][18][3][6144]
+    uint16_t *kc = nullptr, *vc = nullptr;    // [lanes][6][2][cap][256]
+    uint16_t *mkc = nullptr, *mvc = nullptr;  // [lanes][2][mtp_cap][256]
+    uint16_t* hlast = nullptr;                // [lanes][1024] post-final-norm row of the last body
+    int* cur_dev = nullptr;                   // [lanes]
+    std::vector<int> prefix, mtp_len, cur;
+    long long S_lane() const { return (long long)nslots * kGdnLayers * kSLayer; }
+    long long W_lane() const { return (long long)nslots * kGdnLayers * 18432; }
+    long long kv_lane() const { return (long long)kAttnLayers * 2 * cap * 256; }
+    long long mkv_lane() const { return (long long)2 * mtp_cap * 256; }
+};
+
+struct q35_engine {
+    int device = 0, R = 0, max_ctx = 0, use_graph = 0;
+    int n_layers = kLayers;          // diagnostic: run only the first n layers of a body
+    hipStream_t st = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    uint16_t* blob = nullptr;
+    size_t blob_bytes = 0;
+    bool weights_ready = false;
+    std::map<std::string, Placement> reg;
+    std::vector<std::string> order;
+    LayerW L[kLayers];
+    LayerW M;                        // MTP block (attention layer shape)
+    uint16_t *E = nullptr, *final_norm = nullptr, *mtp_pre_e = nullptr, *mtp_pre_h = nullptr,
+             *mtp_fc = nullptr, *mtp_norm = nullptr;
+    // scratch
+    uint16_t *x, *h, *delta, *nrm, *proj, *gu, *aout, *cat;
+    float *o, *q, *sc, *stats, *part, *pval, *inv_freq;
+    int *pidx, *counters, *tok_dev, *rlane, *rpos, *rslot, *ridx_src, *ridx_dst;
+    int sc_ld = 0, max_chunks = 0;
+    float* logits_dev = nullptr;
+    int logits_rows = 0;
+    // pinned staging
+    int *h_tok, *h_lane, *h_pos, *h_slot, *h_out, *h_src, *h_dst;
+};
+
+namespace {
+
+template <typename T>
+T* dalloc(size_t n) {
+    void* p = nullptr;
+    HCK(hipMalloc(&p, n * sizeof(T) > 0 ? n * sizeof(T) : 16));
+    return (T*)p;
+}
+template <typename T>
+T* halloc(size_t n) {
+    void* p = nullptr;
+    HCK(hipHostMalloc(&p, n * sizeof(T) > 0 ? n * sizeof(T) : 16, hipHostMallocDefault));
+    return (T*)p;
+}
+
+// ------------------------------------------------------------------ weight registry
+struct Planner {
+    size_t off = 0;
+    std::vector<std::pair<uint16_t**, size_t>> pending;
+    void take(uint16_t** p, size_t elems) {
+        pending.push_back({p, off});
+        off += (elems * 2 + 255) / 256 * 256;
+    }
+};
+
+void plan_weights(q35_engine* e) {
+    Planner pl;
+    auto& reg = e->reg;
+    auto add_plain = [&](const std::string& n, uint16_t** slot, int rows, Kind k) {
+        pl.take(slot, rows);
+        Placement p;
+        p.rows = rows; p.cols = 1; p.kind = k;
+        reg[n] = p;
+        e->order.push_back(n);
+    };
+    // tiled tensors are registered after allocation; remember (name, combined ptr, rows, K, off)
+    struct TDef { std::string n; uint16_t** base; int rows, K, off; };
+    std::vector<TDef> tdefs;
+    auto add_tiled = [&](const std::string& n, uint16_t** base, int rows, int K, int off) {
+        tdefs.push_back({n, base, rows, K, off});
+        e->order.push_back(n);
+    };
+    auto attn_layer = [&](LayerW& w, const std::string& p, const std::string& sa) {
+        pl.take(&w.W_in, (size_t)kAttnInRows * kHidden);
+        add_tiled(sa + "q_proj.weight", &w.W_in, 4096, kHidden, 0);
+        add_tiled(sa + "k_proj.weight", &w.W_in, 512, kHidden, kAttnKOff);
+        add_tiled(sa + "v_proj.weight", &w.W_in, 512, kHidden, kAttnVOff);
+        add_plain(sa + "q_norm.weight", &w.q_norm, 256, kOne);
+        add_plain(sa + "k_norm.weight", &w.k_norm, 256, kOne);
+        pl.take(&w.W_out, (size_t)kHidden * 2048);
+        add_tiled(sa + "o_proj.weight", &w.W_out, kHidden, 2048, 0);
+        (void)p;
+    };
+    auto mlp = [&](LayerW& w, const std::string& p) {
+        pl.take(&w.W_gu, (size_t)kGuRows * kHidden);
+        add_tiled(p + "gate_proj.weight", &w.W_gu, kFF, kHidden, 0);
+        add_tiled(p + "up_proj.weight", &w.W_gu, kFF, kHidden, kFF);
+        pl.take(&w.W_down, (size_t)kHidden * kFF);
+        add_tiled(p + "down_proj.weight", &w.W_down, kHidden, kFF, 0);
+    };
+    for (int l = 0; l < kLayers; ++l) {
+        LayerW& w = e->L[l];
+        std::memset(&w, 0, sizeof(w));
+        std::string pre = "model.language_model.layers." + std::to_string(l) + ".";
+        add_plain(pre + "input_layernorm.weight", &w.norm_in, kHidden, kOne);
+        add_plain(pre + "post_attention_layernorm.weight", &w.norm_post, kHidden, kOne);
+        if (!is_attn_layer(l)) {
+            std::string la = pre + "linear_attn.";
+            pl.take(&w.W_in, (size_t)kGdnInRows * kHidden);
+            add_tiled(la + "in_proj_qkv.weight", &w.W_in, kConvCh, kHidden, 0);
+            add_tiled(la + "in_proj_z.weight", &w.W_in, 2048, kHidden, kGdnZOff);
+            add_tiled(la + "in_proj_b.weight", &w.W_in, 16, kHidden, kGdnBOff);
+            add_tiled(la + "in_proj_a.weight", &w.W_in, 16, kHidden, kGdnAOff);
+            add_plain(la + "conv1d.weight", &w.conv_w, kConvCh * 4, kNormal);
+            add_plain(la + "A_log", &w.A_log, 16, kAlog);
+            add_plain(la + "dt_bias", &w.dt_bias, 16, kDtBias);
+            add_plain(la + "norm.weight", &w.gnorm, 128, kOne);
+            pl.take(&w.W_out, (size_t)kHidden * 2048);
+            add_tiled(la + "out_proj.weight", &w.W_out, kHidden, 2048, 0);
+        } else {
+            attn_layer(w, pre, pre + "self_attn.");
+        }
+        mlp(w, pre + "mlp.");
+    }
+    pl.take(&e->E, (size_t)kVocab * kHidden);
+    add_tiled("model.language_model.embed_tokens.weight", &e->E, kVocab, kHidden, 0);
+    add_plain("model.language_model.norm.weight", &e->final_norm, kHidden, kOne);
+    add_plain("mtp.pre_fc_norm_embedding.weight", &e->mtp_pre_e, kHidden, kOne);
+    add_plain("mtp.pre_fc_norm_hidden.weight", &e->mtp_pre_h, kHidden, kOne);
+    pl.take(&e->mtp_fc, (size_t)kHidden * 2048);
+    add_tiled("mtp.fc.weight", &e->mtp_fc, kHidden, 2048, 0);
+    std::memset(&e->M, 0, sizeof(e->M));
+    add_plain("mtp.layers.0.input_layernorm.weight", &e->M.norm_in, kHidden, kOne);
+    attn_layer(e->M, "mtp.layers.0.", "mtp.layers.0.self_attn.");
+    add_plain("mtp.layers.0.post_attention_layernorm.weight", &e->M.norm_post, kHidden, kOne);
+    mlp(e->M, "mtp.layers.0.mlp.");
+    add_plain("mtp.norm.weight", &e->mtp_norm, kHidden, kOne);
+
+    e->blob_bytes = pl.off;
+    HCK(hipMalloc(&e->blob, e->blob_bytes));
+    for (auto& pp : pl.pending) *pp.first = (uint16_t*)((char*)e->blob + pp.second);
+    // plain placements: re-walk pointers in registration order (pending order == add order)
+    // simpler: resolve by name below
+    for (auto& t : tdefs) {
+        Placement p;
+        p.base = *t.base; p.rows = t.rows; p.cols = t.K; p.tiled = true; p.row_off = t.off; p.kind = kNormal;
+        reg[t.n] = p;
+    }
+}
+
+// plain placements need their pointers: build a name->pointer table after planning
+void resolve_plain(q35_engine* e) {
+    auto set = [&](const std::string& n, uint16_t* p) { e->reg.at(n).base = p; };
+    for (int l = 0; l < kLayers; ++l) {
+        LayerW& w = e->L[l];
+        std::string pre = "model.language_model.layers." + std::to_string(l) + ".";
+        set(pre + "input_layernorm.weight", w.norm_in);
+        set(pre + "post_attention_layernorm.weight", w.norm_post);
+        if (!is_attn_layer(l)) {
+            std::string la = pre + "linear_attn.";
+            set(la + "conv1d.weight", w.conv_w);
+            set(la + "A_log", w.A_log);
+            set(la + "dt_bias", w.dt_bias);
+            set(la + "norm.weight", w.gnorm);
+        } else {
+            set(pre + "self_attn.q_norm.weight", w.q_norm);
+            set(pre + "self_attn.k_norm.weight", w.k_norm);
+        }
+    }
+    set("model.language_model.norm.weight", e->final_norm);
+    set("mtp.pre_fc_norm_embedding.weight", e->mtp_pre_e);
+    set("mtp.pre_fc_norm_hidden.weight", e->mtp_pre_h);
+    set("mtp.layers.0.input_layernorm.weight", e->M.norm_in);
+    set("mtp.layers.0.self_attn.q_norm.weight", e->M.q_norm);
+    set("mtp.layers.0.self_attn.k_norm.weight", e->M.k_norm);
+    set("mtp.layers.0.post_attention_layernorm.weight", e->M.norm_post);
+    set("mtp.norm.weight", e->mtp_norm);
+}
+
+void alloc_scratch(q35_engine* e) {
+    const size_t R = e->R;
+    e->x = dalloc<uint16_t>(R * kHidden);
+    e->h = dalloc<uint16_t>(R * kHidden);
+    e->delta = dalloc<uint16_t>(R * kHidden);
+    e->nrm = dalloc<uint16_t>(R * kHidden);
+    e->proj = dalloc<uint16_t>(R * kGdnInRows);
+    e->gu = dalloc<uint16_t>(R * kGuRows);
+    e->aout = dalloc<uint16_t>(R * 2048);
+    e->cat = dalloc<uint16_t>(R * 2048);
+    e->o = dalloc<float>(R * 2048);
+    e->q = dalloc<float>(R * kNq * 256);
+    e->sc_ld = (e->max_ctx + 255) / 256 * 256;
+    e->max_chunks = e->sc_ld / 256;
+    e->sc = dalloc<float>(R * kNq * (size_t)e->sc_ld);
+    e->stats = dalloc<float>(R * kNq * (size_t)e->max_chunks * 2);
+    e->part = dalloc<float>(R * (size_t)e->max_chunks * kNq * 256);
+    e->pval = dalloc<float>(R * (size_t)(kVocab / 16));
+    e->pidx = dalloc<int>(R * (size_t)(kVocab / 16));
+    e->counters = dalloc<int>(R * 2);
+    HCK(hipMemset(e->counters, 0, R * 2 * sizeof(int)));
+    e->tok_dev = dalloc<int>(R);
+    e->rlane = dalloc<int>(R);
+    e->rpos = dalloc<int>(R);
+    e->rslot = dalloc<int>(R);
+    e->ridx_src = dalloc<int>(R);
+    e->ridx_dst = dalloc<int>(R);
+    e->h_tok = halloc<int>(R);
+    e->h_lane = halloc<int>(R);
+    e->h_pos = halloc<int>(R);
+    e->h_slot = halloc<int>(R);
+    e->h_out = halloc<int>(R);
+    e->h_src = halloc<int>(R);
+    e->h_dst = halloc<int>(R);
+    // rope inverse frequencies, f32 as the oracle forms them (specimpl.py:151-156):
+    // inv_i = 1 / f32(theta ** f32(2i/64))
+    float invf[32];
+    for (int i = 0; i < 32; ++i) {
+        float ex = (float)(2 * i) / 64.0f;
+        float pw = (float)std::pow(1e7, (double)ex);
+        invf[i] = 1.0f / pw;
+    }
+    e->inv_freq = dalloc<float>(32);
+    HCK(hipMemcpy(e->inv_freq, invf, sizeof(invf), hipMemcpyHostToDevice));
+}
+
+void ensure_logits(q35_engine* e, int rows) {
+    if (e->logits_rows >= rows) return;
+    if (e->logits_dev) HCK(hipFree(e->logits_dev));
+    e->logits_dev = dalloc<float>((size_t)rows * kVocab);
+    e->logits_rows = rows;
+}
+
+// ------------------------------------------------------------------ body pass
+// Row metadata must already be staged in e->h_lane/h_pos/h_slot/h_tok for R rows.
+void upload_rows(q35_engine* e, int R) {
+    HCK(hipMemcpyAsync(e->tok_dev, e->h_tok, R * sizeof(int), hipMemcpyHostToDevice, e->st));
+    HCK(hipMemcpyAsync(e->rlane, e->h_lane, R * sizeof(int), hipMemcpyHostToDevice, e->st));
+    HCK(hipMemcpyAsync(e->rpos, e->h_pos, R * sizeof(int), hipMemcpyHostToDevice, e->st));
+    HCK(hipMemcpyAsync(e->rslot, e->h_slot, R * sizeof(int), hipMemcpyHostToDevice, e->st));
+}
+
+void gemm(q35_engine* e, const uint16_t* W, int N, int K, int M, const void* X, int ldx,
+          uint16_t* Y, int ldy, int amode = kAPlain, const void* X2 = nullptr, int ldx2 = 0,
+          const uint16_t* aux = nullptr) {
+    GemmArgs a{};
+    a.W = W; a.N = N; a.K = K; a.M = M; a.X = X; a.ldx = ldx; a.X2 = X2; a.ldx2 = ldx2;
+    a.aux_w = aux; a.Y = Y; a.ldy = ldy;
+    HCK(launch_gemm(a, amode, kEStore, e->st));
+}
+
+void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16_t* vc,
+                     long long kv_lane, long long layer_off, int cap) {
+    gemm(e, w.W_in, kAttnInRows, kHidden, R, e->h, kHidden, e->proj, kAttnInRows);
+    AttnArgs a{};
+    a.proj = e->proj; a.q_norm = w.q_norm; a.k_norm = w.k_norm;
+    a.kc = kc; a.vc = vc; a.kv_lane = kv_lane; a.kv_layer_off = layer_off; a.cap = cap;
+    a.rm.lane = e->rlane; a.rm.pos = e->rpos; a.rm.slot = e->rslot;
+    a.q = e->q; a.sc = e->sc; a.sc_ld = e->sc_ld; a.stats = e->stats; a.part = e->part;
+    a.counters = e->counters;
+    a.max_chunks = (cap + 255) / 256;
+    REQ(a.max_chunks <= e->max_chunks, Q35_ERR_CAP, "cache capacity exceeds engine max_ctx");
+    a.out = e->aout; a.R = R; a.inv_freq = e->inv_freq;
+    HCK(launch_attention(a, e->st));
+    gemm(e, w.W_out, kHidden, 2048, R, e->aout, 2048, e->delta, kHidden);
+}
+
+void mlp_layer(q35_engine* e, const LayerW& w, int R) {
+    HCK(launch_addnorm(1, nullptr, nullptr, e->x, e->delta, w.norm_post, e->h, R, e->st));
+    gemm(e, w.W_gu, kGuRows, kHidden, R, e->h, kHidden, e->gu, kGuRows);
+    gemm(e, w.W_down, kHidden, kFF, R, e->gu, kGuRows, e->delta, kHidden, kASiluMul, e->gu + kFF, kGuRows);
+}
+
+// Runs the 24-layer body over R = nl * T rows (rows of one lane consecutive) and leaves the
+// final-normed rows in e->nrm. ckpt: write the GDN state after every row (MTP verify).
+void body(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
+    REQ(e->weights_ready, Q35_ERR_STATE, "weights not initialised");
+    REQ(R > 0 && R <= e->R, Q35_ERR_CAP, "rows exceed engine max_rows");
+    upload_rows(e, R);
+    HCK(hipMemcpyAsync(s->cur_dev, s->cur.data(), s->lanes * sizeof(int), hipMemcpyHostToDevice, e->st));
+    const int nl = R / T;
+    const int cs = nl <= 8 ? 8 : nl <= 32 ? 4 : nl <= 64 ? 2 : 1;
+    HCK(launch_addnorm(0, e->tok_dev, e->E, e->x, nullptr, e->L[0].norm_in, e->h, R, e->st));
+    for (int l = 0; l < e->n_layers; ++l) {
+        const LayerW& w = e->L[l];
+        if (!is_attn_layer(l)) {
+            gemm(e, w.W_in, kGdnInRows, kHidden, R, e->h, kHidden, e->proj, kGdnInRows);
+            GdnArgs g{};
+            g.proj = e->proj; g.o = e->o; g.conv_w = w.conv_w; g.A_log = w.A_log; g.dt_bias = w.dt_bias;
+            g.S = s->S; g.S_lane = s->S_lane(); g.S_slot = (long long)kGdnLayers * kSLayer;
+            g.S_layer = (long long)gdn_slot(l) * kSLayer;
+            g.win = s->win; g.W_lane = s->W_lane(); g.W_slot = (long long)kGdnLayers * 18432;
+            g.W_layer = (long long)gdn_slot(l) * 18432;
+            g.cur = s->cur_dev; g.nslots = s->nslots; g.ckpt = ckpt ? 1 : 0;
+            g.lane = e->rlane; g.T = T; g.nlanes = nl;
+            HCK(launch_gdn(g, cs, e->st));
+            gemm(e, w.W_out, kHidden, 2048, R, e->o, 2048, e->delta, kHidden, kAGatedNorm,
+                 e->proj + kGdnZOff, kGdnInRows, w.gnorm);
+        } else {
+            attention_layer(e, w, R, s->kc, s->vc, s->kv_lane(),
+                            (long long)attn_slot(l) * 2 * s->cap * 256, s->cap);
+        }
+        mlp_layer(e, w, R);
+        const bool lastl = l + 1 == e->n_layers;
+        const uint16_t* nw = lastl ? e->final_norm : e->L[l + 1].norm_in;
+        HCK(launch_addnorm(1, nullptr, nullptr, e->x, e->delta, nw, lastl ? e->nrm : e->h, R, e->st));
+    }
+}
+
+// lm_head + argmax over rows [row0, row0 + M) of e->nrm; tokens into e->tok_dev[0..M).
+void lm_head(q35_engine* e, int row0, int M, bool want_logits) {
+    GemmArgs a{};
+    a.W = e->E; a.N = kVocab; a.K = kHidden; a.M = M; a.X = e->nrm + (size_t)row0 * kHidden; a.ldx = kHidden;
+    if (want_logits) { ensure_logits(e, M); a.logits = e->logits_dev; a.ldl = kVocab; }
+    a.part_val = e->pval; a.part_idx = e->pidx; a.ldp = kVocab / 16;
+    HCK(launch_gemm(a, kAPlain, kEArgmax, e->st));
+    HCK(launch_argmax(e->pval, e->pidx, kVocab / 16, kVocab / 16, M, e->tok_dev, nullptr, e->st));
+}
+
+void save_hlast(q35_engine* e, q35_state* s, const std::vector<int>& src_rows, const std::vector<int>& lanes) {
+    const int n = (int)src_rows.size();
+    HCK(hipStreamSynchronize(e->st));
+    for (int i = 0; i < n; ++i) { e->h_src[i] = src_rows[i]; e->h_dst[i] = lanes[i]; }
+    HCK(hipMemcpyAsync(e->ridx_src, e->h_src, n * sizeof(int), hipMemcpyHostToDevice, e->st));
+    HCK(hipMemcpyAsync(e->ridx_dst, e->h_dst, n * sizeof(int), hipMemcpyHostToDevice, e->st));
+    HCK(launch_copy_rows(e->nrm, e->ridx_src, s->hlast, e->ridx_dst, n, kHidden, e->st));
+}
+
+void check_lane(q35_state* s, int lane) { REQ(lane >= 0 && lane < s->lanes, Q35_ERR_ARG, "lane out of range"); }
+void check_tok(int t) { REQ(t >= 0 && t < kVocab, Q35_ERR_ARG, "token out of range"); }
+
+// One MTP draft pass over n lanes (speccheck/mtp.py:57-83).  hsrc: [n][1024] device rows of
+// h; tokens, pos staged by the caller in h_tok / h_pos; slots = mtp_len + step.
+void mtp_draft_pass(q35_engine* e, q35_state* s, int n, const uint16_t* hsrc) {
+    REQ(s->mtp_cap > 0, Q35_ERR_STATE, "state has no MTP cache");
+    upload_rows(e, n);
+    HCK(launch_mtp_concat(e->tok_dev, e->E, hsrc, kHidden, e->mtp_pre_e, e->mtp_pre_h, e->cat, n, e->st));
+    gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, e->x, kHidden);
+    HCK(launch_addnorm(2, nullptr, nullptr, e->x, nullptr, e->M.norm_in, e->h, n, e->st));
+    attention_layer(e, e->M, n, s->mkc, s->mvc, s->mkv_lane(), 0, s->mtp_cap);
+    mlp_layer(e, e->M, n);
+    HCK(launch_addnorm(1, nullptr, nullptr, e->x, e->delta, e->mtp_norm, e->nrm, n, e->st));
+}
+
+int guard(const std::function<void()>& f) {
+    try {
+        f();
+        return Q35_OK;
+    } catch (const Q35Error& ex) {
+        g_err = ex.what();
+        return ex.code;
+    } catch (const std::exception& ex) {
+        g_err = ex.what();
+        return Q35_ERR_STATE;
+    }
+}
+}  // namespace
+
+// ====================================================================== C ABI
+extern "C" {
+
+const char* q35_last_error(void) { return g_err.c_str(); }
+
+int q35_create(const q35_config* cfg, q35_engine** out) {
+    return guard([&] {
+        REQ(cfg && out, Q35_ERR_ARG, "null argument");
+        REQ(cfg->max_rows > 0 && cfg->max_rows <= 65536, Q35_ERR_ARG, "max_rows out of range");
+        REQ(cfg->max_ctx > 0 && cfg->max_ctx <= 262144, Q35_ERR_ARG, "max_ctx out of range");
+        auto* e = new q35_engine();
+        e->device = cfg->device; e->R = cfg->max_rows; e->max_ctx = cfg->max_ctx; e->use_graph = cfg->use_graph;
+        HCK(hipSetDevice(e->device));
+        HCK(hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking));
+        HCK(hipEventCreate(&e->ev0));
+        HCK(hipEventCreate(&e->ev1));
+        plan_weights(e);
+        resolve_plain(e);
+        alloc_scratch(e);
+        *out = e;
+    });
+}
+
+int q35_destroy(q35_engine* e) {
+    return guard([&] {
+        if (!e) return;
+        hipStreamSynchronize(e->st);
+        void* ds[] = {e->blob, e->x, e->h, e->delta, e->nrm, e->proj, e->gu, e->aout, e->cat, e->o, e->q,
+                      e->sc, e->stats, e->part, e->pval, e->pidx, e->counters, e->tok_dev, e->rlane,
+                      e->rpos, e->rslot, e->ridx_src, e->ridx_dst, e->inv_freq, e->logits_dev};
+        for (void* p : ds) if (p) hipFree(p);
+        void* hs[] = {e->h_tok, e->h_lane, e->h_pos, e->h_slot, e->h_out, e->h_src, e->h_dst};
+        for (void* p : hs) if (p) hipHostFree(p);
+        hipEventDestroy(e->ev0);
+        hipEventDestroy(e->ev1);
+        hipStreamDestroy(e->st);
+        delete e;
+    });
+}
+
+int q35_init_random(q35_engine* e, uint64_t seed) {
+    return guard([&] {
+        REQ(e, Q35_ERR_ARG, "null engine");
+        const float scale = (float)(0.02 / 65536.0);
+        for (const auto& n : e->order) {
+            const Placement& p = e->reg.at(n);
+            const uint64_t key = stream_key(seed, n);
+            if (p.kind == kNormal) {
+                if (p.tiled) HCK(launch_gen_normal_tiled(key, scale, p.rows, p.cols, p.row_off, p.base, p.cols, e->st));
+                else HCK(launch_gen_normal_plain(key, scale, p.rows, p.base, e->st));
+            } else if (p.kind == kOne) {
+                HCK(hipMemsetD16Async((hipDeviceptr_t)p.base, 0x3F80, p.rows, e->st));
+            } else {
+                std::vector<uint16_t> v(p.rows);
+                for (int i = 0; i < p.rows; ++i) {
+                    float u = (float)(hmix(key + 3ull * i) >> 40) * (1.0f / 16777216.0f);
+                    double d = p.kind == kAlog ? std::log(1.0 + 15.0 * (double)u) : -1.0 + 2.0 * (double)u;
+                    v[i] = h_f2bf((float)d);
+                }
+                HCK(hipMemcpyAsync(p.base, v.data(), v.size() * 2, hipMemcpyHostToDevice, e->st));
+                HCK(hipStreamSynchronize(e->st));
+            }
+        }
+        HCK(hipStreamSynchronize(e->st));
+        e->weights_ready = true;
+    });
+}
+
+int q35_load_tensor(q35_engine* e, const char* name, const uint16_t* host, size_t n) {
+    return guard([&] {
+        REQ(e && name && host, Q35_ERR_ARG, "null argument");
+        auto it = e->reg.find(name);
+        REQ(it != e->reg.end(), Q35_ERR_ARG, std::string("unknown tensor ") + name);
+        const Placement& p = it->second;
+        REQ(n == (size_t)p.rows * p.cols, Q35_ERR_ARG, "element count mismatch");
+        if (p.tiled) {
+            uint16_t* tmp = dalloc<uint16_t>(n);
+            HCK(hipMemcpy(tmp, host, n * 2, hipMemcpyHostToDevice));
+            HCK(launch_tile(tmp, p.rows, p.cols, p.base, p.row_off, 0, e->st));
+            HCK(hipStreamSynchronize(e->st));
+            HCK(hipFree(tmp));
+        } else {
+            HCK(hipMemcpy(p.base, host, n * 2, hipMemcpyHostToDevice));
+        }
+        e->weights_ready = true;
+    });
+}
+
+int q35_read_tensor(q35_engine* e, const char* name, uint16_t* host, size_t n) {
+    return guard([&] {
+        REQ(e && name && host, Q35_ERR_ARG, "null argument");
+        auto it = e->reg.find(name);
+        REQ(it != e->reg.end(), Q35_ERR_ARG, std::string("unknown tensor ") + name);
+        const Placement& p = it->second;
+        REQ(n == (size_t)p.rows * p.cols, Q35_ERR_ARG, "element count mismatch");
+        if (p.tiled) {
+            uint16_t* tmp = dalloc<uint16_t>(n);
+            HCK(launch_tile(p.base, p.rows, p.cols, tmp, p.row_off, 1, e->st));
+            HCK(hipStreamSynchronize(e->st));
+            HCK(hipMemcpy(host, tmp, n * 2, hipMemcpyDeviceToHost));
+            HCK(hipFree(tmp));
+        } else {
+            HCK(hipStreamSynchronize(e->st));
+            HCK(hipMemcpy(host, p.base, n * 2, hipMemcpyDeviceToHost));
+        }
+    });
+}
+
+int q35_state_alloc(q35_engine* e, int lanes, int cap, int mtp_k, int mtp_cap, q35_state** out) {
+    return guard([&] {
+        REQ(e && out, Q35_ERR_ARG, "null argument");
+        REQ(lanes > 0 && cap > 0 && mtp_k >= 0 && mtp_k <= 4 && mtp_cap >= 0, Q35_ERR_ARG, "bad state shape");
+        REQ(cap <= e->max_ctx && mtp_cap <= e->max_ctx, Q35_ERR_CAP, "cap exceeds engine max_ctx");
+        auto* s = new q35_state();
+        s->lanes = lanes; s->cap = cap; s->mtp_cap = mtp_cap; s->mtp_k = mtp_k;
+        s->nslots = mtp_k > 0 ? mtp_k + 2 : 2;
+        s->S = dalloc<float>((size_t)lanes * s->S_lane());
+        s->win = dalloc<float>((size_t)lanes * s->W_lane());
+        s->kc = dalloc<uint16_t>((size_t)lanes * s->kv_lane());
+        s->vc = dalloc<uint16_t>((size_t)lanes * s->kv_lane());
+        if (mtp_cap > 0) {
+            s->mkc = dalloc<uint16_t>((size_t)lanes * s->mkv_lane());
+            s->mvc = dalloc<uint16_t>((size_t)lanes * s->mkv_lane());
+        }
+        s->hlast = dalloc<uint16_t>((size_t)lanes * kHidden);
+        s->cur_dev = dalloc<int>(lanes);
+        s->prefix.assign(lanes, 0);
+        s->mtp_len.assign(lanes, 0);
+        s->cur.assign(lanes, 0);
+        HCK(hipMemset(s->S, 0, (size_t)lanes * s->S_lane() * 4));
+        HCK(hipMemset(s->win, 0, (size_t)lanes * s->W_lane() * 4));
+        HCK(hipMemset(s->hlast, 0, (size_t)lanes * kHidden * 2));
+        *out = s;
+    });
+}
+
+int q35_state_free(q35_engine* e, q35_state* s) {
+    return guard([&] {
+        if (!s) return;
+        if (e) hipStreamSynchronize(e->st);
+        void* ds[] = {s->S, s->win, s->kc, s->vc, s->mkc, s->mvc, s->hlast, s->cur_dev};
+        for (void* p : ds) if (p) hipFree(p);
+        delete s;
+    });
+}
+
+int q35_state_reset(q35_engine* e, q35_state* s, const int32_t* lanes, int n) {
+    return guard([&] {
+        REQ(e && s, Q35_ERR_ARG, "null argument");
+        HCK(hipStreamSynchronize(e->st));
+        for (int i = 0; i < (lanes ? n : s->lanes); ++i) {
+            int l = lanes ? lanes[i] : i;
+            check_lane(s, l);
+            HCK(hipMemsetAsync(s->S + l * s->S_lane(), 0, s->S_lane() * 4, e->st));
+            HCK(hipMemsetAsync(s->win + l * s->W_lane(), 0, s->W_lane() * 4, e->st));
+            s->prefix[l] = 0; s->mtp_len[l] = 0; s->cur[l] = 0;
+        }
+        HCK(hipStreamSynchronize(e->st));
+    });
+}
+
+int q35_state_seed(q35_engine* e, q35_state* s, uint64_t seed, int prefix_len) {
+    return guard([&] {
+        REQ(e && s, Q35_ERR_ARG, "null argument");
+        REQ(prefix_len >= 0 && prefix_len < s->cap, Q35_ERR_CAP, "prefix_len must leave room in the cache");
+        const float s01 = (float)(0.1 / 65536.0), s1 = (float)(1.0 / 65536.0);
+        for (int l = 0; l < s->lanes; ++l) {
+            float* S0 = s->S + l * s->S_lane();   // slot 0
+            HCK(launch_gen_normal_f32(stream_key(seed, "state.gdn." + std::to_string(l)), s01,
+                                      (long long)kGdnLayers * kSLayer, S0, e->st));
+            HCK(hipMemsetAsync(s->win + l * s->W_lane(), 0, s->W_lane() * 4, e->st));
+            for (int a = 0; a < kAttnLayers; ++a)
+                for (int j = 0; j < kNkv; ++j) {
+                    size_t off = l * s->kv_lane() + ((size_t)(a * 2 + j) * s->cap) * 256;
+                    std::string tag = std::to_string(l) + "." + std::to_string(a) + "." + std::to_string(j);
+                    HCK(launch_gen_normal_plain(stream_key(seed, "state.k." + tag), s1, (long long)prefix_len * 256, s->kc + off, e->st));
+                    HCK(launch_gen_normal_plain(stream_key(seed, "state.v." + tag), s1, (long long)prefix_len * 256, s->vc + off, e->st));
+                }
+            s->prefix[l] = prefix_len; s->mtp_len[l] = 0; s->cur[l] = 0;
+        }
+        HCK(hipStreamSynchronize(e->st));
+    });
+}
+
+int q35_state_prefix_len(q35_engine* e, q35_state* s, int lane, int32_t* out) {
+    return guard([&] {
+        REQ(e && s && out, Q35_ERR_ARG, "null argument");
+        check_lane(s, lane);
+        *out = s->prefix[lane];
+    });
+}
+
+static void state_io(q35_engine* e, q35_state* s, int lane, int which, int n_slots, void* host,
+                     size_t bytes, bool write) {
+    REQ(e && s && host, Q35_ERR_ARG, "null argument");
+    check_lane(s, lane);
+    HCK(hipStreamSynchronize(e->st));
+    auto cp = [&](void* dev, size_t off_bytes, size_t nb) {
+        REQ(off_bytes + nb <= bytes, Q35_ERR_ARG, "host buffer too small");
+        if (write) HCK(hipMemcpy(dev, (char*)host + off_bytes, nb, hipMemcpyHostToDevice));
+        else HCK(hipMemcpy((char*)host + off_bytes, dev, nb, hipMemcpyDeviceToHost));
+    };
+    const int cur = s->cur[lane];
+    if (which == 0) {
+        cp(s->S + lane * s->S_lane() + (long long)cur * kGdnLayers * kSLayer, 0, (size_t)kGdnLayers * kSLayer * 4);
+    } else if (which == 1) {
+        cp(s->win + lane * s->W_lane() + (long long)cur * kGdnLayers * 18432, 0, (size_t)kGdnLayers * 18432 * 4);
+    } else if (which == 2 || which == 3) {
+        REQ(n_slots >= 0 && n_slots <= s->cap, Q35_ERR_ARG, "n_slots out of range");
+        uint16_t* base = (which == 2 ? s->kc : s->vc) + lane * s->kv_lane();
+        for (int a = 0; a < kAttnLayers * 2; ++a)
+            cp(base + (size_t)a * s->cap * 256, (size_t)a * n_slots * 512, (size_t)n_slots * 512);
+    } else if (which == 4 || which == 5) {
+        REQ(s->mtp_cap > 0 && n_slots >= 0 && n_slots <= s->mtp_cap, Q35_ERR_ARG, "n_slots out of range");
+        uint16_t* base = (which == 4 ? s->mkc : s->mvc) + lane * s->mkv_lane();
+        for (int a = 0; a < 2; ++a)
+            cp(base + (size_t)a * s->mtp_cap * 256, (size_t)a * n_slots * 512, (size_t)n_slots * 512);
+    } else {
+        throw Q35Error(Q35_ERR_ARG, "unknown state tensor");
+    }
+}
+
+int q35_state_read(q35_engine* e, q35_state* s, int lane, int which, int n_slots, void* host, size_t bytes) {
+    return guard([&] { state_io(e, s, lane, which, n_slots, host, bytes, false); });
+}
+int q35_state_write(q35_engine* e, q35_state* s, int lane, int which, int n_slots, const void* host, size_t bytes) {
+    return guard([&] { state_io(e, s, lane, which, n_slots, const_cast<void*>(host), bytes, true); });
+}
+
+int q35_prefill(q35_engine* e, q35_state* s, int lane, const int32_t* ids, int n, int32_t* y0, float* logits) {
+    return guard([&] {
+        REQ(e && s && ids && y0, Q35_ERR_ARG, "null argument");
+        REQ(n > 0, Q35_ERR_ARG, "empty prompt");
+        check_lane(s, lane);
+        REQ(s->prefix[lane] + n <= s->cap, Q35_ERR_CAP, "prompt exceeds the lane's cache capacity");
+        for (int i = 0; i < n; ++i) check_tok(ids[i]);
+        int done = 0;
+        while (done < n) {
+            const int T = std::min(e->R, n - done);
+            HCK(hipStreamSynchronize(e->st));
+            for (int t = 0; t < T; ++t) {
+                e->h_tok[t] = ids[done + t];
+                e->h_lane[t] = lane;
+                e->h_pos[t] = s->prefix[lane] + t;
+                e->h_slot[t] = s->prefix[lane] + t;
+            }
+            body(e, s, T, T, false);
+            s->prefix[lane] += T;
+            s->cur[lane] = (s->cur[lane] + 1) % s->nslots;
+            done += T;
+            if (done == n) {
+                lm_head(e, T - 1, 1, logits != nullptr);
+                save_hlast(e, s, {T - 1}, {lane});
+            }
+        }
+        HCK(hipMemcpyAsync(e->h_out, e->tok_dev, sizeof(int), hipMemcpyDeviceToHost, e->st));
+        if (logits) HCK(hipMemcpyAsync(logits, e->logits_dev, (size_t)kVocab * 4, hipMemcpyDeviceToHost, e->st));
+        HCK(hipStreamSynchronize(e->st));
+        *y0 = e->h_out[0];
+    });
+}
+
+int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* tokens,
+                    int32_t* out_tok, float* out_logits) {
+    return guard([&] {
+        REQ(e && s && tokens && out_tok, Q35_ERR_ARG, "null argument");
+        REQ(n > 0 && n <= e->R, Q35_ERR_CAP, "lane count exceeds max_rows");
+        HCK(hipStreamSynchronize(e->st));
+        std::vector<int> ls(n);
+        for (int i = 0; i < n; ++i) {
+            const int l = lanes ? lanes[i] : i;
+            check_lane(s, l);
+            check_tok(tokens[i]);
+            REQ(s->prefix[l] < s->cap, Q35_ERR_CAP, "lane cache is full");
+            for (int j = 0; j < i; ++j) REQ(ls[j] != l, Q35_ERR_ARG, "duplicate lane in one step");
+            ls[i] = l;
+            e->h_tok[i] = tokens[i]; e->h_lane[i] = l; e->h_pos[i] = s->prefix[l]; e->h_slot[i] = s->prefix[l];
+        }
+        body(e, s, n, 1, false);
+        lm_head(e, 0, n, out_logits != nullptr);
+        std::vector<int> rows(n);
+        for (int i = 0; i < n; ++i) {
+            rows[i] = i;
+            s->prefix[ls[i]] += 1;
+            s->cur[ls[i]] = (s->cur[ls[i]] + 1) % s->nslots;
+        }
+        HCK(hipMemcpyAsync(e->h_out, e->tok_dev, n * sizeof(int), hipMemcpyDeviceToHost, e->st));
+        save_hlast(e, s, rows, ls);
+        if (out_logits) HCK(hipMemcpyAsync(out_logits, e->logits_dev, (size_t)n * kVocab * 4, hipMemcpyDeviceToHost, e->st));
+        HCK(hipStreamSynchronize(e->st));
+        for (int i = 0; i < n; ++i) out_tok[i] = e->h_out[i];
+    });
+}
+
+int q35_mtp_draft(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* y,
+                  const int32_t* pos, int step, int32_t* out_tok, uint16_t* out_xd, float* out_logits) {
+    return guard([&] {
+        REQ(e && s && y && pos && out_tok, Q35_ERR_ARG, "null argument");
+        REQ(n > 0 && n <= e->R, Q35_ERR_CAP, "lane count exceeds max_rows");
+        HCK(hipStreamSynchronize(e->st));
+        std::vector<int> ls(n);
+        for (int i = 0; i < n; ++i) {
+            const int l = lanes ? lanes[i] : i;
+            check_lane(s, l);
+            check_tok(y[i]);
+            REQ(s->mtp_len[l] + step < s->mtp_cap, Q35_ERR_CAP, "MTP cache is full");
+            ls[i] = l;
+            e->h_tok[i] = y[i]; e->h_lane[i] = l; e->h_pos[i] = pos[i]; e->h_slot[i] = s->mtp_len[l] + step;
+            e->h_src[i] = l; e->h_dst[i] = i;
+        }
+        // h rows: lane's hlast (post-final-norm row of the last body) -> e->h as scratch source
+        HCK(hipMemcpyAsync(e->ridx_src, e->h_src, n * sizeof(int), hipMemcpyHostToDevice, e->st));
+        HCK(hipMemcpyAsync(e->ridx_dst, e->h_dst, n * sizeof(int), hipMemcpyHostToDevice, e->st));
+        HCK(launch_copy_rows(s->hlast, e->ridx_src, e->delta, e->ridx_dst, n, kHidden, e->st));
+        mtp_draft_pass(e, s, n, e->delta);
+        lm_head(e, 0, n, out_logits != nullptr);
+        // x_d becomes the lane's h for the next draft (speccheck/mtp.py:153-157)
+        std::vector<int> rows(n);
+        for (int i = 0; i < n; ++i) rows[i] = i;
+        HCK(hipMemcpyAsync(e->h_out, e->tok_dev, n * sizeof(int), hipMemcpyDeviceToHost, e->st));
+        if (out_xd) HCK(hipMemcpyAsync(out_xd, e->nrm, (size_t)n * kHidden * 2, hipMemcpyDeviceToHost, e->st));
+        save_hlast(e, s, rows, ls);
+        if (out_logits) HCK(hipMemcpyAsync(out_logits, e->logits_dev, (size_t)n * kVocab * 4, hipMemcpyDeviceToHost, e->st));
+        HCK(hipStreamSynchronize(e->st));
+        for (int i = 0; i < n; ++i) out_tok[i] = e->h_out[i];
+    });
+}
+
+int q35_mtp_round(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* cur,
+                  int k, int32_t* emit, int32_t* n_emit, int64_t* stats) {
+    return guard([&] {
+        REQ(e && s && cur && emit && n_emit, Q35_ERR_ARG, "null argument");
+        REQ(k >= 1 && k <= s->mtp_k, Q35_ERR_STATE, "k exceeds the state's MTP slots");
+        REQ(n > 0 && n * (k + 1) <= e->R, Q35_ERR_CAP, "rows exceed max_rows");
+        std::vector<int> ls(n), P(n);
+        for (int i = 0; i < n; ++i) {
+            ls[i] = lanes ? lanes[i] : i;
+            check_lane(s, ls[i]);
+            P[i] = s->prefix[ls[i]];
+            REQ(P[i] + k + 1 <= s->cap, Q35_ERR_CAP, "lane cache is full");
+        }
+        // each draft leaves x_d in hlast (the next draft's h); the verify row a replaces it
+        std::vector<std::vector<int>> drafts(n, std::vector<int>(k));
+        std::vector<int32_t> y(cur, cur + n), pos(n), dt(n);
+        for (int j = 0; j < k; ++j) {
+            for (int i = 0; i < n; ++i) pos[i] = P[i] + 1 + j;
+            int rc = q35_mtp_draft(e, s, ls.data(), n, y.data(), pos.data(), j, dt.data(), nullptr, nullptr);
+            if (rc) throw Q35Error(rc, g_err);
+            for (int i = 0; i < n; ++i) { drafts[i][j] = dt[i]; y[i] = dt[i]; }
+        }
+        // verify body over [cur, d1..dk] per lane with per-row GDN checkpoints
+        HCK(hipStreamSynchronize(e->st));
+        const int T = k + 1, R = n * T;
+        for (int i = 0; i < n; ++i)
+            for (int t = 0; t < T; ++t) {
+                int r = i * T + t;
+                e->h_tok[r] = t == 0 ? cur[i] : drafts[i][t - 1];
+                e->h_lane[r] = ls[i]; e->h_pos[r] = P[i] + t; e->h_slot[r] = P[i] + t;
+            }
+        body(e, s, R, T, true);
+        lm_head(e, 0, R, false);
+        HCK(hipMemcpyAsync(e->h_out, e->tok_dev, R * sizeof(int), hipMemcpyDeviceToHost, e->st));
+        HCK(hipStreamSynchronize(e->st));
+        std::vector<int> rows(n);
+        for (int i = 0; i < n; ++i) {
+            const int* tgt = e->h_out + i * T;
+            int a = 0;
+            while (a < k && drafts[i][a] == tgt[a]) ++a;
+            int m = 0;
+            for (int j = 0; j < a; ++j) emit[i * (k + 1) + m++] = drafts[i][j];
+            emit[i * (k + 1) + m++] = tgt[a];
+            n_emit[i] = m;
+            const int l = ls[i];
+            s->prefix[l] = P[i] + a + 1;
+            s->cur[l] = (s->cur[l] + 1 + a) % s->nslots;
+            if (a == k) s->mtp_len[l] += k;
+            rows[i] = i * T + a;
+            if (stats) { stats[0] += k; stats[1] += a; stats[2] += 1; stats[3] += T; }
+        }
+        save_hlast(e, s, rows, ls);
+        HCK(hipStreamSynchronize(e->st));
+    });
+}
+
+int q35_op_tile_weight(q35_engine* e, const uint16_t* w, int N, int K, uint16_t* wt) {
+    return guard([&] {
+        REQ(e && w && wt && N > 0 && N % 16 == 0 && K > 0 && K % 256 == 0, Q35_ERR_ARG, "bad weight shape");
+        HCK(launch_tile(w, N, K, wt, 0, 0, e->st));
+    });
+}
+
+int q35_op_gemm(q35_engine* e, const uint16_t* wt, int N, int K, const uint16_t* x, int M, uint16_t* y) {
+    return guard([&] {
+        REQ(e && wt && x && y && M > 0 && N % 16 == 0 && K % 256 == 0 && K <= 4096, Q35_ERR_ARG, "bad gemm shape");
+        gemm(e, wt, N, K, M, x, K, y, N);
+    });
+}
+
+int q35_op_lm_head_argmax(q35_engine* e, const uint16_t* x, int M, int32_t* tok, float* logits) {
+    return guard([&] {
+        REQ(e && x && tok && M > 0 && M <= e->R, Q35_ERR_ARG, "bad lm_head call");
+        GemmArgs a{};
+        a.W = e->E; a.N = kVocab; a.K = kHidden; a.M = M; a.X = x; a.ldx = kHidden;
+        a.logits = logits; a.ldl = kVocab;
+        a.part_val = e->pval; a.part_idx = e->pidx; a.ldp = kVocab / 16;
+        HCK(launch_gemm(a, kAPlain, kEArgmax, e->st));
+        HCK(launch_argmax(e->pval, e->pidx, kVocab / 16, kVocab / 16, M, tok, nullptr, e->st));
+    });
+}
+
+int q35_set_option(q35_engine* e, const char* name, int value) {
+    return guard([&] {
+        REQ(e && name, Q35_ERR_ARG, "null argument");
+        std::string n(name);
+        if (n == "layers") {
+            REQ(value >= 1 && value <= kLayers, Q35_ERR_ARG, "layers out of range");
+            e->n_layers = value;
+        } else if (n == "graph") {
+            e->use_graph = value;
+        } else {
+            throw Q35Error(Q35_ERR_ARG, "unknown option " + n);
+        }
+    });
+}
+
+int q35_read_scratch(q35_engine* e, const char* name, void* host, size_t bytes) {
+    return guard([&] {
+        REQ(e && name && host, Q35_ERR_ARG, "null argument");
+        std::string n(name);
+        const void* p = nullptr;
+        size_t cap = 0;
+        const size_t R = e->R;
+        if (n == "x") { p = e->x; cap = R * kHidden * 2; }
+        else if (n == "h") { p = e->h; cap = R * kHidden * 2; }
+        else if (n == "nrm") { p = e->nrm; cap = R * kHidden * 2; }
+        else if (n == "delta") { p = e->delta; cap = R * kHidden * 2; }
+        else if (n == "proj") { p = e->proj; cap = R * kGdnInRows * 2; }
+        else if (n == "o") { p = e->o; cap = R * 2048 * 4; }
+        else if (n == "gu") { p = e->gu; cap = R * kGuRows * 2; }
+        else if (n == "aout") { p = e->aout; cap = R * 2048 * 2; }
+        else if (n == "q") { p = e->q; cap = R * kNq * 256 * 4; }
+        else throw Q35Error(Q35_ERR_ARG, "unknown scratch " + n);
+        REQ(bytes <= cap, Q35_ERR_ARG, "read exceeds scratch size");
+        HCK(hipStreamSynchronize(e->st));
+        HCK(hipMemcpy(host, p, bytes, hipMemcpyDeviceToHost));
+    });
+}
+
+int q35_sync(q35_engine* e) {
+    return guard([&] { REQ(e, Q35_ERR_ARG, "null engine"); HCK(hipStreamSynchronize(e->st)); });
+}
+int q35_timer_begin(q35_engine* e) {
+    return guard([&] { REQ(e, Q35_ERR_ARG, "null engine"); HCK(hipEventRecord(e->ev0, e->st)); });
+}
+int q35_timer_end(q35_engine* e, float* ms) {
+    return guard([&] {
+        REQ(e && ms, Q35_ERR_ARG, "null argument");
+        HCK(hipEventRecord(e->ev1, e->st));
+        HCK(hipEventSynchronize(e->ev1));
+        HCK(hipEventElapsedTime(ms, e->ev0, e->ev1));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,162 @@
+// GatedDeltaNet mixer for R = nlanes x T rows: causal conv (kernel 4) + SiLU, gates,
+// L2 norms and the delta-rule recurrence, with the fp32 state held in VGPRs across the
+// T rows of a lane. Output o (f32, pre gated-norm); the gated RMSNorm is fused into the
+// out_proj GEMM's A operand (q35_gemm.hip).
+//
+// Math (speccheck/specimpl.py:252-294): u = bf16silu(bf16(sum_j win[j] C[:,j])) over the
+// pre-conv window (f32 taps in tap order), beta = sigmoid(b),
+// g = -exp(A_log) softplus(a + dt_bias), q~ = q rsqrt(|q|^2+1e-6) 128^-1/2,
+// k~ = k rsqrt(|k|^2+1e-6); S = e^g S; r = S^T k~; dv = beta (v - r); S += k~ dv^T;
+// o = S^T q~. Replaces engine/kernels_gdn.cpp:35-536 (conv, gates, rec) of the reference.
+//
+// The state is never updated in place (the conv window's q/k channels are read by every
+// column-slice block of a head): the state after row t goes to slot (cur + 1 + t) % nslots,
+// for every row when `ckpt` is set (MTP verify candidates), else only the last row's
+// state, to slot (cur + 1) % nslots;
+// the engine advances `cur` after the step.
+//
+// Grid: (lane group, head, column slice). A block owns VC = 128/CS value columns of one
+// head; thread (jl, kg) holds S[kg*KR .. kg*KR+KR)[jl] in registers.
+#include "q35_common.h"
+#include "q35_kernels.h"
+
+namespace q35 {
+
+template <int CS>
+__global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
+    constexpr int VC = 128 / CS;
+    constexpr int NKG = 256 / VC;
+    constexpr int KR = 128 / NKG;
+    const int gi = blockIdx.x, h = blockIdx.y, cs = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int jl = tid % VC, kg = tid / VC;
+    const int lane = a.lane[gi * a.T];
+    const int cur = a.cur ? a.cur[lane] : 0;
+
+    __shared__ float qs[128], ks[128], vs[VC];
+    __shared__ float red_r[NKG][VC], red_o[NKG][VC];
+    __shared__ float wred[4];
+    __shared__ float gate_s[2];
+
+    float* Sbase = a.S + lane * a.S_lane + a.S_layer + (long long)h * 16384;
+    float* Wbase = a.win + lane * a.W_lane + a.W_layer;
+    const float* Sin = Sbase + cur * a.S_slot;
+    const float* Win = Wbase + cur * a.W_slot;
+
+    // channels: tid < 128 -> q channel, else k channel; tid < VC also a v channel
+    const int cqk = tid < 128 ? h * 128 + tid : 2048 + h * 128 + (tid - 128);
+    const int cv = 4096 + h * 128 + cs * VC + tid;
+    const bool hasv = tid < VC;
+    float w0 = Win[cqk], w1 = Win[6144 + cqk], w2 = Win[12288 + cqk];
+    float v0 = 0.f, v1 = 0.f, v2 = 0.f;
+    if (hasv) { v0 = Win[cv]; v1 = Win[6144 + cv]; v2 = Win[12288 + cv]; }
+    float cw[4], cvw[4] = {0.f, 0.f, 0.f, 0.f};
+    {
+        uint2 c = *(const uint2*)(a.conv_w + (size_t)cqk * 4);
+        cw[0] = __uint_as_float(c.x << 16); cw[1] = __uint_as_float(c.x & 0xffff0000u);
+        cw[2] = __uint_as_float(c.y << 16); cw[3] = __uint_as_float(c.y & 0xffff0000u);
+        if (hasv) {
+            uint2 d = *(const uint2*)(a.conv_w + (size_t)cv * 4);
+            cvw[0] = __uint_as_float(d.x << 16); cvw[1] = __uint_as_float(d.x & 0xffff0000u);
+            cvw[2] = __uint_as_float(d.y << 16); cvw[3] = __uint_as_float(d.y & 0xffff0000u);
+        }
+    }
+    float s[KR];
+#pragma unroll
+    for (int i = 0; i < KR; ++i) s[i] = Sin[(kg * KR + i) * 128 + cs * VC + jl];
+
+    const float A = -expf(bf2f(a.A_log[h]));
+    const float dtb = bf2f(a.dt_bias[h]);
+
+    for (int t = 0; t < a.T; ++t) {
+        const int r = gi * a.T + t;
+        const uint16_t* pr = a.proj + (size_t)r * kGdnInRows;
+        // causal conv: taps over [w0, w1, w2, raw] in order, f32, one rounding, bf16 SiLU
+        {
+            float x = bf2f(pr[cqk]);
+            float u = 0.f;
+            u = u + w0 * cw[0]; u = u + w1 * cw[1]; u = u + w2 * cw[2]; u = u + x * cw[3];
+            float uq = rbf(silu_f(rbf(u)));
+            w0 = w1; w1 = w2; w2 = x;
+            if (tid < 128) qs[tid] = uq; else ks[tid - 128] = uq;
+            if (hasv) {
+                float xv = bf2f(pr[cv]);
+                float uv = 0.f;
+                uv = uv + v0 * cvw[0]; uv = uv + v1 * cvw[1]; uv = uv + v2 * cvw[2]; uv = uv + xv * cvw[3];
+                vs[tid] = rbf(silu_f(rbf(uv)));
+                v0 = v1; v1 = v2; v2 = xv;
+            }
+            // squared norms: waves 0-1 hold q, waves 2-3 hold k
+            float ss = wave_sum(uq * uq);
+            if ((tid & 63) == 0) wred[tid >> 6] = ss;
+            if (tid == 0) {
+                float bb = bf2f(pr[kGdnBOff + h]);
+                float aa = bf2f(pr[kGdnAOff + h]) + dtb;
+                float sp = aa > 20.f ? aa : log1pf(expf(aa));
+                float g = A * sp;
+                gate_s[0] = expf(g);
+                gate_s[1] = sigmoid_f(bb);
+            }
+        }
+        __syncthreads();
+        {
+            const float rq = rsqrtf((wred[0] + wred[1]) + 1e-6f);
+            const float rk = rsqrtf((wred[2] + wred[3]) + 1e-6f);
+            if (tid < 128) qs[tid] = __fmul_rn(__fmul_rn(qs[tid], rq), 0.08838834764831845f);
+            else ks[tid - 128] = __fmul_rn(ks[tid - 128], rk);
+        }
+        __syncthreads();
+        const float gam = gate_s[0], beta = gate_s[1];
+        float rp = 0.f;
+#pragma unroll
+        for (int i = 0; i < KR; ++i) {
+            s[i] = __fmul_rn(s[i], gam);
+            rp = fmaf(s[i], ks[kg * KR + i], rp);
+        }
+        red_r[kg][jl] = rp;
+        __syncthreads();
+        float rj = 0.f;
+#pragma unroll
+        for (int i = 0; i < NKG; ++i) rj += red_r[i][jl];
+        const float dv = __fmul_rn(beta, vs[jl] - rj);
+        float op = 0.f;
+#pragma unroll
+        for (int i = 0; i < KR; ++i) {
+            s[i] = __fadd_rn(s[i], __fmul_rn(ks[kg * KR + i], dv));
+            op = fmaf(qs[kg * KR + i], s[i], op);
+        }
+        red_o[kg][jl] = op;
+        __syncthreads();
+        if (kg == 0) {
+            float oj = 0.f;
+#pragma unroll
+            for (int i = 0; i < NKG; ++i) oj += red_o[i][jl];
+            a.o[(size_t)r * 2048 + h * 128 + cs * VC + jl] = oj;
+        }
+        if (a.ckpt || t == a.T - 1) {
+            const int slot = (cur + 1 + (a.ckpt ? t : 0)) % a.nslots;
+            float* So = Sbase + slot * a.S_slot;
+#pragma unroll
+            for (int i = 0; i < KR; ++i) So[(kg * KR + i) * 128 + cs * VC + jl] = s[i];
+            float* Wo = Wbase + slot * a.W_slot;
+            if (cs == 0) { Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2; }
+            if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
+        }
+        __syncthreads();
+    }
+}
+
+hipError_t launch_gdn(const GdnArgs& a, int col_slices, hipStream_t st) {
+    if (a.nlanes <= 0 || a.T <= 0) return hipErrorInvalidValue;
+    dim3 grid(a.nlanes, kHv, col_slices);
+    switch (col_slices) {
+        case 1: hipLaunchKernelGGL(gdn_kernel<1>, grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL(gdn_kernel<2>, grid, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL(gdn_kernel<4>, grid, dim3(256), 0, st, a); break;
+        case 8: hipLaunchKernelGGL(gdn_kernel<8>, grid, dim3(256), 0, st, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace q35

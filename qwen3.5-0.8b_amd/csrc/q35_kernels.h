@@ -1,0 +1,107 @@
+// Internal launcher interface between the engine (q35_engine.cpp) and the device code.
+// Raw device pointers, no synchronisation; every launcher returns the launch status.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q35 {
+
+enum { kAPlain = 0, kASiluMul = 1, kAGatedNorm = 2 };
+enum { kEStore = 0, kEArgmax = 1 };
+
+struct GemmArgs {
+    const uint16_t* W;     // tiled [N/16][K/256] x 8 KiB
+    int N, K, M;
+    const void* X;         // A source (bf16, or f32 o for kAGatedNorm)
+    int ldx;
+    const void* X2;        // second source: u (kASiluMul) or z (kAGatedNorm)
+    int ldx2;
+    const uint16_t* aux_w; // gated-norm weight [128]
+    uint16_t* Y;           // kEStore output
+    int ldy;
+    float* logits;         // kEArgmax: optional f32 copy of the bf16 logits
+    int ldl;
+    float* part_val;       // kEArgmax: per-(row, tile) max
+    int* part_idx;
+    int ldp;
+};
+hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st);
+hipError_t launch_argmax(const float* pv, const int* pi, int ldp, int n, int rows, int* tok,
+                         float* val, hipStream_t st);
+
+// Row metadata of one engine call: rows are grouped by lane, T consecutive rows per lane.
+struct RowMeta {
+    const int* lane;       // [R] state lane of the row
+    const int* pos;        // [R] rope position
+    const int* slot;       // [R] cache slot written by this row; the row attends to slots [0, slot]
+};
+
+// Residual add + zero-centred RMSNorm (specimpl.py:135-139, pairing :426-451).
+//   mode 0: x = E[tok[r]];  mode 1: x = bf16(x + delta);  mode 2: x unchanged
+//   then h = rmsnorm_zc(x, w) (skipped when h == nullptr)
+hipError_t launch_addnorm(int mode, const int* tok, const uint16_t* E, uint16_t* x,
+                          const uint16_t* delta, const uint16_t* w, uint16_t* h, int rows,
+                          hipStream_t st);
+// MTP fc input: cat[rmsnorm_zc(E[tok], we) | rmsnorm_zc(hin, wh)] -> out [rows][2048]
+hipError_t launch_mtp_concat(const int* tok, const uint16_t* E, const uint16_t* hin, int ldh,
+                             const uint16_t* we, const uint16_t* wh, uint16_t* out, int rows,
+                             hipStream_t st);
+
+struct GdnArgs {
+    const uint16_t* proj;      // [R][8224]: qkv | z | b | a
+    float* o;                  // [R][2048] f32 output (pre gated-norm)
+    const uint16_t* conv_w;    // [6144][4]
+    const uint16_t* A_log;     // [16]
+    const uint16_t* dt_bias;   // [16]
+    // State S f32 [16][128][128] and conv window f32 [3][6144] of (lane, slot, layer) at
+    // base + lane*X_lane + slot*X_slot + X_layer (element offsets).
+    float* S;
+    long long S_lane, S_slot, S_layer;
+    float* win;
+    long long W_lane, W_slot, W_layer;
+    const int* cur;            // [lanes] current slot of each state lane
+    int nslots;
+    int ckpt;                  // 0: state after the last row -> slot (cur + 1) % nslots;
+                               // 1: state after row t -> slot (cur + 1 + t) % nslots
+    const int* lane;           // [R] state lane of each row
+    int T;                     // rows per lane (rows of one lane are consecutive)
+    int nlanes;
+};
+hipError_t launch_gdn(const GdnArgs& a, int col_slices, hipStream_t st);
+
+struct AttnArgs {
+    const uint16_t* proj;  // [R][5120]: (q|gate) x 8 heads interleaved, k, v
+    const uint16_t* q_norm;    // [256]
+    const uint16_t* k_norm;    // [256]
+    uint16_t* kc;          // key cache base: lane stride kv_lane, layer at + kv_layer_off, [2][cap][256]
+    uint16_t* vc;
+    long long kv_lane, kv_layer_off;
+    int cap;
+    RowMeta rm;
+    float* q;              // scratch [R][8][256] f32 post-rope q
+    float* sc;             // scratch scores [R][8][sc_ld]
+    int sc_ld;
+    float* stats;          // scratch [R][8][max_chunks][2]
+    float* part;           // scratch [R][max_chunks][8][256]
+    int* counters;         // [R][2] zero-initialised, restored to zero by the kernel
+    int max_chunks;
+    uint16_t* out;         // [R][2048] gated attention output (input of o_proj)
+    int R;
+    const float* inv_freq; // [32] f32 rope inverse frequencies
+};
+hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
+
+// Synthetic init (portable stream, see q35_init.hip).
+hipError_t launch_gen_normal_tiled(uint64_t key, float scale, int N, int K, int row_off_dst,
+                                   uint16_t* dst, int Kdst, hipStream_t st);
+hipError_t launch_gen_normal_plain(uint64_t key, float scale, long long n, uint16_t* dst,
+                                   hipStream_t st);
+hipError_t launch_gen_normal_f32(uint64_t key, float scale, long long n, float* dst,
+                                 hipStream_t st);
+
+hipError_t launch_tile(const uint16_t* src, int N, int K, uint16_t* dst, int row_off, int inverse,
+                       hipStream_t st);
+hipError_t launch_copy_rows(const uint16_t* src, const int* src_rows, uint16_t* dst, const int* dst_rows,
+                            int n, int width, hipStream_t st);
+
+}  // namespace q35

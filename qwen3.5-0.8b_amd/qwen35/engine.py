@@ -1,0 +1,308 @@
+"""ctypes host over libqwen35.so (include/q35.h)."""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+VOCAB = 248320
+HIDDEN = 1024
+EOS_IDS = (248046, 248044)       # speccheck/specimpl.py:38-40
+
+_PKG = Path(__file__).resolve().parents[1]
+_LIB = None
+
+
+class EngineError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"q35 error {code}: {msg}")
+        self.code = code
+
+
+def lib_path() -> Path:
+    return _PKG / "libqwen35.so"
+
+
+class _Config(C.Structure):
+    _fields_ = [("device", C.c_int), ("max_rows", C.c_int), ("max_ctx", C.c_int),
+                ("use_graph", C.c_int)]
+
+
+_SIGS = {
+    "q35_last_error": ([], C.c_char_p),
+    "q35_create": ([C.POINTER(_Config), C.POINTER(C.c_void_p)], C.c_int),
+    "q35_destroy": ([C.c_void_p], C.c_int),
+    "q35_init_random": ([C.c_void_p, C.c_uint64], C.c_int),
+    "q35_load_tensor": ([C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t], C.c_int),
+    "q35_read_tensor": ([C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t], C.c_int),
+    "q35_state_alloc": ([C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_void_p)], C.c_int),
+    "q35_state_free": ([C.c_void_p, C.c_void_p], C.c_int),
+    "q35_state_reset": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int], C.c_int),
+    "q35_state_seed": ([C.c_void_p, C.c_void_p, C.c_uint64, C.c_int], C.c_int),
+    "q35_state_prefix_len": ([C.c_void_p, C.c_void_p, C.c_int, C.POINTER(C.c_int32)], C.c_int),
+    "q35_state_read": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_size_t], C.c_int),
+    "q35_state_write": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_size_t], C.c_int),
+    "q35_prefill": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.POINTER(C.c_int32), C.c_void_p], C.c_int),
+    "q35_decode_step": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "q35_mtp_draft": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int,
+                       C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "q35_mtp_round": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
+                       C.c_void_p, C.c_void_p], C.c_int),
+    "q35_op_tile_weight": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p], C.c_int),
+    "q35_op_gemm": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p], C.c_int),
+    "q35_op_lm_head_argmax": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p], C.c_int),
+    "q35_sync": ([C.c_void_p], C.c_int),
+    "q35_set_option": ([C.c_void_p, C.c_char_p, C.c_int], C.c_int),
+    "q35_read_scratch": ([C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t], C.c_int),
+    "q35_timer_begin": ([C.c_void_p], C.c_int),
+    "q35_timer_end": ([C.c_void_p, C.POINTER(C.c_float)], C.c_int),
+}
+
+
+def load_library():
+    """Loads libqwen35.so (raises if it was not built: there is no fallback path)."""
+    global _LIB
+    if _LIB is None:
+        p = lib_path()
+        if not p.exists():
+            raise EngineError(-3, f"{p} is missing; build it with qwen3.5-0.8b_amd/build.py")
+        L = C.CDLL(str(p))
+        for name, (args, res) in _SIGS.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = res
+        _LIB = L
+    return _LIB
+
+
+def _ck(rc: int):
+    if rc != 0:
+        raise EngineError(rc, load_library().q35_last_error().decode())
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int32))
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class Engine:
+    """Weights + scratch + stream (WeightStore / DecodeScratch of the reference)."""
+
+    def __init__(self, max_rows: int = 256, max_ctx: int = 4352, device: int = 0, seed: int | None = 0,
+                 use_graph: bool = False):
+        L = load_library()
+        cfg = _Config(device, max_rows, max_ctx, int(use_graph))
+        h = C.c_void_p()
+        _ck(L.q35_create(C.byref(cfg), C.byref(h)))
+        self.h = h
+        self.max_rows = max_rows
+        self.max_ctx = max_ctx
+        if seed is not None:
+            self.init_random(seed)
+
+    def init_random(self, seed: int):
+        _ck(load_library().q35_init_random(self.h, seed))
+
+    def load_tensor(self, name: str, bits: np.ndarray):
+        b = np.ascontiguousarray(bits, dtype=np.uint16)
+        _ck(load_library().q35_load_tensor(self.h, name.encode(), _p(b), b.size))
+
+    def read_tensor(self, name: str, n: int) -> np.ndarray:
+        out = np.empty(n, dtype=np.uint16)
+        _ck(load_library().q35_read_tensor(self.h, name.encode(), _p(out), n))
+        return out
+
+    def set_option(self, name: str, value: int):
+        _ck(load_library().q35_set_option(self.h, name.encode(), int(value)))
+
+    def read_scratch(self, name: str, shape, dtype) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        _ck(load_library().q35_read_scratch(self.h, name.encode(), _p(out), out.nbytes))
+        return out
+
+    def sync(self):
+        _ck(load_library().q35_sync(self.h))
+
+    def close(self):
+        if self.h:
+            load_library().q35_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # per-op (device pointers as ints, e.g. torch tensor.data_ptr())
+    def op_tile_weight(self, w_ptr: int, N: int, K: int, wt_ptr: int):
+        _ck(load_library().q35_op_tile_weight(self.h, C.c_void_p(w_ptr), N, K, C.c_void_p(wt_ptr)))
+
+    def op_gemm(self, wt_ptr: int, N: int, K: int, x_ptr: int, M: int, y_ptr: int):
+        _ck(load_library().q35_op_gemm(self.h, C.c_void_p(wt_ptr), N, K, C.c_void_p(x_ptr), M, C.c_void_p(y_ptr)))
+
+    def op_lm_head_argmax(self, x_ptr: int, M: int, tok_ptr: int, logits_ptr: int = 0):
+        _ck(load_library().q35_op_lm_head_argmax(self.h, C.c_void_p(x_ptr), M, C.c_void_p(tok_ptr),
+                                                 C.c_void_p(logits_ptr) if logits_ptr else None))
+
+    def timer_begin(self):
+        _ck(load_library().q35_timer_begin(self.h))
+
+    def timer_end(self) -> float:
+        ms = C.c_float()
+        _ck(load_library().q35_timer_end(self.h, C.byref(ms)))
+        return ms.value
+
+
+class State:
+    """`lanes` independent requests (RequestState, engine/state.h:83-116)."""
+
+    def __init__(self, eng: Engine, lanes: int = 1, cap: int = 4352, mtp_k: int = 0, mtp_cap: int = 0):
+        self.eng = eng
+        self.lanes, self.cap, self.mtp_k, self.mtp_cap = lanes, cap, mtp_k, mtp_cap
+        h = C.c_void_p()
+        _ck(load_library().q35_state_alloc(eng.h, lanes, cap, mtp_k, mtp_cap, C.byref(h)))
+        self.h = h
+
+    def reset(self, lanes=None):
+        if lanes is None:
+            _ck(load_library().q35_state_reset(self.eng.h, self.h, None, 0))
+        else:
+            a = _i32(lanes)
+            _ck(load_library().q35_state_reset(self.eng.h, self.h, _p(a), a.size))
+
+    def seed(self, seed: int, prefix_len: int):
+        _ck(load_library().q35_state_seed(self.eng.h, self.h, seed, prefix_len))
+
+    def prefix_len(self, lane: int = 0) -> int:
+        v = C.c_int32()
+        _ck(load_library().q35_state_prefix_len(self.eng.h, self.h, lane, C.byref(v)))
+        return v.value
+
+    def read(self, lane: int, which: str, n_slots: int = 0) -> np.ndarray:
+        shapes = {"S": ((18, 16, 128, 128), np.float32, 0), "win": ((18, 3, 6144), np.float32, 1),
+                  "k": ((6, 2, n_slots, 256), np.uint16, 2), "v": ((6, 2, n_slots, 256), np.uint16, 3),
+                  "mk": ((2, n_slots, 256), np.uint16, 4), "mv": ((2, n_slots, 256), np.uint16, 5)}
+        shape, dt, w = shapes[which]
+        out = np.empty(shape, dtype=dt)
+        _ck(load_library().q35_state_read(self.eng.h, self.h, lane, w, n_slots, _p(out), out.nbytes))
+        return out
+
+    def write(self, lane: int, which: str, arr: np.ndarray, n_slots: int = 0):
+        w = {"S": 0, "win": 1, "k": 2, "v": 3, "mk": 4, "mv": 5}[which]
+        a = np.ascontiguousarray(arr)
+        _ck(load_library().q35_state_write(self.eng.h, self.h, lane, w, n_slots, _p(a), a.nbytes))
+
+    def close(self):
+        if self.h:
+            load_library().q35_state_free(self.eng.h, self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- engine calls over this state
+    def prefill(self, lane: int, ids, logits: bool = False):
+        ids = _i32(ids)
+        y0 = C.c_int32()
+        lg = np.empty(VOCAB, np.float32) if logits else None
+        _ck(load_library().q35_prefill(self.eng.h, self.h, lane, _p(ids), ids.size, C.byref(y0),
+                                       _p(lg) if logits else None))
+        return (y0.value, lg) if logits else y0.value
+
+    def decode_step(self, tokens, lanes=None, logits: bool = False):
+        t = _i32(tokens)
+        n = t.size
+        ln = _i32(lanes) if lanes is not None else None
+        out = np.empty(n, np.int32)
+        lg = np.empty((n, VOCAB), np.float32) if logits else None
+        _ck(load_library().q35_decode_step(self.eng.h, self.h, _p(ln) if ln is not None else None, n,
+                                           _p(t), _p(out), _p(lg) if logits else None))
+        return (out, lg) if logits else out
+
+    def mtp_draft(self, y, pos, step: int, lanes=None, logits: bool = False):
+        y, pos = _i32(y), _i32(pos)
+        n = y.size
+        ln = _i32(lanes) if lanes is not None else None
+        out = np.empty(n, np.int32)
+        xd = np.empty((n, HIDDEN), np.uint16)
+        lg = np.empty((n, VOCAB), np.float32) if logits else None
+        _ck(load_library().q35_mtp_draft(self.eng.h, self.h, _p(ln) if ln is not None else None, n, _p(y),
+                                         _p(pos), step, _p(out), _p(xd), _p(lg) if logits else None))
+        return out, xd, lg
+
+    def mtp_round(self, cur, k: int, lanes=None, stats: np.ndarray | None = None):
+        c = _i32(cur)
+        n = c.size
+        ln = _i32(lanes) if lanes is not None else None
+        emit = np.zeros((n, k + 1), np.int32)
+        ne = np.zeros(n, np.int32)
+        st = stats if stats is not None else np.zeros(4, np.int64)
+        _ck(load_library().q35_mtp_round(self.eng.h, self.h, _p(ln) if ln is not None else None, n, _p(c), k,
+                                         _p(emit), _p(ne), _p(st)))
+        return [list(emit[i, :ne[i]]) for i in range(n)]
+
+
+class Forward:
+    """One lane driven like specimpl.Forward (prefill / decode / greedy)."""
+
+    def __init__(self, eng: Engine, state: State | None = None, lane: int = 0, cap: int = 4352):
+        self.eng = eng
+        self.state = state if state is not None else State(eng, 1, cap)
+        self.lane = lane
+
+    @property
+    def P(self) -> int:
+        return self.state.prefix_len(self.lane)
+
+    def reset(self):
+        self.state.reset([self.lane])
+
+    def prefill(self, ids, logits: bool = False):
+        return self.state.prefill(self.lane, ids, logits)
+
+    def decode(self, tok: int, logits: bool = False):
+        r = self.state.decode_step([tok], [self.lane], logits)
+        return (int(r[0][0]), r[1][0]) if logits else int(r[0])
+
+    def greedy(self, ids, steps: int, stop_on_eos: bool = True, logits_out=None):
+        """specimpl.py:496-517: first token from the prompt, then `steps` decodes."""
+        want = logits_out is not None
+        r = self.prefill(ids, want)
+        if want:
+            tok, lg = r
+            logits_out.append(lg)
+        else:
+            tok = r
+        out = [tok]
+        for _ in range(steps):
+            if stop_on_eos and out[-1] in EOS_IDS:
+                break
+            r = self.decode(out[-1], want)
+            if want:
+                tok, lg = r
+                logits_out.append(lg)
+            else:
+                tok = r
+            out.append(tok)
+        return out
+
+
+def greedy_mtp(f: Forward, ids, steps: int, k: int = 2, stop_on_eos: bool = True):
+    """speccheck/mtp.py:97-179 with the batched verify and rollback done in the engine."""
+    assert f.state.mtp_k >= k
+    stats = np.zeros(4, np.int64)
+    t = f.prefill(ids)
+    out = [t]
+    while len(out) < steps + 1 and not (stop_on_eos and out[-1] in EOS_IDS):
+        em = f.state.mtp_round([out[-1]], k, [f.lane], stats)[0]
+        out.extend(int(x) for x in em)
+    return out, dict(drafted=int(stats[0]), accepted=int(stats[1]), bonus=int(stats[2]),
+                     verify_tokens=int(stats[3]), target_forwards=int(stats[2]) + 1)

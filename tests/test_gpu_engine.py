@@ -1,0 +1,203 @@
+"""End-to-end parity of the engine against the torch-CPU oracle (a restatement of the
+reference's speccheck/specimpl.py, itself pinned bit-exact to vectors written from the
+reference in tests/golden/).
+
+Tolerances (bf16 path, stated here and checked). They are set at ~1.5x the spread of
+the reference's own torch-CPU path between two x86 hosts (this container vs the GPU box,
+same weights and ids): logits max |d| 0.22, mean |d| 0.034 over config 0.
+  * logits: max |engine - oracle| <= 0.375 and mean |diff| <= 0.05 on teacher-forced steps
+    (logits are ~N(0,1.3) bf16 values; 1 bf16 ulp at 4..8 is 0.03125)
+  * greedy ids: identical wherever the oracle's top-1/top-2 gap exceeds 0.375
+  * GDN fp32 state after the prompt: max |diff| <= 2e-2, relative Frobenius error <= 6e-2
+    (the layer inputs themselves differ at bf16 level by then, so this grows with depth)
+Bit-exact by construction (checked exactly): batched lane == single lane, prompt-then-
+decode == longer prompt (incremental == batch), MTP greedy == plain greedy."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_MAX, LOGIT_MEAN, GAP = 0.375, 0.05, 0.375
+
+
+@pytest.fixture(scope="module")
+def eng():
+    import torch
+    assert torch.cuda.is_available()
+    from qwen35 import Engine
+    e = Engine(max_rows=128, max_ctx=512, seed=0)
+    yield e
+    e.close()
+
+
+@pytest.fixture(scope="module")
+def oracle_run(oracle_weights, golden):
+    from oracle import model
+    ids = [int(t) for t in golden["config0_greedy"]["prompt"]]
+    f = model.Forward(oracle_weights)
+    rows = []
+    toks = f.greedy(ids, 64, stop_on_eos=False, logits_out=rows)
+    # torch's CPU bf16 GEMM takes a CPU-dependent path (e.g. AVX512-BF16), so the oracle
+    # is pinned to the golden vectors in the CPU suite of the build container, and here it
+    # is this host's own instance of the same algorithm.
+    gold = [int(t) for t in golden["config0_greedy"]["tokens"]]
+    same = next((i for i, (a, b) in enumerate(zip(toks, gold)) if a != b), len(gold))
+    print(f"oracle on this host: {same}/65 ids equal to the golden run", flush=True)
+    return ids, toks, [r.float().numpy() for r in rows], f
+
+
+def test_weights_match_oracle(eng, oracle_weights):
+    from oracle.weights import registry
+    import torch
+    for name, shape, kind in registry():
+        n = int(np.prod(shape))
+        if n > 5_000_000:
+            continue
+        got = eng.read_tensor(name, n)
+        want = oracle_weights.p[name].contiguous().view(torch.int16).numpy().view(np.uint16).reshape(-1)
+        assert np.array_equal(got, want), name
+    e = eng.read_tensor("model.language_model.embed_tokens.weight", 248320 * 1024)
+    want = oracle_weights.p["model.language_model.embed_tokens.weight"].view(torch.int16).numpy().view(np.uint16).reshape(-1)
+    assert np.array_equal(e, want)
+
+
+def test_teacher_forced_logits(eng, oracle_run):
+    from qwen35 import State, Forward
+    ids, toks, rows, _ = oracle_run
+    st = State(eng, 1, 512)
+    f = Forward(eng, st)
+    y0, lg = f.prefill(ids, logits=True)
+    errs = [np.abs(lg - rows[0])]
+    mism = []
+    for s in range(64):
+        t, lg = f.decode(toks[s], logits=True)
+        errs.append(np.abs(lg - rows[s + 1]))
+        ref = rows[s + 1]
+        top2 = np.sort(ref)[-2:]
+        if top2[1] - top2[0] > GAP and t != toks[s + 1]:
+            mism.append(s)
+        # argmax is bit-exact given the engine's logits
+        assert t == int(np.flatnonzero(lg == lg.max())[0])
+    mx = max(e.max() for e in errs)
+    mean = float(np.mean([e.mean() for e in errs]))
+    print(f"teacher-forced logits: max|d|={mx:.4f} mean|d|={mean:.5f}", flush=True)
+    assert mx <= LOGIT_MAX and mean <= LOGIT_MEAN
+    assert not mism, mism
+
+
+def test_free_running_greedy(eng, oracle_run):
+    from qwen35 import State, Forward
+    ids, toks, rows, _ = oracle_run
+    st = State(eng, 1, 512)
+    got = Forward(eng, st).greedy(ids, 64, stop_on_eos=False)
+    agree = 0
+    while agree < len(got) and got[agree] == toks[agree]:
+        agree += 1
+    print(f"free-running greedy: {agree}/65 identical before first divergence", flush=True)
+    if agree < 65:
+        ref = rows[agree]
+        top2 = np.sort(ref)[-2:]
+        assert top2[1] - top2[0] <= GAP, (agree, top2)
+
+
+def test_gdn_state_after_prompt(eng, oracle_weights, golden):
+    import torch
+    from oracle import model
+    from qwen35 import State
+    ids = [int(t) for t in golden["config0_greedy"]["prompt"]][:16]
+    f = model.Forward(oracle_weights)
+    f.prefill(ids)
+    st = State(eng, 1, 512)
+    st.prefill(0, ids)
+    S = st.read(0, "S")
+    for gi, l in enumerate([l for l in range(24) if l % 4 != 3]):
+        ref = f.rec[l].numpy()
+        d = np.abs(S[gi] - ref)
+        rel = np.linalg.norm(S[gi] - ref) / np.linalg.norm(ref)
+        assert d.max() <= 2e-2 and rel <= 6e-2, (l, d.max(), rel)
+    w = st.read(0, "win")
+    for gi, l in enumerate([l for l in range(24) if l % 4 != 3]):
+        assert np.array_equal(w[gi], f.conv_win[l].float().numpy()), l   # raw bf16 values
+    k = st.read(0, "k", len(ids))
+    kf = (k.astype(np.uint32) << 16).view(np.float32)
+    for ai, l in enumerate([3, 7, 11, 15, 19, 23]):
+        ref = torch.cat(f.kv[l]["k"], 0).numpy().transpose(1, 0, 2)   # [2, T, 256]
+        assert np.abs(kf[ai] - ref).max() <= 0.05 * max(1.0, np.abs(ref).max())
+
+
+def test_batched_lanes_equal_single(eng):
+    from oracle.weights import lane_prompt_ids
+    from qwen35 import State
+    B = 4
+    prompts = [lane_prompt_ids(0, b, 5 + 3 * b) for b in range(B)]
+    sb = State(eng, B, 512)
+    y = [sb.prefill(b, prompts[b]) for b in range(B)]
+    seqb = [[t] for t in y]
+    for _ in range(6):
+        out = sb.decode_step([s[-1] for s in seqb])
+        for b in range(B):
+            seqb[b].append(int(out[b]))
+    for b in range(B):
+        s1 = State(eng, 1, 512)
+        t = s1.prefill(0, prompts[b])
+        seq = [t]
+        for _ in range(6):
+            seq.append(int(s1.decode_step([seq[-1]])[0]))
+        assert seq == seqb[b], b
+        assert np.array_equal(s1.read(0, "S"), sb.read(b, "S"))
+
+
+def test_incremental_equals_batch(eng, golden):
+    """G5 (specification/08-state-management.md:111-117): prompt T then decode == prompt T+D."""
+    from qwen35 import State
+    ids = [int(t) for t in golden["config0_greedy"]["prompt"]]
+    a = State(eng, 1, 512)
+    a.prefill(0, ids[:20])
+    for t in ids[20:31]:
+        a.decode_step([t])
+    ya, la = a.decode_step([ids[31]], logits=True)
+    b = State(eng, 1, 512)
+    yb, lb = b.prefill(0, ids, logits=True)
+    assert int(ya[0]) == yb
+    assert np.array_equal(la[0], lb)
+    assert np.array_equal(a.read(0, "S"), b.read(0, "S"))
+    assert np.array_equal(a.read(0, "k", 32), b.read(0, "k", 32))
+
+
+def test_mtp_k2_lossless_and_oracle(eng, golden):
+    from qwen35 import State, Forward, greedy_mtp
+    g = golden["mtp_k2"]
+    ids = [int(t) for t in golden["config0_greedy"]["prompt"]]
+    st = State(eng, 1, 512, mtp_k=2, mtp_cap=256)
+    f = Forward(eng, st)
+    out, stats = greedy_mtp(f, ids, 16, k=2, stop_on_eos=False)
+    plain = Forward(eng, State(eng, 1, 512)).greedy(ids, len(out) - 1, stop_on_eos=False)
+    assert out == plain[:len(out)]
+    assert stats["drafted"] == 2 * stats["bonus"]
+    n = min(len(out), len(g["batch_tokens"]))
+    agree = 0
+    while agree < n and out[agree] == int(g["batch_tokens"][agree]):
+        agree += 1
+    print(f"mtp k=2: {agree}/{n} ids agree with the reference's greedy_mtp; stats {stats}", flush=True)
+    assert agree >= 1
+
+
+def test_mtp_draft_vs_oracle(eng, oracle_weights, golden):
+    from oracle import model
+    from qwen35 import State
+    ids = [int(t) for t in golden["config0_greedy"]["prompt"]]
+    st = State(eng, 1, 512, mtp_k=2, mtp_cap=64)
+    y0 = st.prefill(0, ids)
+    d, xd, lg = st.mtp_draft([y0], [len(ids) + 1], 0, logits=True)
+    f = model.Forward(oracle_weights)
+    normed = f.prefill(ids)
+    m = model.MTPDraft(oracle_weights)
+    dd = {}
+    rd, rxd = m.draft(y0, normed[-1:], len(ids) + 1, dd)
+    ref = dd["logits"].float().numpy()
+    assert np.abs(lg[0] - ref).max() <= LOGIT_MAX
+    top2 = np.sort(ref)[-2:]
+    if top2[1] - top2[0] > GAP:
+        assert int(d[0]) == rd
+    xdf = (xd[0].astype(np.uint32) << 16).view(np.float32)
+    assert np.abs(xdf - rxd[0].float().numpy()).max() <= LOGIT_MAX

@@ -1,0 +1,74 @@
+"""Per-op parity on the GPU through the C ABI: GEMM family and tied lm_head argmax.
+
+Bar: every bf16 output within 1 bf16 ulp of the float64 product of the same bf16 inputs
+rounded once (the reference's torch bf16 matmul: f32 accumulate, one rounding); argmax
+bit-exact given the engine's own bf16 logits, lowest id on ties."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def bf16_to_f32(b):
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+@pytest.fixture(scope="module")
+def eng():
+    import torch
+    assert torch.cuda.is_available()
+    from qwen35 import Engine
+    e = Engine(max_rows=64, max_ctx=1024, seed=0)
+    yield e
+    e.close()
+
+
+@pytest.mark.parametrize("N,K,M", [(16, 256, 1), (6144, 1024, 1), (1024, 2048, 3), (1024, 3584, 16), (512, 1024, 33)])
+def test_gemm_vs_float64(eng, N, K, M):
+    import torch
+    print(f"gemm N={N} K={K} M={M}", flush=True)
+    g = torch.Generator().manual_seed(N + K + M)
+    W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    X = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    Wd, Xd = W.cuda(), X.cuda()
+    Wt = torch.empty_like(Wd)
+    Y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    eng.op_tile_weight(Wd.data_ptr(), N, K, Wt.data_ptr())
+    eng.op_gemm(Wt.data_ptr(), N, K, Xd.data_ptr(), M, Y.data_ptr())
+    eng.sync()
+    ref = X.double() @ W.double().t()
+    got = Y.cpu().double()
+    # one bf16 rounding of the result plus f32 accumulation error (cancellation-aware)
+    ulp = torch.maximum(ref.abs(), torch.full_like(ref, 1e-30)).log2().floor().sub(7).exp2()
+    acc = (X.double().abs() @ W.double().abs().t()) * (K * 2.0 ** -24)
+    excess = (got - ref).abs() - ulp
+    assert (excess <= acc).all(), (excess - acc).max().item()
+    # row independence: row 0 alone gives the same bits
+    Y1 = torch.empty(1, N, dtype=torch.bfloat16, device="cuda")
+    eng.op_gemm(Wt.data_ptr(), N, K, Xd[-1:].contiguous().data_ptr(), 1, Y1.data_ptr())
+    eng.sync()
+    assert torch.equal(Y1.cpu(), Y[-1:].cpu())
+
+
+def test_lm_head_argmax(eng, oracle_weights):
+    import torch
+    E = oracle_weights.p["model.language_model.embed_tokens.weight"]
+    g = torch.Generator().manual_seed(5)
+    X = torch.randn(5, 1024, generator=g).to(torch.bfloat16)
+    X[3] = X[2]
+    tok = torch.empty(5, dtype=torch.int32, device="cuda")
+    lg = torch.empty(5, 248320, dtype=torch.float32, device="cuda")
+    eng.op_lm_head_argmax(X.cuda().data_ptr(), 5, tok.data_ptr(), lg.data_ptr())
+    eng.sync()
+    lg = lg.cpu()
+    ref = (X.float() @ E.float().t())
+    # engine logits are bf16 values
+    assert torch.equal(lg.to(torch.bfloat16).float(), lg)
+    rel = ((lg - ref).abs() / ref.abs().clamp_min(1e-3))
+    assert (lg - ref).abs().max().item() < 0.05
+    # argmax is the lowest index of the max of the engine's own logits
+    for r in range(5):
+        row = lg[r]
+        m = row.max()
+        assert tok[r].item() == int(torch.nonzero(row == m)[0])
+    assert tok[2].item() == tok[3].item()
