@@ -1,0 +1,178 @@
+"""Decode throughput of the MI355X Qwen3.5-0.8B engine (BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 256] [--ctx 4096]
+
+A step is one greedy decode step of every lane through the full 24-layer tower plus the
+tied lm_head and argmax. Lanes carry seeded state (GDN S ~ N(0,0.1) f32, K/V ~ N(0,1) bf16
+over `ctx` slots), weights are the seeded random-init bf16 weights; inputs are resident in
+HBM before timing. Prints ONE JSON line: `value` is the batch-`--batch` aggregate tok/s;
+the batch-1 figures of the same metric are under "batch1".
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for p in (REPO, REPO / "qwen3.5-0.8b_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+HBM_PEAK = 8000.0            # GB/s, MI355X
+WEIGHT_BYTES = 1_504_793_280  # bf16 weights streamed per pass (text tower + tied E)
+S_BYTES = 18 * 16 * 128 * 128 * 4
+WIN_BYTES = 18 * 3 * 6144 * 4
+KV_BYTES_PER_SLOT = 6 * 2 * 2 * 256 * 2   # K and V, 6 layers, 2 kv heads
+FAM = {"gemm": 1, "lm_head": 2, "gdn": 3, "attn": 4}
+
+
+def step_bytes(B: int, L: int) -> int:
+    """Algorithmic HBM bytes of one decode step over B lanes at context L."""
+    return WEIGHT_BYTES + B * (2 * S_BYTES + 2 * WIN_BYTES + KV_BYTES_PER_SLOT * (L + 1))
+
+
+def family_bytes(fam: str, B: int, L: int) -> int:
+    """Algorithmic bytes of all launches of one kernel family in one decode step."""
+    if fam == "gdn":       # per layer: S read+write, window r+w, qkv/a/b in, o out
+        return 18 * B * (2 * (1 << 20) + 2 * 73728 + 6176 * 2 + 2048 * 4)
+    if fam == "attn":      # per layer: K and V of L+1 slots, q/k/v in, output
+        return 6 * B * (2048 * (L + 1) + 5120 * 2 + 2048 * 2)
+    if fam == "lm_head":
+        return 248320 * 1024 * 2 + B * (1024 * 2 + 248320 // 16 * 8)
+    if fam == "gemm":      # all projection + MLP GEMMs: weights once + activations
+        w = WEIGHT_BYTES - 248320 * 1024 * 2 - 24 * 2048 - 1024 * 2
+        act = B * 24 * 2 * (1024 + 8224 + 2048 + 1024 + 1024 + 7168 + 7168 + 1024)
+        return w + act
+    raise ValueError(fam)
+
+
+def run_decode(eng, B: int, ctx: int, steps: int, warmup: int, kprof: str | None):
+    import numpy as np
+    import torch
+    from qwen35 import State
+    st = State(eng, B, ctx + steps + warmup + 8)
+    st.seed(1, ctx)
+    rng = np.random.default_rng(0)
+    tok = rng.integers(0, 248320, size=B).astype(np.int32)
+    for _ in range(warmup):
+        tok = st.decode_step(tok)
+    if kprof:
+        eng.set_option("kprof", FAM[kprof])
+    eng.sync()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    eng.timer_begin()
+    for _ in range(steps):
+        tok = st.decode_step(tok)
+    ev_ms = eng.timer_end()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kt = None
+    if kprof:
+        kt = eng.kprof_read()
+        eng.set_option("kprof", 0)
+    st.close()
+    return wall, ev_ms / 1e3, kt
+
+
+def cpu_baseline(ctx: int, budget_s: float = 15.0):
+    """The torch-CPU oracle (restatement of the reference's specimpl.py path) decoding lane 0
+    of the same seeded workload on the host cores: tok/s."""
+    import numpy as np
+    import torch
+    from oracle import model, prng
+    from oracle.weights import WeightDict
+    torch.set_grad_enabled(False)
+    w = WeightDict(0)
+    f = model.Forward(w)
+    gl = [l for l in range(24) if l % 4 != 3]
+    S_all = prng.normal_f32(1, prng.fnv1a64("state.gdn.0"), 0.1, 18 * 262144).reshape(18, 16, 128, 128)
+    for i, l in enumerate(gl):
+        f.rec[l] = torch.from_numpy(S_all[i].copy())
+        f.conv_win[l] = torch.zeros(3, 6144, dtype=torch.bfloat16)
+    for a, l in enumerate([3, 7, 11, 15, 19, 23]):
+        ks, vs = [], []
+        for j in range(2):
+            tag = f"0.{a}.{j}"
+            kb = prng.normal_bf16(1, prng.fnv1a64("state.k." + tag), 1.0, ctx * 256)
+            vb = prng.normal_bf16(1, prng.fnv1a64("state.v." + tag), 1.0, ctx * 256)
+            ks.append(torch.from_numpy((kb.astype(np.uint32) << 16).view(np.float32).reshape(ctx, 256)))
+            vs.append(torch.from_numpy(vb.view(np.int16).copy()).view(torch.bfloat16).reshape(ctx, 256))
+        f.kv[l] = {"k": [torch.stack(ks, 1)], "v": [torch.stack(vs, 1)]}
+    f.P = ctx
+    tok, n = 1234, 0
+    f.decode(tok)                      # warm
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or n < 2:
+        tok = int(f.logits(f.decode(tok))[-1].argmax())
+        n += 1
+    dt = time.perf_counter() - t0
+    return n / dt, torch.get_num_threads(), n
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=256)
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--b1-steps", type=int, default=100)
+    ap.add_argument("--kprof", default="gdn", choices=list(FAM) + ["none"])
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: lanes are independent sequences, so more GPUs would "
+              "each run their own B/N lanes with no collective; multi-GPU runs are not part of "
+              "this build.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from qwen35 import Engine
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    B, L = args.batch, args.ctx
+    eng = Engine(max_rows=max(B, 64), max_ctx=L + args.steps + args.warmup + 64, seed=0)
+    kp = None if args.kprof == "none" else args.kprof
+    wall, ev_s, kt = run_decode(eng, B, L, args.steps, args.warmup, kp)
+    ms = wall / args.steps * 1e3
+    value = B * args.steps / wall
+    wall1, ev1, kt1 = run_decode(eng, 1, L, args.b1_steps, args.warmup, None)
+    ms1 = wall1 / args.b1_steps * 1e3
+    gbs = step_bytes(B, L) / (ms / 1e3) / 1e9
+    gbs1 = step_bytes(1, L) / (ms1 / 1e3) / 1e9
+    roof = None
+    if kt is not None and kt[1] > 0:
+        per_launch_ms = kt[0] / kt[1]
+        launches_per_step = kt[1] / args.steps
+        byt = family_bytes(kp, B, L) / launches_per_step
+        ach = byt / (per_launch_ms / 1e3) / 1e9
+        roof = {"kernel": kp, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK, 4), "traffic": None,
+                "bytes_per_launch": int(byt), "avg_launch_us": round(per_launch_ms * 1e3, 2),
+                "launches_per_step": launches_per_step}
+    cpu = None
+    if not args.no_cpu:
+        tps, thr, n = cpu_baseline(L)
+        cpu = {"value": round(tps, 3), "unit": "tok/s", "cores": thr, "kind": "port",
+               "sample": f"oracle (torch CPU restatement of speccheck/specimpl.py) greedy decode of lane 0 "
+                         f"of this workload (seeded state, ctx {L}), batch 1, {n} tokens"}
+    out = {"metric": "decode tok/s at batch 1 and 256 (ctx 4k); achieved HBM GB/s vs 8 TB/s peak",
+           "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "bf16", "data": "synthetic (seeded random-init weights and state)",
+           "config": {"workload": f"decode_b{B}_ctx{L}", "model": "Qwen3.5-0.8B text tower", "global_batch": B,
+                      "seq_len": L, "parallelism": "none (1 GPU)"},
+           "hbm_gbs_step": round(gbs, 1), "hbm_frac_step": round(gbs / HBM_PEAK, 4),
+           "event_ms_per_step": round(ev_s / args.steps * 1e3, 4),
+           "batch1": {"tok_s": round(args.b1_steps / wall1, 2), "ms_per_step": round(ms1, 4),
+                      "hbm_gbs": round(gbs1, 1), "hbm_frac": round(gbs1 / HBM_PEAK, 4),
+                      "bytes_per_token": step_bytes(1, L)},
+           "roofline": roof, "cpu_baseline": cpu}
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -104,6 +104,11 @@ int q35_op_gemm(q35_engine* e, const uint16_t* w_tiled_dev, int N, int K, const 
                 int M, uint16_t* y_dev);
 int q35_op_lm_head_argmax(q35_engine* e, const uint16_t* x_dev, int M, int32_t* tok_dev, float* logits_dev);
 int q35_sync(q35_engine* e);
+/* Live per-kernel timing: with option "kprof" = family (1 projection/MLP GEMMs, 2 lm_head
+ * GEMM, 3 GDN recurrence, 4 attention core, 0 off), each launch of that family is bracketed
+ * by HIP events on the engine stream; this returns the summed duration and launch count
+ * since the option was set or last read, and resets them. */
+int q35_kprof_read(q35_engine* e, float* total_ms, int* launches);
 /* Options: "layers" (diagnostic: bodies run only the first n of the 24 layers, the final
  * norm then applies to that layer's output), "graph" (0/1). */
 int q35_set_option(q35_engine* e, const char* name, int value);

@@ -99,6 +99,9 @@ struct q35_state {
 struct q35_engine {
     int device = 0, R = 0, max_ctx = 0, use_graph = 0;
     int n_layers = kLayers;          // diagnostic: run only the first n layers of a body
+    int kprof = 0;                   // kernel family timed with HIP events (0 = off)
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> kev;
+    size_t kev_used = 0;
     hipStream_t st = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     uint16_t* blob = nullptr;
@@ -122,6 +125,30 @@ struct q35_engine {
 };
 
 namespace {
+
+// Kernel families for the live per-kernel timing (q35_set_option "kprof").
+enum KFam { kFamNone = 0, kFamGemm = 1, kFamLmHead = 2, kFamGdn = 3, kFamAttn = 4, kFamGlue = 5 };
+
+struct KTimer {
+    q35_engine* e;
+    bool on;
+    KTimer(q35_engine* e_, int fam) : e(e_), on(e_->kprof == fam) {
+        if (!on) return;
+        if (e->kev_used == e->kev.size()) {
+            hipEvent_t a, b;
+            HCK(hipEventCreate(&a));
+            HCK(hipEventCreate(&b));
+            e->kev.push_back({a, b});
+        }
+        HCK(hipEventRecord(e->kev[e->kev_used].first, e->st));
+    }
+    ~KTimer() {
+        if (on) {
+            hipEventRecord(e->kev[e->kev_used].second, e->st);
+            ++e->kev_used;
+        }
+    }
+};
 
 template <typename T>
 T* dalloc(size_t n) {
@@ -328,6 +355,7 @@ void gemm(q35_engine* e, const uint16_t* W, int N, int K, int M, const void* X, 
     GemmArgs a{};
     a.W = W; a.N = N; a.K = K; a.M = M; a.X = X; a.ldx = ldx; a.X2 = X2; a.ldx2 = ldx2;
     a.aux_w = aux; a.Y = Y; a.ldy = ldy;
+    KTimer kt(e, kFamGemm);
     HCK(launch_gemm(a, amode, kEStore, e->st));
 }
 
@@ -343,7 +371,10 @@ void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16
     a.max_chunks = (cap + 255) / 256;
     REQ(a.max_chunks <= e->max_chunks, Q35_ERR_CAP, "cache capacity exceeds engine max_ctx");
     a.out = e->aout; a.R = R; a.inv_freq = e->inv_freq;
-    HCK(launch_attention(a, e->st));
+    {
+        KTimer kt(e, kFamAttn);
+        HCK(launch_attention(a, e->st));
+    }
     gemm(e, w.W_out, kHidden, 2048, R, e->aout, 2048, e->delta, kHidden);
 }
 
@@ -375,7 +406,10 @@ void body(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
             g.W_layer = (long long)gdn_slot(l) * 18432;
             g.cur = s->cur_dev; g.nslots = s->nslots; g.ckpt = ckpt ? 1 : 0;
             g.lane = e->rlane; g.T = T; g.nlanes = nl;
-            HCK(launch_gdn(g, cs, e->st));
+            {
+                KTimer kt(e, kFamGdn);
+                HCK(launch_gdn(g, cs, e->st));
+            }
             gemm(e, w.W_out, kHidden, 2048, R, e->o, 2048, e->delta, kHidden, kAGatedNorm,
                  e->proj + kGdnZOff, kGdnInRows, w.gnorm);
         } else {
@@ -395,7 +429,10 @@ void lm_head(q35_engine* e, int row0, int M, bool want_logits) {
     a.W = e->E; a.N = kVocab; a.K = kHidden; a.M = M; a.X = e->nrm + (size_t)row0 * kHidden; a.ldx = kHidden;
     if (want_logits) { ensure_logits(e, M); a.logits = e->logits_dev; a.ldl = kVocab; }
     a.part_val = e->pval; a.part_idx = e->pidx; a.ldp = kVocab / 16;
-    HCK(launch_gemm(a, kAPlain, kEArgmax, e->st));
+    {
+        KTimer kt(e, kFamLmHead);
+        HCK(launch_gemm(a, kAPlain, kEArgmax, e->st));
+    }
     HCK(launch_argmax(e->pval, e->pidx, kVocab / 16, kVocab / 16, M, e->tok_dev, nullptr, e->st));
 }
 
@@ -855,6 +892,11 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
         if (n == "layers") {
             REQ(value >= 1 && value <= kLayers, Q35_ERR_ARG, "layers out of range");
             e->n_layers = value;
+        } else if (n == "kprof") {
+            REQ(value >= 0 && value <= 5, Q35_ERR_ARG, "kprof family out of range");
+            HCK(hipStreamSynchronize(e->st));
+            e->kprof = value;
+            e->kev_used = 0;
         } else if (n == "graph") {
             e->use_graph = value;
         } else {
@@ -883,6 +925,22 @@ int q35_read_scratch(q35_engine* e, const char* name, void* host, size_t bytes) 
         REQ(bytes <= cap, Q35_ERR_ARG, "read exceeds scratch size");
         HCK(hipStreamSynchronize(e->st));
         HCK(hipMemcpy(host, p, bytes, hipMemcpyDeviceToHost));
+    });
+}
+
+int q35_kprof_read(q35_engine* e, float* total_ms, int* launches) {
+    return guard([&] {
+        REQ(e && total_ms && launches, Q35_ERR_ARG, "null argument");
+        HCK(hipStreamSynchronize(e->st));
+        float tot = 0.f;
+        for (size_t i = 0; i < e->kev_used; ++i) {
+            float ms = 0.f;
+            HCK(hipEventElapsedTime(&ms, e->kev[i].first, e->kev[i].second));
+            tot += ms;
+        }
+        *total_ms = tot;
+        *launches = (int)e->kev_used;
+        e->kev_used = 0;
     });
 }
 

@@ -53,6 +53,7 @@ _SIGS = {
     "q35_op_gemm": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p], C.c_int),
     "q35_op_lm_head_argmax": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p], C.c_int),
     "q35_sync": ([C.c_void_p], C.c_int),
+    "q35_kprof_read": ([C.c_void_p, C.POINTER(C.c_float), C.POINTER(C.c_int)], C.c_int),
     "q35_set_option": ([C.c_void_p, C.c_char_p, C.c_int], C.c_int),
     "q35_read_scratch": ([C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t], C.c_int),
     "q35_timer_begin": ([C.c_void_p], C.c_int),
@@ -123,6 +124,11 @@ class Engine:
         out = np.empty(shape, dtype=dtype)
         _ck(load_library().q35_read_scratch(self.h, name.encode(), _p(out), out.nbytes))
         return out
+
+    def kprof_read(self):
+        ms, n = C.c_float(), C.c_int()
+        _ck(load_library().q35_kprof_read(self.h, C.byref(ms), C.byref(n)))
+        return ms.value, n.value
 
     def sync(self):
         _ck(load_library().q35_sync(self.h))
