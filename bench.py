@@ -60,7 +60,7 @@ def run_decode(eng, B: int, ctx: int, steps: int, warmup: int, kprof: str | None
     tok = rng.integers(0, 248320, size=B).astype(np.int32)
     for _ in range(warmup):
         tok = st.decode_step(tok)
-    if kprof:
+    if kprof:                       # timed with per-kernel events: launched eagerly
         eng.set_option("kprof", FAM[kprof])
     eng.sync()
     torch.cuda.synchronize()
@@ -124,6 +124,7 @@ def main():
     ap.add_argument("--b1-steps", type=int, default=100)
     ap.add_argument("--kprof", default="gdn", choices=list(FAM) + ["none"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="launch kernels eagerly (no hipGraph)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: lanes are independent sequences, so more GPUs would "
@@ -134,7 +135,8 @@ def main():
     from qwen35 import Engine
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     B, L = args.batch, args.ctx
-    eng = Engine(max_rows=max(B, 64), max_ctx=L + args.steps + args.warmup + 64, seed=0)
+    eng = Engine(max_rows=max(B, 64), max_ctx=L + max(args.steps, args.b1_steps) + args.warmup + 64, seed=0,
+                 use_graph=not args.eager)
     kp = None if args.kprof == "none" else args.kprof
     wall, ev_s, kt = run_decode(eng, B, L, args.steps, args.warmup, kp)
     ms = wall / args.steps * 1e3

@@ -7,12 +7,12 @@
 // bf16(sigmoid(gate)). GQA: query head i reads kv head i / 4.
 // Replaces engine/kernels_attn.cpp:415-1108 (prep, core, combine) of the reference.
 //
-// Three launches per layer:
+// Four launches per layer:
 //   attn_prep   (row, head)         q norm+rope -> f32 scratch; k norm+rope, v -> cache
 //   attn_scores (row, kv head, chunk) f32 scores -> scratch, per-chunk (max, sum e^(s-max))
-//   attn_pv     (row, kv head, chunk) global (max, sum) from the chunk stats, p = bf16(e/l),
-//               partial P.V per chunk; the last chunk block to finish sums the partials
-//               in chunk order and applies the sigmoid gate.
+//   attn_pv     (row, kv head, 64-slot part) global (max, sum) from the chunk stats,
+//               p = bf16(e/l), partial P.V per part
+//   attn_combine (row, q head)      sum of the parts in order, bf16, times bf16(sigmoid(gate))
 // The k cache holds bf16(k post-rope); the reference's torch path keeps it in f32, so
 // k's rotated dims carry one extra bf16 rounding here (the cache layout is bf16 by design).
 #include "q35_common.h"
@@ -122,14 +122,19 @@ __global__ void __launch_bounds__(256) attn_scores(AttnArgs a) {
     }
 }
 
+// P.V over one 64-slot part: thread (dg, tg) owns dims dg*8..+8 for slots tg*8..+8 of the
+// part (16-byte V loads), the 8 slot groups are summed in order through LDS.
+constexpr int kPart = 64;
+
 __global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
-    __shared__ float p[4][kChunk];
+    __shared__ float p[4][kPart];
     __shared__ float ml[4][2];
-    __shared__ int last;
-    const int r = blockIdx.x, j = blockIdx.y, c = blockIdx.z, tid = threadIdx.x;
+    __shared__ float red[8][4][256];
+    const int r = blockIdx.x, j = blockIdx.y, pc = blockIdx.z, tid = threadIdx.x;
     const int slot = a.rm.slot[r];
+    const int nparts = slot / kPart + 1;
+    if (pc >= nparts) return;
     const int nch = slot / kChunk + 1;
-    if (c >= nch) return;
     const int lane = a.rm.lane[r];
     if (tid < 4) {
         const float* st = a.stats + ((size_t)r * kNq + 4 * j + tid) * a.max_chunks * 2;
@@ -141,56 +146,84 @@ __global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
         ml[tid][1] = l;
     }
     __syncthreads();
-    const int t0 = c * kChunk;
-    const int n = min(kChunk, slot + 1 - t0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    const int t0 = pc * kPart;
+    const int n = min(kPart, slot + 1 - t0);
+    {
+        const int i = tid >> 6, t = tid & 63;
         float pv = 0.f;
-        if (tid < n) {
-            float s = a.sc[((size_t)r * kNq + 4 * j + i) * a.sc_ld + t0 + tid];
+        if (t < n) {
+            float s = a.sc[((size_t)r * kNq + 4 * j + i) * a.sc_ld + t0 + t];
             pv = rbf(expf(s - ml[i][0]) / ml[i][1]);
         }
-        p[i][tid] = pv;
+        p[i][t] = pv;
     }
     __syncthreads();
-    const uint16_t* vr = a.vc + lane * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + t0) * 256 + tid;
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    for (int t = 0; t < n; ++t) {
-        float v = bf2f(vr[(size_t)t * 256]);
-        a0 = fmaf(p[0][t], v, a0); a1 = fmaf(p[1][t], v, a1);
-        a2 = fmaf(p[2][t], v, a2); a3 = fmaf(p[3][t], v, a3);
+    const int dg = tid & 31, tg = tid >> 5;
+    const uint16_t* vr = a.vc + lane * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + t0) * 256 + dg * 8;
+    float acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
+    q35_u32x4 vv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int t = tg * 8 + u;
+        if (t < n) vv[u] = *(const q35_u32x4*)(vr + (size_t)t * 256);
+        else vv[u] = (q35_u32x4){0u, 0u, 0u, 0u};
     }
-    float* pp = a.part + (((size_t)r * a.max_chunks + c) * kNq + 4 * j) * 256 + tid;
-    pp[0] = a0; pp[256] = a1; pp[512] = a2; pp[768] = a3;
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        int old = __hip_atomic_fetch_add(a.counters + r * 2 + j, 1, __ATOMIC_ACQ_REL,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-        last = (old == nch - 1);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int t = tg * 8 + u;
+        float pp[4] = {p[0][t], p[1][t], p[2][t], p[3][t]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float v = (e & 1) ? __uint_as_float(vv[u][e >> 1] & 0xffff0000u) : __uint_as_float(vv[u][e >> 1] << 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i][e] = fmaf(pp[i], v, acc[i][e]);
+        }
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[tg][i][dg * 8 + e] = acc[i][e];
     __syncthreads();
-    if (!last) return;
-    __threadfence();
-    const uint16_t* pr = a.proj + (size_t)r * kAttnInRows;
+    float* pp = a.part + (((size_t)r * a.max_chunks * 4 + pc) * kNq + 4 * j) * 256 + tid;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int qh = 4 * j + i;
-        float acc = 0.f;
-        for (int cc = 0; cc < nch; ++cc)
-            acc += __builtin_nontemporal_load(a.part + (((size_t)r * a.max_chunks + cc) * kNq + qh) * 256 + tid);
-        const float o = rbf(acc);
-        const float g = rbf(sigmoid_f(bf2f(pr[qh * 512 + 256 + tid])));
-        a.out[(size_t)r * 2048 + qh * 256 + tid] = f2bf(o * g);
+        float sum = red[0][i][tid];
+#pragma unroll
+        for (int g = 1; g < 8; ++g) sum += red[g][i][tid];
+        pp[i * 256] = sum;
     }
-    if (tid == 0) a.counters[r * 2 + j] = 0;
+}
+
+// Sum of the 64-slot partials in part order, bf16, times bf16(sigmoid(gate)).
+__global__ void __launch_bounds__(256) attn_combine(AttnArgs a) {
+    const int r = blockIdx.x, qh = blockIdx.y, tid = threadIdx.x;
+    const int nparts = a.rm.slot[r] / kPart + 1;
+    const float* pp = a.part + ((size_t)r * a.max_chunks * 4 * kNq + qh) * 256 + tid;
+    float acc = 0.f;
+    for (int c0 = 0; c0 < nparts; c0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = c0 + u < nparts ? pp[(size_t)(c0 + u) * kNq * 256] : 0.f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (c0 + u < nparts) acc += v[u];
+    }
+    const uint16_t* pr = a.proj + (size_t)r * kAttnInRows;
+    const float o = rbf(acc);
+    const float g = rbf(sigmoid_f(bf2f(pr[qh * 512 + 256 + tid])));
+    a.out[(size_t)r * 2048 + qh * 256 + tid] = f2bf(o * g);
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (a.R <= 0 || a.max_chunks <= 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(attn_prep, dim3(a.R, kNq + kNkv), dim3(256), 0, st, a);
     hipLaunchKernelGGL(attn_scores, dim3(a.R, kNkv, a.max_chunks), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(attn_pv, dim3(a.R, kNkv, a.max_chunks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(attn_pv, dim3(a.R, kNkv, a.max_chunks * 4), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(attn_combine, dim3(a.R, kNq), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

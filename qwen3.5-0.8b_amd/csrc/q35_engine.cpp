@@ -116,10 +116,13 @@ struct q35_engine {
     // scratch
     uint16_t *x, *h, *delta, *nrm, *proj, *gu, *aout, *cat;
     float *o, *q, *sc, *stats, *part, *pval, *inv_freq;
-    int *pidx, *counters, *tok_dev, *rlane, *rpos, *rslot, *ridx_src, *ridx_dst;
+    float* kpart;
+    uint16_t* prod;
+    int *pidx, *tok_dev, *rlane, *rpos, *rslot, *ridx_src, *ridx_dst;
     int sc_ld = 0, max_chunks = 0;
     float* logits_dev = nullptr;
     int logits_rows = 0;
+    std::map<std::string, hipGraphExec_t> graphs;   // captured decode steps
     // pinned staging
     int *h_tok, *h_lane, *h_pos, *h_slot, *h_out, *h_src, *h_dst;
 };
@@ -303,11 +306,11 @@ void alloc_scratch(q35_engine* e) {
     e->max_chunks = e->sc_ld / 256;
     e->sc = dalloc<float>(R * kNq * (size_t)e->sc_ld);
     e->stats = dalloc<float>(R * kNq * (size_t)e->max_chunks * 2);
-    e->part = dalloc<float>(R * (size_t)e->max_chunks * kNq * 256);
+    e->part = dalloc<float>(R * (size_t)e->max_chunks * 4 * kNq * 256);
     e->pval = dalloc<float>(R * (size_t)(kVocab / 16));
     e->pidx = dalloc<int>(R * (size_t)(kVocab / 16));
-    e->counters = dalloc<int>(R * 2);
-    HCK(hipMemset(e->counters, 0, R * 2 * sizeof(int)));
+    e->kpart = dalloc<float>(R * 16 * kHidden);
+    e->prod = dalloc<uint16_t>(R * kFF);
     e->tok_dev = dalloc<int>(R);
     e->rlane = dalloc<int>(R);
     e->rpos = dalloc<int>(R);
@@ -335,7 +338,13 @@ void alloc_scratch(q35_engine* e) {
 
 void ensure_logits(q35_engine* e, int rows) {
     if (e->logits_rows >= rows) return;
-    if (e->logits_dev) HCK(hipFree(e->logits_dev));
+    if (e->logits_dev) {
+        // captured graphs hold the old pointer
+        HCK(hipStreamSynchronize(e->st));
+        for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
+        e->graphs.clear();
+        HCK(hipFree(e->logits_dev));
+    }
     e->logits_dev = dalloc<float>((size_t)rows * kVocab);
     e->logits_rows = rows;
 }
@@ -355,8 +364,9 @@ void gemm(q35_engine* e, const uint16_t* W, int N, int K, int M, const void* X, 
     GemmArgs a{};
     a.W = W; a.N = N; a.K = K; a.M = M; a.X = X; a.ldx = ldx; a.X2 = X2; a.ldx2 = ldx2;
     a.aux_w = aux; a.Y = Y; a.ldy = ldy;
+    a.kpart = e->kpart; a.prod = e->prod;
     KTimer kt(e, kFamGemm);
-    HCK(launch_gemm(a, amode, kEStore, e->st));
+    HCK(launch_gemm(a, amode, Y ? kEStore : kEPartial, e->st));
 }
 
 void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16_t* vc,
@@ -367,7 +377,6 @@ void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16
     a.kc = kc; a.vc = vc; a.kv_lane = kv_lane; a.kv_layer_off = layer_off; a.cap = cap;
     a.rm.lane = e->rlane; a.rm.pos = e->rpos; a.rm.slot = e->rslot;
     a.q = e->q; a.sc = e->sc; a.sc_ld = e->sc_ld; a.stats = e->stats; a.part = e->part;
-    a.counters = e->counters;
     a.max_chunks = (cap + 255) / 256;
     REQ(a.max_chunks <= e->max_chunks, Q35_ERR_CAP, "cache capacity exceeds engine max_ctx");
     a.out = e->aout; a.R = R; a.inv_freq = e->inv_freq;
@@ -375,25 +384,32 @@ void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16
         KTimer kt(e, kFamAttn);
         HCK(launch_attention(a, e->st));
     }
-    gemm(e, w.W_out, kHidden, 2048, R, e->aout, 2048, e->delta, kHidden);
+    gemm(e, w.W_out, kHidden, 2048, R, e->aout, 2048, nullptr, 0);
 }
 
 void mlp_layer(q35_engine* e, const LayerW& w, int R) {
-    HCK(launch_addnorm(1, nullptr, nullptr, e->x, e->delta, w.norm_post, e->h, R, e->st));
+    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, 2048 / 256, w.norm_post, e->h, R, e->st));
     gemm(e, w.W_gu, kGuRows, kHidden, R, e->h, kHidden, e->gu, kGuRows);
-    gemm(e, w.W_down, kHidden, kFF, R, e->gu, kGuRows, e->delta, kHidden, kASiluMul, e->gu + kFF, kGuRows);
+    gemm(e, w.W_down, kHidden, kFF, R, e->gu, kGuRows, nullptr, 0, kASiluMul, e->gu + kFF, kGuRows);
 }
 
 // Runs the 24-layer body over R = nl * T rows (rows of one lane consecutive) and leaves the
 // final-normed rows in e->nrm. ckpt: write the GDN state after every row (MTP verify).
+void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt);
+
 void body(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
     REQ(e->weights_ready, Q35_ERR_STATE, "weights not initialised");
     REQ(R > 0 && R <= e->R, Q35_ERR_CAP, "rows exceed engine max_rows");
     upload_rows(e, R);
     HCK(hipMemcpyAsync(s->cur_dev, s->cur.data(), s->lanes * sizeof(int), hipMemcpyHostToDevice, e->st));
+    body_kernels(e, s, R, T, ckpt);
+}
+
+// The launches of one body pass (no host transfers: capturable in a hipGraph).
+void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
     const int nl = R / T;
     const int cs = nl <= 8 ? 8 : nl <= 32 ? 4 : nl <= 64 ? 2 : 1;
-    HCK(launch_addnorm(0, e->tok_dev, e->E, e->x, nullptr, e->L[0].norm_in, e->h, R, e->st));
+    HCK(launch_addnorm(0, e->tok_dev, e->E, e->x, nullptr, nullptr, 0, e->L[0].norm_in, e->h, R, e->st));
     for (int l = 0; l < e->n_layers; ++l) {
         const LayerW& w = e->L[l];
         if (!is_attn_layer(l)) {
@@ -410,7 +426,7 @@ void body(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
                 KTimer kt(e, kFamGdn);
                 HCK(launch_gdn(g, cs, e->st));
             }
-            gemm(e, w.W_out, kHidden, 2048, R, e->o, 2048, e->delta, kHidden, kAGatedNorm,
+            gemm(e, w.W_out, kHidden, 2048, R, e->o, 2048, nullptr, 0, kAGatedNorm,
                  e->proj + kGdnZOff, kGdnInRows, w.gnorm);
         } else {
             attention_layer(e, w, R, s->kc, s->vc, s->kv_lane(),
@@ -419,7 +435,7 @@ void body(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
         mlp_layer(e, w, R);
         const bool lastl = l + 1 == e->n_layers;
         const uint16_t* nw = lastl ? e->final_norm : e->L[l + 1].norm_in;
-        HCK(launch_addnorm(1, nullptr, nullptr, e->x, e->delta, nw, lastl ? e->nrm : e->h, R, e->st));
+        HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, kFF / 256, nw, lastl ? e->nrm : e->h, R, e->st));
     }
 }
 
@@ -454,11 +470,11 @@ void mtp_draft_pass(q35_engine* e, q35_state* s, int n, const uint16_t* hsrc) {
     REQ(s->mtp_cap > 0, Q35_ERR_STATE, "state has no MTP cache");
     upload_rows(e, n);
     HCK(launch_mtp_concat(e->tok_dev, e->E, hsrc, kHidden, e->mtp_pre_e, e->mtp_pre_h, e->cat, n, e->st));
-    gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, e->x, kHidden);
-    HCK(launch_addnorm(2, nullptr, nullptr, e->x, nullptr, e->M.norm_in, e->h, n, e->st));
+    gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, nullptr, 0);
+    HCK(launch_addnorm(4, nullptr, nullptr, e->x, nullptr, e->kpart, 2048 / 256, e->M.norm_in, e->h, n, e->st));
     attention_layer(e, e->M, n, s->mkc, s->mvc, s->mkv_lane(), 0, s->mtp_cap);
     mlp_layer(e, e->M, n);
-    HCK(launch_addnorm(1, nullptr, nullptr, e->x, e->delta, e->mtp_norm, e->nrm, n, e->st));
+    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, kFF / 256, e->mtp_norm, e->nrm, n, e->st));
 }
 
 int guard(const std::function<void()>& f) {
@@ -502,9 +518,11 @@ int q35_destroy(q35_engine* e) {
     return guard([&] {
         if (!e) return;
         hipStreamSynchronize(e->st);
+        for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
+        e->graphs.clear();
         void* ds[] = {e->blob, e->x, e->h, e->delta, e->nrm, e->proj, e->gu, e->aout, e->cat, e->o, e->q,
-                      e->sc, e->stats, e->part, e->pval, e->pidx, e->counters, e->tok_dev, e->rlane,
-                      e->rpos, e->rslot, e->ridx_src, e->ridx_dst, e->inv_freq, e->logits_dev};
+                      e->sc, e->stats, e->part, e->pval, e->pidx, e->prod, e->tok_dev, e->rlane,
+                      e->rpos, e->rslot, e->ridx_src, e->ridx_dst, e->inv_freq, e->logits_dev, e->kpart};
         for (void* p : ds) if (p) hipFree(p);
         void* hs[] = {e->h_tok, e->h_lane, e->h_pos, e->h_slot, e->h_out, e->h_src, e->h_dst};
         for (void* p : hs) if (p) hipHostFree(p);
@@ -614,7 +632,15 @@ int q35_state_alloc(q35_engine* e, int lanes, int cap, int mtp_k, int mtp_cap, q
 int q35_state_free(q35_engine* e, q35_state* s) {
     return guard([&] {
         if (!s) return;
-        if (e) hipStreamSynchronize(e->st);
+        if (e) {
+            hipStreamSynchronize(e->st);
+            char pre[64];
+            std::snprintf(pre, sizeof pre, "dec:%p:", (void*)s);
+            for (auto it = e->graphs.begin(); it != e->graphs.end();) {
+                if (it->first.rfind(pre, 0) == 0) { hipGraphExecDestroy(it->second); it = e->graphs.erase(it); }
+                else ++it;
+            }
+        }
         void* ds[] = {s->S, s->win, s->kc, s->vc, s->mkc, s->mvc, s->hlast, s->cur_dev};
         for (void* p : ds) if (p) hipFree(p);
         delete s;
@@ -753,16 +779,46 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
             ls[i] = l;
             e->h_tok[i] = tokens[i]; e->h_lane[i] = l; e->h_pos[i] = s->prefix[l]; e->h_slot[i] = s->prefix[l];
         }
-        body(e, s, n, 1, false);
-        lm_head(e, 0, n, out_logits != nullptr);
-        std::vector<int> rows(n);
+        REQ(e->weights_ready, Q35_ERR_STATE, "weights not initialised");
+        for (int i = 0; i < n; ++i) { e->h_src[i] = i; e->h_dst[i] = ls[i]; }
+        upload_rows(e, n);
+        HCK(hipMemcpyAsync(s->cur_dev, s->cur.data(), s->lanes * sizeof(int), hipMemcpyHostToDevice, e->st));
+        HCK(hipMemcpyAsync(e->ridx_src, e->h_src, n * sizeof(int), hipMemcpyHostToDevice, e->st));
+        HCK(hipMemcpyAsync(e->ridx_dst, e->h_dst, n * sizeof(int), hipMemcpyHostToDevice, e->st));
+        auto step = [&] {
+            body_kernels(e, s, n, 1, false);
+            lm_head(e, 0, n, out_logits != nullptr);
+            HCK(launch_copy_rows(e->nrm, e->ridx_src, s->hlast, e->ridx_dst, n, kHidden, e->st));
+        };
+        if (e->use_graph && e->kprof == 0) {
+            if (out_logits) ensure_logits(e, n);
+            char key[128];
+            std::snprintf(key, sizeof key, "dec:%p:%d:%d:%d", (void*)s, n, out_logits ? 1 : 0, e->n_layers);
+            auto it = e->graphs.find(key);
+            if (it == e->graphs.end()) {
+                hipGraph_t g;
+                HCK(hipStreamBeginCapture(e->st, hipStreamCaptureModeThreadLocal));
+                try {
+                    step();
+                } catch (...) {
+                    hipStreamEndCapture(e->st, &g);
+                    throw;
+                }
+                HCK(hipStreamEndCapture(e->st, &g));
+                hipGraphExec_t ex;
+                HCK(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0));
+                HCK(hipGraphDestroy(g));
+                it = e->graphs.emplace(key, ex).first;
+            }
+            HCK(hipGraphLaunch(it->second, e->st));
+        } else {
+            step();
+        }
         for (int i = 0; i < n; ++i) {
-            rows[i] = i;
             s->prefix[ls[i]] += 1;
             s->cur[ls[i]] = (s->cur[ls[i]] + 1) % s->nslots;
         }
         HCK(hipMemcpyAsync(e->h_out, e->tok_dev, n * sizeof(int), hipMemcpyDeviceToHost, e->st));
-        save_hlast(e, s, rows, ls);
         if (out_logits) HCK(hipMemcpyAsync(out_logits, e->logits_dev, (size_t)n * kVocab * 4, hipMemcpyDeviceToHost, e->st));
         HCK(hipStreamSynchronize(e->st));
         for (int i = 0; i < n; ++i) out_tok[i] = e->h_out[i];

@@ -34,7 +34,9 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     const int cur = a.cur ? a.cur[lane] : 0;
 
     __shared__ float qs[128], ks[128], vs[VC];
-    __shared__ float red_r[NKG][VC], red_o[NKG][VC];
+    constexpr int NG = 16;            // fixed reduction groups of 8 k-rows, for every CS
+    constexpr int GPT = KR / 8;       // groups per thread
+    __shared__ float red_r[NG][VC], red_o[NG][VC];
     __shared__ float wred[4];
     __shared__ float gate_s[2];
 
@@ -107,30 +109,38 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
         }
         __syncthreads();
         const float gam = gate_s[0], beta = gate_s[1];
-        float rp = 0.f;
+        // reductions over k: 8-row partial sums, then the 16 partials in order -- the same
+        // arithmetic for every column-slice count, so batched lanes match batch 1 exactly
 #pragma unroll
-        for (int i = 0; i < KR; ++i) {
-            s[i] = __fmul_rn(s[i], gam);
-            rp = fmaf(s[i], ks[kg * KR + i], rp);
+        for (int gq = 0; gq < GPT; ++gq) {
+            float rp = 0.f;
+#pragma unroll
+            for (int i = gq * 8; i < gq * 8 + 8; ++i) {
+                s[i] = __fmul_rn(s[i], gam);
+                rp = fmaf(s[i], ks[kg * KR + i], rp);
+            }
+            red_r[kg * GPT + gq][jl] = rp;
         }
-        red_r[kg][jl] = rp;
         __syncthreads();
         float rj = 0.f;
 #pragma unroll
-        for (int i = 0; i < NKG; ++i) rj += red_r[i][jl];
+        for (int i = 0; i < NG; ++i) rj += red_r[i][jl];
         const float dv = __fmul_rn(beta, vs[jl] - rj);
-        float op = 0.f;
 #pragma unroll
-        for (int i = 0; i < KR; ++i) {
-            s[i] = __fadd_rn(s[i], __fmul_rn(ks[kg * KR + i], dv));
-            op = fmaf(qs[kg * KR + i], s[i], op);
+        for (int gq = 0; gq < GPT; ++gq) {
+            float op = 0.f;
+#pragma unroll
+            for (int i = gq * 8; i < gq * 8 + 8; ++i) {
+                s[i] = __fadd_rn(s[i], __fmul_rn(ks[kg * KR + i], dv));
+                op = fmaf(qs[kg * KR + i], s[i], op);
+            }
+            red_o[kg * GPT + gq][jl] = op;
         }
-        red_o[kg][jl] = op;
         __syncthreads();
         if (kg == 0) {
             float oj = 0.f;
 #pragma unroll
-            for (int i = 0; i < NKG; ++i) oj += red_o[i][jl];
+            for (int i = 0; i < NG; ++i) oj += red_o[i][jl];
             a.o[(size_t)r * 2048 + h * 128 + cs * VC + jl] = oj;
         }
         if (a.ckpt || t == a.T - 1) {

@@ -8,127 +8,126 @@
 //
 // Canonical reduction (shared by every kernel in this file, for any M): for each 256-wide
 // k-block kb, one chain of 8 v_mfma_f32_16x16x32_bf16 starting from zero gives c_kb; the
-// output is ((c_0 + c_1) + c_2) + ... in k-block order. Each output element therefore
-// depends only on its own row of A, never on M or on the other rows, so batched lanes, the
-// MTP verify rows and a batch-1 decode produce identical bits for the same row.
+// output is ((c_0 + c_1) + c_2) + ... in k-block order. Within a chain, step s of lane
+// (row or column i, group g) carries k = kb*256 + g*64 + s*8 .. +8. Each output element
+// therefore depends only on its own row of A, never on M or on the other rows, so batched
+// lanes, the MTP verify rows and a batch-1 decode produce identical bits for the same row.
+//
+// Kernels (all follow the order above):
+//   gemm_small_m   one 16-row tile; wave w of a block owns k-block w (M <= 16, batch 1);
+//                  with a producer the wave builds its A tile cooperatively in LDS
+//   gemm_large_m   4 waves x 16 columns, 64 or 128 rows per block; the A tile of each
+//                  k-block is staged once in LDS in MFMA fragment order (batched lanes);
+//                  a non-plain producer runs first as its own elementwise kernel
+// kEPartial (N = 1024 outputs feeding the residual add): each block computes ONE k-block
+// chain and stores it to kpart[kb][M][N]; the following add+norm kernel sums the chains in
+// k-block order. That keeps ~KB x more blocks in flight without cross-block atomics.
 //
 // A operand "producers" fuse the elementwise work of the consumer's input:
 //   kAPlain     bf16 rows
 //   kASiluMul   act = bf16(bf16(silu(g)) * u)          (specimpl.py:404-407)
 //   kAGatedNorm y = bf16(w * (o * rsqrt(mean_head(o^2)+eps)) * silu(z)), per 128-wide
 //               head, o f32, z bf16                    (specimpl.py:142-147, 304-305)
-// Epilogues: kEStore (bf16 rows) and kEArgmax (bf16-rounded logits, per-tile max with
-// the lowest index, optional f32 copy of the logits).
+// Epilogues: kEStore (bf16 rows), kEPartial (one f32 k-block chain) and kEArgmax
+// (bf16-rounded logits, per-tile max with the lowest index, optional f32 logits copy).
 #include "q35_common.h"
 #include "q35_kernels.h"
 
 namespace q35 {
 
+// ---------------------------------------------------------------- shared producers
+// Sum of squares of 64 consecutive f32 (half of a 128-wide head), fixed order.
+__device__ __forceinline__ float half_head_ss_regs(const float* v) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; i += 4)
+        ss = __fadd_rn(ss, __fadd_rn(__fadd_rn(__fmul_rn(v[i], v[i]), __fmul_rn(v[i + 1], v[i + 1])),
+                                     __fadd_rn(__fmul_rn(v[i + 2], v[i + 2]), __fmul_rn(v[i + 3], v[i + 3]))));
+    return ss;
+}
+__device__ __forceinline__ float half_head_ss(const float* po) {
+    float v[64];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) *(float4*)&v[4 * i] = *(const float4*)(po + 4 * i);
+    return half_head_ss_regs(v);
+}
+__device__ __forceinline__ float head_rsqrt(float ss_lo, float ss_hi) {
+    return rsqrtf(__fadd_rn(__fmul_rn(__fadd_rn(ss_lo, ss_hi), 1.0f / 128.0f), kEps));
+}
+// act = bf16(bf16(silu(g)) * u) for 8 packed bf16 pairs
+__device__ __forceinline__ q35_u32x4 silu_mul8(q35_u32x4 g, q35_u32x4 u) {
+    q35_u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float g0 = __uint_as_float(g[i] << 16), g1 = __uint_as_float(g[i] & 0xffff0000u);
+        float u0 = __uint_as_float(u[i] << 16), u1 = __uint_as_float(u[i] & 0xffff0000u);
+        uint32_t lo = f2bf(__fmul_rn(rbf(silu_f(g0)), u0));
+        uint32_t hi = f2bf(__fmul_rn(rbf(silu_f(g1)), u1));
+        r[i] = lo | (hi << 16);
+    }
+    return r;
+}
+// y = bf16(w * (o * rs) * silu(z)) for 8 elements
+__device__ __forceinline__ q35_u32x4 gated8(const float* ov, q35_u32x4 zz, q35_u32x4 ww, float rs) {
+    q35_u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t out2[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float z = h ? __uint_as_float(zz[i] & 0xffff0000u) : __uint_as_float(zz[i] << 16);
+            float w = h ? __uint_as_float(ww[i] & 0xffff0000u) : __uint_as_float(ww[i] << 16);
+            float n = __fmul_rn(ov[2 * i + h], rs);
+            out2[h] = f2bf(__fmul_rn(__fmul_rn(w, n), silu_f(z)));
+        }
+        r[i] = out2[0] | (out2[1] << 16);
+    }
+    return r;
+}
+
+// 8 A elements of row m at k0 (k0 % 8 == 0); rs = rsqrt of the head holding k0 (gated norm).
 template <int AM>
-__device__ __forceinline__ q35_bf16x8 load_a_frag(const GemmArgs& a, int m, int k0,
-                                                  const float* rs) {
+__device__ __forceinline__ q35_u32x4 produce_a(const GemmArgs& a, int m, int k0, float rs) {
     if (AM == kAPlain) {
-        const uint16_t* p = (const uint16_t*)a.X + (size_t)m * a.ldx + k0;
-        return *(const q35_bf16x8*)p;
+        return *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + k0);
     } else if (AM == kASiluMul) {
-        const uint16_t* pg = (const uint16_t*)a.X + (size_t)m * a.ldx + k0;
-        const uint16_t* pu = (const uint16_t*)a.X2 + (size_t)m * a.ldx2 + k0;
-        q35_u32x4 g = *(const q35_u32x4*)pg, u = *(const q35_u32x4*)pu;
-        q35_u32x4 r;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float g0 = __uint_as_float(g[i] << 16), g1 = __uint_as_float(g[i] & 0xffff0000u);
-            float u0 = __uint_as_float(u[i] << 16), u1 = __uint_as_float(u[i] & 0xffff0000u);
-            uint32_t lo = f2bf(rbf(silu_f(g0)) * u0), hi = f2bf(rbf(silu_f(g1)) * u1);
-            r[i] = lo | (hi << 16);
-        }
-        return *(q35_bf16x8*)&r;
-    } else {  // kAGatedNorm: rs[0] = rsqrt for this lane's head, handled by caller
+        q35_u32x4 g = *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + k0);
+        q35_u32x4 u = *(const q35_u32x4*)((const uint16_t*)a.X2 + (size_t)m * a.ldx2 + k0);
+        return silu_mul8(g, u);
+    } else {
         const float* po = (const float*)a.X + (size_t)m * a.ldx + k0;
-        const uint16_t* pz = (const uint16_t*)a.X2 + (size_t)m * a.ldx2 + k0;
-        const uint16_t* pw = a.aux_w + (k0 & 127);
-        q35_u32x4 zz = *(const q35_u32x4*)pz, ww = *(const q35_u32x4*)pw;
-        float4 o0 = *(const float4*)po, o1 = *(const float4*)(po + 4);
-        float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
-        q35_u32x4 r;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            uint32_t out2[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                float z = h ? __uint_as_float(zz[i] & 0xffff0000u) : __uint_as_float(zz[i] << 16);
-                float w = h ? __uint_as_float(ww[i] & 0xffff0000u) : __uint_as_float(ww[i] << 16);
-                float n = __fmul_rn(ov[2 * i + h], rs[0]);
-                out2[h] = f2bf(__fmul_rn(__fmul_rn(w, n), silu_f(z)));
-            }
-            r[i] = out2[0] | (out2[1] << 16);
-        }
-        return *(q35_bf16x8*)&r;
+        q35_u32x4 zz = *(const q35_u32x4*)((const uint16_t*)a.X2 + (size_t)m * a.ldx2 + k0);
+        q35_u32x4 ww = *(const q35_u32x4*)(a.aux_w + (k0 & 127));
+        float ov[8];
+        *(float4*)&ov[0] = *(const float4*)po;
+        *(float4*)&ov[4] = *(const float4*)(po + 4);
+        return gated8(ov, zz, ww, rs);
     }
 }
 
-// Small-M kernel: one block = one 16-column tile x one 16-row tile; wave w owns k-block w.
-template <int AM, int EM>
-__global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
-    const int nt = blockIdx.x;
-    const int mt = blockIdx.y;
-    const int lane = threadIdx.x & 63;
-    const int kb = threadIdx.x >> 6;
-    const int KB = a.K >> 8;
-    const int m = mt * 16 + (lane & 15);
-    const int g = lane >> 4;
-    const bool mvalid = m < a.M;
+__device__ __forceinline__ q35_bf16x8 as_bf(q35_u32x4 v) { return *(q35_bf16x8*)&v; }
 
-    // W fragments: 8 contiguous 1 KiB wave loads.
-    const q35_bf16x8* wp = (const q35_bf16x8*)(a.W + ((size_t)nt * KB + kb) * 4096) + lane;
-    q35_bf16x8 wf[8];
-#pragma unroll
-    for (int s = 0; s < 8; ++s) wf[s] = __builtin_nontemporal_load(wp + s * 64);
-
-    float rs = 0.f;
-    const int kbase = kb * 256 + g * 64;
-    if (AM == kAGatedNorm && mvalid) {
-        const float* po = (const float*)a.X + (size_t)m * a.ldx + kbase;
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < 64; i += 4) {
-            float4 v = *(const float4*)(po + i);
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-        }
-        ss += __shfl_xor(ss, 16, 64);     // the other half of the 128-wide head
-        rs = rsqrtf(ss * (1.0f / 128.0f) + kEps);
-    }
-    q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        q35_bf16x8 af;
-        if (mvalid) af = load_a_frag<AM>(a, m, kbase + s * 8, &rs);
-        else af = (q35_bf16x8){};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf[s], acc, 0, 0, 0);
-    }
-
-    __shared__ q35_f32x4 part[16][64];
-    part[kb][lane] = acc;
-    __syncthreads();
-    if (kb != 0) return;
-    q35_f32x4 sum = part[0][lane];
-    for (int w = 1; w < KB; ++w) {
-        q35_f32x4 p = part[w][lane];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sum[r] = sum[r] + p[r];
-    }
-    // lane holds D[row = 4*(lane/16) + r][col = lane%16]
+// Epilogue of one 16x16 tile: lane holds D[row0 + 4*(lane/16) + r][col0 + lane%16].
+template <int EM>
+__device__ __forceinline__ void epilogue(const GemmArgs& a, q35_f32x4 sum, int nt, int row0, int lane) {
     const int col = nt * 16 + (lane & 15);
-    if (EM == kEStore) {
+    const int g = lane >> 4;
+    if (EM == kEPartial) {      // sum is one k-block chain: blockIdx.z is its k-block
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            int row = mt * 16 + 4 * g + r;
+            int row = row0 + 4 * g + r;
+            if (row < a.M) a.kpart[((size_t)blockIdx.z * a.M + row) * a.N + col] = sum[r];
+        }
+    } else if (EM == kEStore) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            int row = row0 + 4 * g + r;
             if (row < a.M) a.Y[(size_t)row * a.ldy + col] = f2bf(sum[r]);
         }
     } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            int row = mt * 16 + 4 * g + r;
+            int row = row0 + 4 * g + r;
             float v = rbf(sum[r]);
             if (row < a.M && a.logits) a.logits[(size_t)row * a.ldl + col] = v;
             int idx = col;
@@ -146,13 +145,163 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- small M
+// kEStore / kEArgmax: grid (N/16, ceil(M/16)); block = KB waves, wave w owns k-block w.
+// kEPartial: grid (N/16, ceil(M/16), KB); one wave per block, storing its k-block chain.
+template <int AM, int EM>
+__global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
+    const int nt = blockIdx.x;
+    const int mt = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int KB = a.K >> 8;
+    const int kb = EM == kEPartial ? blockIdx.z : wv;
+    const int m = mt * 16 + (lane & 15);
+    const int g = lane >> 4;
+    const bool mvalid = m < a.M;
+
+    const q35_bf16x8* wp = (const q35_bf16x8*)(a.W + ((size_t)nt * KB + kb) * 4096) + lane;
+    q35_bf16x8 wf[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) wf[s] = __builtin_nontemporal_load(wp + s * 64);
+
+    const int kbase = kb * 256 + g * 64;
+    q35_u32x4 af[8];
+    if (AM == kAPlain) {
+        // all 8 fragment loads issued before the MFMAs
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            af[s] = mvalid ? *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + kbase + s * 8)
+                           : (q35_u32x4){0u, 0u, 0u, 0u};
+    } else {
+        // Producer modes (one wave per block, kEPartial): the wave builds its 16 x 256 A tile
+        // cooperatively -- only the M valid rows, 8 elements per (lane, chunk) -- into LDS in
+        // fragment order, so the per-element work is spread over all 64 lanes.
+        __shared__ q35_u32x4 As[8][64];
+        __shared__ float hss[16][4];
+        const int M = min(a.M - mt * 16, 16);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) As[s][lane] = (q35_u32x4){0u, 0u, 0u, 0u};
+        if (AM == kAGatedNorm) {
+            for (int c = lane; c < M * 4; c += 64) {
+                const int row = c >> 2, q = c & 3;
+                hss[row][q] = half_head_ss((const float*)a.X + (size_t)(mt * 16 + row) * a.ldx + kb * 256 + q * 64);
+            }
+        }
+        __syncthreads();
+        for (int c = lane; c < M * 32; c += 64) {
+            const int row = c >> 5, kc = c & 31;
+            const float rs = AM == kAGatedNorm ? head_rsqrt(hss[row][(kc >> 4) * 2], hss[row][(kc >> 4) * 2 + 1]) : 0.f;
+            As[kc & 7][(kc >> 3) * 16 + row] = produce_a<AM>(a, mt * 16 + row, kb * 256 + kc * 8, rs);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 8; ++s) af[s] = As[s][lane];
+    }
+    q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(af[s]), wf[s], acc, 0, 0, 0);
+    if (EM == kEPartial) {
+        epilogue<EM>(a, acc, nt, mt * 16, lane);
+        return;
+    }
+    __shared__ q35_f32x4 part[16][64];
+    part[wv][lane] = acc;
+    __syncthreads();
+    if (wv != 0) return;
+    q35_f32x4 sum = part[0][lane];
+    for (int w = 1; w < KB; ++w) {
+        q35_f32x4 p = part[w][lane];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sum[r] = sum[r] + p[r];
+    }
+    epilogue<EM>(a, sum, nt, mt * 16, lane);
+}
+
+// Elementwise A producer for batched launches: Y[m][k] = produce_a(m, k) (bf16), so the
+// GEMM that follows reads plain bf16 and each element is produced once.
+template <int AM>
+__global__ void __launch_bounds__(256) produce_kernel(GemmArgs a) {
+    const int m = blockIdx.x;
+    for (int c = threadIdx.x; c < a.K / 8; c += 256) {
+        const int k0 = c * 8;
+        float rs = 0.f;
+        if (AM == kAGatedNorm) {
+            const int hq = (k0 / 128) * 128;    // head start
+            const float* po = (const float*)a.X + (size_t)m * a.ldx;
+            rs = head_rsqrt(half_head_ss(po + hq), half_head_ss(po + hq + 64));
+        }
+        *(q35_u32x4*)(a.Y + (size_t)m * a.ldy + k0) = produce_a<AM>(a, m, k0, rs);
+    }
+}
+
+// ---------------------------------------------------------------- large M
+// Plain bf16 A. grid (ceil(N/64), ceil(M/(16*MT)), kEPartial ? KB : 1); 4 waves, wave w ->
+// column tile 4*blockIdx.x + w; the block's A rows of one k-block are staged in LDS in
+// MFMA fragment order (As[m-tile][step][lane]).
+template <int EM, int MT>
+__global__ void __launch_bounds__(256) gemm_large_m(GemmArgs a) {
+    __shared__ q35_u32x4 As[MT][8][64];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nt = blockIdx.x * 4 + wv;
+    const bool nvalid = nt < a.N / 16;
+    const int row0 = blockIdx.y * MT * 16;
+    const int KB = a.K >> 8;
+    const int kb0 = EM == kEPartial ? blockIdx.z : 0;
+    const int kb1 = EM == kEPartial ? blockIdx.z + 1 : KB;
+    q35_f32x4 sum[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) sum[i] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
+
+    for (int kb = kb0; kb < kb1; ++kb) {
+        q35_bf16x8 wf[8];
+        if (nvalid) {
+            const q35_bf16x8* wp = (const q35_bf16x8*)(a.W + ((size_t)nt * KB + kb) * 4096) + lane;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) wf[s] = wp[s * 64];
+        }
+        q35_u32x4 av[MT * 2];
+#pragma unroll
+        for (int i = 0; i < MT * 2; ++i) {
+            const int c = tid + i * 256;
+            const int row = c >> 5, kc = c & 31;
+            const int m = row0 + row;
+            av[i] = m < a.M ? *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + kb * 256 + kc * 8)
+                            : (q35_u32x4){0u, 0u, 0u, 0u};
+        }
+        __syncthreads();   // previous k-block's fragments are consumed
+#pragma unroll
+        for (int i = 0; i < MT * 2; ++i) {
+            const int c = tid + i * 256;
+            const int row = c >> 5, kc = c & 31;
+            As[row >> 4][kc & 7][(kc >> 3) * 16 + (row & 15)] = av[i];
+        }
+        __syncthreads();
+        if (nvalid) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                q35_f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < 8; ++s)
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(As[mt][s][lane]), wf[s], c, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sum[mt][r] = kb == kb0 ? c[r] : sum[mt][r] + c[r];
+            }
+        }
+    }
+    if (!nvalid) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) epilogue<EM>(a, sum[mt], nt, row0 + mt * 16, lane);
+}
+
 // Final argmax over the per-tile partials of each row: lowest id among the maxima.
-__global__ void __launch_bounds__(256) argmax_rows(const float* pv, const int* pi, int ldp, int n,
-                                                   int* out_tok, float* out_val) {
+__global__ void __launch_bounds__(1024) argmax_rows(const float* pv, const int* pi, int ldp, int n,
+                                                    int* out_tok, float* out_val) {
     const int row = blockIdx.x;
     float best = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += 256) {
+#pragma unroll 4
+    for (int i = threadIdx.x; i < n; i += 1024) {
         float v = pv[(size_t)row * ldp + i];
         int id = pi[(size_t)row * ldp + i];
         if (v > best || (v == best && id < bi)) { best = v; bi = id; }
@@ -163,42 +312,76 @@ __global__ void __launch_bounds__(256) argmax_rows(const float* pv, const int* p
         int i2 = __shfl_xor(bi, o, 64);
         if (v2 > best || (v2 == best && i2 < bi)) { best = v2; bi = i2; }
     }
-    __shared__ float sv[4];
-    __shared__ int si[4];
+    __shared__ float sv[16];
+    __shared__ int si[16];
     if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = best; si[threadIdx.x >> 6] = bi; }
     __syncthreads();
     if (threadIdx.x == 0) {
         best = sv[0];
         bi = si[0];
-        for (int w = 1; w < 4; ++w)
+        for (int w = 1; w < 16; ++w)
             if (sv[w] > best || (sv[w] == best && si[w] < bi)) { best = sv[w]; bi = si[w]; }
         out_tok[row] = bi;
         if (out_val) out_val[row] = best;
     }
 }
 
+template <int EM>
+static void launch_large(const GemmArgs& a, hipStream_t st) {
+    const int KB = a.K / 256;
+    const int gz = EM == kEPartial ? KB : 1;
+    if (a.M <= 64)
+        hipLaunchKernelGGL((gemm_large_m<EM, 4>), dim3((a.N / 16 + 3) / 4, (a.M + 63) / 64, gz), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((gemm_large_m<EM, 8>), dim3((a.N / 16 + 3) / 4, (a.M + 127) / 128, gz), dim3(256), 0, st, a);
+}
+
+template <int AM, int EM>
+static hipError_t launch_am_em(const GemmArgs& a, hipStream_t st) {
+    const int KB = a.K / 256;
+    if (a.M <= 16) {
+        if (AM != kAPlain && EM != kEPartial) return hipErrorInvalidValue;
+        if (EM == kEPartial)
+            hipLaunchKernelGGL((gemm_small_m<AM, EM>), dim3(a.N / 16, 1, KB), dim3(64), 0, st, a);
+        else
+            hipLaunchKernelGGL((gemm_small_m<AM, EM>), dim3(a.N / 16, 1, 1), dim3(64 * KB), 0, st, a);
+        return hipGetLastError();
+    }
+    if (AM != kAPlain) {
+        // produce A once into a.prod (bf16 [M][K]), then the plain batched GEMM
+        if (!a.prod) return hipErrorInvalidValue;
+        GemmArgs p = a;
+        p.Y = a.prod;
+        p.ldy = a.K;
+        hipLaunchKernelGGL((produce_kernel<AM>), dim3(a.M), dim3(256), 0, st, p);
+        GemmArgs g = a;
+        g.X = a.prod;
+        g.ldx = a.K;
+        launch_large<EM>(g, st);
+    } else {
+        launch_large<EM>(a, st);
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st) {
     if (a.K % 256 || a.N % 16 || a.K > 4096 || a.M <= 0) return hipErrorInvalidValue;
-    dim3 grid(a.N / 16, (a.M + 15) / 16);
-    dim3 block(64 * (a.K / 256));
-#define Q35_L(AMV, EMV) hipLaunchKernelGGL((gemm_small_m<AMV, EMV>), grid, block, 0, st, a)
-    if (emode == kEStore) {
-        if (amode == kAPlain) Q35_L(kAPlain, kEStore);
-        else if (amode == kASiluMul) Q35_L(kASiluMul, kEStore);
-        else if (amode == kAGatedNorm) Q35_L(kAGatedNorm, kEStore);
-        else return hipErrorInvalidValue;
-    } else if (emode == kEArgmax && amode == kAPlain) {
-        Q35_L(kAPlain, kEArgmax);
-    } else {
-        return hipErrorInvalidValue;
-    }
-#undef Q35_L
-    return hipGetLastError();
+    if (emode == kEPartial && (!a.kpart || a.K / 256 > 16)) return hipErrorInvalidValue;
+#define Q35_AM(EMV)                                                          \
+    if (amode == kAPlain) return launch_am_em<kAPlain, EMV>(a, st);          \
+    if (amode == kASiluMul) return launch_am_em<kASiluMul, EMV>(a, st);      \
+    if (amode == kAGatedNorm) return launch_am_em<kAGatedNorm, EMV>(a, st);  \
+    return hipErrorInvalidValue;
+    if (emode == kEStore) { Q35_AM(kEStore) }
+    if (emode == kEPartial) { Q35_AM(kEPartial) }
+    if (emode == kEArgmax && amode == kAPlain) return launch_am_em<kAPlain, kEArgmax>(a, st);
+#undef Q35_AM
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_argmax(const float* pv, const int* pi, int ldp, int n, int rows, int* tok,
                          float* val, hipStream_t st) {
-    hipLaunchKernelGGL(argmax_rows, dim3(rows), dim3(256), 0, st, pv, pi, ldp, n, tok, val);
+    hipLaunchKernelGGL(argmax_rows, dim3(rows), dim3(1024), 0, st, pv, pi, ldp, n, tok, val);
     return hipGetLastError();
 }
 

@@ -20,6 +20,7 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 // One row per block, 256 threads x 4 elements.
 __global__ void __launch_bounds__(256) addnorm_kernel(int mode, const int* tok, const uint16_t* E,
                                                       uint16_t* x, const uint16_t* delta,
+                                                      const float* kpart, int kblocks,
                                                       const uint16_t* w, uint16_t* h) {
     __shared__ float red[4];
     const int r = blockIdx.x;
@@ -36,10 +37,26 @@ __global__ void __launch_bounds__(256) addnorm_kernel(int mode, const int* tok, 
         uint2 a = *(const uint2*)xr;
         xv[0] = __uint_as_float(a.x << 16); xv[1] = __uint_as_float(a.x & 0xffff0000u);
         xv[2] = __uint_as_float(a.y << 16); xv[3] = __uint_as_float(a.y & 0xffff0000u);
-        if (mode == 1) {
-            uint2 d = *(const uint2*)(delta + (size_t)r * kHidden + k);
-            float dv[4] = {__uint_as_float(d.x << 16), __uint_as_float(d.x & 0xffff0000u),
-                           __uint_as_float(d.y << 16), __uint_as_float(d.y & 0xffff0000u)};
+        if (mode == 1 || mode == 3 || mode == 4) {
+            float dv[4];
+            if (mode == 1) {
+                uint2 d = *(const uint2*)(delta + (size_t)r * kHidden + k);
+                dv[0] = __uint_as_float(d.x << 16); dv[1] = __uint_as_float(d.x & 0xffff0000u);
+                dv[2] = __uint_as_float(d.y << 16); dv[3] = __uint_as_float(d.y & 0xffff0000u);
+            } else {
+                // GEMM k-block chains summed in k-block order, rounded once to bf16
+                const size_t stride = (size_t)gridDim.x * kHidden;
+                float4 d[16];
+#pragma unroll
+                for (int kb = 0; kb < 16; ++kb)
+                    if (kb < kblocks) d[kb] = *(const float4*)(kpart + kb * stride + (size_t)r * kHidden + k);
+                float4 c = d[0];
+#pragma unroll
+                for (int kb = 1; kb < 16; ++kb)
+                    if (kb < kblocks) { c.x = c.x + d[kb].x; c.y = c.y + d[kb].y; c.z = c.z + d[kb].z; c.w = c.w + d[kb].w; }
+                dv[0] = rbf(c.x); dv[1] = rbf(c.y); dv[2] = rbf(c.z); dv[3] = rbf(c.w);
+                if (mode == 4) { xv[0] = 0.f; xv[1] = 0.f; xv[2] = 0.f; xv[3] = 0.f; }
+            }
             uint16_t o[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) { o[i] = f2bf(xv[i] + dv[i]); xv[i] = bf2f(o[i]); }
@@ -97,10 +114,11 @@ __global__ void __launch_bounds__(256) mtp_concat_kernel(const int* tok, const u
 }
 
 hipError_t launch_addnorm(int mode, const int* tok, const uint16_t* E, uint16_t* x,
-                          const uint16_t* delta, const uint16_t* w, uint16_t* h, int rows,
-                          hipStream_t st) {
+                          const uint16_t* delta, const float* kpart, int kblocks,
+                          const uint16_t* w, uint16_t* h, int rows, hipStream_t st) {
     if (rows <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(addnorm_kernel, dim3(rows), dim3(256), 0, st, mode, tok, E, x, delta, w, h);
+    hipLaunchKernelGGL(addnorm_kernel, dim3(rows), dim3(256), 0, st, mode, tok, E, x, delta, kpart,
+                       kblocks, w, h);
     return hipGetLastError();
 }
 

@@ -7,7 +7,7 @@
 namespace q35 {
 
 enum { kAPlain = 0, kASiluMul = 1, kAGatedNorm = 2 };
-enum { kEStore = 0, kEArgmax = 1 };
+enum { kEStore = 0, kEArgmax = 1, kEPartial = 2 };
 
 struct GemmArgs {
     const uint16_t* W;     // tiled [N/16][K/256] x 8 KiB
@@ -24,6 +24,8 @@ struct GemmArgs {
     float* part_val;       // kEArgmax: per-(row, tile) max
     int* part_idx;
     int ldp;
+    float* kpart;          // kEPartial: k-block chains [K/256][M][N] f32
+    uint16_t* prod;        // M > 16 with a producer: bf16 [M][K] staging of the produced A
 };
 hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st);
 hipError_t launch_argmax(const float* pv, const int* pi, int ldp, int n, int rows, int* tok,
@@ -37,11 +39,13 @@ struct RowMeta {
 };
 
 // Residual add + zero-centred RMSNorm (specimpl.py:135-139, pairing :426-451).
-//   mode 0: x = E[tok[r]];  mode 1: x = bf16(x + delta);  mode 2: x unchanged
+//   mode 0: x = E[tok[r]];  mode 1: x = bf16(x + delta);  mode 2: x unchanged;
+//   mode 3: x = bf16(x + bf16(sum_kb kpart[kb][r]));  mode 4: x = bf16(sum_kb kpart[kb][r])
+//   (k-block chains summed in k-block order, the GEMM's canonical reduction)
 //   then h = rmsnorm_zc(x, w) (skipped when h == nullptr)
 hipError_t launch_addnorm(int mode, const int* tok, const uint16_t* E, uint16_t* x,
-                          const uint16_t* delta, const uint16_t* w, uint16_t* h, int rows,
-                          hipStream_t st);
+                          const uint16_t* delta, const float* kpart, int kblocks,
+                          const uint16_t* w, uint16_t* h, int rows, hipStream_t st);
 // MTP fc input: cat[rmsnorm_zc(E[tok], we) | rmsnorm_zc(hin, wh)] -> out [rows][2048]
 hipError_t launch_mtp_concat(const int* tok, const uint16_t* E, const uint16_t* hin, int ldh,
                              const uint16_t* we, const uint16_t* wh, uint16_t* out, int rows,
@@ -82,8 +86,7 @@ struct AttnArgs {
     float* sc;             // scratch scores [R][8][sc_ld]
     int sc_ld;
     float* stats;          // scratch [R][8][max_chunks][2]
-    float* part;           // scratch [R][max_chunks][8][256]
-    int* counters;         // [R][2] zero-initialised, restored to zero by the kernel
+    float* part;           // scratch [R][4 * max_chunks][8][256] (64-slot parts)
     int max_chunks;
     uint16_t* out;         // [R][2048] gated attention output (input of o_proj)
     int R;

@@ -23,7 +23,7 @@ def eng():
     e.close()
 
 
-@pytest.mark.parametrize("N,K,M", [(16, 256, 1), (6144, 1024, 1), (1024, 2048, 3), (1024, 3584, 16), (512, 1024, 33)])
+@pytest.mark.parametrize("N,K,M", [(16, 256, 1), (6144, 1024, 1), (1024, 2048, 3), (1024, 3584, 16), (512, 1024, 33), (1024, 2048, 200), (8224, 1024, 64)])
 def test_gemm_vs_float64(eng, N, K, M):
     import torch
     print(f"gemm N={N} K={K} M={M}", flush=True)
