@@ -109,8 +109,8 @@ def l2_scale(q: torch.Tensor, k: torch.Tensor):
 
 def gdn_recurrent(qn, kn, v, gam, beta, S):
     """Delta-rule recurrence, token loop (specimpl.py:287-294). S [H,Dk,Dv] f32."""
-    T = qn.shape[0]
-    o = torch.zeros((T, H_V, D_V), dtype=torch.float32)
+    T, H = qn.shape[0], qn.shape[1]
+    o = torch.zeros((T, H, v.shape[-1]), dtype=torch.float32)
     for t in range(T):
         gam_t, kt, qt, vt, bt = gam[t], kn[t], qn[t], v[t].float(), beta[t]
         S = S * gam_t[:, None, None]
