@@ -9,7 +9,7 @@
 //
 // Four launches per layer:
 //   attn_prep   (row, head)         q norm+rope -> f32 scratch; k norm+rope, v -> cache
-//   attn_scores (row, kv head, chunk) f32 scores -> scratch, per-chunk (max, sum e^(s-max))
+//   attn_scores (row, kv head, chunk) scores on MFMA -> scratch, per-chunk (max, sum e^(s-max))
 //   attn_pv     (row, kv head, 64-slot part) global (max, sum) from the chunk stats,
 //               p = bf16(e/l), partial P.V per part
 //   attn_combine (row, q head)      sum of the parts in order, bf16, times bf16(sigmoid(gate))
@@ -62,63 +62,102 @@ __global__ void __launch_bounds__(256) attn_prep(AttnArgs a) {
     }
 }
 
-// Thread = one cache slot of the chunk; 4 query heads of the kv group.
+// Scores on MFMA: a wave takes 16 cache slots per v_mfma_f32_16x16x32_bf16 chain with the
+// K rows as the A operand (lane (slot t, group g) reads dims g*64..+64 of slot t: one full
+// 128-byte line) and B = [q_hi(4 heads) | q_lo(4 heads) | 0], q_hi = bf16(q),
+// q_lo = bf16(q - q_hi), so s = C[t][h] + C[t][h+4] carries q to ~2^-16 relative.
+// Block = 4 waves = 256 slots (one chunk).
 __global__ void __launch_bounds__(256) attn_scores(AttnArgs a) {
-    __shared__ float4 qv[256];          // qv[d] = (q0[d], q1[d], q2[d], q3[d])
+    __shared__ float qs[4][256];
     __shared__ float red[4][4];
     const int r = blockIdx.x, j = blockIdx.y, c = blockIdx.z, tid = threadIdx.x;
+    const int lane = tid & 63, wv = tid >> 6;
     const int slot = a.rm.slot[r];
     if (c * kChunk > slot) return;
-    const int lane = a.rm.lane[r];
+    const int lrow = a.rm.lane[r];
     {
         const float* q = a.q + ((size_t)r * kNq + 4 * j) * 256;
-        qv[tid] = make_float4(q[tid], q[256 + tid], q[512 + tid], q[768 + tid]);
+        qs[0][tid] = q[tid]; qs[1][tid] = q[256 + tid]; qs[2][tid] = q[512 + tid]; qs[3][tid] = q[768 + tid];
+    }
+    const int n = lane & 15, g = lane >> 4;
+    const int t0 = c * kChunk + wv * 64;
+    // K fragments: 4 sub-tiles of 16 slots, 8 steps each (issued before the q setup)
+    const uint16_t* kbase = a.kc + lrow * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256;
+    q35_u32x4 kf[4][8];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        const int t = t0 + st * 16 + n;
+        const bool ok = t <= slot;
+        const q35_u32x4* kp = (const q35_u32x4*)(kbase + (size_t)t * 256 + g * 64);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) kf[st][s] = ok ? kp[s] : (q35_u32x4){0u, 0u, 0u, 0u};
     }
     __syncthreads();
-    const int t = c * kChunk + tid;
-    const bool valid = t <= slot;
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-    if (valid) {
-        const uint16_t* kr = a.kc + lane * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + t) * 256;
-#pragma unroll 4
-        for (int dd = 0; dd < 256; dd += 8) {
-            q35_u32x4 kk = *(const q35_u32x4*)(kr + dd);
+    q35_u32x4 qf[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float kf = (e & 1) ? __uint_as_float(kk[e >> 1] & 0xffff0000u) : __uint_as_float(kk[e >> 1] << 16);
-                float4 q = qv[dd + e];
-                s0 = fmaf(q.x, kf, s0); s1 = fmaf(q.y, kf, s1);
-                s2 = fmaf(q.z, kf, s2); s3 = fmaf(q.w, kf, s3);
+    for (int s = 0; s < 8; ++s) {
+        uint32_t w4[4];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+            uint32_t h2[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int d = g * 64 + s * 8 + e2 * 2 + h;
+                uint16_t v = 0;
+                if (n < 8) {
+                    const float qv = qs[n & 3][d];
+                    const uint16_t hi = f2bf(qv);
+                    v = n < 4 ? hi : f2bf(qv - bf2f(hi));
+                }
+                h2[h] = v;
             }
+            w4[e2] = h2[0] | (h2[1] << 16);
+        }
+        qf[s] = (q35_u32x4){w4[0], w4[1], w4[2], w4[3]};
+    }
+    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    float sv[4][4];      // [sub-tile][r] for this lane's head (lanes n < 4)
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&kf[st][s], *(q35_bf16x8*)&qf[s], acc, 0, 0, 0);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const float lo = __shfl_down(acc[rr], 4, 64);
+            const float sc = (acc[rr] + lo) * 0.0625f;
+            const int t = t0 + st * 16 + 4 * g + rr;
+            const bool ok = n < 4 && t <= slot;
+            sv[st][rr] = ok ? sc : -INFINITY;
+            if (ok) a.sc[((size_t)r * kNq + 4 * j + n) * a.sc_ld + t] = sc;
         }
     }
-    float sv[4] = {s0 * 0.0625f, s1 * 0.0625f, s2 * 0.0625f, s3 * 0.0625f};
-    float mx[4];
+    // per-head chunk max and sum of exp: lanes with n == h hold that head's 64 values
+    float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (valid) a.sc[((size_t)r * kNq + 4 * j + i) * a.sc_ld + t] = sv[i];
-        mx[i] = wave_max(valid ? sv[i] : -INFINITY);
-        if ((tid & 63) == 0) red[i][tid >> 6] = mx[i];
-    }
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) m = fmaxf(m, sv[st][rr]);
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (lane < 4) red[lane][wv] = m;
     __syncthreads();
-    float m[4], e[4];
+    const float mb = n < 4 ? fmaxf(fmaxf(red[n][0], red[n][1]), fmaxf(red[n][2], red[n][3])) : 0.f;
+    float e = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        m[i] = fmaxf(fmaxf(red[i][0], red[i][1]), fmaxf(red[i][2], red[i][3]));
-        e[i] = valid ? expf(sv[i] - m[i]) : 0.f;
-    }
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) e += (n < 4 && sv[st][rr] > -INFINITY) ? expf(sv[st][rr] - mb) : 0.f;
+    e += __shfl_xor(e, 16, 64);
+    e += __shfl_xor(e, 32, 64);
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float se = wave_sum(e[i]);
-        if ((tid & 63) == 0) red[i][tid >> 6] = se;
-    }
+    if (lane < 4) red[lane][wv] = e;
     __syncthreads();
     if (tid < 4) {
-        float l = (red[tid][0] + red[tid][1]) + (red[tid][2] + red[tid][3]);
         float* st = a.stats + (((size_t)r * kNq + 4 * j + tid) * a.max_chunks + c) * 2;
-        st[0] = m[tid];
-        st[1] = l;
+        st[0] = mb;
+        st[1] = (red[tid][0] + red[tid][1]) + (red[tid][2] + red[tid][3]);
     }
 }
 
@@ -136,42 +175,52 @@ __global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
     if (pc >= nparts) return;
     const int nch = slot / kChunk + 1;
     const int lane = a.rm.lane[r];
+    const int t0 = pc * kPart;
+    const int n = min(kPart, slot + 1 - t0);
+    // V loads first: they do not depend on the softmax bookkeeping below
+    const int dg = tid & 31, tg = tid >> 5;
+    const uint16_t* vr = a.vc + lane * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + t0) * 256 + dg * 8;
+    q35_u32x4 vv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int t = tg * 8 + u;
+        vv[u] = t < n ? *(const q35_u32x4*)(vr + (size_t)t * 256) : (q35_u32x4){0u, 0u, 0u, 0u};
+    }
     if (tid < 4) {
         const float* st = a.stats + ((size_t)r * kNq + 4 * j + tid) * a.max_chunks * 2;
+        float mv[32], lv[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i)
+            if (i < nch) { mv[i] = st[2 * i]; lv[i] = st[2 * i + 1]; }
         float m = -INFINITY;
-        for (int i = 0; i < nch; ++i) m = fmaxf(m, st[2 * i]);
+#pragma unroll
+        for (int i = 0; i < 32; ++i)
+            if (i < nch) m = fmaxf(m, mv[i]);
+        for (int i = 32; i < nch; ++i) m = fmaxf(m, st[2 * i]);
         float l = 0.f;
-        for (int i = 0; i < nch; ++i) l += st[2 * i + 1] * expf(st[2 * i] - m);
+#pragma unroll
+        for (int i = 0; i < 32; ++i)
+            if (i < nch) l += lv[i] * expf(mv[i] - m);
+        for (int i = 32; i < nch; ++i) l += st[2 * i + 1] * expf(st[2 * i] - m);
         ml[tid][0] = m;
         ml[tid][1] = l;
     }
-    __syncthreads();
-    const int t0 = pc * kPart;
-    const int n = min(kPart, slot + 1 - t0);
+    float sraw = 0.f;
     {
         const int i = tid >> 6, t = tid & 63;
-        float pv = 0.f;
-        if (t < n) {
-            float s = a.sc[((size_t)r * kNq + 4 * j + i) * a.sc_ld + t0 + t];
-            pv = rbf(expf(s - ml[i][0]) / ml[i][1]);
-        }
-        p[i][t] = pv;
+        if (t < n) sraw = a.sc[((size_t)r * kNq + 4 * j + i) * a.sc_ld + t0 + t];
     }
     __syncthreads();
-    const int dg = tid & 31, tg = tid >> 5;
-    const uint16_t* vr = a.vc + lane * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + t0) * 256 + dg * 8;
+    {
+        const int i = tid >> 6, t = tid & 63;
+        p[i][t] = t < n ? rbf(expf(sraw - ml[i][0]) / ml[i][1]) : 0.f;
+    }
+    __syncthreads();
     float acc[4][8];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
-    q35_u32x4 vv[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        const int t = tg * 8 + u;
-        if (t < n) vv[u] = *(const q35_u32x4*)(vr + (size_t)t * 256);
-        else vv[u] = (q35_u32x4){0u, 0u, 0u, 0u};
-    }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
         const int t = tg * 8 + u;

@@ -89,6 +89,7 @@ struct q35_state {
     uint16_t *mkc = nullptr, *mvc = nullptr;  // [lanes][2][mtp_cap][256]
     uint16_t* hlast = nullptr;                // [lanes][1024] post-final-norm row of the last body
     int* cur_dev = nullptr;                   // [lanes]
+    int* h_cur = nullptr;                     // [lanes] pinned staging of `cur` for the upload
     std::vector<int> prefix, mtp_len, cur;
     long long S_lane() const { return (long long)nslots * kGdnLayers * kSLayer; }
     long long W_lane() const { return (long long)nslots * kGdnLayers * 18432; }
@@ -164,6 +165,13 @@ T* halloc(size_t n) {
     void* p = nullptr;
     HCK(hipHostMalloc(&p, n * sizeof(T) > 0 ? n * sizeof(T) : 16, hipHostMallocDefault));
     return (T*)p;
+}
+
+// Blocking copy ordered on the engine stream (the stream is non-blocking, so null-stream
+// copies would not be ordered with its kernels).
+void copy_sync(q35_engine* e, void* dst, const void* src, size_t n, hipMemcpyKind kind) {
+    HCK(hipMemcpyAsync(dst, src, n, kind, e->st));
+    HCK(hipStreamSynchronize(e->st));
 }
 
 // ------------------------------------------------------------------ weight registry
@@ -333,7 +341,7 @@ void alloc_scratch(q35_engine* e) {
         invf[i] = 1.0f / pw;
     }
     e->inv_freq = dalloc<float>(32);
-    HCK(hipMemcpy(e->inv_freq, invf, sizeof(invf), hipMemcpyHostToDevice));
+    copy_sync(e, e->inv_freq, invf, sizeof(invf), hipMemcpyHostToDevice);
 }
 
 void ensure_logits(q35_engine* e, int rows) {
@@ -356,6 +364,13 @@ void upload_rows(q35_engine* e, int R) {
     HCK(hipMemcpyAsync(e->rlane, e->h_lane, R * sizeof(int), hipMemcpyHostToDevice, e->st));
     HCK(hipMemcpyAsync(e->rpos, e->h_pos, R * sizeof(int), hipMemcpyHostToDevice, e->st));
     HCK(hipMemcpyAsync(e->rslot, e->h_slot, R * sizeof(int), hipMemcpyHostToDevice, e->st));
+}
+
+// `cur` goes through pinned staging: the host advances s->cur right after enqueueing a
+// body, so the copy must not read the live vector. Callers drain the stream before a body.
+void upload_cur(q35_engine* e, q35_state* s) {
+    for (int i = 0; i < s->lanes; ++i) s->h_cur[i] = s->cur[i];
+    HCK(hipMemcpyAsync(s->cur_dev, s->h_cur, s->lanes * sizeof(int), hipMemcpyHostToDevice, e->st));
 }
 
 void gemm(q35_engine* e, const uint16_t* W, int N, int K, int M, const void* X, int ldx,
@@ -401,7 +416,7 @@ void body(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
     REQ(e->weights_ready, Q35_ERR_STATE, "weights not initialised");
     REQ(R > 0 && R <= e->R, Q35_ERR_CAP, "rows exceed engine max_rows");
     upload_rows(e, R);
-    HCK(hipMemcpyAsync(s->cur_dev, s->cur.data(), s->lanes * sizeof(int), hipMemcpyHostToDevice, e->st));
+    upload_cur(e, s);
     body_kernels(e, s, R, T, ckpt);
 }
 
@@ -570,12 +585,12 @@ int q35_load_tensor(q35_engine* e, const char* name, const uint16_t* host, size_
         REQ(n == (size_t)p.rows * p.cols, Q35_ERR_ARG, "element count mismatch");
         if (p.tiled) {
             uint16_t* tmp = dalloc<uint16_t>(n);
-            HCK(hipMemcpy(tmp, host, n * 2, hipMemcpyHostToDevice));
+            copy_sync(e, tmp, host, n * 2, hipMemcpyHostToDevice);
             HCK(launch_tile(tmp, p.rows, p.cols, p.base, p.row_off, 0, e->st));
             HCK(hipStreamSynchronize(e->st));
             HCK(hipFree(tmp));
         } else {
-            HCK(hipMemcpy(p.base, host, n * 2, hipMemcpyHostToDevice));
+            copy_sync(e, p.base, host, n * 2, hipMemcpyHostToDevice);
         }
         e->weights_ready = true;
     });
@@ -592,11 +607,11 @@ int q35_read_tensor(q35_engine* e, const char* name, uint16_t* host, size_t n) {
             uint16_t* tmp = dalloc<uint16_t>(n);
             HCK(launch_tile(p.base, p.rows, p.cols, tmp, p.row_off, 1, e->st));
             HCK(hipStreamSynchronize(e->st));
-            HCK(hipMemcpy(host, tmp, n * 2, hipMemcpyDeviceToHost));
+            copy_sync(e, host, tmp, n * 2, hipMemcpyDeviceToHost);
             HCK(hipFree(tmp));
         } else {
             HCK(hipStreamSynchronize(e->st));
-            HCK(hipMemcpy(host, p.base, n * 2, hipMemcpyDeviceToHost));
+            copy_sync(e, host, p.base, n * 2, hipMemcpyDeviceToHost);
         }
     });
 }
@@ -619,12 +634,16 @@ int q35_state_alloc(q35_engine* e, int lanes, int cap, int mtp_k, int mtp_cap, q
         }
         s->hlast = dalloc<uint16_t>((size_t)lanes * kHidden);
         s->cur_dev = dalloc<int>(lanes);
+        s->h_cur = halloc<int>(lanes);
         s->prefix.assign(lanes, 0);
         s->mtp_len.assign(lanes, 0);
         s->cur.assign(lanes, 0);
-        HCK(hipMemset(s->S, 0, (size_t)lanes * s->S_lane() * 4));
-        HCK(hipMemset(s->win, 0, (size_t)lanes * s->W_lane() * 4));
-        HCK(hipMemset(s->hlast, 0, (size_t)lanes * kHidden * 2));
+        // zeroed on the engine stream (non-blocking: a null-stream memset could still be
+        // running when the first body's kernels start)
+        HCK(hipMemsetAsync(s->S, 0, (size_t)lanes * s->S_lane() * 4, e->st));
+        HCK(hipMemsetAsync(s->win, 0, (size_t)lanes * s->W_lane() * 4, e->st));
+        HCK(hipMemsetAsync(s->hlast, 0, (size_t)lanes * kHidden * 2, e->st));
+        HCK(hipStreamSynchronize(e->st));
         *out = s;
     });
 }
@@ -643,6 +662,7 @@ int q35_state_free(q35_engine* e, q35_state* s) {
         }
         void* ds[] = {s->S, s->win, s->kc, s->vc, s->mkc, s->mvc, s->hlast, s->cur_dev};
         for (void* p : ds) if (p) hipFree(p);
+        if (s->h_cur) hipHostFree(s->h_cur);
         delete s;
     });
 }
@@ -700,8 +720,8 @@ static void state_io(q35_engine* e, q35_state* s, int lane, int which, int n_slo
     HCK(hipStreamSynchronize(e->st));
     auto cp = [&](void* dev, size_t off_bytes, size_t nb) {
         REQ(off_bytes + nb <= bytes, Q35_ERR_ARG, "host buffer too small");
-        if (write) HCK(hipMemcpy(dev, (char*)host + off_bytes, nb, hipMemcpyHostToDevice));
-        else HCK(hipMemcpy((char*)host + off_bytes, dev, nb, hipMemcpyDeviceToHost));
+        if (write) copy_sync(e, dev, (char*)host + off_bytes, nb, hipMemcpyHostToDevice);
+        else copy_sync(e, (char*)host + off_bytes, dev, nb, hipMemcpyDeviceToHost);
     };
     const int cur = s->cur[lane];
     if (which == 0) {
@@ -782,7 +802,7 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
         REQ(e->weights_ready, Q35_ERR_STATE, "weights not initialised");
         for (int i = 0; i < n; ++i) { e->h_src[i] = i; e->h_dst[i] = ls[i]; }
         upload_rows(e, n);
-        HCK(hipMemcpyAsync(s->cur_dev, s->cur.data(), s->lanes * sizeof(int), hipMemcpyHostToDevice, e->st));
+        upload_cur(e, s);
         HCK(hipMemcpyAsync(e->ridx_src, e->h_src, n * sizeof(int), hipMemcpyHostToDevice, e->st));
         HCK(hipMemcpyAsync(e->ridx_dst, e->h_dst, n * sizeof(int), hipMemcpyHostToDevice, e->st));
         auto step = [&] {
@@ -980,7 +1000,7 @@ int q35_read_scratch(q35_engine* e, const char* name, void* host, size_t bytes) 
         else throw Q35Error(Q35_ERR_ARG, "unknown scratch " + n);
         REQ(bytes <= cap, Q35_ERR_ARG, "read exceeds scratch size");
         HCK(hipStreamSynchronize(e->st));
-        HCK(hipMemcpy(host, p, bytes, hipMemcpyDeviceToHost));
+        copy_sync(e, host, p, bytes, hipMemcpyDeviceToHost);
     });
 }
 

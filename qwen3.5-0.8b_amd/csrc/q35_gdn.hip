@@ -16,7 +16,8 @@
 // the engine advances `cur` after the step.
 //
 // Grid: (lane group, head, column slice). A block owns VC = 128/CS value columns of one
-// head; thread (jl, kg) holds S[kg*KR .. kg*KR+KR)[jl] in registers.
+// head; thread (column group, kg) holds S[kg*KR .. kg*KR+KR) of CW adjacent columns in
+// registers (CW = 4 when a block owns the whole head: 16-byte state loads and stores).
 #include "q35_common.h"
 #include "q35_kernels.h"
 
@@ -24,12 +25,14 @@ namespace q35 {
 
 template <int CS>
 __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
-    constexpr int VC = 128 / CS;
-    constexpr int NKG = 256 / VC;
-    constexpr int KR = 128 / NKG;
+    constexpr int VC = 128 / CS;                 // value columns of this block
+    constexpr int CW = CS == 1 ? 4 : 1;          // adjacent columns per thread (16-byte I/O)
+    constexpr int CG = VC / CW;                  // column groups
+    constexpr int NKG = 256 / CG;                // k-row groups
+    constexpr int KR = 128 / NKG;                // k rows per thread (a multiple of 8)
     const int gi = blockIdx.x, h = blockIdx.y, cs = blockIdx.z;
     const int tid = threadIdx.x;
-    const int jl = tid % VC, kg = tid / VC;
+    const int jc = (tid % CG) * CW, kg = tid / CG;
     const int lane = a.lane[gi * a.T];
     const int cur = a.cur ? a.cur[lane] : 0;
 
@@ -63,9 +66,17 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
             cvw[2] = __uint_as_float(d.y << 16); cvw[3] = __uint_as_float(d.y & 0xffff0000u);
         }
     }
-    float s[KR];
+    float s[KR][CW];
 #pragma unroll
-    for (int i = 0; i < KR; ++i) s[i] = Sin[(kg * KR + i) * 128 + cs * VC + jl];
+    for (int i = 0; i < KR; ++i) {
+        const float* p = Sin + (kg * KR + i) * 128 + cs * VC + jc;
+        if (CW == 4) {
+            float4 v = *(const float4*)p;
+            s[i][0] = v.x; s[i][CW > 1 ? 1 : 0] = v.y; s[i][CW > 2 ? 2 : 0] = v.z; s[i][CW > 3 ? 3 : 0] = v.w;
+        } else {
+            s[i][0] = p[0];
+        }
+    }
 
     const float A = -expf(bf2f(a.A_log[h]));
     const float dtb = bf2f(a.dt_bias[h]);
@@ -112,42 +123,57 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
         // reductions over k: 8-row partial sums, then the 16 partials in order -- the same
         // arithmetic for every column-slice count, so batched lanes match batch 1 exactly
 #pragma unroll
-        for (int gq = 0; gq < GPT; ++gq) {
-            float rp = 0.f;
+        for (int c = 0; c < CW; ++c)
 #pragma unroll
-            for (int i = gq * 8; i < gq * 8 + 8; ++i) {
-                s[i] = __fmul_rn(s[i], gam);
-                rp = fmaf(s[i], ks[kg * KR + i], rp);
+            for (int gq = 0; gq < GPT; ++gq) {
+                float rp = 0.f;
+#pragma unroll
+                for (int i = gq * 8; i < gq * 8 + 8; ++i) {
+                    s[i][c] = __fmul_rn(s[i][c], gam);
+                    rp = fmaf(s[i][c], ks[kg * KR + i], rp);
+                }
+                red_r[kg * GPT + gq][jc + c] = rp;
             }
-            red_r[kg * GPT + gq][jl] = rp;
-        }
         __syncthreads();
-        float rj = 0.f;
+        float dv[CW];
 #pragma unroll
-        for (int i = 0; i < NG; ++i) rj += red_r[i][jl];
-        const float dv = __fmul_rn(beta, vs[jl] - rj);
+        for (int c = 0; c < CW; ++c) {
+            float rj = 0.f;
 #pragma unroll
-        for (int gq = 0; gq < GPT; ++gq) {
-            float op = 0.f;
-#pragma unroll
-            for (int i = gq * 8; i < gq * 8 + 8; ++i) {
-                s[i] = __fadd_rn(s[i], __fmul_rn(ks[kg * KR + i], dv));
-                op = fmaf(qs[kg * KR + i], s[i], op);
-            }
-            red_o[kg * GPT + gq][jl] = op;
+            for (int i = 0; i < NG; ++i) rj += red_r[i][jc + c];
+            dv[c] = __fmul_rn(beta, vs[jc + c] - rj);
         }
+#pragma unroll
+        for (int c = 0; c < CW; ++c)
+#pragma unroll
+            for (int gq = 0; gq < GPT; ++gq) {
+                float op = 0.f;
+#pragma unroll
+                for (int i = gq * 8; i < gq * 8 + 8; ++i) {
+                    s[i][c] = __fadd_rn(s[i][c], __fmul_rn(ks[kg * KR + i], dv[c]));
+                    op = fmaf(qs[kg * KR + i], s[i][c], op);
+                }
+                red_o[kg * GPT + gq][jc + c] = op;
+            }
         __syncthreads();
         if (kg == 0) {
-            float oj = 0.f;
 #pragma unroll
-            for (int i = 0; i < NG; ++i) oj += red_o[i][jl];
-            a.o[(size_t)r * 2048 + h * 128 + cs * VC + jl] = oj;
+            for (int c = 0; c < CW; ++c) {
+                float oj = 0.f;
+#pragma unroll
+                for (int i = 0; i < NG; ++i) oj += red_o[i][jc + c];
+                a.o[(size_t)r * 2048 + h * 128 + cs * VC + jc + c] = oj;
+            }
         }
         if (a.ckpt || t == a.T - 1) {
             const int slot = (cur + 1 + (a.ckpt ? t : 0)) % a.nslots;
             float* So = Sbase + slot * a.S_slot;
 #pragma unroll
-            for (int i = 0; i < KR; ++i) So[(kg * KR + i) * 128 + cs * VC + jl] = s[i];
+            for (int i = 0; i < KR; ++i) {
+                float* p = So + (kg * KR + i) * 128 + cs * VC + jc;
+                if (CW == 4) *(float4*)p = make_float4(s[i][0], s[i][CW > 1 ? 1 : 0], s[i][CW > 2 ? 2 : 0], s[i][CW > 3 ? 3 : 0]);
+                else p[0] = s[i][0];
+            }
             float* Wo = Wbase + slot * a.W_slot;
             if (cs == 0) { Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2; }
             if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
