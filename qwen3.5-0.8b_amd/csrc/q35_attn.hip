@@ -10,7 +10,7 @@
 // Four launches per layer:
 //   attn_prep   (row, head)         q norm+rope -> f32 scratch; k norm+rope, v -> cache
 //   attn_scores (row, kv head, chunk) scores on MFMA -> scratch, per-chunk (max, sum e^(s-max))
-//   attn_pv     (row, kv head, 64-slot part) global (max, sum) from the chunk stats,
+//   attn_pv     (row, kv head, 128-slot part) global (max, sum) from the chunk stats,
 //               p = bf16(e/l), partial P.V per part
 //   attn_combine (row, q head)      sum of the parts in order, bf16, times bf16(sigmoid(gate))
 // The k cache holds bf16(k post-rope); the reference's torch path keeps it in f32, so
@@ -63,58 +63,46 @@ __global__ void __launch_bounds__(256) attn_prep(AttnArgs a) {
 }
 
 // Scores on MFMA: a wave takes 16 cache slots per v_mfma_f32_16x16x32_bf16 chain with the
-// K rows as the A operand (lane (slot t, group g) reads dims g*64..+64 of slot t: one full
-// 128-byte line) and B = [q_hi(4 heads) | q_lo(4 heads) | 0], q_hi = bf16(q),
+// K rows as the A operand (step s of lane (slot t, group g) carries dims s*32 + g*8 .. +8,
+// so each load instruction reads 64 contiguous bytes of 16 slots) and B = [q_hi(4 heads) | q_lo(4 heads) | 0], q_hi = bf16(q),
 // q_lo = bf16(q - q_hi), so s = C[t][h] + C[t][h+4] carries q to ~2^-16 relative.
 // Block = 4 waves = 256 slots (one chunk).
 __global__ void __launch_bounds__(256) attn_scores(AttnArgs a) {
-    __shared__ float qs[4][256];
+    __shared__ uint16_t qb[16][256];   // B operand columns: q_hi heads 0-3, q_lo heads 0-3, zeros
     __shared__ float red[4][4];
     const int r = blockIdx.x, j = blockIdx.y, c = blockIdx.z, tid = threadIdx.x;
     const int lane = tid & 63, wv = tid >> 6;
     const int slot = a.rm.slot[r];
     if (c * kChunk > slot) return;
     const int lrow = a.rm.lane[r];
-    {
-        const float* q = a.q + ((size_t)r * kNq + 4 * j) * 256;
-        qs[0][tid] = q[tid]; qs[1][tid] = q[256 + tid]; qs[2][tid] = q[512 + tid]; qs[3][tid] = q[768 + tid];
-    }
     const int n = lane & 15, g = lane >> 4;
     const int t0 = c * kChunk + wv * 64;
-    // K fragments: 4 sub-tiles of 16 slots, 8 steps each (issued before the q setup)
+    // K fragments: 4 sub-tiles of 16 slots, 8 steps each, issued first
     const uint16_t* kbase = a.kc + lrow * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256;
     q35_u32x4 kf[4][8];
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-        const int t = t0 + st * 16 + n;
-        const bool ok = t <= slot;
-        const q35_u32x4* kp = (const q35_u32x4*)(kbase + (size_t)t * 256 + g * 64);
+        const int t = min(t0 + st * 16 + n, slot);        // clamped: masked below
+        const uint16_t* kp = kbase + (size_t)t * 256 + g * 8;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) kf[st][s] = ok ? kp[s] : (q35_u32x4){0u, 0u, 0u, 0u};
+        for (int s = 0; s < 8; ++s) kf[st][s] = *(const q35_u32x4*)(kp + s * 32);
+    }
+    {
+        const float* q = a.q + ((size_t)r * kNq + 4 * j) * 256;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const float qv = q[h * 256 + tid];
+            const uint16_t hi = f2bf(qv);
+            qb[h][tid] = hi;
+            qb[4 + h][tid] = f2bf(qv - bf2f(hi));
+            qb[8 + h][tid] = 0;
+            qb[12 + h][tid] = 0;
+        }
     }
     __syncthreads();
     q35_u32x4 qf[8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        uint32_t w4[4];
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-            uint32_t h2[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int d = g * 64 + s * 8 + e2 * 2 + h;
-                uint16_t v = 0;
-                if (n < 8) {
-                    const float qv = qs[n & 3][d];
-                    const uint16_t hi = f2bf(qv);
-                    v = n < 4 ? hi : f2bf(qv - bf2f(hi));
-                }
-                h2[h] = v;
-            }
-            w4[e2] = h2[0] | (h2[1] << 16);
-        }
-        qf[s] = (q35_u32x4){w4[0], w4[1], w4[2], w4[3]};
-    }
+    for (int s = 0; s < 8; ++s) qf[s] = *(const q35_u32x4*)&qb[n][s * 32 + g * 8];
     float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     float sv[4][4];      // [sub-tile][r] for this lane's head (lanes n < 4)
 #pragma unroll
@@ -161,14 +149,15 @@ __global__ void __launch_bounds__(256) attn_scores(AttnArgs a) {
     }
 }
 
-// P.V over one 64-slot part: thread (dg, tg) owns dims dg*8..+8 for slots tg*8..+8 of the
-// part (16-byte V loads), the 8 slot groups are summed in order through LDS.
-constexpr int kPart = 64;
+// P.V over one 128-slot part: thread (dg, tg) owns dims dg*8..+8 for slots tg*16..+16 of
+// the part (16-byte V loads, issued before the softmax bookkeeping); the 8 slot groups are
+// summed in order (pairs in a wave by a lane swap, then the 4 waves through LDS).
+constexpr int kPart = 128;
 
 __global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
     __shared__ float p[4][kPart];
     __shared__ float ml[4][2];
-    __shared__ float red[8][4][256];
+    __shared__ float red[4][4][256];
     const int r = blockIdx.x, j = blockIdx.y, pc = blockIdx.z, tid = threadIdx.x;
     const int slot = a.rm.slot[r];
     const int nparts = slot / kPart + 1;
@@ -177,13 +166,12 @@ __global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
     const int lane = a.rm.lane[r];
     const int t0 = pc * kPart;
     const int n = min(kPart, slot + 1 - t0);
-    // V loads first: they do not depend on the softmax bookkeeping below
     const int dg = tid & 31, tg = tid >> 5;
     const uint16_t* vr = a.vc + lane * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + t0) * 256 + dg * 8;
-    q35_u32x4 vv[8];
+    q35_u32x4 vv[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        const int t = tg * 8 + u;
+    for (int u = 0; u < 16; ++u) {
+        const int t = tg * 16 + u;
         vv[u] = t < n ? *(const q35_u32x4*)(vr + (size_t)t * 256) : (q35_u32x4){0u, 0u, 0u, 0u};
     }
     if (tid < 4) {
@@ -205,15 +193,17 @@ __global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
         ml[tid][0] = m;
         ml[tid][1] = l;
     }
-    float sraw = 0.f;
-    {
-        const int i = tid >> 6, t = tid & 63;
-        if (t < n) sraw = a.sc[((size_t)r * kNq + 4 * j + i) * a.sc_ld + t0 + t];
+    float sraw[2] = {0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int idx = tid + q * 256, i = idx >> 7, t = idx & 127;
+        if (t < n) sraw[q] = a.sc[((size_t)r * kNq + 4 * j + i) * a.sc_ld + t0 + t];
     }
     __syncthreads();
-    {
-        const int i = tid >> 6, t = tid & 63;
-        p[i][t] = t < n ? rbf(expf(sraw - ml[i][0]) / ml[i][1]) : 0.f;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int idx = tid + q * 256, i = idx >> 7, t = idx & 127;
+        p[i][t] = t < n ? rbf(expf(sraw[q] - ml[i][0]) / ml[i][1]) : 0.f;
     }
     __syncthreads();
     float acc[4][8];
@@ -222,8 +212,8 @@ __global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        const int t = tg * 8 + u;
+    for (int u = 0; u < 16; ++u) {
+        const int t = tg * 16 + u;
         float pp[4] = {p[0][t], p[1][t], p[2][t], p[3][t]};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -232,26 +222,32 @@ __global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
             for (int i = 0; i < 4; ++i) acc[i][e] = fmaf(pp[i], v, acc[i][e]);
         }
     }
+    // slot groups 2w and 2w+1 live in wave w (lanes 0-31 and 32-63): add in group order
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) red[tg][i][dg * 8 + e] = acc[i][e];
-    __syncthreads();
-    float* pp = a.part + (((size_t)r * a.max_chunks * 4 + pc) * kNq + 4 * j) * 256 + tid;
+        for (int e = 0; e < 8; ++e) {
+            const float other = __shfl_xor(acc[i][e], 32, 64);
+            acc[i][e] = (tg & 1) ? other + acc[i][e] : acc[i][e] + other;
+        }
+    if ((tg & 1) == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float sum = red[0][i][tid];
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int g = 1; g < 8; ++g) sum += red[g][i][tid];
-        pp[i * 256] = sum;
+            for (int e = 0; e < 8; ++e) red[tg >> 1][i][dg * 8 + e] = acc[i][e];
     }
+    __syncthreads();
+    float* pp = a.part + (((size_t)r * a.max_chunks * 2 + pc) * kNq + 4 * j) * 256 + tid;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        pp[i * 256] = ((red[0][i][tid] + red[1][i][tid]) + red[2][i][tid]) + red[3][i][tid];
 }
 
-// Sum of the 64-slot partials in part order, bf16, times bf16(sigmoid(gate)).
+// Sum of the 128-slot partials in part order, bf16, times bf16(sigmoid(gate)).
 __global__ void __launch_bounds__(256) attn_combine(AttnArgs a) {
     const int r = blockIdx.x, qh = blockIdx.y, tid = threadIdx.x;
     const int nparts = a.rm.slot[r] / kPart + 1;
-    const float* pp = a.part + ((size_t)r * a.max_chunks * 4 * kNq + qh) * 256 + tid;
+    const float* pp = a.part + ((size_t)r * a.max_chunks * 2 * kNq + qh) * 256 + tid;
     float acc = 0.f;
     for (int c0 = 0; c0 < nparts; c0 += 8) {
         float v[8];
@@ -271,7 +267,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (a.R <= 0 || a.max_chunks <= 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(attn_prep, dim3(a.R, kNq + kNkv), dim3(256), 0, st, a);
     hipLaunchKernelGGL(attn_scores, dim3(a.R, kNkv, a.max_chunks), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(attn_pv, dim3(a.R, kNkv, a.max_chunks * 4), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(attn_pv, dim3(a.R, kNkv, a.max_chunks * 2), dim3(256), 0, st, a);
     hipLaunchKernelGGL(attn_combine, dim3(a.R, kNq), dim3(256), 0, st, a);
     return hipGetLastError();
 }

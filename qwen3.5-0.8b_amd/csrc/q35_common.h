@@ -64,11 +64,12 @@ typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t q35_u32x
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 
 // Round-to-nearest-even f32 -> bf16 bits (NaN stays a quiet NaN).
+// Branchless (selects, no divergent branch per element).
 __device__ __forceinline__ uint16_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffffu) ? 0x40u : 0u));
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t nan = (u >> 16) | 0x40u;
+    return (uint16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? nan : rne);
 }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
