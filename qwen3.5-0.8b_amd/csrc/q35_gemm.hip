@@ -16,8 +16,9 @@
 // Kernels (all follow the order above):
 //   gemm_small_m   one 16-row tile; wave w of a block owns k-block w (M <= 16, batch 1);
 //                  with a producer the wave builds its A tile cooperatively in LDS
-//   gemm_large_m   4 waves x 16 columns, 64 or 128 rows per block; the A tile of each
-//                  k-block is staged once in LDS in MFMA fragment order (batched lanes);
+//   gemm_large_m   4 waves x 16 columns, 64 rows per block; the A tile of each k-block is
+//                  staged once in LDS in MFMA fragment order, the next k-block's loads in
+//                  flight meanwhile (batched lanes);
 //                  a non-plain producer runs first as its own elementwise kernel
 // kEPartial (N = 1024 outputs feeding the residual add): each block computes ONE k-block
 // chain and stores it to kpart[kb][M][N]; the following add+norm kernel sums the chains in
@@ -236,16 +237,30 @@ __global__ void __launch_bounds__(256) produce_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------- large M
-// Plain bf16 A. grid (ceil(N/64), ceil(M/(16*MT)), kEPartial ? KB : 1); 4 waves, wave w ->
-// column tile 4*blockIdx.x + w; the block's A rows of one k-block are staged in LDS in
+// Plain bf16 A. grid (8 * ceil(N/64 / 8) * ceil(M/(16*MT)), 1, kEPartial ? KB : 1); 4 waves,
+// wave w -> column tile 4*(column block) + w; the block's A rows of one k-block are staged in LDS in
 // MFMA fragment order (As[m-tile][step][lane]).
+// LDS slot of fragment lane (g, r16) at step s: an XOR swizzle that keeps the MFMA reads
+// (fixed s, 64 lanes) a permutation of 64 consecutive slots and spreads the staging writes
+// (one row: s = 0..7, g = 0..3) over 16 bank groups.
+__device__ __forceinline__ int lds_swz(int s, int g, int r16) {
+    return g * 16 + (r16 ^ ((s + 8 * (g & 1)) & 15));
+}
+
 template <int EM, int MT>
 __global__ void __launch_bounds__(256) gemm_large_m(GemmArgs a) {
     __shared__ q35_u32x4 As[MT][8][64];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int nt = blockIdx.x * 4 + wv;
+    // XCD-aware block order: consecutive blocks go round-robin to the 8 XCDs, so block b
+    // runs on XCD b % 8; give the M tiles of one column block consecutive slots on the
+    // same XCD, so its weight tiles are fetched from HBM once and then hit that XCD's L2.
+    const int mb = (a.M + MT * 16 - 1) / (MT * 16);
+    const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
+    const int nblk = (idx / mb) * 8 + xcd;
+    if (nblk * 4 >= a.N / 16) return;
+    const int nt = nblk * 4 + wv;
     const bool nvalid = nt < a.N / 16;
-    const int row0 = blockIdx.y * MT * 16;
+    const int row0 = (idx % mb) * MT * 16;
     const int KB = a.K >> 8;
     const int kb0 = EM == kEPartial ? blockIdx.z : 0;
     const int kb1 = EM == kEPartial ? blockIdx.z + 1 : KB;
@@ -253,37 +268,46 @@ __global__ void __launch_bounds__(256) gemm_large_m(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < MT; ++i) sum[i] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
 
-    for (int kb = kb0; kb < kb1; ++kb) {
-        q35_bf16x8 wf[8];
+    // register double buffer: the loads of k-block kb+1 are in flight while kb computes
+    q35_bf16x8 wf[8];
+    q35_u32x4 av[MT * 2];
+    auto load_kb = [&](int kb, q35_bf16x8* w, q35_u32x4* x) {
         if (nvalid) {
             const q35_bf16x8* wp = (const q35_bf16x8*)(a.W + ((size_t)nt * KB + kb) * 4096) + lane;
 #pragma unroll
-            for (int s = 0; s < 8; ++s) wf[s] = wp[s * 64];
+            for (int s = 0; s < 8; ++s) w[s] = wp[s * 64];
         }
-        q35_u32x4 av[MT * 2];
+        // row-contiguous global reads: 32 consecutive threads cover one row's 512 bytes
 #pragma unroll
         for (int i = 0; i < MT * 2; ++i) {
             const int c = tid + i * 256;
             const int row = c >> 5, kc = c & 31;
             const int m = row0 + row;
-            av[i] = m < a.M ? *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + kb * 256 + kc * 8)
-                            : (q35_u32x4){0u, 0u, 0u, 0u};
+            x[i] = m < a.M ? *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + kb * 256 + kc * 8)
+                           : (q35_u32x4){0u, 0u, 0u, 0u};
         }
+    };
+    load_kb(kb0, wf, av);
+    for (int kb = kb0; kb < kb1; ++kb) {
         __syncthreads();   // previous k-block's fragments are consumed
 #pragma unroll
         for (int i = 0; i < MT * 2; ++i) {
             const int c = tid + i * 256;
             const int row = c >> 5, kc = c & 31;
-            As[row >> 4][kc & 7][(kc >> 3) * 16 + (row & 15)] = av[i];
+            As[row >> 4][kc & 7][lds_swz(kc & 7, kc >> 3, row & 15)] = av[i];
         }
+        q35_bf16x8 wcur[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) wcur[s] = wf[s];
         __syncthreads();
+        if (kb + 1 < kb1) load_kb(kb + 1, wf, av);
         if (nvalid) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 q35_f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int s = 0; s < 8; ++s)
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(As[mt][s][lane]), wf[s], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(As[mt][s][lds_swz(s, lane >> 4, lane & 15)]), wcur[s], c, 0, 0, 0);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) sum[mt][r] = kb == kb0 ? c[r] : sum[mt][r] + c[r];
             }
@@ -330,10 +354,9 @@ template <int EM>
 static void launch_large(const GemmArgs& a, hipStream_t st) {
     const int KB = a.K / 256;
     const int gz = EM == kEPartial ? KB : 1;
-    if (a.M <= 64)
-        hipLaunchKernelGGL((gemm_large_m<EM, 4>), dim3((a.N / 16 + 3) / 4, (a.M + 63) / 64, gz), dim3(256), 0, st, a);
-    else
-        hipLaunchKernelGGL((gemm_large_m<EM, 8>), dim3((a.N / 16 + 3) / 4, (a.M + 127) / 128, gz), dim3(256), 0, st, a);
+    // 64-row tiles: more blocks in flight (W tiles are re-read from L2 by the M tiles)
+    const int nb = (a.N / 16 + 3) / 4, mb = (a.M + 63) / 64;
+    hipLaunchKernelGGL((gemm_large_m<EM, 4>), dim3((nb + 7) / 8 * 8 * mb, 1, gz), dim3(256), 0, st, a);
 }
 
 template <int AM, int EM>
