@@ -125,6 +125,9 @@ def main():
     ap.add_argument("--kprof", default="gdn", choices=list(FAM) + ["none"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch kernels eagerly (no hipGraph)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="run one 1 GiB device-to-device torch copy first (counter calibration: "
+                         "FETCH_SIZE/WRITE_SIZE of a known-size copy)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: lanes are independent sequences, so more GPUs would "
@@ -135,6 +138,13 @@ def main():
     from qwen35 import Engine
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     B, L = args.batch, args.ctx
+    if args.calib_copy:
+        src = torch.empty(1 << 29, dtype=torch.float16, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     eng = Engine(max_rows=max(B, 64), max_ctx=L + max(args.steps, args.b1_steps) + args.warmup + 64, seed=0,
                  use_graph=not args.eager)
     kp = None if args.kprof == "none" else args.kprof

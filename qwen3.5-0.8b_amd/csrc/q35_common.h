@@ -87,3 +87,20 @@ __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
 }
+
+// ---------------------------------------------------------------- 1024-wide RMSNorm pieces
+// The zero-centred RMSNorm's reduction tree, written once so every kernel that normalises a
+// hidden row (the add+norm kernel, the GEMM A-producer) gives identical bits: element
+// quad t (0..255) -> ((x0^2 + x1^2) + x2^2) + x3^2; quads t = 64w + lane summed by the
+// wave xor tree; the four wave sums as (w0 + w1) + (w2 + w3).
+__device__ __forceinline__ float quad_ss(float x0, float x1, float x2, float x3) {
+    return __fadd_rn(__fadd_rn(__fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1)), __fmul_rn(x2, x2)),
+                     __fmul_rn(x3, x3));
+}
+__device__ __forceinline__ float hidden_rsqrt(float ss) {
+    return rsqrtf(__fadd_rn(__fmul_rn(ss, 1.0f / 1024.0f), 1e-6f));
+}
+// h = bf16((x * rs) * (1 + w))
+__device__ __forceinline__ float norm_elem(float x, float rs, float w) {
+    return rbf(__fmul_rn(__fmul_rn(x, rs), __fadd_rn(1.0f, w)));
+}

@@ -373,20 +373,29 @@ void upload_cur(q35_engine* e, q35_state* s) {
     HCK(hipMemcpyAsync(s->cur_dev, s->h_cur, s->lanes * sizeof(int), hipMemcpyHostToDevice, e->st));
 }
 
+// Y != nullptr: bf16 store; Y == nullptr: k-block chains to e->kpart (summed by the next
+// add+norm); emode kEResidual: x <- bf16(x + bf16(sum)) (batch-1 path).
 void gemm(q35_engine* e, const uint16_t* W, int N, int K, int M, const void* X, int ldx,
           uint16_t* Y, int ldy, int amode = kAPlain, const void* X2 = nullptr, int ldx2 = 0,
-          const uint16_t* aux = nullptr) {
+          const uint16_t* aux = nullptr, int emode = -1, uint16_t* xres = nullptr) {
     GemmArgs a{};
     a.W = W; a.N = N; a.K = K; a.M = M; a.X = X; a.ldx = ldx; a.X2 = X2; a.ldx2 = ldx2;
     a.aux_w = aux; a.Y = Y; a.ldy = ldy;
-    a.kpart = e->kpart; a.prod = e->prod;
+    a.kpart = e->kpart; a.prod = e->prod; a.xres = xres;
     KTimer kt(e, kFamGemm);
-    HCK(launch_gemm(a, amode, Y ? kEStore : kEPartial, e->st));
+    HCK(launch_gemm(a, amode, emode >= 0 ? emode : (Y ? kEStore : kEPartial), e->st));
 }
+
+// Batch-1 path (<= 16 rows): the residual add lives in the producing GEMM's epilogue and the
+// RMSNorm in the consuming GEMM's A operand, so no add+norm launches remain.
+inline bool small_rows(int R) { return R <= 16; }
 
 void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16_t* vc,
                      long long kv_lane, long long layer_off, int cap) {
-    gemm(e, w.W_in, kAttnInRows, kHidden, R, e->h, kHidden, e->proj, kAttnInRows);
+    if (small_rows(R))
+        gemm(e, w.W_in, kAttnInRows, kHidden, R, e->x, kHidden, e->proj, kAttnInRows, kANormX, nullptr, 0, w.norm_in);
+    else
+        gemm(e, w.W_in, kAttnInRows, kHidden, R, e->h, kHidden, e->proj, kAttnInRows);
     AttnArgs a{};
     a.proj = e->proj; a.q_norm = w.q_norm; a.k_norm = w.k_norm;
     a.kc = kc; a.vc = vc; a.kv_lane = kv_lane; a.kv_layer_off = layer_off; a.cap = cap;
@@ -399,13 +408,29 @@ void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16
         KTimer kt(e, kFamAttn);
         HCK(launch_attention(a, e->st));
     }
-    gemm(e, w.W_out, kHidden, 2048, R, e->aout, 2048, nullptr, 0);
+    if (small_rows(R))
+        gemm(e, w.W_out, kHidden, 2048, R, e->aout, 2048, nullptr, 0, kAPlain, nullptr, 0, nullptr, kEResidual, e->x);
+    else
+        gemm(e, w.W_out, kHidden, 2048, R, e->aout, 2048, nullptr, 0);
 }
 
+// MLP sub-block; on the batched path it leaves chains that `finish_norm` folds in.
 void mlp_layer(q35_engine* e, const LayerW& w, int R) {
+    if (small_rows(R)) {
+        gemm(e, w.W_gu, kGuRows, kHidden, R, e->x, kHidden, e->gu, kGuRows, kANormX, nullptr, 0, w.norm_post);
+        gemm(e, w.W_down, kHidden, kFF, R, e->gu, kGuRows, nullptr, 0, kASiluMul, e->gu + kFF, kGuRows,
+             nullptr, kEResidual, e->x);
+        return;
+    }
     HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, 2048 / 256, w.norm_post, e->h, R, e->st));
     gemm(e, w.W_gu, kGuRows, kHidden, R, e->h, kHidden, e->gu, kGuRows);
     gemm(e, w.W_down, kHidden, kFF, R, e->gu, kGuRows, nullptr, 0, kASiluMul, e->gu + kFF, kGuRows);
+}
+
+// Batched path: fold the down-projection chains into x and normalise for the next consumer.
+void finish_norm(q35_engine* e, int R, const uint16_t* nw, uint16_t* out) {
+    if (small_rows(R)) return;
+    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, kFF / 256, nw, out, R, e->st));
 }
 
 // Runs the 24-layer body over R = nl * T rows (rows of one lane consecutive) and leaves the
@@ -424,11 +449,16 @@ void body(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
 void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
     const int nl = R / T;
     const int cs = nl <= 8 ? 8 : nl <= 32 ? 4 : nl <= 64 ? 2 : 1;
-    HCK(launch_addnorm(0, e->tok_dev, e->E, e->x, nullptr, nullptr, 0, e->L[0].norm_in, e->h, R, e->st));
+    const bool small = small_rows(R);
+    HCK(launch_addnorm(0, e->tok_dev, e->E, e->x, nullptr, nullptr, 0, e->L[0].norm_in, small ? nullptr : e->h,
+                       R, e->st));
     for (int l = 0; l < e->n_layers; ++l) {
         const LayerW& w = e->L[l];
         if (!is_attn_layer(l)) {
-            gemm(e, w.W_in, kGdnInRows, kHidden, R, e->h, kHidden, e->proj, kGdnInRows);
+            if (small)
+                gemm(e, w.W_in, kGdnInRows, kHidden, R, e->x, kHidden, e->proj, kGdnInRows, kANormX, nullptr, 0, w.norm_in);
+            else
+                gemm(e, w.W_in, kGdnInRows, kHidden, R, e->h, kHidden, e->proj, kGdnInRows);
             GdnArgs g{};
             g.proj = e->proj; g.o = e->o; g.conv_w = w.conv_w; g.A_log = w.A_log; g.dt_bias = w.dt_bias;
             g.S = s->S; g.S_lane = s->S_lane(); g.S_slot = (long long)kGdnLayers * kSLayer;
@@ -442,7 +472,7 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
                 HCK(launch_gdn(g, cs, e->st));
             }
             gemm(e, w.W_out, kHidden, 2048, R, e->o, 2048, nullptr, 0, kAGatedNorm,
-                 e->proj + kGdnZOff, kGdnInRows, w.gnorm);
+                 e->proj + kGdnZOff, kGdnInRows, w.gnorm, small ? kEResidual : -1, e->x);
         } else {
             attention_layer(e, w, R, s->kc, s->vc, s->kv_lane(),
                             (long long)attn_slot(l) * 2 * s->cap * 256, s->cap);
@@ -450,19 +480,25 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
         mlp_layer(e, w, R);
         const bool lastl = l + 1 == e->n_layers;
         const uint16_t* nw = lastl ? e->final_norm : e->L[l + 1].norm_in;
-        HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, kFF / 256, nw, lastl ? e->nrm : e->h, R, e->st));
+        finish_norm(e, R, nw, lastl ? e->nrm : e->h);
     }
 }
 
-// lm_head + argmax over rows [row0, row0 + M) of e->nrm; tokens into e->tok_dev[0..M).
-void lm_head(q35_engine* e, int row0, int M, bool want_logits) {
+// lm_head + argmax over rows [row0, row0 + M); tokens into e->tok_dev[0..M). After a
+// batched body the normed rows are in e->nrm; after a batch-1 body (`normw` given) the
+// final RMSNorm of the residual rows is applied first.
+void lm_head(q35_engine* e, int row0, int M, bool want_logits, const uint16_t* normw = nullptr) {
     GemmArgs a{};
     a.W = e->E; a.N = kVocab; a.K = kHidden; a.M = M; a.X = e->nrm + (size_t)row0 * kHidden; a.ldx = kHidden;
+    const int amode = kAPlain;
+    if (normw)   // one small norm launch: cheaper than normalising in each of the 15,520 blocks
+        HCK(launch_addnorm(2, nullptr, nullptr, e->x + (size_t)row0 * kHidden, nullptr, nullptr, 0, normw,
+                           e->nrm + (size_t)row0 * kHidden, M, e->st));
     if (want_logits) { ensure_logits(e, M); a.logits = e->logits_dev; a.ldl = kVocab; }
     a.part_val = e->pval; a.part_idx = e->pidx; a.ldp = kVocab / 16;
     {
         KTimer kt(e, kFamLmHead);
-        HCK(launch_gemm(a, kAPlain, kEArgmax, e->st));
+        HCK(launch_gemm(a, amode, kEArgmax, e->st));
     }
     HCK(launch_argmax(e->pval, e->pidx, kVocab / 16, kVocab / 16, M, e->tok_dev, nullptr, e->st));
 }
@@ -485,11 +521,15 @@ void mtp_draft_pass(q35_engine* e, q35_state* s, int n, const uint16_t* hsrc) {
     REQ(s->mtp_cap > 0, Q35_ERR_STATE, "state has no MTP cache");
     upload_rows(e, n);
     HCK(launch_mtp_concat(e->tok_dev, e->E, hsrc, kHidden, e->mtp_pre_e, e->mtp_pre_h, e->cat, n, e->st));
-    gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, nullptr, 0);
-    HCK(launch_addnorm(4, nullptr, nullptr, e->x, nullptr, e->kpart, 2048 / 256, e->M.norm_in, e->h, n, e->st));
+    if (small_rows(n)) {
+        gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, e->x, kHidden);
+    } else {
+        gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, nullptr, 0);
+        HCK(launch_addnorm(4, nullptr, nullptr, e->x, nullptr, e->kpart, 2048 / 256, e->M.norm_in, e->h, n, e->st));
+    }
     attention_layer(e, e->M, n, s->mkc, s->mvc, s->mkv_lane(), 0, s->mtp_cap);
     mlp_layer(e, e->M, n);
-    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, kFF / 256, e->mtp_norm, e->nrm, n, e->st));
+    finish_norm(e, n, e->mtp_norm, e->nrm);
 }
 
 int guard(const std::function<void()>& f) {
@@ -519,6 +559,7 @@ int q35_create(const q35_config* cfg, q35_engine** out) {
         auto* e = new q35_engine();
         e->device = cfg->device; e->R = cfg->max_rows; e->max_ctx = cfg->max_ctx; e->use_graph = cfg->use_graph;
         HCK(hipSetDevice(e->device));
+        HCK(gemm_init());
         HCK(hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking));
         HCK(hipEventCreate(&e->ev0));
         HCK(hipEventCreate(&e->ev1));
@@ -772,7 +813,7 @@ int q35_prefill(q35_engine* e, q35_state* s, int lane, const int32_t* ids, int n
             s->cur[lane] = (s->cur[lane] + 1) % s->nslots;
             done += T;
             if (done == n) {
-                lm_head(e, T - 1, 1, logits != nullptr);
+                lm_head(e, T - 1, 1, logits != nullptr, small_rows(T) ? e->final_norm : nullptr);
                 save_hlast(e, s, {T - 1}, {lane});
             }
         }
@@ -807,7 +848,7 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
         HCK(hipMemcpyAsync(e->ridx_dst, e->h_dst, n * sizeof(int), hipMemcpyHostToDevice, e->st));
         auto step = [&] {
             body_kernels(e, s, n, 1, false);
-            lm_head(e, 0, n, out_logits != nullptr);
+            lm_head(e, 0, n, out_logits != nullptr, small_rows(n) ? e->final_norm : nullptr);
             HCK(launch_copy_rows(e->nrm, e->ridx_src, s->hlast, e->ridx_dst, n, kHidden, e->st));
         };
         if (e->use_graph && e->kprof == 0) {
@@ -866,7 +907,7 @@ int q35_mtp_draft(q35_engine* e, q35_state* s, const int32_t* lanes, int n, cons
         HCK(hipMemcpyAsync(e->ridx_dst, e->h_dst, n * sizeof(int), hipMemcpyHostToDevice, e->st));
         HCK(launch_copy_rows(s->hlast, e->ridx_src, e->delta, e->ridx_dst, n, kHidden, e->st));
         mtp_draft_pass(e, s, n, e->delta);
-        lm_head(e, 0, n, out_logits != nullptr);
+        lm_head(e, 0, n, out_logits != nullptr, small_rows(n) ? e->mtp_norm : nullptr);
         // x_d becomes the lane's h for the next draft (speccheck/mtp.py:153-157)
         std::vector<int> rows(n);
         for (int i = 0; i < n; ++i) rows[i] = i;
@@ -911,7 +952,7 @@ int q35_mtp_round(q35_engine* e, q35_state* s, const int32_t* lanes, int n, cons
                 e->h_lane[r] = ls[i]; e->h_pos[r] = P[i] + t; e->h_slot[r] = P[i] + t;
             }
         body(e, s, R, T, true);
-        lm_head(e, 0, R, false);
+        lm_head(e, 0, R, false, small_rows(R) ? e->final_norm : nullptr);
         HCK(hipMemcpyAsync(e->h_out, e->tok_dev, R * sizeof(int), hipMemcpyDeviceToHost, e->st));
         HCK(hipStreamSynchronize(e->st));
         std::vector<int> rows(n);

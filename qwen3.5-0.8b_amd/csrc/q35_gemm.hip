@@ -29,7 +29,9 @@
 //   kASiluMul   act = bf16(bf16(silu(g)) * u)          (specimpl.py:404-407)
 //   kAGatedNorm y = bf16(w * (o * rsqrt(mean_head(o^2)+eps)) * silu(z)), per 128-wide
 //               head, o f32, z bf16                    (specimpl.py:142-147, 304-305)
-// Epilogues: kEStore (bf16 rows), kEPartial (one f32 k-block chain) and kEArgmax
+//   kANormX     h = rmsnorm_zc(x) of the residual row (specimpl.py:135-139), batch-1 only
+// Epilogues: kEStore (bf16 rows), kEPartial (one f32 k-block chain), kEResidual (batch-1:
+// x <- bf16(x + bf16(sum)), the residual add of specimpl.py:445-448) and kEArgmax
 // (bf16-rounded logits, per-tile max with the lowest index, optional f32 logits copy).
 #include "q35_common.h"
 #include "q35_kernels.h"
@@ -95,6 +97,17 @@ __device__ __forceinline__ q35_u32x4 produce_a(const GemmArgs& a, int m, int k0,
         q35_u32x4 g = *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + k0);
         q35_u32x4 u = *(const q35_u32x4*)((const uint16_t*)a.X2 + (size_t)m * a.ldx2 + k0);
         return silu_mul8(g, u);
+    } else if (AM == kANormX) {
+        q35_u32x4 x = *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + k0);
+        q35_u32x4 w = *(const q35_u32x4*)(a.aux_w + k0);
+        q35_u32x4 r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t lo = f2bf(norm_elem(__uint_as_float(x[i] << 16), rs, __uint_as_float(w[i] << 16)));
+            uint32_t hi = f2bf(norm_elem(__uint_as_float(x[i] & 0xffff0000u), rs, __uint_as_float(w[i] & 0xffff0000u)));
+            r[i] = lo | (hi << 16);
+        }
+        return r;
     } else {
         const float* po = (const float*)a.X + (size_t)m * a.ldx + k0;
         q35_u32x4 zz = *(const q35_u32x4*)((const uint16_t*)a.X2 + (size_t)m * a.ldx2 + k0);
@@ -124,6 +137,15 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, q35_f32x4 sum, int n
         for (int r = 0; r < 4; ++r) {
             int row = row0 + 4 * g + r;
             if (row < a.M) a.Y[(size_t)row * a.ldy + col] = f2bf(sum[r]);
+        }
+    } else if (EM == kEResidual) {   // the same add as the add+norm kernel's partial mode
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            int row = row0 + 4 * g + r;
+            if (row < a.M) {
+                uint16_t* px = a.xres + (size_t)row * kHidden + col;
+                *px = f2bf(bf2f(*px) + rbf(sum[r]));
+            }
         }
     } else {
 #pragma unroll
@@ -175,25 +197,45 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
             af[s] = mvalid ? *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + kbase + s * 8)
                            : (q35_u32x4){0u, 0u, 0u, 0u};
     } else {
-        // Producer modes (one wave per block, kEPartial): the wave builds its 16 x 256 A tile
-        // cooperatively -- only the M valid rows, 8 elements per (lane, chunk) -- into LDS in
-        // fragment order, so the per-element work is spread over all 64 lanes.
-        __shared__ q35_u32x4 As[8][64];
-        __shared__ float hss[16][4];
+        // Producer modes: each wave builds its 16 x 256 A tile cooperatively -- only the M
+        // valid rows, 8 elements per (lane, chunk) -- into its own LDS region in fragment
+        // order, so the per-element work is spread over all 64 lanes.
+        extern __shared__ q35_u32x4 dyn_lds[];
+        q35_u32x4(*As)[64] = (q35_u32x4(*)[64])(dyn_lds + wv * 512);
+        float* rowv = (float*)(dyn_lds + (EM == kEPartial ? 1 : KB) * 512) + wv * 64;   // [16][4]
         const int M = min(a.M - mt * 16, 16);
 #pragma unroll
         for (int s = 0; s < 8; ++s) As[s][lane] = (q35_u32x4){0u, 0u, 0u, 0u};
         if (AM == kAGatedNorm) {
             for (int c = lane; c < M * 4; c += 64) {
                 const int row = c >> 2, q = c & 3;
-                hss[row][q] = half_head_ss((const float*)a.X + (size_t)(mt * 16 + row) * a.ldx + kb * 256 + q * 64);
+                rowv[row * 4 + q] = half_head_ss((const float*)a.X + (size_t)(mt * 16 + row) * a.ldx + kb * 256 + q * 64);
+            }
+        } else if (AM == kANormX) {
+            // row rsqrt with the add+norm kernel's reduction tree (quad t = 64w + lane)
+            for (int row = 0; row < M; ++row) {
+                const uint16_t* xr = (const uint16_t*)a.X + (size_t)(mt * 16 + row) * a.ldx;
+                float wsum[4];
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    uint2 v = *(const uint2*)(xr + 4 * (64 * w + lane));
+                    wsum[w] = wave_sum(quad_ss(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                                               __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)));
+                }
+                if (lane == 0) rowv[row * 4] = hidden_rsqrt((wsum[0] + wsum[1]) + (wsum[2] + wsum[3]));
             }
         }
         __syncthreads();
         for (int c = lane; c < M * 32; c += 64) {
             const int row = c >> 5, kc = c & 31;
-            const float rs = AM == kAGatedNorm ? head_rsqrt(hss[row][(kc >> 4) * 2], hss[row][(kc >> 4) * 2 + 1]) : 0.f;
-            As[kc & 7][(kc >> 3) * 16 + row] = produce_a<AM>(a, mt * 16 + row, kb * 256 + kc * 8, rs);
+            const int k0 = kb * 256 + kc * 8;
+            float rs = 0.f;
+            if (AM == kAGatedNorm) rs = head_rsqrt(rowv[row * 4 + (kc >> 4) * 2], rowv[row * 4 + (kc >> 4) * 2 + 1]);
+            if (AM == kANormX) rs = rowv[row * 4];
+            const q35_u32x4 v = produce_a<AM>(a, mt * 16 + row, k0, rs);
+            As[kc & 7][(kc >> 3) * 16 + row] = v;
+            if (AM == kANormX && a.hout && blockIdx.x == 0)
+                *(q35_u32x4*)(a.hout + (size_t)(mt * 16 + row) * kHidden + k0) = v;
         }
         __syncthreads();
 #pragma unroll
@@ -324,11 +366,18 @@ __global__ void __launch_bounds__(1024) argmax_rows(const float* pv, const int* 
     const int row = blockIdx.x;
     float best = -INFINITY;
     int bi = 0x7fffffff;
-#pragma unroll 4
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        float v = pv[(size_t)row * ldp + i];
-        int id = pi[(size_t)row * ldp + i];
-        if (v > best || (v == best && id < bi)) { best = v; bi = id; }
+    for (int i0 = 0; i0 < n; i0 += 16 * 1024) {
+        float v[16];
+        int id[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {       // all loads first
+            const int i = i0 + u * 1024 + threadIdx.x;
+            v[u] = i < n ? pv[(size_t)row * ldp + i] : -INFINITY;
+            id[u] = i < n ? pi[(size_t)row * ldp + i] : 0x7fffffff;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+            if (v[u] > best || (v[u] == best && id[u] < bi)) { best = v[u]; bi = id[u]; }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -363,13 +412,15 @@ template <int AM, int EM>
 static hipError_t launch_am_em(const GemmArgs& a, hipStream_t st) {
     const int KB = a.K / 256;
     if (a.M <= 16) {
-        if (AM != kAPlain && EM != kEPartial) return hipErrorInvalidValue;
+        const int waves = EM == kEPartial ? 1 : KB;
+        const size_t lds = AM == kAPlain ? 0 : (size_t)waves * (512 * 16 + 64 * 4);
         if (EM == kEPartial)
-            hipLaunchKernelGGL((gemm_small_m<AM, EM>), dim3(a.N / 16, 1, KB), dim3(64), 0, st, a);
+            hipLaunchKernelGGL((gemm_small_m<AM, EM>), dim3(a.N / 16, 1, KB), dim3(64), lds, st, a);
         else
-            hipLaunchKernelGGL((gemm_small_m<AM, EM>), dim3(a.N / 16, 1, 1), dim3(64 * KB), 0, st, a);
+            hipLaunchKernelGGL((gemm_small_m<AM, EM>), dim3(a.N / 16, 1, 1), dim3(64 * KB), lds, st, a);
         return hipGetLastError();
     }
+    if (EM == kEResidual || AM == kANormX) return hipErrorInvalidValue;   // batch-1 forms only
     if (AM != kAPlain) {
         // produce A once into a.prod (bf16 [M][K]), then the plain batched GEMM
         if (!a.prod) return hipErrorInvalidValue;
@@ -380,24 +431,43 @@ static hipError_t launch_am_em(const GemmArgs& a, hipStream_t st) {
         GemmArgs g = a;
         g.X = a.prod;
         g.ldx = a.K;
-        launch_large<EM>(g, st);
+        launch_large<EM == kEResidual ? kEStore : EM>(g, st);
     } else {
-        launch_large<EM>(a, st);
+        launch_large<EM == kEResidual ? kEStore : EM>(a, st);
     }
     return hipGetLastError();
+}
+
+hipError_t gemm_init() {
+    const int big = 16 * (512 * 16 + 64 * 4);
+#define Q35_ATTR(AMV, EMV)                                                                              \
+    if (hipFuncSetAttribute((const void*)gemm_small_m<AMV, EMV>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                            big) != hipSuccess) return hipGetLastError();
+    Q35_ATTR(kASiluMul, kEStore) Q35_ATTR(kASiluMul, kEPartial) Q35_ATTR(kASiluMul, kEResidual)
+    Q35_ATTR(kAGatedNorm, kEStore) Q35_ATTR(kAGatedNorm, kEPartial) Q35_ATTR(kAGatedNorm, kEResidual)
+    Q35_ATTR(kANormX, kEStore) Q35_ATTR(kANormX, kEArgmax)
+#undef Q35_ATTR
+    return hipSuccess;
 }
 
 hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st) {
     if (a.K % 256 || a.N % 16 || a.K > 4096 || a.M <= 0) return hipErrorInvalidValue;
     if (emode == kEPartial && (!a.kpart || a.K / 256 > 16)) return hipErrorInvalidValue;
+    if (emode == kEResidual && (!a.xres || a.N != kHidden)) return hipErrorInvalidValue;
+    if (amode == kANormX && a.K != kHidden) return hipErrorInvalidValue;
 #define Q35_AM(EMV)                                                          \
     if (amode == kAPlain) return launch_am_em<kAPlain, EMV>(a, st);          \
     if (amode == kASiluMul) return launch_am_em<kASiluMul, EMV>(a, st);      \
     if (amode == kAGatedNorm) return launch_am_em<kAGatedNorm, EMV>(a, st);  \
     return hipErrorInvalidValue;
-    if (emode == kEStore) { Q35_AM(kEStore) }
+    if (emode == kEStore) {
+        if (amode == kANormX) return launch_am_em<kANormX, kEStore>(a, st);
+        Q35_AM(kEStore)
+    }
     if (emode == kEPartial) { Q35_AM(kEPartial) }
+    if (emode == kEResidual) { Q35_AM(kEResidual) }
     if (emode == kEArgmax && amode == kAPlain) return launch_am_em<kAPlain, kEArgmax>(a, st);
+    if (emode == kEArgmax && amode == kANormX) return launch_am_em<kANormX, kEArgmax>(a, st);
 #undef Q35_AM
     return hipErrorInvalidValue;
 }

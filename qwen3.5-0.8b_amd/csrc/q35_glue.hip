@@ -67,15 +67,15 @@ __global__ void __launch_bounds__(256) addnorm_kernel(int mode, const int* tok, 
         }
     }
     if (!h) return;
-    float ss = xv[0] * xv[0] + xv[1] * xv[1] + xv[2] * xv[2] + xv[3] * xv[3];
+    float ss = quad_ss(xv[0], xv[1], xv[2], xv[3]);
     ss = block_sum256(ss, red);
-    const float rs = rsqrtf(ss * (1.0f / kHidden) + kEps);
+    const float rs = hidden_rsqrt(ss);
     uint2 wv = *(const uint2*)(w + k);
     float wf[4] = {__uint_as_float(wv.x << 16), __uint_as_float(wv.x & 0xffff0000u),
                    __uint_as_float(wv.y << 16), __uint_as_float(wv.y & 0xffff0000u)};
     uint16_t o[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = f2bf(__fmul_rn(__fmul_rn(xv[i], rs), 1.0f + wf[i]));
+    for (int i = 0; i < 4; ++i) o[i] = f2bf(norm_elem(xv[i], rs, wf[i]));
     uint2 st;
     st.x = o[0] | ((uint32_t)o[1] << 16);
     st.y = o[2] | ((uint32_t)o[3] << 16);
@@ -96,16 +96,16 @@ __global__ void __launch_bounds__(256) mtp_concat_kernel(const int* tok, const u
                             : *(const uint2*)(hin + (size_t)r * ldh + k);
         float xv[4] = {__uint_as_float(a.x << 16), __uint_as_float(a.x & 0xffff0000u),
                        __uint_as_float(a.y << 16), __uint_as_float(a.y & 0xffff0000u)};
-        float ss = xv[0] * xv[0] + xv[1] * xv[1] + xv[2] * xv[2] + xv[3] * xv[3];
+        float ss = quad_ss(xv[0], xv[1], xv[2], xv[3]);
         ss = block_sum256(ss, red);
-        const float rs = rsqrtf(ss * (1.0f / kHidden) + kEps);
+        const float rs = hidden_rsqrt(ss);
         const uint16_t* w = part == 0 ? we : wh;
         uint2 wv = *(const uint2*)(w + k);
         float wf[4] = {__uint_as_float(wv.x << 16), __uint_as_float(wv.x & 0xffff0000u),
                        __uint_as_float(wv.y << 16), __uint_as_float(wv.y & 0xffff0000u)};
         uint16_t o[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = f2bf(__fmul_rn(__fmul_rn(xv[i], rs), 1.0f + wf[i]));
+        for (int i = 0; i < 4; ++i) o[i] = f2bf(norm_elem(xv[i], rs, wf[i]));
         uint2 st;
         st.x = o[0] | ((uint32_t)o[1] << 16);
         st.y = o[2] | ((uint32_t)o[3] << 16);

@@ -6,17 +6,17 @@
 
 namespace q35 {
 
-enum { kAPlain = 0, kASiluMul = 1, kAGatedNorm = 2 };
-enum { kEStore = 0, kEArgmax = 1, kEPartial = 2 };
+enum { kAPlain = 0, kASiluMul = 1, kAGatedNorm = 2, kANormX = 3 };
+enum { kEStore = 0, kEArgmax = 1, kEPartial = 2, kEResidual = 3 };
 
 struct GemmArgs {
     const uint16_t* W;     // tiled [N/16][K/256] x 8 KiB
     int N, K, M;
-    const void* X;         // A source (bf16, or f32 o for kAGatedNorm)
+    const void* X;         // A source (bf16; f32 o for kAGatedNorm; residual x for kANormX)
     int ldx;
     const void* X2;        // second source: u (kASiluMul) or z (kAGatedNorm)
     int ldx2;
-    const uint16_t* aux_w; // gated-norm weight [128]
+    const uint16_t* aux_w; // gated-norm weight [128] / RMSNorm weight [1024] (kANormX)
     uint16_t* Y;           // kEStore output
     int ldy;
     float* logits;         // kEArgmax: optional f32 copy of the bf16 logits
@@ -26,7 +26,11 @@ struct GemmArgs {
     int ldp;
     float* kpart;          // kEPartial: k-block chains [K/256][M][N] f32
     uint16_t* prod;        // M > 16 with a producer: bf16 [M][K] staging of the produced A
+    uint16_t* xres;        // kEResidual: residual rows [M][1024], x <- bf16(x + bf16(sum))
+    uint16_t* hout;        // kANormX (optional): the normalised rows [M][1024] are written here
 };
+// One-time kernel attribute setup (dynamic LDS above 64 KiB for the batch-1 producers).
+hipError_t gemm_init();
 hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st);
 hipError_t launch_argmax(const float* pv, const int* pi, int ldp, int n, int rows, int* tok,
                          float* val, hipStream_t st);
