@@ -28,6 +28,10 @@ S_BYTES = 18 * 16 * 128 * 128 * 4
 WIN_BYTES = 18 * 3 * 6144 * 4
 KV_BYTES_PER_SLOT = 6 * 2 * 2 * 256 * 2   # K and V, 6 layers, 2 kv heads
 FAM = {"gemm": 1, "lm_head": 2, "gdn": 3, "attn": 4}
+# HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled by what
+# the same counter reads for a 1 GiB copy (FETCH x2.0, WRITE x1.0); the runs and the
+# calibration are in profiles/gdn_kernel_b256_ctx4096_traffic.md.
+MEASURED_TRAFFIC = {("gdn", 256, 4096): (142505 * 2.0 + 282624 * 1.0) * 1024}
 
 
 def step_bytes(B: int, L: int) -> int:
@@ -162,7 +166,7 @@ def main():
         byt = family_bytes(kp, B, L) / launches_per_step
         ach = byt / (per_launch_ms / 1e3) / 1e9
         roof = {"kernel": kp, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK, 4), "traffic": None,
+                "frac": round(ach / HBM_PEAK, 4), "traffic": MEASURED_TRAFFIC.get((kp, B, L)),
                 "bytes_per_launch": int(byt), "avg_launch_us": round(per_launch_ms * 1e3, 2),
                 "launches_per_step": launches_per_step}
     cpu = None
