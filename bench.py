@@ -86,28 +86,11 @@ def run_decode(eng, B: int, ctx: int, steps: int, warmup: int, kprof: str | None
 def cpu_baseline(ctx: int, budget_s: float = 15.0):
     """The torch-CPU oracle (restatement of the reference's specimpl.py path) decoding lane 0
     of the same seeded workload on the host cores: tok/s."""
-    import numpy as np
     import torch
-    from oracle import model, prng
+    from oracle.seeded import seeded_forward
     from oracle.weights import WeightDict
     torch.set_grad_enabled(False)
-    w = WeightDict(0)
-    f = model.Forward(w)
-    gl = [l for l in range(24) if l % 4 != 3]
-    S_all = prng.normal_f32(1, prng.fnv1a64("state.gdn.0"), 0.1, 18 * 262144).reshape(18, 16, 128, 128)
-    for i, l in enumerate(gl):
-        f.rec[l] = torch.from_numpy(S_all[i].copy())
-        f.conv_win[l] = torch.zeros(3, 6144, dtype=torch.bfloat16)
-    for a, l in enumerate([3, 7, 11, 15, 19, 23]):
-        ks, vs = [], []
-        for j in range(2):
-            tag = f"0.{a}.{j}"
-            kb = prng.normal_bf16(1, prng.fnv1a64("state.k." + tag), 1.0, ctx * 256)
-            vb = prng.normal_bf16(1, prng.fnv1a64("state.v." + tag), 1.0, ctx * 256)
-            ks.append(torch.from_numpy((kb.astype(np.uint32) << 16).view(np.float32).reshape(ctx, 256)))
-            vs.append(torch.from_numpy(vb.view(np.int16).copy()).view(torch.bfloat16).reshape(ctx, 256))
-        f.kv[l] = {"k": [torch.stack(ks, 1)], "v": [torch.stack(vs, 1)]}
-    f.P = ctx
+    f = seeded_forward(WeightDict(0), 1, 0, ctx)
     tok, n = 1234, 0
     f.decode(tok)                      # warm
     t0 = time.perf_counter()

@@ -235,3 +235,32 @@ def test_graph_replay_equals_eager(eng):
     for a, b in zip(res[0][1], res[1][1]):
         assert np.array_equal(a, b)
     assert np.array_equal(res[0][2], res[1][2])
+
+
+@pytest.mark.parametrize("P", [4096, 9000])
+def test_seeded_state_decode(oracle_weights, P):
+    """The benchmark's seeded workload: lanes with N(0,0.1) GDN state and N(0,1) K/V over P
+    slots (P = 9000: 36 score chunks, 71 P.V parts) decode one step like the oracle
+    holding the same state (oracle/seeded.py)."""
+    import torch
+    from oracle.seeded import seeded_forward
+    from qwen35 import Engine, State
+    e = Engine(max_rows=16, max_ctx=P + 64, seed=0)
+    st = State(e, 2, P + 16)
+    st.seed(1, P)
+    toks = [1234, 99]
+    out, lg = st.decode_step(toks, logits=True)
+    for lane in (0, 1):
+        f = seeded_forward(oracle_weights, 1, lane, P)
+        ref = f.logits(f.decode(toks[lane]))[-1].float().numpy()
+        d = np.abs(lg[lane] - ref)
+        print(f"seeded P={P} lane {lane}: max|d|={d.max():.4f} mean|d|={d.mean():.5f}", flush=True)
+        assert d.max() <= LOGIT_MAX and d.mean() <= LOGIT_MEAN
+        top2 = np.sort(ref)[-2:]
+        if top2[1] - top2[0] > GAP:
+            assert int(out[lane]) == int(ref.argmax())
+        S = st.read(lane, "S")
+        for gi, l in enumerate([l for l in range(24) if l % 4 != 3]):
+            assert np.abs(S[gi] - f.rec[l].numpy()).max() <= 2e-2
+    st.close()
+    e.close()
