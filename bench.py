@@ -83,6 +83,38 @@ def run_decode(eng, B: int, ctx: int, steps: int, warmup: int, kprof: str | None
     return wall, ev_ms / 1e3, kt
 
 
+def run_mtp(eng, B: int, ctx: int, rounds: int, warmup: int):
+    """Config 4: B seeded lanes at context ctx, each round = 2 MTP drafts + a 3-row verify with
+    greedy accept and rollback (q35_mtp_round). Returns emitted tokens/s and accept stats."""
+    import numpy as np
+    import torch
+    from qwen35 import State
+    st = State(eng, B, ctx + 3 * (rounds + warmup) + 16, mtp_k=2, mtp_cap=2 * (rounds + warmup) + 16)
+    st.seed(1, ctx)
+    tok = np.random.default_rng(1).integers(0, 248320, size=B).astype(np.int32)
+    tok = st.decode_step(tok)             # one plain step: sets each lane's last hidden row
+    stats = np.zeros(4, np.int64)
+    for _ in range(warmup):
+        em = st.mtp_round(tok, 2, stats=stats)
+        tok = np.array([e[-1] for e in em], np.int32)
+    stats[:] = 0
+    eng.sync()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    emitted = 0
+    for _ in range(rounds):
+        em = st.mtp_round(tok, 2, stats=stats)
+        emitted += sum(len(e) for e in em)
+        tok = np.array([e[-1] for e in em], np.int32)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    st.close()
+    return {"tok_s": round(emitted / wall, 2), "ms_per_round": round(wall / rounds * 1e3, 3),
+            "accept_rate": round(float(stats[1]) / max(int(stats[0]), 1), 4),
+            "tokens_per_round_per_lane": round(emitted / rounds / B, 3), "lanes": B, "k": 2,
+            "note": "random-init weights: the drafter almost never agrees with the target"}
+
+
 def cpu_baseline(ctx: int, budget_s: float = 15.0):
     """The torch-CPU oracle (restatement of the reference's specimpl.py path) decoding lane 0
     of the same seeded workload on the host cores: tok/s."""
@@ -111,6 +143,7 @@ def main():
     ap.add_argument("--b1-steps", type=int, default=100)
     ap.add_argument("--kprof", default="gdn", choices=list(FAM) + ["none"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mtp-rounds", type=int, default=5, help="config 4 (MTP k=2) rounds; 0 skips it")
     ap.add_argument("--eager", action="store_true", help="launch kernels eagerly (no hipGraph)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run one 1 GiB device-to-device torch copy first (counter calibration: "
@@ -132,7 +165,7 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    eng = Engine(max_rows=max(B, 64), max_ctx=L + max(args.steps, args.b1_steps) + args.warmup + 64, seed=0,
+    eng = Engine(max_rows=max(3 * B, 64), max_ctx=L + max(args.steps, args.b1_steps) + args.warmup + 64, seed=0,
                  use_graph=not args.eager)
     kp = None if args.kprof == "none" else args.kprof
     wall, ev_s, kt = run_decode(eng, B, L, args.steps, args.warmup, kp)
@@ -152,6 +185,7 @@ def main():
                 "frac": round(ach / HBM_PEAK, 4), "traffic": MEASURED_TRAFFIC.get((kp, B, L)),
                 "bytes_per_launch": int(byt), "avg_launch_us": round(per_launch_ms * 1e3, 2),
                 "launches_per_step": launches_per_step}
+    mtp = run_mtp(eng, B, L, args.mtp_rounds, 1) if args.mtp_rounds > 0 else None
     cpu = None
     if not args.no_cpu:
         tps, thr, n = cpu_baseline(L)
@@ -169,7 +203,7 @@ def main():
            "batch1": {"tok_s": round(args.b1_steps / wall1, 2), "ms_per_step": round(ms1, 4),
                       "hbm_gbs": round(gbs1, 1), "hbm_frac": round(gbs1 / HBM_PEAK, 4),
                       "bytes_per_token": step_bytes(1, L)},
-           "roofline": roof, "cpu_baseline": cpu}
+           "mtp_k2": mtp, "roofline": roof, "cpu_baseline": cpu}
     print(json.dumps(out))
 
 

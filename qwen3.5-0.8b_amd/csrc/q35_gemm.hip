@@ -279,8 +279,8 @@ __global__ void __launch_bounds__(256) produce_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------- large M
-// Plain bf16 A. grid (8 * ceil(N/64 / 8) * ceil(M/(16*MT)), 1, kEPartial ? KB : 1); 4 waves,
-// wave w -> column tile 4*(column block) + w; the block's A rows of one k-block are staged in LDS in
+// Plain bf16 A. grid (8 * ceil(N/(16*NW) / 8) * ceil(M/(16*MT)), 1, kEPartial ? KB : 1); NW waves,
+// wave w -> column tile NW*(column block) + w; the block's A rows of one k-block are staged in LDS in
 // MFMA fragment order (As[m-tile][step][lane]).
 // LDS slot of fragment lane (g, r16) at step s: an XOR swizzle that keeps the MFMA reads
 // (fixed s, 64 lanes) a permutation of 64 consecutive slots and spreads the staging writes
@@ -289,9 +289,11 @@ __device__ __forceinline__ int lds_swz(int s, int g, int r16) {
     return g * 16 + (r16 ^ ((s + 8 * (g & 1)) & 15));
 }
 
-template <int EM, int MT>
-__global__ void __launch_bounds__(256) gemm_large_m(GemmArgs a) {
+template <int EM, int MT, int NW>
+__global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
     __shared__ q35_u32x4 As[MT][8][64];
+    constexpr int NT = 64 * NW;                    // threads
+    constexpr int CPT = MT * 512 / NT;             // 16-byte A chunks per thread per k-block
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     // XCD-aware block order: consecutive blocks go round-robin to the 8 XCDs, so block b
     // runs on XCD b % 8; give the M tiles of one column block consecutive slots on the
@@ -299,8 +301,8 @@ __global__ void __launch_bounds__(256) gemm_large_m(GemmArgs a) {
     const int mb = (a.M + MT * 16 - 1) / (MT * 16);
     const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
     const int nblk = (idx / mb) * 8 + xcd;
-    if (nblk * 4 >= a.N / 16) return;
-    const int nt = nblk * 4 + wv;
+    if (nblk * NW >= a.N / 16) return;
+    const int nt = nblk * NW + wv;
     const bool nvalid = nt < a.N / 16;
     const int row0 = (idx % mb) * MT * 16;
     const int KB = a.K >> 8;
@@ -312,7 +314,7 @@ __global__ void __launch_bounds__(256) gemm_large_m(GemmArgs a) {
 
     // register double buffer: the loads of k-block kb+1 are in flight while kb computes
     q35_bf16x8 wf[8];
-    q35_u32x4 av[MT * 2];
+    q35_u32x4 av[CPT];
     auto load_kb = [&](int kb, q35_bf16x8* w, q35_u32x4* x) {
         if (nvalid) {
             const q35_bf16x8* wp = (const q35_bf16x8*)(a.W + ((size_t)nt * KB + kb) * 4096) + lane;
@@ -321,8 +323,8 @@ __global__ void __launch_bounds__(256) gemm_large_m(GemmArgs a) {
         }
         // row-contiguous global reads: 32 consecutive threads cover one row's 512 bytes
 #pragma unroll
-        for (int i = 0; i < MT * 2; ++i) {
-            const int c = tid + i * 256;
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * NT;
             const int row = c >> 5, kc = c & 31;
             const int m = row0 + row;
             x[i] = m < a.M ? *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + kb * 256 + kc * 8)
@@ -333,8 +335,8 @@ __global__ void __launch_bounds__(256) gemm_large_m(GemmArgs a) {
     for (int kb = kb0; kb < kb1; ++kb) {
         __syncthreads();   // previous k-block's fragments are consumed
 #pragma unroll
-        for (int i = 0; i < MT * 2; ++i) {
-            const int c = tid + i * 256;
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * NT;
             const int row = c >> 5, kc = c & 31;
             As[row >> 4][kc & 7][lds_swz(kc & 7, kc >> 3, row & 15)] = av[i];
         }
@@ -405,7 +407,7 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
     const int gz = EM == kEPartial ? KB : 1;
     // 64-row tiles: more blocks in flight (W tiles are re-read from L2 by the M tiles)
     const int nb = (a.N / 16 + 3) / 4, mb = (a.M + 63) / 64;
-    hipLaunchKernelGGL((gemm_large_m<EM, 4>), dim3((nb + 7) / 8 * 8 * mb, 1, gz), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_large_m<EM, 4, 4>), dim3((nb + 7) / 8 * 8 * mb, 1, gz), dim3(256), 0, st, a);
 }
 
 template <int AM, int EM>
