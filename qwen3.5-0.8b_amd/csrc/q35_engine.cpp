@@ -467,12 +467,17 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
             g.W_layer = (long long)gdn_slot(l) * 18432;
             g.cur = s->cur_dev; g.nslots = s->nslots; g.ckpt = ckpt ? 1 : 0;
             g.lane = e->rlane; g.T = T; g.nlanes = nl;
+            const bool fused_norm = !small && cs == 1;   // whole-head blocks: norm in the GDN kernel
+            if (fused_norm) { g.y = e->prod; g.gnorm = w.gnorm; }
             {
                 KTimer kt(e, kFamGdn);
                 HCK(launch_gdn(g, cs, e->st));
             }
-            gemm(e, w.W_out, kHidden, 2048, R, e->o, 2048, nullptr, 0, kAGatedNorm,
-                 e->proj + kGdnZOff, kGdnInRows, w.gnorm, small ? kEResidual : -1, e->x);
+            if (fused_norm)
+                gemm(e, w.W_out, kHidden, 2048, R, e->prod, 2048, nullptr, 0);
+            else
+                gemm(e, w.W_out, kHidden, 2048, R, e->o, 2048, nullptr, 0, kAGatedNorm,
+                     e->proj + kGdnZOff, kGdnInRows, w.gnorm, small ? kEResidual : -1, e->x);
         } else {
             attention_layer(e, w, R, s->kc, s->vc, s->kv_lane(),
                             (long long)attn_slot(l) * 2 * s->cap * 256, s->cap);

@@ -42,6 +42,8 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     __shared__ float red_r[NG][VC], red_o[NG][VC];
     __shared__ float wred[4];
     __shared__ float gate_s[2];
+    __shared__ float ohead[CS == 1 ? 128 : 1];
+    __shared__ float hss2[2];
 
     float* Sbase = a.S + lane * a.S_lane + a.S_layer + (long long)h * 16384;
     float* Wbase = a.win + lane * a.W_lane + a.W_layer;
@@ -163,6 +165,19 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
 #pragma unroll
                 for (int i = 0; i < NG; ++i) oj += red_o[i][jc + c];
                 a.o[(size_t)r * 2048 + h * 128 + cs * VC + jc + c] = oj;
+                if (CS == 1) ohead[jc + c] = oj;
+            }
+        }
+        if (CS == 1 && a.y) {
+            // fused gated RMSNorm over the head: the GEMM producer's arithmetic, in LDS
+            __syncthreads();
+            if (tid < 2) hss2[tid] = half_head_ss_regs(ohead + 64 * tid);
+            __syncthreads();
+            if (tid < 128) {
+                const float rs = head_rsqrt(hss2[0], hss2[1]);
+                const float z = bf2f(pr[kGdnZOff + h * 128 + tid]);
+                const float w = bf2f(a.gnorm[tid]);
+                a.y[(size_t)r * 2048 + h * 128 + tid] = f2bf(__fmul_rn(__fmul_rn(w, __fmul_rn(ohead[tid], rs)), silu_f(z)));
             }
         }
         if (a.ckpt || t == a.T - 1) {

@@ -39,55 +39,6 @@
 namespace q35 {
 
 // ---------------------------------------------------------------- shared producers
-// Sum of squares of 64 consecutive f32 (half of a 128-wide head), fixed order.
-__device__ __forceinline__ float half_head_ss_regs(const float* v) {
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 64; i += 4)
-        ss = __fadd_rn(ss, __fadd_rn(__fadd_rn(__fmul_rn(v[i], v[i]), __fmul_rn(v[i + 1], v[i + 1])),
-                                     __fadd_rn(__fmul_rn(v[i + 2], v[i + 2]), __fmul_rn(v[i + 3], v[i + 3]))));
-    return ss;
-}
-__device__ __forceinline__ float half_head_ss(const float* po) {
-    float v[64];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) *(float4*)&v[4 * i] = *(const float4*)(po + 4 * i);
-    return half_head_ss_regs(v);
-}
-__device__ __forceinline__ float head_rsqrt(float ss_lo, float ss_hi) {
-    return rsqrtf(__fadd_rn(__fmul_rn(__fadd_rn(ss_lo, ss_hi), 1.0f / 128.0f), kEps));
-}
-// act = bf16(bf16(silu(g)) * u) for 8 packed bf16 pairs
-__device__ __forceinline__ q35_u32x4 silu_mul8(q35_u32x4 g, q35_u32x4 u) {
-    q35_u32x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float g0 = __uint_as_float(g[i] << 16), g1 = __uint_as_float(g[i] & 0xffff0000u);
-        float u0 = __uint_as_float(u[i] << 16), u1 = __uint_as_float(u[i] & 0xffff0000u);
-        uint32_t lo = f2bf(__fmul_rn(rbf(silu_f(g0)), u0));
-        uint32_t hi = f2bf(__fmul_rn(rbf(silu_f(g1)), u1));
-        r[i] = lo | (hi << 16);
-    }
-    return r;
-}
-// y = bf16(w * (o * rs) * silu(z)) for 8 elements
-__device__ __forceinline__ q35_u32x4 gated8(const float* ov, q35_u32x4 zz, q35_u32x4 ww, float rs) {
-    q35_u32x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t out2[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            float z = h ? __uint_as_float(zz[i] & 0xffff0000u) : __uint_as_float(zz[i] << 16);
-            float w = h ? __uint_as_float(ww[i] & 0xffff0000u) : __uint_as_float(ww[i] << 16);
-            float n = __fmul_rn(ov[2 * i + h], rs);
-            out2[h] = f2bf(__fmul_rn(__fmul_rn(w, n), silu_f(z)));
-        }
-        r[i] = out2[0] | (out2[1] << 16);
-    }
-    return r;
-}
-
 // 8 A elements of row m at k0 (k0 % 8 == 0); rs = rsqrt of the head holding k0 (gated norm).
 template <int AM>
 __device__ __forceinline__ q35_u32x4 produce_a(const GemmArgs& a, int m, int k0, float rs) {

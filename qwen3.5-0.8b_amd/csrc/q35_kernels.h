@@ -74,6 +74,10 @@ struct GdnArgs {
     const int* lane;           // [R] state lane of each row
     int T;                     // rows per lane (rows of one lane are consecutive)
     int nlanes;
+    // Optional fused gated RMSNorm (whole-head blocks only, col_slices == 1):
+    // y[r][h*128 + j] = bf16(w[j] * (o * rsqrt(mean_head(o^2) + eps)) * silu(z)), bf16 [R][2048]
+    uint16_t* y;
+    const uint16_t* gnorm;     // [128]
 };
 hipError_t launch_gdn(const GdnArgs& a, int col_slices, hipStream_t st);
 
