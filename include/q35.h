@@ -102,6 +102,13 @@ int q35_mtp_round(q35_engine* e, q35_state* s, const int32_t* lanes, int n, cons
 int q35_op_tile_weight(q35_engine* e, const uint16_t* w_rowmajor_dev, int N, int K, uint16_t* w_tiled_dev);
 int q35_op_gemm(q35_engine* e, const uint16_t* w_tiled_dev, int N, int K, const uint16_t* x_dev,
                 int M, uint16_t* y_dev);
+/* One GatedDeltaNet decode step for B independent lanes (the layer's
+ * conv + gates + L2 norms + delta rule, engine/kernels_gdn.cpp:35-536): proj [B][8224] bf16
+ * (qkv 6144 | z 2048 | b 16 | a 16), conv_w [6144][4] bf16, A_log / dt_bias [16] bf16;
+ * S2 [B][2][16][128][128] f32 and W2 [B][2][3][6144] f32 hold the input state in slot 0 and
+ * receive the new state in slot 1; o [B][2048] f32 (before the gated norm). */
+int q35_op_gdn_step(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w, const uint16_t* A_log,
+                    const uint16_t* dt_bias, float* S2, float* W2, float* o, int B);
 int q35_op_lm_head_argmax(q35_engine* e, const uint16_t* x_dev, int M, int32_t* tok_dev, float* logits_dev);
 int q35_sync(q35_engine* e);
 /* Live per-kernel timing: with option "kprof" = family (1 projection/MLP GEMMs, 2 lm_head

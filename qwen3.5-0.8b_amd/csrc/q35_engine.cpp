@@ -995,6 +995,29 @@ int q35_op_gemm(q35_engine* e, const uint16_t* wt, int N, int K, const uint16_t*
     });
 }
 
+int q35_op_gdn_step(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w, const uint16_t* A_log,
+                    const uint16_t* dt_bias, float* S2, float* W2, float* o, int B) {
+    return guard([&] {
+        REQ(e && proj && conv_w && A_log && dt_bias && S2 && W2 && o && B > 0, Q35_ERR_ARG, "bad gdn call");
+        REQ(B <= 65536, Q35_ERR_ARG, "B too large");
+        // rows b = lanes b (T = 1); per lane two slots: 0 = input state, 1 = output state
+        std::vector<int> lanes(B);
+        for (int i = 0; i < B; ++i) lanes[i] = i;
+        int* dl = dalloc<int>(B);
+        copy_sync(e, dl, lanes.data(), B * sizeof(int), hipMemcpyHostToDevice);
+        GdnArgs g{};
+        g.proj = proj; g.o = o; g.conv_w = conv_w; g.A_log = A_log; g.dt_bias = dt_bias;
+        g.S = S2; g.S_lane = 2 * kSLayer; g.S_slot = kSLayer; g.S_layer = 0;
+        g.win = W2; g.W_lane = 2 * kWLayer; g.W_slot = kWLayer; g.W_layer = 0;
+        g.cur = nullptr; g.nslots = 2; g.ckpt = 0;
+        g.lane = dl; g.T = 1; g.nlanes = B;
+        const int cs = B <= 8 ? 8 : B <= 32 ? 4 : B <= 64 ? 2 : 1;
+        HCK(launch_gdn(g, cs, e->st));
+        HCK(hipStreamSynchronize(e->st));
+        HCK(hipFree(dl));
+    });
+}
+
 int q35_op_lm_head_argmax(q35_engine* e, const uint16_t* x, int M, int32_t* tok, float* logits) {
     return guard([&] {
         REQ(e && x && tok && M > 0 && M <= e->R, Q35_ERR_ARG, "bad lm_head call");

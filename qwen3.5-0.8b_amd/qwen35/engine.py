@@ -51,6 +51,7 @@ _SIGS = {
                        C.c_void_p, C.c_void_p], C.c_int),
     "q35_op_tile_weight": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p], C.c_int),
     "q35_op_gemm": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p], C.c_int),
+    "q35_op_gdn_step": ([C.c_void_p] * 8 + [C.c_int], C.c_int),
     "q35_op_lm_head_argmax": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p], C.c_int),
     "q35_sync": ([C.c_void_p], C.c_int),
     "q35_kprof_read": ([C.c_void_p, C.POINTER(C.c_float), C.POINTER(C.c_int)], C.c_int),
@@ -150,6 +151,9 @@ class Engine:
 
     def op_gemm(self, wt_ptr: int, N: int, K: int, x_ptr: int, M: int, y_ptr: int):
         _ck(load_library().q35_op_gemm(self.h, C.c_void_p(wt_ptr), N, K, C.c_void_p(x_ptr), M, C.c_void_p(y_ptr)))
+
+    def op_gdn_step(self, proj: int, conv_w: int, A_log: int, dt_bias: int, S2: int, W2: int, o: int, B: int):
+        _ck(load_library().q35_op_gdn_step(self.h, *[C.c_void_p(p) for p in (proj, conv_w, A_log, dt_bias, S2, W2, o)], B))
 
     def op_lm_head_argmax(self, x_ptr: int, M: int, tok_ptr: int, logits_ptr: int = 0):
         _ck(load_library().q35_op_lm_head_argmax(self.h, C.c_void_p(x_ptr), M, C.c_void_p(tok_ptr),

@@ -1,0 +1,113 @@
+"""BASELINE.json parity configs on the GPU, op by op through the C ABI.
+
+config 1: every decode projection shape at batch 1, 16 and 256 (W ~ N(0,0.02), x ~ N(0,1)
+          bf16), plus the tied lm_head with argmax. Bar: within one bf16 rounding plus the f32
+          accumulation bound of the float64 product; rows bit-identical across batch sizes;
+          argmax = lowest id of the maximum of the engine's own bf16 logits.
+config 2: one GatedDeltaNet decode step at batch 1, 64 and 1024 (inputs N(0,1), state
+          N(0,0.1), layer-0 weights) against the oracle's conv / gates / L2 / recurrence
+          (speccheck/specimpl.py:252-294). Inputs are identical, so the bar is tight:
+          new state max |d| <= 1e-5 + 1e-4 |S|, o max |d| <= 1e-4 max |o|, window exact.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [("in_proj_qkv", 6144, 1024), ("in_proj_z", 2048, 1024), ("in_proj_a", 16, 1024),
+          ("out_proj", 1024, 2048), ("q_proj", 4096, 1024), ("k_proj", 512, 1024),
+          ("o_proj", 1024, 2048), ("gate_proj", 3584, 1024), ("down_proj", 1024, 3584)]
+
+
+@pytest.fixture(scope="module")
+def eng():
+    import torch
+    assert torch.cuda.is_available()
+    from qwen35 import Engine
+    e = Engine(max_rows=256, max_ctx=512, seed=0)
+    yield e
+    e.close()
+
+
+@pytest.mark.parametrize("name,N,K", SHAPES)
+def test_config1_projection_sweep(eng, name, N, K):
+    import torch
+    print(f"config1 {name} {K}->{N}", flush=True)
+    g = torch.Generator().manual_seed(N * 7 + K)
+    W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    X = torch.randn(256, K, generator=g).to(torch.bfloat16)
+    Wd = W.cuda()
+    Wt = torch.empty_like(Wd)
+    eng.op_tile_weight(Wd.data_ptr(), N, K, Wt.data_ptr())
+    outs = {}
+    for B in (1, 16, 256):
+        Xd = X[:B].contiguous().cuda()
+        Y = torch.empty(B, N, dtype=torch.bfloat16, device="cuda")
+        eng.op_gemm(Wt.data_ptr(), N, K, Xd.data_ptr(), B, Y.data_ptr())
+        eng.sync()
+        outs[B] = Y.cpu()
+    ref = X.double() @ W.double().t()
+    ulp = torch.maximum(ref.abs(), torch.full_like(ref, 1e-30)).log2().floor().sub(7).exp2()
+    acc = (X.double().abs() @ W.double().abs().t()) * (K * 2.0 ** -24)
+    got = outs[256].double()
+    assert ((got - ref).abs() - ulp <= acc).all()
+    assert torch.equal(outs[1], outs[256][:1]) and torch.equal(outs[16], outs[256][:16])
+
+
+def test_config1_lm_head_argmax(eng, oracle_weights):
+    import torch
+    E = oracle_weights.p["model.language_model.embed_tokens.weight"]
+    g = torch.Generator().manual_seed(11)
+    X = torch.randn(256, 1024, generator=g).to(torch.bfloat16)
+    res = {}
+    for B in (1, 16, 256):
+        tok = torch.empty(B, dtype=torch.int32, device="cuda")
+        lg = torch.empty(B, 248320, dtype=torch.float32, device="cuda")
+        eng.op_lm_head_argmax(X[:B].contiguous().cuda().data_ptr(), B, tok.data_ptr(), lg.data_ptr())
+        eng.sync()
+        res[B] = (tok.cpu(), lg.cpu())
+    tok, lg = res[256]
+    assert torch.equal(res[1][1], lg[:1]) and torch.equal(res[16][1], lg[:16])
+    for r in range(256):
+        row = lg[r]
+        assert tok[r].item() == int(torch.nonzero(row == row.max())[0])
+    ref = X[:16].double() @ E.double().t()
+    assert (lg[:16].double() - ref).abs().max().item() < 0.06
+
+
+@pytest.mark.parametrize("B", [1, 64, 1024])
+def test_config2_gdn_step(eng, oracle_weights, B):
+    import torch
+    from oracle import model
+    print(f"config2 gdn B={B}", flush=True)
+    p = "model.language_model.layers.0.linear_attn."
+    conv_w, A_log, dt_bias = (oracle_weights.p[p + n] for n in ("conv1d.weight", "A_log", "dt_bias"))
+    g = torch.Generator().manual_seed(B)
+    proj = torch.randn(B, 8224, generator=g).to(torch.bfloat16)
+    S0 = (torch.randn(B, 16, 128, 128, generator=g) * 0.1).float()
+    W0 = torch.randn(B, 3, 6144, generator=g).to(torch.bfloat16)
+    S2 = torch.zeros(B, 2, 16, 128, 128, dtype=torch.float32)
+    S2[:, 0] = S0
+    W2 = torch.zeros(B, 2, 3, 6144, dtype=torch.float32)
+    W2[:, 0] = W0.float()
+    dS2, dW2 = S2.cuda(), W2.cuda()
+    o = torch.empty(B, 2048, dtype=torch.float32, device="cuda")
+    dproj = proj.cuda()
+    cw, al, db = conv_w.contiguous().cuda(), A_log.contiguous().cuda(), dt_bias.contiguous().cuda()
+    eng.op_gdn_step(dproj.data_ptr(), cw.data_ptr(), al.data_ptr(), db.data_ptr(), dS2.data_ptr(),
+                    dW2.data_ptr(), o.data_ptr(), B)
+    S1, W1, o = dS2[:, 1].cpu(), dW2[:, 1].cpu(), o.cpu()
+    lanes = range(B) if B <= 64 else range(0, B, 97)
+    for b in lanes:
+        raw = proj[b:b + 1, :6144]
+        u, win = model.gdn_conv(raw, conv_w, W0[b])
+        q = u[:, :2048].reshape(1, 16, 128)
+        k = u[:, 2048:4096].reshape(1, 16, 128)
+        v = u[:, 4096:].reshape(1, 16, 128)
+        gg, beta = model.gdn_gates(proj[b:b + 1, 8208:8224], proj[b:b + 1, 8192:8208], A_log, dt_bias)
+        qn, kn = model.l2_scale(q, k)
+        ro, rS = model.gdn_recurrent(qn, kn, v, gg.exp(), beta, S0[b].clone())
+        assert torch.equal(W1[b], win.float()), b
+        dS = (S1[b] - rS).abs()
+        assert (dS <= 1e-5 + 1e-4 * rS.abs()).all(), (b, dS.max().item())
+        assert (o[b] - ro.reshape(-1)).abs().max().item() <= 1e-4 * ro.abs().max().item() + 1e-7, b

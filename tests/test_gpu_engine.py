@@ -237,10 +237,11 @@ def test_graph_replay_equals_eager(eng):
     assert np.array_equal(res[0][2], res[1][2])
 
 
-@pytest.mark.parametrize("P", [4096, 9000])
+@pytest.mark.parametrize("P", [4096, 9000, 32768])
 def test_seeded_state_decode(oracle_weights, P):
     """The benchmark's seeded workload: lanes with N(0,0.1) GDN state and N(0,1) K/V over P
-    slots (P = 9000: 36 score chunks, 71 P.V parts) decode one step like the oracle
+    slots (P = 9000 and 32768: up to 128 score chunks and 256 P.V parts; BASELINE config 3's
+    longest context) decode one step like the oracle
     holding the same state (oracle/seeded.py)."""
     import torch
     from oracle.seeded import seeded_forward
