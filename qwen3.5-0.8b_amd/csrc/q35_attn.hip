@@ -7,7 +7,8 @@
 // bf16(sigmoid(gate)). GQA: query head i reads kv head i / 4.
 // Replaces engine/kernels_attn.cpp:415-1108 (prep, core, combine) of the reference.
 //
-// Four launches per layer:
+// Four launches per layer (batched lanes with short enough contexts: prep + one fused
+// kernel, attn_fused):
 //   attn_prep   (row, head)         q norm+rope -> f32 scratch; k norm+rope, v -> cache
 //   attn_scores (row, kv head, chunk) scores on MFMA -> scratch, per-chunk (max, sum e^(s-max))
 //   attn_pv     (row, kv head, 128-slot part) global (max, sum) from the chunk stats,
@@ -64,20 +65,41 @@ __global__ void __launch_bounds__(256) attn_prep(AttnArgs a) {
 
 // Scores on MFMA: a wave takes 16 cache slots per v_mfma_f32_16x16x32_bf16 chain with the
 // K rows as the A operand (step s of lane (slot t, group g) carries dims s*32 + g*8 .. +8,
-// so each load instruction reads 64 contiguous bytes of 16 slots) and B = [q_hi(4 heads) | q_lo(4 heads) | 0], q_hi = bf16(q),
-// q_lo = bf16(q - q_hi), so s = C[t][h] + C[t][h+4] carries q to ~2^-16 relative.
-// Block = 4 waves = 256 slots (one chunk).
-__global__ void __launch_bounds__(256) attn_scores(AttnArgs a) {
-    __shared__ uint16_t qb[16][256];   // B operand columns: q_hi heads 0-3, q_lo heads 0-3, zeros
-    __shared__ float red[4][4];
-    const int r = blockIdx.x, j = blockIdx.y, c = blockIdx.z, tid = threadIdx.x;
-    const int lane = tid & 63, wv = tid >> 6;
-    const int slot = a.rm.slot[r];
-    if (c * kChunk > slot) return;
-    const int lrow = a.rm.lane[r];
+// so each load instruction reads 64 contiguous bytes of 16 slots) and B = [q_hi(4 heads) |
+// q_lo(4 heads) | 0], q_hi = bf16(q), q_lo = bf16(q - q_hi), so s = C[t][h] + C[t][h+4]
+// carries q to ~2^-16 relative. A chunk = 4 waves x 64 slots.
+//
+// The chunk score pass, the part P.V pass and the part sum are device functions shared by
+// the split kernels (any batch, any context) and the fused per-lane kernel (batched lanes,
+// contexts that fit LDS), so both give the same bits.
+
+// q fragments of kv group j for row r (all 256 threads; contains a barrier).
+__device__ __forceinline__ void load_q_frags(const AttnArgs& a, int r, int j, uint16_t (*qb)[256],
+                                             q35_u32x4* qf) {
+    const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
+    const float* q = a.q + ((size_t)r * kNq + 4 * j) * 256;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        const float qv = q[h * 256 + tid];
+        const uint16_t hi = f2bf(qv);
+        qb[h][tid] = hi;
+        qb[4 + h][tid] = f2bf(qv - bf2f(hi));
+        qb[8 + h][tid] = 0;
+        qb[12 + h][tid] = 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[s] = *(const q35_u32x4*)&qb[n][s * 32 + g * 8];
+}
+
+// Scores of chunk c (slots c*256 .. +256, masked beyond `slot`) -> dst[h * dst_stride + t],
+// chunk stats (max, sum e^(s - max)) -> stats[h * stats_stride + 2c .. +1]. Contains barriers.
+__device__ __forceinline__ void score_chunk(const AttnArgs& a, int lrow, int j, int c, int slot,
+                                            const q35_u32x4* qf, float* dst, size_t dst_stride,
+                                            float* stats, size_t stats_stride, float (*red)[4]) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int t0 = c * kChunk + wv * 64;
-    // K fragments: 4 sub-tiles of 16 slots, 8 steps each, issued first
     const uint16_t* kbase = a.kc + lrow * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256;
     q35_u32x4 kf[4][8];
 #pragma unroll
@@ -87,30 +109,13 @@ __global__ void __launch_bounds__(256) attn_scores(AttnArgs a) {
 #pragma unroll
         for (int s = 0; s < 8; ++s) kf[st][s] = *(const q35_u32x4*)(kp + s * 32);
     }
-    {
-        const float* q = a.q + ((size_t)r * kNq + 4 * j) * 256;
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            const float qv = q[h * 256 + tid];
-            const uint16_t hi = f2bf(qv);
-            qb[h][tid] = hi;
-            qb[4 + h][tid] = f2bf(qv - bf2f(hi));
-            qb[8 + h][tid] = 0;
-            qb[12 + h][tid] = 0;
-        }
-    }
-    __syncthreads();
-    q35_u32x4 qf[8];
-#pragma unroll
-    for (int s = 0; s < 8; ++s) qf[s] = *(const q35_u32x4*)&qb[n][s * 32 + g * 8];
-    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     float sv[4][4];      // [sub-tile][r] for this lane's head (lanes n < 4)
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
         q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 8; ++s)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&kf[st][s], *(q35_bf16x8*)&qf[s], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&kf[st][s], *(const q35_bf16x8*)&qf[s], acc, 0, 0, 0);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const float lo = __shfl_down(acc[rr], 4, 64);
@@ -118,10 +123,9 @@ __global__ void __launch_bounds__(256) attn_scores(AttnArgs a) {
             const int t = t0 + st * 16 + 4 * g + rr;
             const bool ok = n < 4 && t <= slot;
             sv[st][rr] = ok ? sc : -INFINITY;
-            if (ok) a.sc[((size_t)r * kNq + 4 * j + n) * a.sc_ld + t] = sc;
+            if (ok) dst[n * dst_stride + t] = sc;
         }
     }
-    // per-head chunk max and sum of exp: lanes with n == h hold that head's 64 values
     float m = -INFINITY;
 #pragma unroll
     for (int st = 0; st < 4; ++st)
@@ -143,10 +147,23 @@ __global__ void __launch_bounds__(256) attn_scores(AttnArgs a) {
     if (lane < 4) red[lane][wv] = e;
     __syncthreads();
     if (tid < 4) {
-        float* st = a.stats + (((size_t)r * kNq + 4 * j + tid) * a.max_chunks + c) * 2;
+        float* st = stats + tid * stats_stride + 2 * c;
         st[0] = mb;
         st[1] = (red[tid][0] + red[tid][1]) + (red[tid][2] + red[tid][3]);
     }
+    __syncthreads();
+}
+
+__global__ void __launch_bounds__(256) attn_scores(AttnArgs a) {
+    __shared__ uint16_t qb[16][256];
+    __shared__ float red[4][4];
+    const int r = blockIdx.x, j = blockIdx.y, c = blockIdx.z;
+    const int slot = a.rm.slot[r];
+    if (c * kChunk > slot) return;
+    q35_u32x4 qf[8];
+    load_q_frags(a, r, j, qb, qf);
+    score_chunk(a, a.rm.lane[r], j, c, slot, qf, a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld, a.sc_ld,
+                a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 2, (size_t)a.max_chunks * 2, red);
 }
 
 // P.V over one 128-slot part: thread (dg, tg) owns dims dg*8..+8 for slots tg*16..+16 of
@@ -154,28 +171,11 @@ __global__ void __launch_bounds__(256) attn_scores(AttnArgs a) {
 // summed in order (pairs in a wave by a lane swap, then the 4 waves through LDS).
 constexpr int kPart = 128;
 
-__global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
-    __shared__ float p[4][kPart];
-    __shared__ float ml[4][2];
-    __shared__ float red[4][4][256];
-    const int r = blockIdx.x, j = blockIdx.y, pc = blockIdx.z, tid = threadIdx.x;
-    const int slot = a.rm.slot[r];
-    const int nparts = slot / kPart + 1;
-    if (pc >= nparts) return;
-    const int nch = slot / kChunk + 1;
-    const int lane = a.rm.lane[r];
-    const int t0 = pc * kPart;
-    const int n = min(kPart, slot + 1 - t0);
-    const int dg = tid & 31, tg = tid >> 5;
-    const uint16_t* vr = a.vc + lane * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + t0) * 256 + dg * 8;
-    q35_u32x4 vv[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-        const int t = tg * 16 + u;
-        vv[u] = t < n ? *(const q35_u32x4*)(vr + (size_t)t * 256) : (q35_u32x4){0u, 0u, 0u, 0u};
-    }
+// Softmax (max, sum) of the row's 4 heads from the chunk stats -> ml[h][0..1] (threads 0-3).
+__device__ __forceinline__ void softmax_ml(const float* stats, size_t stats_stride, int nch, float (*ml)[2]) {
+    const int tid = threadIdx.x;
     if (tid < 4) {
-        const float* st = a.stats + ((size_t)r * kNq + 4 * j + tid) * a.max_chunks * 2;
+        const float* st = stats + tid * stats_stride;
         float mv[32], lv[32];
 #pragma unroll
         for (int i = 0; i < 32; ++i)
@@ -193,11 +193,29 @@ __global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
         ml[tid][0] = m;
         ml[tid][1] = l;
     }
+}
+
+// Partial P.V of part pc for dims d = tid of the 4 heads -> out[4]. `scores` points at head 0
+// of the row's scores (head stride s_stride); ml must be ready. Contains barriers.
+__device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int pc, int slot,
+                                        const float* scores, size_t s_stride, float (*ml)[2],
+                                        float (*p)[kPart], float (*red)[4][256], float* out) {
+    const int tid = threadIdx.x;
+    const int t0 = pc * kPart;
+    const int n = min(kPart, slot + 1 - t0);
+    const int dg = tid & 31, tg = tid >> 5;
+    const uint16_t* vr = a.vc + lrow * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + t0) * 256 + dg * 8;
+    q35_u32x4 vv[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int t = tg * 16 + u;
+        vv[u] = t < n ? *(const q35_u32x4*)(vr + (size_t)t * 256) : (q35_u32x4){0u, 0u, 0u, 0u};
+    }
     float sraw[2] = {0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const int idx = tid + q * 256, i = idx >> 7, t = idx & 127;
-        if (t < n) sraw[q] = a.sc[((size_t)r * kNq + 4 * j + i) * a.sc_ld + t0 + t];
+        if (t < n) sraw[q] = scores[i * s_stride + t0 + t];
     }
     __syncthreads();
 #pragma unroll
@@ -237,10 +255,33 @@ __global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
             for (int e = 0; e < 8; ++e) red[tg >> 1][i][dg * 8 + e] = acc[i][e];
     }
     __syncthreads();
-    float* pp = a.part + (((size_t)r * a.max_chunks * 2 + pc) * kNq + 4 * j) * 256 + tid;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        pp[i * 256] = ((red[0][i][tid] + red[1][i][tid]) + red[2][i][tid]) + red[3][i][tid];
+    for (int i = 0; i < 4; ++i) out[i] = ((red[0][i][tid] + red[1][i][tid]) + red[2][i][tid]) + red[3][i][tid];
+    __syncthreads();
+}
+
+// attention output element: bf16(bf16(sum of parts) * bf16(sigmoid(gate)))
+__device__ __forceinline__ uint16_t gated_out(const AttnArgs& a, int r, int qh, int d, float acc) {
+    const uint16_t* pr = a.proj + (size_t)r * kAttnInRows;
+    const float o = rbf(acc);
+    const float g = rbf(sigmoid_f(bf2f(pr[qh * 512 + 256 + d])));
+    return f2bf(o * g);
+}
+
+__global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
+    __shared__ float p[4][kPart];
+    __shared__ float ml[4][2];
+    __shared__ float red[4][4][256];
+    const int r = blockIdx.x, j = blockIdx.y, pc = blockIdx.z;
+    const int slot = a.rm.slot[r];
+    if (pc >= slot / kPart + 1) return;
+    softmax_ml(a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 2, (size_t)a.max_chunks * 2,
+               slot / kChunk + 1, ml);
+    float out[4];
+    pv_part(a, a.rm.lane[r], j, pc, slot, a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld, a.sc_ld, ml, p, red, out);
+    float* pp = a.part + (((size_t)r * a.max_chunks * 2 + pc) * kNq + 4 * j) * 256 + threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pp[i * 256] = out[i];
 }
 
 // Sum of the 128-slot partials in part order, bf16, times bf16(sigmoid(gate)).
@@ -257,18 +298,57 @@ __global__ void __launch_bounds__(256) attn_combine(AttnArgs a) {
         for (int u = 0; u < 8; ++u)
             if (c0 + u < nparts) acc += v[u];
     }
-    const uint16_t* pr = a.proj + (size_t)r * kAttnInRows;
-    const float o = rbf(acc);
-    const float g = rbf(sigmoid_f(bf2f(pr[qh * 512 + 256 + tid])));
-    a.out[(size_t)r * 2048 + qh * 256 + tid] = f2bf(o * g);
+    a.out[(size_t)r * 2048 + qh * 256 + tid] = gated_out(a, r, qh, tid, acc);
+}
+
+// Batched lanes: one block per (row, kv head) runs every chunk's scores into LDS, the
+// softmax, every part's P.V and the gated sum -- the same device functions and orders as the
+// split kernels, without the score / stats / partial round trips through HBM.
+__global__ void __launch_bounds__(256) attn_fused(AttnArgs a, int lds_slots) {
+    extern __shared__ float fl[];
+    float* scl = fl;                                    // [4][lds_slots]
+    float* stl = fl + 4 * lds_slots;                    // [4][2 * max_chunks]
+    __shared__ uint16_t qb[16][256];
+    __shared__ float red4[4][4];
+    __shared__ float p[4][kPart];
+    __shared__ float ml[4][2];
+    __shared__ float red[4][4][256];
+    const int r = blockIdx.x, j = blockIdx.y, tid = threadIdx.x;
+    const int slot = a.rm.slot[r];
+    const int lrow = a.rm.lane[r];
+    const int nch = slot / kChunk + 1, nparts = slot / kPart + 1;
+    const size_t sst = (size_t)a.max_chunks * 2;
+    q35_u32x4 qf[8];
+    load_q_frags(a, r, j, qb, qf);
+    for (int c = 0; c < nch; ++c) score_chunk(a, lrow, j, c, slot, qf, scl, lds_slots, stl, sst, red4);
+    softmax_ml(stl, sst, nch, ml);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int pc = 0; pc < nparts; ++pc) {
+        float out[4];
+        pv_part(a, lrow, j, pc, slot, scl, lds_slots, ml, p, red, out);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] += out[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a.out[(size_t)r * 2048 + (4 * j + i) * 256 + tid] = gated_out(a, r, 4 * j + i, tid, acc[i]);
+}
+
+hipError_t attn_init() {
+    return hipFuncSetAttribute((const void*)attn_fused, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (a.R <= 0 || a.max_chunks <= 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(attn_prep, dim3(a.R, kNq + kNkv), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(attn_scores, dim3(a.R, kNkv, a.max_chunks), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(attn_pv, dim3(a.R, kNkv, a.max_chunks * 2), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(attn_combine, dim3(a.R, kNq), dim3(256), 0, st, a);
+    const int lds_slots = a.max_chunks * kChunk;
+    const size_t lds = (size_t)(4 * lds_slots + 4 * 2 * a.max_chunks) * 4;
+    if (a.R >= 64 && lds <= 96 * 1024) {
+        hipLaunchKernelGGL(attn_fused, dim3(a.R, kNkv), dim3(256), lds, st, a, lds_slots);
+    } else {
+        hipLaunchKernelGGL(attn_scores, dim3(a.R, kNkv, a.max_chunks), dim3(256), 0, st, a);
+        hipLaunchKernelGGL(attn_pv, dim3(a.R, kNkv, a.max_chunks * 2), dim3(256), 0, st, a);
+        hipLaunchKernelGGL(attn_combine, dim3(a.R, kNq), dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 

@@ -565,6 +565,7 @@ int q35_create(const q35_config* cfg, q35_engine** out) {
         e->device = cfg->device; e->R = cfg->max_rows; e->max_ctx = cfg->max_ctx; e->use_graph = cfg->use_graph;
         HCK(hipSetDevice(e->device));
         HCK(gemm_init());
+        HCK(attn_init());
         HCK(hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking));
         HCK(hipEventCreate(&e->ev0));
         HCK(hipEventCreate(&e->ev1));

@@ -101,6 +101,7 @@ struct AttnArgs {
     const float* inv_freq; // [32] f32 rope inverse frequencies
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
+hipError_t attn_init();   // one-time kernel attribute setup
 
 // Synthetic init (portable stream, see q35_init.hip).
 hipError_t launch_gen_normal_tiled(uint64_t key, float scale, int N, int K, int row_off_dst,
