@@ -199,7 +199,7 @@ __device__ __forceinline__ void softmax_ml(const float* stats, size_t stats_stri
 // of the row's scores (head stride s_stride); ml must be ready. Contains barriers.
 __device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int pc, int slot,
                                         const float* scores, size_t s_stride, float (*ml)[2],
-                                        float (*p)[kPart], float (*red)[4][256], float* out) {
+                                        float (*p)[kPart], float (*red)[2][256], float* out) {
     const int tid = threadIdx.x;
     const int t0 = pc * kPart;
     const int n = min(kPart, slot + 1 - t0);
@@ -248,16 +248,21 @@ __device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int 
             const float other = __shfl_xor(acc[i][e], 32, 64);
             acc[i][e] = (tg & 1) ? other + acc[i][e] : acc[i][e] + other;
         }
-    if ((tg & 1) == 0) {
+    // then the 4 waves in order, two heads per pass through an 8 KiB LDS buffer
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+    for (int hp = 0; hp < 2; ++hp) {
+        if ((tg & 1) == 0) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) red[tg >> 1][i][dg * 8 + e] = acc[i][e];
+            for (int k = 0; k < 2; ++k)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) red[tg >> 1][k][dg * 8 + e] = acc[2 * hp + k][e];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+            out[2 * hp + k] = ((red[0][k][tid] + red[1][k][tid]) + red[2][k][tid]) + red[3][k][tid];
+        __syncthreads();
     }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = ((red[0][i][tid] + red[1][i][tid]) + red[2][i][tid]) + red[3][i][tid];
-    __syncthreads();
 }
 
 // attention output element: bf16(bf16(sum of parts) * bf16(sigmoid(gate)))
@@ -271,7 +276,7 @@ __device__ __forceinline__ uint16_t gated_out(const AttnArgs& a, int r, int qh, 
 __global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
     __shared__ float p[4][kPart];
     __shared__ float ml[4][2];
-    __shared__ float red[4][4][256];
+    __shared__ float red[4][2][256];
     const int r = blockIdx.x, j = blockIdx.y, pc = blockIdx.z;
     const int slot = a.rm.slot[r];
     if (pc >= slot / kPart + 1) return;
@@ -308,11 +313,12 @@ __global__ void __launch_bounds__(256) attn_fused(AttnArgs a, int lds_slots) {
     extern __shared__ float fl[];
     float* scl = fl;                                    // [4][lds_slots]
     float* stl = fl + 4 * lds_slots;                    // [4][2 * max_chunks]
-    __shared__ uint16_t qb[16][256];
+    __shared__ float ubuf[2048];                        // q staging, then the P.V reduction
+    uint16_t(*qb)[256] = (uint16_t(*)[256])ubuf;
+    float(*red)[2][256] = (float(*)[2][256])ubuf;
     __shared__ float red4[4][4];
     __shared__ float p[4][kPart];
     __shared__ float ml[4][2];
-    __shared__ float red[4][4][256];
     const int r = blockIdx.x, j = blockIdx.y, tid = threadIdx.x;
     const int slot = a.rm.slot[r];
     const int lrow = a.rm.lane[r];
@@ -340,7 +346,7 @@ hipError_t attn_init() {
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (a.R <= 0 || a.max_chunks <= 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(attn_prep, dim3(a.R, kNq + kNkv), dim3(256), 0, st, a);
-    const int lds_slots = a.max_chunks * kChunk;
+    const int lds_slots = (a.cap + 63) / 64 * 64;
     const size_t lds = (size_t)(4 * lds_slots + 4 * 2 * a.max_chunks) * 4;
     if (a.R >= 64 && lds <= 96 * 1024) {
         hipLaunchKernelGGL(attn_fused, dim3(a.R, kNkv), dim3(256), lds, st, a, lds_slots);
