@@ -107,7 +107,7 @@ __device__ __forceinline__ void score_chunk(const AttnArgs& a, int lrow, int j, 
         const int t = min(t0 + st * 16 + n, slot);        // clamped: masked below
         const uint16_t* kp = kbase + (size_t)t * 256 + g * 8;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) kf[st][s] = *(const q35_u32x4*)(kp + s * 32);
+        for (int s = 0; s < 8; ++s) kf[st][s] = __builtin_nontemporal_load((const q35_u32x4*)(kp + s * 32));
     }
     float sv[4][4];      // [sub-tile][r] for this lane's head (lanes n < 4)
 #pragma unroll
@@ -209,7 +209,7 @@ __device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int 
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
         const int t = tg * 16 + u;
-        vv[u] = t < n ? *(const q35_u32x4*)(vr + (size_t)t * 256) : (q35_u32x4){0u, 0u, 0u, 0u};
+        vv[u] = t < n ? __builtin_nontemporal_load((const q35_u32x4*)(vr + (size_t)t * 256)) : (q35_u32x4){0u, 0u, 0u, 0u};
     }
     float sraw[2] = {0.f, 0.f};
 #pragma unroll

@@ -73,8 +73,8 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     for (int i = 0; i < KR; ++i) {
         const float* p = Sin + (kg * KR + i) * 128 + cs * VC + jc;
         if (CW == 4) {
-            float4 v = *(const float4*)p;
-            s[i][0] = v.x; s[i][CW > 1 ? 1 : 0] = v.y; s[i][CW > 2 ? 2 : 0] = v.z; s[i][CW > 3 ? 3 : 0] = v.w;
+            const q35_f32x4 v = __builtin_nontemporal_load((const q35_f32x4*)p);   // streamed once
+            s[i][0] = v[0]; s[i][CW > 1 ? 1 : 0] = v[1]; s[i][CW > 2 ? 2 : 0] = v[2]; s[i][CW > 3 ? 3 : 0] = v[3];
         } else {
             s[i][0] = p[0];
         }
@@ -186,7 +186,9 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
 #pragma unroll
             for (int i = 0; i < KR; ++i) {
                 float* p = So + (kg * KR + i) * 128 + cs * VC + jc;
-                if (CW == 4) *(float4*)p = make_float4(s[i][0], s[i][CW > 1 ? 1 : 0], s[i][CW > 2 ? 2 : 0], s[i][CW > 3 ? 3 : 0]);
+                if (CW == 4)
+                    __builtin_nontemporal_store((q35_f32x4){s[i][0], s[i][CW > 1 ? 1 : 0], s[i][CW > 2 ? 2 : 0], s[i][CW > 3 ? 3 : 0]},
+                                                (q35_f32x4*)p);
                 else p[0] = s[i][0];
             }
             float* Wo = Wbase + slot * a.W_slot;
