@@ -94,21 +94,36 @@ __device__ __forceinline__ void load_q_frags(const AttnArgs& a, int r, int j, ui
 
 // Scores of chunk c (slots c*256 .. +256, masked beyond `slot`) -> dst[h * dst_stride + t],
 // chunk stats (max, sum e^(s - max)) -> stats[h * stats_stride + 2c .. +1]. Contains barriers.
+// K fragments of sub-tile st of chunk c for this lane (slot clamped to `slot`: masked later).
+__device__ __forceinline__ void load_k_sub(const AttnArgs& a, int lrow, int j, int c, int st, int slot,
+                                           q35_u32x4* kf) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int t = min(c * kChunk + wv * 64 + st * 16 + (lane & 15), slot);
+    const uint16_t* kp = a.kc + lrow * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + t) * 256 + (lane >> 4) * 8;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) kf[s] = __builtin_nontemporal_load((const q35_u32x4*)(kp + s * 32));
+}
+
+__device__ __forceinline__ void load_k_chunk(const AttnArgs& a, int lrow, int j, int c, int slot,
+                                             q35_u32x4 (*kf)[8]) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) load_k_sub(a, lrow, j, c, st, slot, kf[st]);
+}
+
+// Scores of chunk c (slots c*256 .. +256, masked beyond `slot`): wave w takes the 64-slot
+// slice q = 4c + w. Scores -> dst[h * dst_stride + t]; slice stats (max, sum e^(s - max)) ->
+// stats[h * stats_stride + 2q .. +1]. No barriers: the waves of a block run independently.
+// kf holds chunk c's K fragments on entry; with REFILL each sub-tile's registers are
+// refilled with chunk cnext's as soon as its MFMA chain has consumed them (unconditionally:
+// past the last chunk every lane reloads row `slot`, so the wait counts stay exact and the
+// loads stay in flight across iterations).
+template <bool REFILL>
 __device__ __forceinline__ void score_chunk(const AttnArgs& a, int lrow, int j, int c, int slot,
-                                            const q35_u32x4* qf, float* dst, size_t dst_stride,
-                                            float* stats, size_t stats_stride, float (*red)[4]) {
+                                            const q35_u32x4* qf, q35_u32x4 (*kf)[8], int cnext,
+                                            float* dst, size_t dst_stride, float* stats, size_t stats_stride) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int t0 = c * kChunk + wv * 64;
-    const uint16_t* kbase = a.kc + lrow * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256;
-    q35_u32x4 kf[4][8];
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-        const int t = min(t0 + st * 16 + n, slot);        // clamped: masked below
-        const uint16_t* kp = kbase + (size_t)t * 256 + g * 8;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) kf[st][s] = __builtin_nontemporal_load((const q35_u32x4*)(kp + s * 32));
-    }
     float sv[4][4];      // [sub-tile][r] for this lane's head (lanes n < 4)
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
@@ -116,6 +131,7 @@ __device__ __forceinline__ void score_chunk(const AttnArgs& a, int lrow, int j, 
 #pragma unroll
         for (int s = 0; s < 8; ++s)
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&kf[st][s], *(const q35_bf16x8*)&qf[s], acc, 0, 0, 0);
+        if (REFILL) load_k_sub(a, lrow, j, cnext, st, slot, kf[st]);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const float lo = __shfl_down(acc[rr], 4, 64);
@@ -133,37 +149,30 @@ __device__ __forceinline__ void score_chunk(const AttnArgs& a, int lrow, int j, 
         for (int rr = 0; rr < 4; ++rr) m = fmaxf(m, sv[st][rr]);
     m = fmaxf(m, __shfl_xor(m, 16, 64));
     m = fmaxf(m, __shfl_xor(m, 32, 64));
-    if (lane < 4) red[lane][wv] = m;
-    __syncthreads();
-    const float mb = n < 4 ? fmaxf(fmaxf(red[n][0], red[n][1]), fmaxf(red[n][2], red[n][3])) : 0.f;
     float e = 0.f;
 #pragma unroll
     for (int st = 0; st < 4; ++st)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) e += (n < 4 && sv[st][rr] > -INFINITY) ? expf(sv[st][rr] - mb) : 0.f;
+        for (int rr = 0; rr < 4; ++rr) e += sv[st][rr] > -INFINITY ? expf(sv[st][rr] - m) : 0.f;
     e += __shfl_xor(e, 16, 64);
     e += __shfl_xor(e, 32, 64);
-    __syncthreads();
-    if (lane < 4) red[lane][wv] = e;
-    __syncthreads();
-    if (tid < 4) {
-        float* st = stats + tid * stats_stride + 2 * c;
-        st[0] = mb;
-        st[1] = (red[tid][0] + red[tid][1]) + (red[tid][2] + red[tid][3]);
+    if (lane < 4 && t0 <= slot) {
+        float* sp = stats + lane * stats_stride + 2 * (4 * c + wv);
+        sp[0] = m;
+        sp[1] = e;
     }
-    __syncthreads();
 }
 
 __global__ void __launch_bounds__(256) attn_scores(AttnArgs a) {
     __shared__ uint16_t qb[16][256];
-    __shared__ float red[4][4];
     const int r = blockIdx.x, j = blockIdx.y, c = blockIdx.z;
     const int slot = a.rm.slot[r];
     if (c * kChunk > slot) return;
-    q35_u32x4 qf[8];
+    q35_u32x4 qf[8], kf[4][8];
+    load_k_chunk(a, a.rm.lane[r], j, c, slot, kf);
     load_q_frags(a, r, j, qb, qf);
-    score_chunk(a, a.rm.lane[r], j, c, slot, qf, a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld, a.sc_ld,
-                a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 2, (size_t)a.max_chunks * 2, red);
+    score_chunk<false>(a, a.rm.lane[r], j, c, slot, qf, kf, 0, a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld, a.sc_ld,
+                a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 8, (size_t)a.max_chunks * 8);
 }
 
 // P.V over one 128-slot part: thread (dg, tg) owns dims dg*8..+8 for slots tg*16..+16 of
@@ -171,46 +180,55 @@ __global__ void __launch_bounds__(256) attn_scores(AttnArgs a) {
 // summed in order (pairs in a wave by a lane swap, then the 4 waves through LDS).
 constexpr int kPart = 128;
 
-// Softmax (max, sum) of the row's 4 heads from the chunk stats -> ml[h][0..1] (threads 0-3).
-__device__ __forceinline__ void softmax_ml(const float* stats, size_t stats_stride, int nch, float (*ml)[2]) {
-    const int tid = threadIdx.x;
-    if (tid < 4) {
-        const float* st = stats + tid * stats_stride;
-        float mv[32], lv[32];
+// Softmax (max, sum) of the row's 4 heads from the nsl slice stats -> ml[h][0..1]: wave h
+// takes head h, lane i folds slices i, i + 64, ... in order, then a fixed xor butterfly.
+// Needs 4 waves.
+__device__ __forceinline__ void softmax_ml(const float* stats, size_t stats_stride, int nsl, float (*ml)[2]) {
+    const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
+    const float* st = stats + h * stats_stride;
+    float m = -INFINITY;
+    for (int i = lane; i < nsl; i += 64) m = fmaxf(m, st[2 * i]);
 #pragma unroll
-        for (int i = 0; i < 32; ++i)
-            if (i < nch) { mv[i] = st[2 * i]; lv[i] = st[2 * i + 1]; }
-        float m = -INFINITY;
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float l = 0.f;
+    for (int i = lane; i < nsl; i += 64) l += st[2 * i + 1] * expf(st[2 * i] - m);
 #pragma unroll
-        for (int i = 0; i < 32; ++i)
-            if (i < nch) m = fmaxf(m, mv[i]);
-        for (int i = 32; i < nch; ++i) m = fmaxf(m, st[2 * i]);
-        float l = 0.f;
-#pragma unroll
-        for (int i = 0; i < 32; ++i)
-            if (i < nch) l += lv[i] * expf(mv[i] - m);
-        for (int i = 32; i < nch; ++i) l += st[2 * i + 1] * expf(st[2 * i] - m);
-        ml[tid][0] = m;
-        ml[tid][1] = l;
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    if (lane == 0) {
+        ml[h][0] = m;
+        ml[h][1] = l;
     }
 }
 
 // Partial P.V of part pc for dims d = tid of the 4 heads -> out[4]. `scores` points at head 0
 // of the row's scores (head stride s_stride); ml must be ready. Contains barriers.
+// V row u of this thread's 16-slot group in part pc (zero beyond `slot`; the load itself is
+// unconditional, from row min(t, slot), so no branch splits the wait counts).
+__device__ __forceinline__ q35_u32x4 load_v(const AttnArgs& a, int lrow, int j, int pc, int u, int slot) {
+    const int tid = threadIdx.x, dg = tid & 31, tg = tid >> 5;
+    const int t = pc * kPart + tg * 16 + u;
+    const uint16_t* vp = a.vc + lrow * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + min(t, slot)) * 256 + dg * 8;
+    const q35_u32x4 v = __builtin_nontemporal_load((const q35_u32x4*)vp);
+    const uint32_t keep = t <= slot ? 0xffffffffu : 0u;
+    return (q35_u32x4){v[0] & keep, v[1] & keep, v[2] & keep, v[3] & keep};
+}
+
+__device__ __forceinline__ void load_v_part(const AttnArgs& a, int lrow, int j, int pc, int slot, q35_u32x4* vv) {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) vv[u] = load_v(a, lrow, j, pc, u, slot);
+}
+
+// vv holds part pc's V rows on entry; with REFILL each row register is refilled with part
+// pnext's as soon as it has been used (unconditionally, as for the K fragments).
+template <bool REFILL>
 __device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int pc, int slot,
+                                        q35_u32x4* vv, int pnext,
                                         const float* scores, size_t s_stride, float (*ml)[2],
                                         float (*p)[kPart], float (*red)[2][256], float* out) {
     const int tid = threadIdx.x;
     const int t0 = pc * kPart;
     const int n = min(kPart, slot + 1 - t0);
     const int dg = tid & 31, tg = tid >> 5;
-    const uint16_t* vr = a.vc + lrow * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + t0) * 256 + dg * 8;
-    q35_u32x4 vv[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-        const int t = tg * 16 + u;
-        vv[u] = t < n ? __builtin_nontemporal_load((const q35_u32x4*)(vr + (size_t)t * 256)) : (q35_u32x4){0u, 0u, 0u, 0u};
-    }
     float sraw[2] = {0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -239,6 +257,7 @@ __device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int 
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i][e] = fmaf(pp[i], v, acc[i][e]);
         }
+        if (REFILL) vv[u] = load_v(a, lrow, j, pnext, u, slot);
     }
     // slot groups 2w and 2w+1 live in wave w (lanes 0-31 and 32-63): add in group order
 #pragma unroll
@@ -280,10 +299,12 @@ __global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
     const int r = blockIdx.x, j = blockIdx.y, pc = blockIdx.z;
     const int slot = a.rm.slot[r];
     if (pc >= slot / kPart + 1) return;
-    softmax_ml(a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 2, (size_t)a.max_chunks * 2,
-               slot / kChunk + 1, ml);
+    q35_u32x4 vv[16];
+    load_v_part(a, a.rm.lane[r], j, pc, slot, vv);
+    softmax_ml(a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 8, (size_t)a.max_chunks * 8,
+               slot / 64 + 1, ml);
     float out[4];
-    pv_part(a, a.rm.lane[r], j, pc, slot, a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld, a.sc_ld, ml, p, red, out);
+    pv_part<false>(a, a.rm.lane[r], j, pc, slot, vv, 0, a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld, a.sc_ld, ml, p, red, out);
     float* pp = a.part + (((size_t)r * a.max_chunks * 2 + pc) * kNq + 4 * j) * 256 + threadIdx.x;
 #pragma unroll
     for (int i = 0; i < 4; ++i) pp[i * 256] = out[i];
@@ -312,26 +333,33 @@ __global__ void __launch_bounds__(256) attn_combine(AttnArgs a) {
 __global__ void __launch_bounds__(256) attn_fused(AttnArgs a, int lds_slots) {
     extern __shared__ float fl[];
     float* scl = fl;                                    // [4][lds_slots]
-    float* stl = fl + 4 * lds_slots;                    // [4][2 * max_chunks]
+    float* stl = fl + 4 * lds_slots;                    // [4][8 * max_chunks]
     __shared__ float ubuf[2048];                        // q staging, then the P.V reduction
     uint16_t(*qb)[256] = (uint16_t(*)[256])ubuf;
     float(*red)[2][256] = (float(*)[2][256])ubuf;
-    __shared__ float red4[4][4];
     __shared__ float p[4][kPart];
     __shared__ float ml[4][2];
     const int r = blockIdx.x, j = blockIdx.y, tid = threadIdx.x;
     const int slot = a.rm.slot[r];
     const int lrow = a.rm.lane[r];
     const int nch = slot / kChunk + 1, nparts = slot / kPart + 1;
-    const size_t sst = (size_t)a.max_chunks * 2;
+    const size_t sst = (size_t)a.max_chunks * 8;
     q35_u32x4 qf[8];
-    load_q_frags(a, r, j, qb, qf);
-    for (int c = 0; c < nch; ++c) score_chunk(a, lrow, j, c, slot, qf, scl, lds_slots, stl, sst, red4);
-    softmax_ml(stl, sst, nch, ml);
+    {
+        q35_u32x4 kf[4][8];
+        load_k_chunk(a, lrow, j, 0, slot, kf);
+        load_q_frags(a, r, j, qb, qf);
+        for (int c = 0; c < nch; ++c)
+            score_chunk<true>(a, lrow, j, c, slot, qf, kf, c + 1, scl, lds_slots, stl, sst);
+    }
+    __syncthreads();
+    q35_u32x4 vv[16];
+    load_v_part(a, lrow, j, 0, slot, vv);
+    softmax_ml(stl, sst, slot / 64 + 1, ml);
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     for (int pc = 0; pc < nparts; ++pc) {
         float out[4];
-        pv_part(a, lrow, j, pc, slot, scl, lds_slots, ml, p, red, out);
+        pv_part<true>(a, lrow, j, pc, slot, vv, pc + 1, scl, lds_slots, ml, p, red, out);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] += out[i];
     }
@@ -347,7 +375,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (a.R <= 0 || a.max_chunks <= 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(attn_prep, dim3(a.R, kNq + kNkv), dim3(256), 0, st, a);
     const int lds_slots = (a.cap + 63) / 64 * 64;
-    const size_t lds = (size_t)(4 * lds_slots + 4 * 2 * a.max_chunks) * 4;
+    const size_t lds = (size_t)(4 * lds_slots + 4 * 8 * a.max_chunks) * 4;
     if (a.R >= 64 && lds <= 96 * 1024) {
         hipLaunchKernelGGL(attn_fused, dim3(a.R, kNkv), dim3(256), lds, st, a, lds_slots);
     } else {

@@ -313,7 +313,7 @@ void alloc_scratch(q35_engine* e) {
     e->sc_ld = (e->max_ctx + 255) / 256 * 256;
     e->max_chunks = e->sc_ld / 256;
     e->sc = dalloc<float>(R * kNq * (size_t)e->sc_ld);
-    e->stats = dalloc<float>(R * kNq * (size_t)e->max_chunks * 2);
+    e->stats = dalloc<float>(R * kNq * (size_t)e->max_chunks * 8);
     e->part = dalloc<float>(R * (size_t)e->max_chunks * 4 * kNq * 256);
     e->pval = dalloc<float>(R * (size_t)(kVocab / 16));
     e->pidx = dalloc<int>(R * (size_t)(kVocab / 16));

@@ -93,8 +93,8 @@ struct AttnArgs {
     float* q;              // scratch [R][8][256] f32 post-rope q
     float* sc;             // scratch scores [R][8][sc_ld]
     int sc_ld;
-    float* stats;          // scratch [R][8][max_chunks][2]
-    float* part;           // scratch [R][4 * max_chunks][8][256] (64-slot parts)
+    float* stats;          // scratch [R][8][4 * max_chunks][2] (64-slot slices)
+    float* part;           // scratch [R][2 * max_chunks][8][256] (128-slot parts)
     int max_chunks;
     uint16_t* out;         // [R][2048] gated attention output (input of o_proj)
     int R;
