@@ -119,13 +119,13 @@ struct q35_engine {
     float *o, *q, *sc, *stats, *part, *pval, *inv_freq;
     float* kpart;
     uint16_t* prod;
-    int *pidx, *tok_dev, *rlane, *rpos, *rslot, *ridx_src, *ridx_dst;
+    int *pidx, *tok_dev, *rlane, *rpos, *rslot, *ridx_src, *ridx_dst, *din = nullptr;
     int sc_ld = 0, max_chunks = 0;
     float* logits_dev = nullptr;
     int logits_rows = 0;
     std::map<std::string, hipGraphExec_t> graphs;   // captured decode steps
     // pinned staging
-    int *h_tok, *h_lane, *h_pos, *h_slot, *h_out, *h_src, *h_dst;
+    int *h_tok, *h_lane, *h_pos, *h_slot, *h_out, *h_src, *h_dst, *hin = nullptr;
 };
 
 namespace {
@@ -319,19 +319,16 @@ void alloc_scratch(q35_engine* e) {
     e->pidx = dalloc<int>(R * (size_t)(kVocab / 16));
     e->kpart = dalloc<float>(R * 16 * kHidden);
     e->prod = dalloc<uint16_t>(R * kFF);
-    e->tok_dev = dalloc<int>(R);
-    e->rlane = dalloc<int>(R);
-    e->rpos = dalloc<int>(R);
-    e->rslot = dalloc<int>(R);
-    e->ridx_src = dalloc<int>(R);
-    e->ridx_dst = dalloc<int>(R);
-    e->h_tok = halloc<int>(R);
-    e->h_lane = halloc<int>(R);
-    e->h_pos = halloc<int>(R);
-    e->h_slot = halloc<int>(R);
+    // row metadata: one device block and one pinned host block, [tok|lane|pos|slot|src|dst]
+    // with stride R, so a step's inputs go up in a single copy
+    e->din = dalloc<int>(6 * (size_t)R);
+    e->hin = halloc<int>(6 * (size_t)R);
+    int* d[6];
+    int* hh[6];
+    for (int i = 0; i < 6; ++i) { d[i] = e->din + (size_t)i * R; hh[i] = e->hin + (size_t)i * R; }
+    e->tok_dev = d[0]; e->rlane = d[1]; e->rpos = d[2]; e->rslot = d[3]; e->ridx_src = d[4]; e->ridx_dst = d[5];
+    e->h_tok = hh[0]; e->h_lane = hh[1]; e->h_pos = hh[2]; e->h_slot = hh[3]; e->h_src = hh[4]; e->h_dst = hh[5];
     e->h_out = halloc<int>(R);
-    e->h_src = halloc<int>(R);
-    e->h_dst = halloc<int>(R);
     // rope inverse frequencies, f32 as the oracle forms them (specimpl.py:151-156):
     // inv_i = 1 / f32(theta ** f32(2i/64))
     float invf[32];
@@ -359,11 +356,14 @@ void ensure_logits(q35_engine* e, int rows) {
 
 // ------------------------------------------------------------------ body pass
 // Row metadata must already be staged in e->h_lane/h_pos/h_slot/h_tok for R rows.
-void upload_rows(q35_engine* e, int R) {
-    HCK(hipMemcpyAsync(e->tok_dev, e->h_tok, R * sizeof(int), hipMemcpyHostToDevice, e->st));
-    HCK(hipMemcpyAsync(e->rlane, e->h_lane, R * sizeof(int), hipMemcpyHostToDevice, e->st));
-    HCK(hipMemcpyAsync(e->rpos, e->h_pos, R * sizeof(int), hipMemcpyHostToDevice, e->st));
-    HCK(hipMemcpyAsync(e->rslot, e->h_slot, R * sizeof(int), hipMemcpyHostToDevice, e->st));
+// One copy of the metadata block from tok through region `upto` (rows [0, n) of it).
+void upload_meta(q35_engine* e, int upto, int n) {
+    HCK(hipMemcpyAsync(e->din, e->hin, ((size_t)upto * e->R + n) * sizeof(int), hipMemcpyHostToDevice, e->st));
+}
+void upload_rows(q35_engine* e, int R) { upload_meta(e, 3, R); }   // tok, lane, pos, slot
+// src / dst row indices only (tok_dev may hold device-written tokens): one copy
+void upload_idx(q35_engine* e, int n) {
+    HCK(hipMemcpyAsync(e->ridx_src, e->h_src, ((size_t)e->R + n) * sizeof(int), hipMemcpyHostToDevice, e->st));
 }
 
 // `cur` goes through pinned staging: the host advances s->cur right after enqueueing a
@@ -512,8 +512,7 @@ void save_hlast(q35_engine* e, q35_state* s, const std::vector<int>& src_rows, c
     const int n = (int)src_rows.size();
     HCK(hipStreamSynchronize(e->st));
     for (int i = 0; i < n; ++i) { e->h_src[i] = src_rows[i]; e->h_dst[i] = lanes[i]; }
-    HCK(hipMemcpyAsync(e->ridx_src, e->h_src, n * sizeof(int), hipMemcpyHostToDevice, e->st));
-    HCK(hipMemcpyAsync(e->ridx_dst, e->h_dst, n * sizeof(int), hipMemcpyHostToDevice, e->st));
+    upload_idx(e, n);
     HCK(launch_copy_rows(e->nrm, e->ridx_src, s->hlast, e->ridx_dst, n, kHidden, e->st));
 }
 
@@ -583,10 +582,10 @@ int q35_destroy(q35_engine* e) {
         for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
         e->graphs.clear();
         void* ds[] = {e->blob, e->x, e->h, e->delta, e->nrm, e->proj, e->gu, e->aout, e->cat, e->o, e->q,
-                      e->sc, e->stats, e->part, e->pval, e->pidx, e->prod, e->tok_dev, e->rlane,
-                      e->rpos, e->rslot, e->ridx_src, e->ridx_dst, e->inv_freq, e->logits_dev, e->kpart};
+                      e->sc, e->stats, e->part, e->pval, e->pidx, e->prod, e->din, e->inv_freq,
+                      e->logits_dev, e->kpart};
         for (void* p : ds) if (p) hipFree(p);
-        void* hs[] = {e->h_tok, e->h_lane, e->h_pos, e->h_slot, e->h_out, e->h_src, e->h_dst};
+        void* hs[] = {e->hin, e->h_out};
         for (void* p : hs) if (p) hipHostFree(p);
         hipEventDestroy(e->ev0);
         hipEventDestroy(e->ev1);
@@ -848,10 +847,8 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
         }
         REQ(e->weights_ready, Q35_ERR_STATE, "weights not initialised");
         for (int i = 0; i < n; ++i) { e->h_src[i] = i; e->h_dst[i] = ls[i]; }
-        upload_rows(e, n);
+        upload_meta(e, 5, n);        // tok, lane, pos, slot, src, dst in one copy
         upload_cur(e, s);
-        HCK(hipMemcpyAsync(e->ridx_src, e->h_src, n * sizeof(int), hipMemcpyHostToDevice, e->st));
-        HCK(hipMemcpyAsync(e->ridx_dst, e->h_dst, n * sizeof(int), hipMemcpyHostToDevice, e->st));
         auto step = [&] {
             body_kernels(e, s, n, 1, false);
             lm_head(e, 0, n, out_logits != nullptr, small_rows(n) ? e->final_norm : nullptr);
@@ -909,8 +906,7 @@ int q35_mtp_draft(q35_engine* e, q35_state* s, const int32_t* lanes, int n, cons
             e->h_src[i] = l; e->h_dst[i] = i;
         }
         // h rows: lane's hlast (post-final-norm row of the last body) -> e->h as scratch source
-        HCK(hipMemcpyAsync(e->ridx_src, e->h_src, n * sizeof(int), hipMemcpyHostToDevice, e->st));
-        HCK(hipMemcpyAsync(e->ridx_dst, e->h_dst, n * sizeof(int), hipMemcpyHostToDevice, e->st));
+        upload_idx(e, n);
         HCK(launch_copy_rows(s->hlast, e->ridx_src, e->delta, e->ridx_dst, n, kHidden, e->st));
         mtp_draft_pass(e, s, n, e->delta);
         lm_head(e, 0, n, out_logits != nullptr, small_rows(n) ? e->mtp_norm : nullptr);

@@ -138,6 +138,15 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
     q35_bf16x8 wf[8];
 #pragma unroll
     for (int s = 0; s < 8; ++s) wf[s] = __builtin_nontemporal_load(wp + s * 64);
+    // residual rows of the epilogue, loaded now so their latency overlaps the k-block work
+    float xr[4] = {0.f, 0.f, 0.f, 0.f};
+    if (EM == kEResidual && wv == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = mt * 16 + 4 * g + r;
+            if (row < a.M) xr[r] = bf2f(a.xres[(size_t)row * kHidden + nt * 16 + (lane & 15)]);
+        }
+    }
 
     const int kbase = kb * 256 + g * 64;
     q35_u32x4 af[8];
@@ -208,6 +217,14 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
         q35_f32x4 p = part[w][lane];
 #pragma unroll
         for (int r = 0; r < 4; ++r) sum[r] = sum[r] + p[r];
+    }
+    if (EM == kEResidual) {     // x <- bf16(x + bf16(sum)), as the epilogue below
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = mt * 16 + 4 * g + r;
+            if (row < a.M) a.xres[(size_t)row * kHidden + nt * 16 + (lane & 15)] = f2bf(xr[r] + rbf(sum[r]));
+        }
+        return;
     }
     epilogue<EM>(a, sum, nt, mt * 16, lane);
 }
