@@ -156,6 +156,43 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
         for (int s = 0; s < 8; ++s)
             af[s] = mvalid ? *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + kbase + s * 8)
                            : (q35_u32x4){0u, 0u, 0u, 0u};
+    } else if (a.M == 1) {
+        // Batch 1: lane c < 32 produces chunk c (k-block elements c*8 .. +8) with the same
+        // produce_a arithmetic and row factors as the cooperative form below; the fragments
+        // of the row-0 lanes (g, s) = chunk 8g + s are gathered with wave shuffles -- no LDS
+        // round trip, no block barrier.
+        const int c = lane & 31;
+        float rs = 0.f;
+        if (AM == kANormX) {
+            const uint16_t* xr = (const uint16_t*)a.X;
+            uint2 v[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) v[w] = *(const uint2*)(xr + 4 * (64 * w + lane));
+            float wsum[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                wsum[w] = wave_sum(quad_ss(__uint_as_float(v[w].x << 16), __uint_as_float(v[w].x & 0xffff0000u),
+                                           __uint_as_float(v[w].y << 16), __uint_as_float(v[w].y & 0xffff0000u)));
+            rs = hidden_rsqrt((wsum[0] + wsum[1]) + (wsum[2] + wsum[3]));
+        } else if (AM == kAGatedNorm) {
+            // lane L sums quarter L/16 (64 contiguous o values); chunk c is in head c/16,
+            // whose quarters are 2(c/16) and 2(c/16)+1
+            const float q = half_head_ss((const float*)a.X + kb * 256 + (lane >> 4) * 64);
+            const int h2 = (c >> 4) * 32;
+            rs = head_rsqrt(__shfl(q, h2, 64), __shfl(q, h2 + 16, 64));
+        }
+        const q35_u32x4 mine = produce_a<AM>(a, 0, kb * 256 + c * 8, rs);
+        if (AM == kANormX && a.hout && blockIdx.x == 0 && lane < 32)
+            *(q35_u32x4*)(a.hout + kb * 256 + c * 8) = mine;
+        const bool row0 = (lane & 15) == 0;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const int src = 8 * g + s;
+            q35_u32x4 f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) f[i] = (uint32_t)__shfl((int)mine[i], src, 64);
+            af[s] = row0 ? f : (q35_u32x4){0u, 0u, 0u, 0u};
+        }
     } else {
         // Producer modes: each wave builds its 16 x 256 A tile cooperatively -- only the M
         // valid rows, 8 elements per (lane, chunk) -- into its own LDS region in fragment
