@@ -94,36 +94,37 @@ __device__ __forceinline__ void load_q_frags(const AttnArgs& a, int r, int j, ui
 
 // Scores of chunk c (slots c*256 .. +256, masked beyond `slot`) -> dst[h * dst_stride + t],
 // chunk stats (max, sum e^(s - max)) -> stats[h * stats_stride + 2c .. +1]. Contains barriers.
-// K fragments of sub-tile st of chunk c for this lane (slot clamped to `slot`: masked later).
-__device__ __forceinline__ void load_k_sub(const AttnArgs& a, int lrow, int j, int c, int st, int slot,
+// K fragments of sub-tile st of 64-slot slice q for this lane (slot clamped to `slot`:
+// masked later).
+__device__ __forceinline__ void load_k_sub(const AttnArgs& a, int lrow, int j, int q, int st, int slot,
                                            q35_u32x4* kf) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int t = min(c * kChunk + wv * 64 + st * 16 + (lane & 15), slot);
+    const int lane = threadIdx.x & 63;
+    const int t = min(q * 64 + st * 16 + (lane & 15), slot);
     const uint16_t* kp = a.kc + lrow * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + t) * 256 + (lane >> 4) * 8;
 #pragma unroll
     for (int s = 0; s < 8; ++s) kf[s] = __builtin_nontemporal_load((const q35_u32x4*)(kp + s * 32));
 }
 
-__device__ __forceinline__ void load_k_chunk(const AttnArgs& a, int lrow, int j, int c, int slot,
+__device__ __forceinline__ void load_k_slice(const AttnArgs& a, int lrow, int j, int q, int slot,
                                              q35_u32x4 (*kf)[8]) {
 #pragma unroll
-    for (int st = 0; st < 4; ++st) load_k_sub(a, lrow, j, c, st, slot, kf[st]);
+    for (int st = 0; st < 4; ++st) load_k_sub(a, lrow, j, q, st, slot, kf[st]);
 }
 
-// Scores of chunk c (slots c*256 .. +256, masked beyond `slot`): wave w takes the 64-slot
-// slice q = 4c + w. Scores -> dst[h * dst_stride + t]; slice stats (max, sum e^(s - max)) ->
-// stats[h * stats_stride + 2q .. +1]. No barriers: the waves of a block run independently.
-// kf holds chunk c's K fragments on entry; with REFILL each sub-tile's registers are
-// refilled with chunk cnext's as soon as its MFMA chain has consumed them (unconditionally:
-// past the last chunk every lane reloads row `slot`, so the wait counts stay exact and the
-// loads stay in flight across iterations).
+// Scores of the 64-slot slice q (slots q*64 .. +64, masked beyond `slot`) by one wave.
+// Scores -> dst[h * dst_stride + t]; slice stats (max, sum e^(s - max)) ->
+// stats[h * stats_stride + 2q .. +1]. No barriers: waves run independently.
+// kf holds slice q's K fragments on entry; with REFILL each sub-tile's registers are
+// refilled with slice qnext's as soon as its MFMA chain has consumed them (unconditionally:
+// past the end every lane reloads row `slot`, so the wait counts stay exact and the loads
+// stay in flight across iterations).
 template <bool REFILL>
-__device__ __forceinline__ void score_chunk(const AttnArgs& a, int lrow, int j, int c, int slot,
-                                            const q35_u32x4* qf, q35_u32x4 (*kf)[8], int cnext,
+__device__ __forceinline__ void score_slice(const AttnArgs& a, int lrow, int j, int q, int slot,
+                                            const q35_u32x4* qf, q35_u32x4 (*kf)[8], int qnext,
                                             float* dst, size_t dst_stride, float* stats, size_t stats_stride) {
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int lane = threadIdx.x & 63;
     const int n = lane & 15, g = lane >> 4;
-    const int t0 = c * kChunk + wv * 64;
+    const int t0 = q * 64;
     float sv[4][4];      // [sub-tile][r] for this lane's head (lanes n < 4)
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
@@ -131,7 +132,7 @@ __device__ __forceinline__ void score_chunk(const AttnArgs& a, int lrow, int j, 
 #pragma unroll
         for (int s = 0; s < 8; ++s)
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&kf[st][s], *(const q35_bf16x8*)&qf[s], acc, 0, 0, 0);
-        if (REFILL) load_k_sub(a, lrow, j, cnext, st, slot, kf[st]);
+        if (REFILL) load_k_sub(a, lrow, j, qnext, st, slot, kf[st]);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const float lo = __shfl_down(acc[rr], 4, 64);
@@ -157,22 +158,46 @@ __device__ __forceinline__ void score_chunk(const AttnArgs& a, int lrow, int j, 
     e += __shfl_xor(e, 16, 64);
     e += __shfl_xor(e, 32, 64);
     if (lane < 4 && t0 <= slot) {
-        float* sp = stats + lane * stats_stride + 2 * (4 * c + wv);
+        float* sp = stats + lane * stats_stride + 2 * q;
         sp[0] = m;
         sp[1] = e;
     }
 }
 
-__global__ void __launch_bounds__(256) attn_scores(AttnArgs a) {
+// q fragments for a one-wave block: lane L converts dims 4L .. 4L+3 of the 4 heads.
+__device__ __forceinline__ void load_q_frags_wave(const AttnArgs& a, int r, int j, uint16_t (*qb)[256],
+                                                  q35_u32x4* qf) {
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const float* q = a.q + ((size_t)r * kNq + 4 * j) * 256;
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int d = 4 * lane + e;
+            const float qv = q[h * 256 + d];
+            const uint16_t hi = f2bf(qv);
+            qb[h][d] = hi;
+            qb[4 + h][d] = f2bf(qv - bf2f(hi));
+            qb[8 + h][d] = 0;
+            qb[12 + h][d] = 0;
+        }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[s] = *(const q35_u32x4*)&qb[n][s * 32 + g * 8];
+}
+
+// One wave per (row, kv head, 64-slot slice): many small blocks, so a single row's scores
+// spread over the CUs.
+__global__ void __launch_bounds__(64) attn_scores(AttnArgs a) {
     __shared__ uint16_t qb[16][256];
-    const int r = blockIdx.x, j = blockIdx.y, c = blockIdx.z;
+    const int r = blockIdx.x, j = blockIdx.y, q = blockIdx.z;
     const int slot = a.rm.slot[r];
-    if (c * kChunk > slot) return;
+    if (q * 64 > slot) return;
     q35_u32x4 qf[8], kf[4][8];
-    load_k_chunk(a, a.rm.lane[r], j, c, slot, kf);
-    load_q_frags(a, r, j, qb, qf);
-    score_chunk<false>(a, a.rm.lane[r], j, c, slot, qf, kf, 0, a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld, a.sc_ld,
-                a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 8, (size_t)a.max_chunks * 8);
+    load_k_slice(a, a.rm.lane[r], j, q, slot, kf);
+    load_q_frags_wave(a, r, j, qb, qf);
+    score_slice<false>(a, a.rm.lane[r], j, q, slot, qf, kf, 0, a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld, a.sc_ld,
+                       a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 8, (size_t)a.max_chunks * 8);
 }
 
 // P.V over one 128-slot part: thread (dg, tg) owns dims dg*8..+8 for slots tg*16..+16 of
@@ -346,11 +371,12 @@ __global__ void __launch_bounds__(256) attn_fused(AttnArgs a, int lds_slots) {
     const size_t sst = (size_t)a.max_chunks * 8;
     q35_u32x4 qf[8];
     {
+        const int wv = tid >> 6;
         q35_u32x4 kf[4][8];
-        load_k_chunk(a, lrow, j, 0, slot, kf);
+        load_k_slice(a, lrow, j, wv, slot, kf);
         load_q_frags(a, r, j, qb, qf);
-        for (int c = 0; c < nch; ++c)
-            score_chunk<true>(a, lrow, j, c, slot, qf, kf, c + 1, scl, lds_slots, stl, sst);
+        for (int c = 0; c < nch; ++c)    // wave wv takes slices 4c + wv
+            score_slice<true>(a, lrow, j, 4 * c + wv, slot, qf, kf, 4 * (c + 1) + wv, scl, lds_slots, stl, sst);
     }
     __syncthreads();
     q35_u32x4 vv[16];
@@ -379,7 +405,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (a.R >= 64 && lds <= 96 * 1024) {
         hipLaunchKernelGGL(attn_fused, dim3(a.R, kNkv), dim3(256), lds, st, a, lds_slots);
     } else {
-        hipLaunchKernelGGL(attn_scores, dim3(a.R, kNkv, a.max_chunks), dim3(256), 0, st, a);
+        hipLaunchKernelGGL(attn_scores, dim3(a.R, kNkv, a.max_chunks * 4), dim3(64), 0, st, a);
         hipLaunchKernelGGL(attn_pv, dim3(a.R, kNkv, a.max_chunks * 2), dim3(256), 0, st, a);
         hipLaunchKernelGGL(attn_combine, dim3(a.R, kNq), dim3(256), 0, st, a);
     }

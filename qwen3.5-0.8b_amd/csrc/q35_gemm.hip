@@ -163,11 +163,14 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
         // round trip, no block barrier.
         const int c = lane & 31;
         float rs = 0.f;
+        q35_u32x4 xc, wc;     // kANormX: this lane's x chunk and norm weights, loaded with the row
         if (AM == kANormX) {
             const uint16_t* xr = (const uint16_t*)a.X;
             uint2 v[4];
 #pragma unroll
             for (int w = 0; w < 4; ++w) v[w] = *(const uint2*)(xr + 4 * (64 * w + lane));
+            xc = *(const q35_u32x4*)(xr + kb * 256 + c * 8);
+            wc = *(const q35_u32x4*)(a.aux_w + kb * 256 + c * 8);
             float wsum[4];
 #pragma unroll
             for (int w = 0; w < 4; ++w)
@@ -181,7 +184,17 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
             const int h2 = (c >> 4) * 32;
             rs = head_rsqrt(__shfl(q, h2, 64), __shfl(q, h2 + 16, 64));
         }
-        const q35_u32x4 mine = produce_a<AM>(a, 0, kb * 256 + c * 8, rs);
+        q35_u32x4 mine;
+        if (AM == kANormX) {      // produce_a<kANormX> on the preloaded chunk
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lo = f2bf(norm_elem(__uint_as_float(xc[i] << 16), rs, __uint_as_float(wc[i] << 16)));
+                const uint32_t hi = f2bf(norm_elem(__uint_as_float(xc[i] & 0xffff0000u), rs, __uint_as_float(wc[i] & 0xffff0000u)));
+                mine[i] = lo | (hi << 16);
+            }
+        } else {
+            mine = produce_a<AM>(a, 0, kb * 256 + c * 8, rs);
+        }
         if (AM == kANormX && a.hout && blockIdx.x == 0 && lane < 32)
             *(q35_u32x4*)(a.hout + kb * 256 + c * 8) = mine;
         const bool row0 = (lane & 15) == 0;
