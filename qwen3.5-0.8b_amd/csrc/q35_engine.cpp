@@ -471,7 +471,8 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
             if (fused_norm) { g.y = e->prod; g.gnorm = w.gnorm; }
             {
                 KTimer kt(e, kFamGdn);
-                HCK(launch_gdn(g, cs, e->st));
+                if (cs == 1 && T == 1 && !ckpt) HCK(launch_gdn_persist(g, e->st));
+                else HCK(launch_gdn(g, cs, e->st));
             }
             if (fused_norm)
                 gemm(e, w.W_out, kHidden, 2048, R, e->prod, 2048, nullptr, 0);
@@ -565,6 +566,7 @@ int q35_create(const q35_config* cfg, q35_engine** out) {
         HCK(hipSetDevice(e->device));
         HCK(gemm_init());
         HCK(attn_init());
+        HCK(gdn_init());
         HCK(hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking));
         HCK(hipEventCreate(&e->ev0));
         HCK(hipEventCreate(&e->ev1));
@@ -1009,7 +1011,8 @@ int q35_op_gdn_step(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w,
         g.cur = nullptr; g.nslots = 2; g.ckpt = 0;
         g.lane = dl; g.T = 1; g.nlanes = B;
         const int cs = B <= 8 ? 8 : B <= 32 ? 4 : B <= 64 ? 2 : 1;
-        HCK(launch_gdn(g, cs, e->st));
+        if (cs == 1) HCK(launch_gdn_persist(g, e->st));
+        else HCK(launch_gdn(g, cs, e->st));
         HCK(hipStreamSynchronize(e->st));
         HCK(hipFree(dl));
     });

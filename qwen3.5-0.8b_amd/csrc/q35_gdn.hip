@@ -199,6 +199,188 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     }
 }
 
+// Persistent form of gdn_kernel<1> for one decode row per lane (T = 1, no checkpoints):
+// each block walks (row, head) items gi*16 + h = blockIdx.x, + gridDim.x, ...; while item i
+// computes, item i+1's 64 KiB state streams into LDS with global_load_lds (no VGPRs), so
+// the CU's memory pipe stays busy through the compute phases. Per item the loads of its own
+// operands are issued before the next item's prefetch, so waiting for them never waits for
+// the prefetch (the vector memory counter completes in order). Same thread mapping and
+// arithmetic, statement for statement, as gdn_kernel<1> with T = 1.
+__global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
+    constexpr int VC = 128, CW = 4, CG = 32, KR = 16, NG = 16, GPT = 2;
+    const int tid = threadIdx.x, lane64 = tid & 63, wv = tid >> 6;
+    const int jc = (tid % CG) * CW, kg = tid / CG;
+    extern __shared__ q35_f32x4 sbuf[];      // [4 waves][16 rows][64 lanes]: next item's state
+    __shared__ float qs[128], ks[128], vs[VC];
+    __shared__ float red[NG][VC];            // r partials, then o partials
+    __shared__ float wred[4];
+    __shared__ float gate_s[2];
+    __shared__ float ohead[128];
+    __shared__ float hss2[2];
+    auto prefetch = [&](int item) {
+        const int gi = item >> 4, h = item & 15;
+        const int ln = a.lane[gi];
+        const int cu = a.cur ? a.cur[ln] : 0;
+        const float* Sin = a.S + ln * a.S_lane + a.S_layer + (long long)h * 16384 + cu * a.S_slot;
+#pragma unroll
+        for (int i = 0; i < KR; ++i)
+            __builtin_amdgcn_global_load_lds((const void*)(Sin + (kg * KR + i) * 128 + jc),
+                                             (__attribute__((address_space(3))) void*)(sbuf + (wv * KR + i) * 64), 16, 0, 0);
+    };
+    int item = blockIdx.x;
+    if (item < nitems) prefetch(item);
+    for (; item < nitems; item += gridDim.x) {
+        const int gi = item >> 4, h = item & 15;
+        const int lane = a.lane[gi];
+        const int cur = a.cur ? a.cur[lane] : 0;
+        float* Sbase = a.S + lane * a.S_lane + a.S_layer + (long long)h * 16384;
+        float* Wbase = a.win + lane * a.W_lane + a.W_layer;
+        const float* Win = Wbase + cur * a.W_slot;
+        const uint16_t* pr = a.proj + (size_t)gi * kGdnInRows;
+        const int cqk = tid < 128 ? h * 128 + tid : 2048 + h * 128 + (tid - 128);
+        const int cv = 4096 + h * 128 + tid;
+        const bool hasv = tid < VC;
+        // this item's operands first
+        float w0 = Win[cqk], w1 = Win[6144 + cqk], w2 = Win[12288 + cqk];
+        float v0 = 0.f, v1 = 0.f, v2 = 0.f;
+        float cw[4], cvw[4] = {0.f, 0.f, 0.f, 0.f};
+        const uint2 cpk = *(const uint2*)(a.conv_w + (size_t)cqk * 4);
+        uint2 dpk = {0u, 0u};
+        float xv = 0.f, zz = 0.f, gw = 0.f;
+        if (hasv) {
+            v0 = Win[cv]; v1 = Win[6144 + cv]; v2 = Win[12288 + cv];
+            dpk = *(const uint2*)(a.conv_w + (size_t)cv * 4);
+            xv = bf2f(pr[cv]);
+            if (a.y) { zz = bf2f(pr[kGdnZOff + h * 128 + tid]); gw = bf2f(a.gnorm[tid]); }
+        }
+        const float x = bf2f(pr[cqk]);
+        float bb = 0.f, aa = 0.f, alog = 0.f;
+        if (tid == 0) { bb = bf2f(pr[kGdnBOff + h]); aa = bf2f(pr[kGdnAOff + h]); alog = bf2f(a.A_log[h]); aa += bf2f(a.dt_bias[h]); }
+        // this item's state: land its prefetch, move it to registers, then prefetch the next
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        float s[KR][CW];
+#pragma unroll
+        for (int i = 0; i < KR; ++i) {
+            const q35_f32x4 v = sbuf[(wv * KR + i) * 64 + lane64];
+            s[i][0] = v[0]; s[i][1] = v[1]; s[i][2] = v[2]; s[i][3] = v[3];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (item + gridDim.x < nitems) prefetch(item + gridDim.x);
+        cw[0] = __uint_as_float(cpk.x << 16); cw[1] = __uint_as_float(cpk.x & 0xffff0000u);
+        cw[2] = __uint_as_float(cpk.y << 16); cw[3] = __uint_as_float(cpk.y & 0xffff0000u);
+        cvw[0] = __uint_as_float(dpk.x << 16); cvw[1] = __uint_as_float(dpk.x & 0xffff0000u);
+        cvw[2] = __uint_as_float(dpk.y << 16); cvw[3] = __uint_as_float(dpk.y & 0xffff0000u);
+        const float A = -expf(alog);
+        // causal conv: taps over [w0, w1, w2, raw] in order, f32, one rounding, bf16 SiLU
+        {
+            float u = 0.f;
+            u = u + w0 * cw[0]; u = u + w1 * cw[1]; u = u + w2 * cw[2]; u = u + x * cw[3];
+            float uq = rbf(silu_f(rbf(u)));
+            w0 = w1; w1 = w2; w2 = x;
+            if (tid < 128) qs[tid] = uq; else ks[tid - 128] = uq;
+            if (hasv) {
+                float uv = 0.f;
+                uv = uv + v0 * cvw[0]; uv = uv + v1 * cvw[1]; uv = uv + v2 * cvw[2]; uv = uv + xv * cvw[3];
+                vs[tid] = rbf(silu_f(rbf(uv)));
+                v0 = v1; v1 = v2; v2 = xv;
+            }
+            float ss = wave_sum(uq * uq);
+            if ((tid & 63) == 0) wred[tid >> 6] = ss;
+            if (tid == 0) {
+                float sp = aa > 20.f ? aa : log1pf(expf(aa));
+                float g = A * sp;
+                gate_s[0] = expf(g);
+                gate_s[1] = sigmoid_f(bb);
+            }
+        }
+        __syncthreads();
+        {
+            const float rq = rsqrtf((wred[0] + wred[1]) + 1e-6f);
+            const float rk = rsqrtf((wred[2] + wred[3]) + 1e-6f);
+            if (tid < 128) qs[tid] = __fmul_rn(__fmul_rn(qs[tid], rq), 0.08838834764831845f);
+            else ks[tid - 128] = __fmul_rn(ks[tid - 128], rk);
+        }
+        __syncthreads();
+        const float gam = gate_s[0], beta = gate_s[1];
+#pragma unroll
+        for (int c = 0; c < CW; ++c)
+#pragma unroll
+            for (int gq = 0; gq < GPT; ++gq) {
+                float rp = 0.f;
+#pragma unroll
+                for (int i = gq * 8; i < gq * 8 + 8; ++i) {
+                    s[i][c] = __fmul_rn(s[i][c], gam);
+                    rp = fmaf(s[i][c], ks[kg * KR + i], rp);
+                }
+                red[kg * GPT + gq][jc + c] = rp;
+            }
+        __syncthreads();
+        float dv[CW];
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            float rj = 0.f;
+#pragma unroll
+            for (int i = 0; i < NG; ++i) rj += red[i][jc + c];
+            dv[c] = __fmul_rn(beta, vs[jc + c] - rj);
+        }
+        __syncthreads();          // red is reused for the o partials
+#pragma unroll
+        for (int c = 0; c < CW; ++c)
+#pragma unroll
+            for (int gq = 0; gq < GPT; ++gq) {
+                float op = 0.f;
+#pragma unroll
+                for (int i = gq * 8; i < gq * 8 + 8; ++i) {
+                    s[i][c] = __fadd_rn(s[i][c], __fmul_rn(ks[kg * KR + i], dv[c]));
+                    op = fmaf(qs[kg * KR + i], s[i][c], op);
+                }
+                red[kg * GPT + gq][jc + c] = op;
+            }
+        __syncthreads();
+        if (kg == 0) {
+#pragma unroll
+            for (int c = 0; c < CW; ++c) {
+                float oj = 0.f;
+#pragma unroll
+                for (int i = 0; i < NG; ++i) oj += red[i][jc + c];
+                a.o[(size_t)gi * 2048 + h * 128 + jc + c] = oj;
+                ohead[jc + c] = oj;
+            }
+        }
+        if (a.y) {
+            __syncthreads();
+            if (tid < 2) hss2[tid] = half_head_ss_regs(ohead + 64 * tid);
+            __syncthreads();
+            if (tid < 128) {
+                const float rs = head_rsqrt(hss2[0], hss2[1]);
+                a.y[(size_t)gi * 2048 + h * 128 + tid] = f2bf(__fmul_rn(__fmul_rn(gw, __fmul_rn(ohead[tid], rs)), silu_f(zz)));
+            }
+        }
+        const int slot = (cur + 1) % a.nslots;
+        float* So = Sbase + slot * a.S_slot;
+#pragma unroll
+        for (int i = 0; i < KR; ++i)
+            __builtin_nontemporal_store((q35_f32x4){s[i][0], s[i][1], s[i][2], s[i][3]},
+                                        (q35_f32x4*)(So + (kg * KR + i) * 128 + jc));
+        float* Wo = Wbase + slot * a.W_slot;
+        Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2;
+        if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
+        __syncthreads();          // LDS scratch (qs, ks, red, ohead) is reused by the next item
+    }
+}
+
+hipError_t gdn_init() {
+    return hipFuncSetAttribute((const void*)gdn_persist, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+}
+
+hipError_t launch_gdn_persist(const GdnArgs& a, hipStream_t st) {
+    if (a.nlanes <= 0 || a.T != 1 || a.ckpt) return hipErrorInvalidValue;
+    const int nitems = a.nlanes * kHv;
+    const int grid = nitems < 512 ? nitems : 512;      // two blocks per CU
+    hipLaunchKernelGGL(gdn_persist, dim3(grid), dim3(256), 64 * 1024, st, a, nitems);
+    return hipGetLastError();
+}
+
 hipError_t launch_gdn(const GdnArgs& a, int col_slices, hipStream_t st) {
     if (a.nlanes <= 0 || a.T <= 0) return hipErrorInvalidValue;
     dim3 grid(a.nlanes, kHv, col_slices);

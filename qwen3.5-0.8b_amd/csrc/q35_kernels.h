@@ -80,6 +80,10 @@ struct GdnArgs {
     const uint16_t* gnorm;     // [128]
 };
 hipError_t launch_gdn(const GdnArgs& a, int col_slices, hipStream_t st);
+// Persistent whole-head form for one decode row per lane (T = 1, ckpt = 0): the same bits
+// as launch_gdn(a, 1, st), with the next item's state prefetched into LDS.
+hipError_t launch_gdn_persist(const GdnArgs& a, hipStream_t st);
+hipError_t gdn_init();     // one-time kernel attribute setup
 
 struct AttnArgs {
     const uint16_t* proj;  // [R][5120]: (q|gate) x 8 heads interleaved, k, v
