@@ -423,8 +423,9 @@ void mlp_layer(q35_engine* e, const LayerW& w, int R) {
         return;
     }
     HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, 2048 / 256, w.norm_post, e->h, R, e->st));
-    gemm(e, w.W_gu, kGuRows, kHidden, R, e->h, kHidden, e->gu, kGuRows);
-    gemm(e, w.W_down, kHidden, kFF, R, e->gu, kGuRows, nullptr, 0, kASiluMul, e->gu + kFF, kGuRows);
+    // gate|up GEMM with the SwiGLU product in its epilogue: act [R][3584] -> plain down GEMM
+    gemm(e, w.W_gu, kGuRows, kHidden, R, e->h, kHidden, e->gu, kFF, kAPlain, nullptr, 0, nullptr, kESiluMul);
+    gemm(e, w.W_down, kHidden, kFF, R, e->gu, kFF, nullptr, 0);
 }
 
 // Batched path: fold the down-projection chains into x and normalise for the next consumer.

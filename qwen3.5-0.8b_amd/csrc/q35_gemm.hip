@@ -319,9 +319,13 @@ __global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
     const int mb = (a.M + MT * 16 - 1) / (MT * 16);
     const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
     const int nblk = (idx / mb) * 8 + xcd;
-    if (nblk * NW >= a.N / 16) return;
-    const int nt = nblk * NW + wv;
-    const bool nvalid = nt < a.N / 16;
+    // kESiluMul: waves 0 .. NW/2-1 take gate tiles j, waves NW/2 .. take the up tiles j
+    constexpr int HW = NW / 2;
+    const int half = a.N / 32;                                  // gate tiles
+    const int jg = nblk * HW + (wv % HW);
+    if (EM == kESiluMul ? nblk * HW >= half : nblk * NW >= a.N / 16) return;
+    const int nt = EM == kESiluMul ? (wv < HW ? jg : half + jg) : nblk * NW + wv;
+    const bool nvalid = EM == kESiluMul ? jg < half : nt < a.N / 16;
     const int row0 = (idx % mb) * MT * 16;
     const int KB = a.K >> 8;
     const int kb0 = EM == kEPartial ? blockIdx.z : 0;
@@ -375,6 +379,29 @@ __global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
             }
         }
     }
+    if (EM == kESiluMul) {
+        // up waves hand bf16(u) to the gate waves through the (now free) A staging area
+        float* ub = (float*)&As[0][0][0];                       // [HW][MT][4][64]
+        __syncthreads();
+        if (wv >= HW && nvalid) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ub[(((wv - HW) * MT + mt) * 4 + r) * 64 + lane] = rbf(sum[mt][r]);
+        }
+        __syncthreads();
+        if (wv >= HW || !nvalid) return;
+        const int col = jg * 16 + (lane & 15);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = row0 + mt * 16 + 4 * (lane >> 4) + r;
+                const float u = ub[((wv * MT + mt) * 4 + r) * 64 + lane];
+                if (row < a.M) a.Y[(size_t)row * a.ldy + col] = f2bf(__fmul_rn(rbf(silu_f(rbf(sum[mt][r]))), u));
+            }
+        return;
+    }
     if (!nvalid) return;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) epilogue<EM>(a, sum[mt], nt, row0 + mt * 16, lane);
@@ -424,7 +451,7 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
     const int KB = a.K / 256;
     const int gz = EM == kEPartial ? KB : 1;
     // 64-row tiles: more blocks in flight (W tiles are re-read from L2 by the M tiles)
-    const int nb = (a.N / 16 + 3) / 4, mb = (a.M + 63) / 64;
+    const int nb = EM == kESiluMul ? (a.N / 32 + 1) / 2 : (a.N / 16 + 3) / 4, mb = (a.M + 63) / 64;
     hipLaunchKernelGGL((gemm_large_m<EM, 4, 4>), dim3((nb + 7) / 8 * 8 * mb, 1, gz), dim3(256), 0, st, a);
 }
 
@@ -486,6 +513,11 @@ hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st) 
     }
     if (emode == kEPartial) { Q35_AM(kEPartial) }
     if (emode == kEResidual) { Q35_AM(kEResidual) }
+    if (emode == kESiluMul) {       // batched lanes only: a plain A operand, Y = act [M][N/2]
+        if (amode != kAPlain || a.M <= 16 || a.N % 32 || !a.Y) return hipErrorInvalidValue;
+        launch_large<kESiluMul>(a, st);
+        return hipGetLastError();
+    }
     if (emode == kEArgmax && amode == kAPlain) return launch_am_em<kAPlain, kEArgmax>(a, st);
     if (emode == kEArgmax && amode == kANormX) return launch_am_em<kANormX, kEArgmax>(a, st);
 #undef Q35_AM

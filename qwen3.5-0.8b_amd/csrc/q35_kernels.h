@@ -7,7 +7,9 @@
 namespace q35 {
 
 enum { kAPlain = 0, kASiluMul = 1, kAGatedNorm = 2, kANormX = 3 };
-enum { kEStore = 0, kEArgmax = 1, kEPartial = 2, kEResidual = 3 };
+enum { kEStore = 0, kEArgmax = 1, kEPartial = 2, kEResidual = 3, kESiluMul = 4 };
+// kESiluMul (batched lanes): N = 2F columns [gate | up]; each block pairs gate tiles with the
+// matching up tiles and stores act = bf16(bf16(silu(bf16 g)) * bf16 u) into Y [M][F].
 
 struct GemmArgs {
     const uint16_t* W;     // tiled [N/16][K/256] x 8 KiB
