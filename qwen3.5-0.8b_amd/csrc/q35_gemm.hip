@@ -452,6 +452,13 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
     const int gz = EM == kEPartial ? KB : 1;
     // 64-row tiles: more blocks in flight (W tiles are re-read from L2 by the M tiles)
     const int nb = EM == kESiluMul ? (a.N / 32 + 1) / 2 : (a.N / 16 + 3) / 4, mb = (a.M + 63) / 64;
+    if (EM == kEArgmax) {
+        // tied lm_head (N = 248,320): 16 waves x 16 columns share each staged A tile, so the
+        // A rows are re-read from L2 by 4x fewer blocks (measured best of 64x64, 128x128, 64x256)
+        const int nb16 = (a.N / 16 + 15) / 16;
+        hipLaunchKernelGGL((gemm_large_m<EM, 4, 16>), dim3((nb16 + 7) / 8 * 8 * mb, 1, gz), dim3(1024), 0, st, a);
+        return;
+    }
     hipLaunchKernelGGL((gemm_large_m<EM, 4, 4>), dim3((nb + 7) / 8 * 8 * mb, 1, gz), dim3(256), 0, st, a);
 }
 
