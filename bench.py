@@ -23,15 +23,23 @@ for p in (REPO, REPO / "qwen3.5-0.8b_amd"):
         sys.path.insert(0, str(p))
 
 HBM_PEAK = 8000.0            # GB/s, MI355X
+MFMA_PEAK = 2500.0           # dense bf16 TFLOP/s, MI355X
 WEIGHT_BYTES = 1_504_793_280  # bf16 weights streamed per pass (text tower + tied E)
 S_BYTES = 18 * 16 * 128 * 128 * 4
 WIN_BYTES = 18 * 3 * 6144 * 4
 KV_BYTES_PER_SLOT = 6 * 2 * 2 * 256 * 2   # K and V, 6 layers, 2 kv heads
 FAM = {"gemm": 1, "lm_head": 2, "gdn": 3, "attn": 4}
+KERNEL_NAMES = {"attn": "attn_fused", "gdn": "gdn_persist", "lm_head": "gemm_large_m<kEArgmax> (tied lm_head)",
+                "gemm": "projection / MLP GEMMs"}
+DOMINANT = "attn"           # largest share of the batch-256 step
 # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled by what
 # the same counter reads for a 1 GiB copy (FETCH x2.0, WRITE x1.0); the runs and the
-# calibration are in profiles/gdn_kernel_b256_ctx4096_traffic.md.
-MEASURED_TRAFFIC = {("gdn", 256, 4096): (142505 * 2.0 + 282624 * 1.0) * 1024}
+# calibration are in profiles/hbm_traffic_decode_b256_ctx4096.md.
+MEASURED_TRAFFIC = {
+    ("attn", 256, 4096): (1057562.5 * 2.0 + 1024.0 * 1.0) * 1024,                        # attn_fused
+    ("gdn", 256, 4096): (143107.0 * 2.0 + 283683.3 * 1.0) * 1024,                         # gdn_persist
+    ("lm_head", 256, 4096): (269641.3 * 2.0 + 31040.7 * 1.0) * 1024,                      # gemm_large_m<kEArgmax>
+}
 
 
 def step_bytes(B: int, L: int) -> int:
@@ -43,8 +51,8 @@ def family_bytes(fam: str, B: int, L: int) -> int:
     """Algorithmic bytes of all launches of one kernel family in one decode step."""
     if fam == "gdn":       # per layer: S read+write, window r+w, qkv/a/b in, o out
         return 18 * B * (2 * (1 << 20) + 2 * 73728 + 6176 * 2 + 2048 * 4)
-    if fam == "attn":      # per layer: K and V of L+1 slots, q/k/v in, output
-        return 6 * B * (2048 * (L + 1) + 5120 * 2 + 2048 * 2)
+    if fam == "attn":      # attention core per layer: K and V of L+1 slots, f32 q, bf16 gate in, output
+        return 6 * B * (2048 * (L + 1) + 8 * 256 * 4 + 2048 * 2 + 2048 * 2)
     if fam == "lm_head":
         return 248320 * 1024 * 2 + B * (1024 * 2 + 248320 // 16 * 8)
     if fam == "gemm":      # all projection + MLP GEMMs: weights once + activations
@@ -52,6 +60,14 @@ def family_bytes(fam: str, B: int, L: int) -> int:
         act = B * 24 * 2 * (1024 + 8224 + 2048 + 1024 + 1024 + 7168 + 7168 + 1024)
         return w + act
     raise ValueError(fam)
+
+
+def family_flops(fam: str, B: int) -> int:
+    """Dense GEMM FLOPs of one decode step's launches of a family (2 per multiply-add)."""
+    if fam == "lm_head":
+        return 2 * B * 248320 * 1024
+    w = (WEIGHT_BYTES - 248320 * 1024 * 2 - 24 * 2048 - 1024 * 2) // 2    # projection + MLP weights
+    return 2 * B * w
 
 
 def run_decode(eng, B: int, ctx: int, steps: int, warmup: int, kprof: str | None):
@@ -141,7 +157,9 @@ def main():
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--b1-steps", type=int, default=100)
-    ap.add_argument("--kprof", default="gdn", choices=list(FAM) + ["none"])
+    ap.add_argument("--kprof", default="all", choices=list(FAM) + ["none", "all"],
+                    help="kernel families timed with per-launch HIP events (separate eager passes)")
+    ap.add_argument("--kprof-steps", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mtp-rounds", type=int, default=5, help="config 4 (MTP k=2) rounds; 0 skips it")
     ap.add_argument("--eager", action="store_true", help="launch kernels eagerly (no hipGraph)")
@@ -167,24 +185,34 @@ def main():
         del src, dst
     eng = Engine(max_rows=max(3 * B, 64), max_ctx=L + max(args.steps, args.b1_steps) + args.warmup + 64, seed=0,
                  use_graph=not args.eager)
-    kp = None if args.kprof == "none" else args.kprof
-    wall, ev_s, kt = run_decode(eng, B, L, args.steps, args.warmup, kp)
+    # timed value: graph replay, no per-kernel events
+    wall, ev_s, _ = run_decode(eng, B, L, args.steps, args.warmup, None)
     ms = wall / args.steps * 1e3
     value = B * args.steps / wall
     wall1, ev1, kt1 = run_decode(eng, 1, L, args.b1_steps, args.warmup, None)
     ms1 = wall1 / args.b1_steps * 1e3
     gbs = step_bytes(B, L) / (ms / 1e3) / 1e9
     gbs1 = step_bytes(1, L) / (ms1 / 1e3) / 1e9
-    roof = None
-    if kt is not None and kt[1] > 0:
+    # kernel rooflines: short eager passes with HIP events around each launch of one family
+    rooflines = {}
+    fams = [] if args.kprof == "none" else ([args.kprof] if args.kprof != "all" else ["attn", "gdn", "lm_head", "gemm"])
+    for kp in fams:
+        _, _, kt = run_decode(eng, B, L, args.kprof_steps, 1, kp)
+        if kt is None or kt[1] <= 0:
+            continue
         per_launch_ms = kt[0] / kt[1]
-        launches_per_step = kt[1] / args.steps
+        launches_per_step = kt[1] / args.kprof_steps
         byt = family_bytes(kp, B, L) / launches_per_step
         ach = byt / (per_launch_ms / 1e3) / 1e9
-        roof = {"kernel": kp, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK, 4), "traffic": MEASURED_TRAFFIC.get((kp, B, L)),
-                "bytes_per_launch": int(byt), "avg_launch_us": round(per_launch_ms * 1e3, 2),
-                "launches_per_step": launches_per_step}
+        rooflines[kp] = {"kernel": KERNEL_NAMES[kp], "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK,
+                         "unit": "GB/s", "frac": round(ach / HBM_PEAK, 4), "traffic": MEASURED_TRAFFIC.get((kp, B, L)),
+                         "bytes_per_launch": int(byt), "avg_launch_us": round(per_launch_ms * 1e3, 2),
+                         "launches_per_step": launches_per_step}
+        if kp in ("lm_head", "gemm"):   # also priced against dense bf16 MFMA
+            tf = family_flops(kp, B) / launches_per_step / (per_launch_ms / 1e3) / 1e12
+            rooflines[kp].update({"achieved_tflops": round(tf, 1), "mfma_peak_tflops": MFMA_PEAK,
+                                  "mfma_frac": round(tf / MFMA_PEAK, 4)})
+    roof = rooflines.get(DOMINANT) or (next(iter(rooflines.values())) if rooflines else None)
     mtp = run_mtp(eng, B, L, args.mtp_rounds, 1) if args.mtp_rounds > 0 else None
     cpu = None
     if not args.no_cpu:
@@ -203,7 +231,8 @@ def main():
            "batch1": {"tok_s": round(args.b1_steps / wall1, 2), "ms_per_step": round(ms1, 4),
                       "hbm_gbs": round(gbs1, 1), "hbm_frac": round(gbs1 / HBM_PEAK, 4),
                       "bytes_per_token": step_bytes(1, L)},
-           "mtp_k2": mtp, "roofline": roof, "cpu_baseline": cpu}
+           "mtp_k2": mtp, "roofline": roof,
+           "kernel_rooflines": {k: v for k, v in rooflines.items() if k != DOMINANT}, "cpu_baseline": cpu}
     print(json.dumps(out))
 
 

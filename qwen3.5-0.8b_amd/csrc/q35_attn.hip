@@ -397,9 +397,14 @@ hipError_t attn_init() {
     return hipFuncSetAttribute((const void*)attn_fused, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
 }
 
-hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
+hipError_t launch_attn_prep(const AttnArgs& a, hipStream_t st) {
     if (a.R <= 0 || a.max_chunks <= 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(attn_prep, dim3(a.R, kNq + kNkv), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
+    if (a.R <= 0 || a.max_chunks <= 0) return hipErrorInvalidValue;
     const int lds_slots = (a.cap + 63) / 64 * 64;
     const size_t lds = (size_t)(4 * lds_slots + 4 * 8 * a.max_chunks) * 4;
     if (a.R >= 64 && lds <= 96 * 1024) {

@@ -404,9 +404,10 @@ void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16
     a.max_chunks = (cap + 255) / 256;
     REQ(a.max_chunks <= e->max_chunks, Q35_ERR_CAP, "cache capacity exceeds engine max_ctx");
     a.out = e->aout; a.R = R; a.inv_freq = e->inv_freq;
+    HCK(launch_attn_prep(a, e->st));
     {
-        KTimer kt(e, kFamAttn);
-        HCK(launch_attention(a, e->st));
+        KTimer kt(e, kFamAttn);      // the attention core alone (scores, softmax, P.V, gate)
+        HCK(launch_attn_core(a, e->st));
     }
     if (small_rows(R))
         gemm(e, w.W_out, kHidden, 2048, R, e->aout, 2048, nullptr, 0, kAPlain, nullptr, 0, nullptr, kEResidual, e->x);

@@ -106,7 +106,8 @@ struct AttnArgs {
     int R;
     const float* inv_freq; // [32] f32 rope inverse frequencies
 };
-hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
+hipError_t launch_attn_prep(const AttnArgs& a, hipStream_t st);   // q/k norm + rope, cache append
+hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st);   // scores, softmax, P.V, gate
 hipError_t attn_init();   // one-time kernel attribute setup
 
 // Synthetic init (portable stream, see q35_init.hip).
