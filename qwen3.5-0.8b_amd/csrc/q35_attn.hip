@@ -135,7 +135,7 @@ __device__ __forceinline__ void score_slice(const AttnArgs& a, int lrow, int j, 
         if (REFILL) load_k_sub(a, lrow, j, qnext, st, slot, kf[st]);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-            const float lo = __shfl_down(acc[rr], 4, 64);
+            const float lo = row_down4(acc[rr]);   // lanes n < 4 add the q_lo column n + 4
             const float sc = (acc[rr] + lo) * 0.0625f;
             const int t = t0 + st * 16 + 4 * g + rr;
             const bool ok = n < 4 && t <= slot;
@@ -149,14 +149,14 @@ __device__ __forceinline__ void score_slice(const AttnArgs& a, int lrow, int j, 
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) m = fmaxf(m, sv[st][rr]);
     m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    m = fmaxf(m, xor32(m));
     float e = 0.f;
 #pragma unroll
     for (int st = 0; st < 4; ++st)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) e += sv[st][rr] > -INFINITY ? expf(sv[st][rr] - m) : 0.f;
     e += __shfl_xor(e, 16, 64);
-    e += __shfl_xor(e, 32, 64);
+    e += xor32(e);
     if (lane < 4 && t0 <= slot) {
         float* sp = stats + lane * stats_stride + 2 * q;
         sp[0] = m;
@@ -289,7 +289,7 @@ __device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int 
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float other = __shfl_xor(acc[i][e], 32, 64);
+            const float other = xor32(acc[i][e]);
             acc[i][e] = (tg & 1) ? other + acc[i][e] : acc[i][e] + other;
         }
     // then the 4 waves in order, two heads per pass through an 8 KiB LDS buffer

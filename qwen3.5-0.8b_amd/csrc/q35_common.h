@@ -82,6 +82,16 @@ __device__ __forceinline__ T wave_sum(T v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
+// __shfl_xor(v, 32) without LDS: v_permlane32_swap exchanges the two 32-lane halves
+// (result [1] holds the upper half's values for lanes < 32, [0] the lower half's for lanes >= 32)
+__device__ __forceinline__ float xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+// lane i <- lane i + 4 within its row of 16 (DPP row_shl:4; 0 for the last 4 lanes of a row)
+__device__ __forceinline__ float row_down4(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x104, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
