@@ -101,6 +101,8 @@ struct q35_engine {
     int device = 0, R = 0, max_ctx = 0, use_graph = 0;
     int n_layers = kLayers;          // diagnostic: run only the first n layers of a body
     int kprof = 0;                   // kernel family timed with HIP events (0 = off)
+    int gdn_chunked = 1;             // prompt waves of one lane use the chunked GDN form
+    float *gchunk = nullptr, *gcdec = nullptr;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> kev;
     size_t kev_used = 0;
     hipStream_t st = nullptr;
@@ -318,6 +320,8 @@ void alloc_scratch(q35_engine* e) {
     e->pval = dalloc<float>(R * (size_t)(kVocab / 16));
     e->pidx = dalloc<int>(R * (size_t)(kVocab / 16));
     e->kpart = dalloc<float>(R * 16 * kHidden);
+    e->gchunk = dalloc<float>(gdn_chunk_ws_floats(R));
+    e->gcdec = dalloc<float>((size_t)((R + 63) / 64) * kHv);
     e->prod = dalloc<uint16_t>(R * kFF);
     // row metadata: one device block and one pinned host block, [tok|lane|pos|slot|src|dst]
     // with stride R, so a step's inputs go up in a single copy
@@ -469,11 +473,15 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
             g.W_layer = (long long)gdn_slot(l) * 18432;
             g.cur = s->cur_dev; g.nslots = s->nslots; g.ckpt = ckpt ? 1 : 0;
             g.lane = e->rlane; g.T = T; g.nlanes = nl;
-            const bool fused_norm = !small && cs == 1;   // whole-head blocks: norm in the GDN kernel
+            // a prompt wave of one lane: chunked (UT-transform) form
+            const bool chunked = e->gdn_chunked && !small && nl == 1 && T >= 64 && !ckpt;
+            const bool fused_norm = !small && cs == 1 && !chunked;   // whole-head blocks: norm in the GDN kernel
             if (fused_norm) { g.y = e->prod; g.gnorm = w.gnorm; }
+            g.chunk_ws = e->gchunk; g.chunk_cdec = e->gcdec;
             {
                 KTimer kt(e, kFamGdn);
-                if (cs == 1 && T == 1 && !ckpt) HCK(launch_gdn_persist(g, e->st));
+                if (chunked) HCK(launch_gdn_chunked(g, e->st));
+                else if (cs == 1 && T == 1 && !ckpt) HCK(launch_gdn_persist(g, e->st));
                 else HCK(launch_gdn(g, cs, e->st));
             }
             if (fused_norm)
@@ -587,7 +595,7 @@ int q35_destroy(q35_engine* e) {
         e->graphs.clear();
         void* ds[] = {e->blob, e->x, e->h, e->delta, e->nrm, e->proj, e->gu, e->aout, e->cat, e->o, e->q,
                       e->sc, e->stats, e->part, e->pval, e->pidx, e->prod, e->din, e->inv_freq,
-                      e->logits_dev, e->kpart};
+                      e->logits_dev, e->kpart, e->gchunk, e->gcdec};
         for (void* p : ds) if (p) hipFree(p);
         void* hs[] = {e->hin, e->h_out};
         for (void* p : hs) if (p) hipHostFree(p);
@@ -1046,6 +1054,9 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             e->kev_used = 0;
         } else if (n == "graph") {
             e->use_graph = value;
+        } else if (n == "gdn_chunked") {
+            HCK(hipStreamSynchronize(e->st));
+            e->gdn_chunked = value ? 1 : 0;
         } else {
             throw Q35Error(Q35_ERR_ARG, "unknown option " + n);
         }

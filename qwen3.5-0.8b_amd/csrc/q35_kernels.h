@@ -80,8 +80,15 @@ struct GdnArgs {
     // y[r][h*128 + j] = bf16(w[j] * (o * rsqrt(mean_head(o^2) + eps)) * silu(z)), bf16 [R][2048]
     uint16_t* y;
     const uint16_t* gnorm;     // [128]
+    // Chunked prompt form (one lane, no checkpoints): per-(chunk, head) workspace and decays
+    float* chunk_ws;
+    float* chunk_cdec;
 };
 hipError_t launch_gdn(const GdnArgs& a, int col_slices, hipStream_t st);
+// Chunked (UT-transform, chunk 64) form over the T rows of one lane: same state/window slot
+// semantics as launch_gdn without checkpoints; o only (the gated norm is the consumer's).
+hipError_t launch_gdn_chunked(const GdnArgs& a, hipStream_t st);
+size_t gdn_chunk_ws_floats(int max_rows);
 // Persistent whole-head form for one decode row per lane (T = 1, ckpt = 0): the same bits
 // as launch_gdn(a, 1, st), with the next item's state prefetched into LDS.
 hipError_t launch_gdn_persist(const GdnArgs& a, hipStream_t st);
