@@ -24,8 +24,21 @@ namespace q35 {
 
 constexpr int kC = 64;                      // chunk rows
 constexpr int kCWs = 4 * kC * 128 + kC * kC; // workspace floats per (chunk, head)
-// workspace layout per (chunk, head): q' | k' | nv | kcd  ([64][128] each), intra [64][64]
-constexpr int kWsQ = 0, kWsK = kC * 128, kWsNv = 2 * kC * 128, kWsKcd = 3 * kC * 128, kWsIntra = 4 * kC * 128;
+// Workspace per (chunk, head), written by the prep kernel directly in the scan's MFMA operand
+// order so that every scan wave reads its operands as contiguous 16-byte vectors
+// (lane = 16 kq + mr, see mfma4):
+//   kcd  [wave 4][lane 64][ks 32]  A[m = 16w + mr][k = 4ks + kq]      (phase 1)
+//   q'   [wave 4][lane 64][ks 32]  A[m = 16w + mr][k = 4ks + kq]      (phase 2)
+//   intra[wave 4][lane 64][ks 16]  A[m = 16w + mr][j = 4ks + kq]      (phase 2)
+//   k'^T [wave 4][half 2][lane 64][ks 16]  A[m = 32w + 16half + mr][i = 4ks + kq] = k'[i][m]  (phase 3)
+//   nv   [slice 8][wave 4][lane 64][r 4]   nv[16w + 4kq + r][16 slice + mr]   (phase 1, C layout)
+constexpr int kWsKcd = 0, kWsQ = 8192, kWsIntra = 16384, kWsK = 20480, kWsNv = 28672;
+
+// MFMA f32 16x16x4: lane l supplies A[l%16][l/16] and B[l/16][l%16] and holds
+// D[4 (l/16) + r][l%16], r = 0..3.
+__device__ __forceinline__ q35_f32x4 mfma4(float av, float bv, q35_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, c, 0, 0, 0);
+}
 
 __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
     const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
@@ -60,17 +73,25 @@ __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
         float w0 = raw(t0 - 3, cqk), w1 = raw(t0 - 2, cqk), w2 = raw(t0 - 1, cqk);
         float v0 = 0.f, v1 = 0.f, v2 = 0.f;
         if (hasv) { v0 = raw(t0 - 3, cv); v1 = raw(t0 - 2, cv); v2 = raw(t0 - 1, cv); }
+        // every row's raw value first (rows past the wave read the last row and are masked)
+        uint16_t xr[kC], xvr[kC];
+#pragma unroll
+        for (int i = 0; i < kC; ++i) {
+            const uint16_t* pr = a.proj + (size_t)min(t0 + i, a.T - 1) * kGdnInRows;
+            xr[i] = pr[cqk];
+            xvr[i] = hasv ? pr[cv] : (uint16_t)0;
+        }
+#pragma unroll
         for (int i = 0; i < kC; ++i) {
             float uq = 0.f, uvv = 0.f;
             if (i < nrow) {
-                const uint16_t* pr = a.proj + (size_t)(t0 + i) * kGdnInRows;
-                const float x = bf2f(pr[cqk]);
+                const float x = bf2f(xr[i]);
                 float u = 0.f;
                 u = u + w0 * cw0; u = u + w1 * cw1; u = u + w2 * cw2; u = u + x * cw3;
                 uq = rbf(silu_f(rbf(u)));
                 w0 = w1; w1 = w2; w2 = x;
                 if (hasv) {
-                    const float xv = bf2f(pr[cv]);
+                    const float xv = bf2f(xvr[i]);
                     float uv = 0.f;
                     uv = uv + v0 * vw0; uv = uv + v1 * vw1; uv = uv + v2 * vw2; uv = uv + xv * vw3;
                     uvv = rbf(silu_f(rbf(uv)));
@@ -115,55 +136,58 @@ __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
             kn[i][ln] = __fmul_rn(k0, rk);
             kn[i][ln + 64] = __fmul_rn(k1, rk);
         }
-        if (tid == 0) {
+        if (tid == 0) {       // cum_i = g_0 + .. + g_i, in order
+            float gv[kC];
+#pragma unroll
+            for (int i = 0; i < kC; ++i) gv[i] = gl[i];
             float s = 0.f;
-            for (int i = 0; i < kC; ++i) { s += gl[i]; cum[i] = s; }
+#pragma unroll
+            for (int i = 0; i < kC; ++i) { s += gv[i]; cum[i] = s; }
         }
     }
     __syncthreads();
     if (tid < kC) ecum[tid] = expf(cum[tid]);
-    // ---- ut (strictly lower) and intra (lower): thread -> row i = tid / 4, columns j = 16 (tid % 4) ..
+    // ---- ut (strictly lower) and intra (lower) on MFMA: wave w takes row tile w against the
+    // column tiles nt <= w; A = k~ (ut) or q~ (intra) rows, B = k~^T
+    float* ws = a.chunk_ws + ((size_t)c * kHv + h) * kCWs;
     {
-        const int i = tid >> 2, j0 = (tid & 3) * 16;
-        float du[16], di[16];
+        const int wv = tid >> 6, ln = tid & 63, mr = ln & 15, kq = ln >> 4;
+        for (int nt = 0; nt <= wv; ++nt) {
+            q35_f32x4 au = {0.f, 0.f, 0.f, 0.f}, ai = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+            for (int ks = 0; ks < 32; ++ks) {
+                const float bk = kn[nt * 16 + mr][ks * 4 + kq];
+                au = mfma4(kn[wv * 16 + mr][ks * 4 + kq], bk, au);
+                ai = mfma4(qn[wv * 16 + mr][ks * 4 + kq], bk, ai);
+            }
 #pragma unroll
-        for (int jj = 0; jj < 16; ++jj) { du[jj] = 0.f; di[jj] = 0.f; }
-        for (int d0 = 0; d0 < 128; d0 += 16) {
-            float kq[16], qq[16];
-#pragma unroll
-            for (int d = 0; d < 16; ++d) { kq[d] = kn[i][d0 + d]; qq[d] = qn[i][d0 + d]; }
-#pragma unroll
-            for (int jj = 0; jj < 16; ++jj) {
-                float su = du[jj], si = di[jj];
-#pragma unroll
-                for (int d = 0; d < 16; ++d) {
-                    const float kj = kn[j0 + jj][d0 + d];
-                    su = fmaf(kq[d], kj, su);
-                    si = fmaf(qq[d], kj, si);
-                }
-                du[jj] = su;
-                di[jj] = si;
+            for (int r = 0; r < 4; ++r) {
+                const int i = wv * 16 + 4 * kq + r, j = nt * 16 + mr;
+                const float pair = j <= i ? expf(cum[i] - cum[j]) : 0.f;
+                ut[i][j] = j < i ? (au[r] * bl[i]) * pair : 0.f;     // (beta_i k~_i) . k~_j, decayed
+                // intra in the scan's operand order: [w][lane (j % 4, i % 16)][j / 4]
+                ws[kWsIntra + ((wv * 64 + (j & 3) * 16 + (i & 15)) * 16 + (j >> 2))] = ai[r] * pair;
             }
         }
-        const float bi = bl[i], ci = cum[i];
-        float* intra = a.chunk_ws + ((size_t)c * kHv + h) * kCWs + kWsIntra;
+        for (int nt = wv + 1; nt < 4; ++nt)       // upper tiles: zero
 #pragma unroll
-        for (int jj = 0; jj < 16; ++jj) {
-            const int j = j0 + jj;
-            const float pair = j <= i ? expf(ci - cum[j]) : 0.f;
-            ut[i][j] = j < i ? (du[jj] * bi) * pair : 0.f;       // (beta_i k~_i) . k~_j, decayed
-            intra[i * kC + j] = di[jj] * pair;
-        }
+            for (int r = 0; r < 4; ++r) {
+                const int i = wv * 16 + 4 * kq + r, j = nt * 16 + mr;
+                ut[i][j] = 0.f;
+                ws[kWsIntra + ((wv * 64 + (j & 3) * 16 + (i & 15)) * 16 + (j >> 2))] = 0.f;
+            }
     }
     __syncthreads();
-    // ---- q' = q~ e^cum, k' = k~ e^(cum_63 - cum) (before the solve reuses qn)
-    float* ws = a.chunk_ws + ((size_t)c * kHv + h) * kCWs;
+    // ---- q' = q~ e^cum and k' = k~ e^(cum_63 - cum) in operand order (before the solve reuses qn)
     {
         const float clast = cum[kC - 1];
         for (int e = tid; e < kC * 128; e += 256) {
             const int i = e >> 7, d = e & 127;
-            ws[kWsQ + e] = qn[i][d] * ecum[i];
-            ws[kWsK + e] = kn[i][d] * expf(clast - cum[i]);
+            // q': A[m = i][k = d] -> [i / 16][lane (d % 4, i % 16)][d / 4]
+            ws[kWsQ + (((i >> 4) * 64 + (d & 3) * 16 + (i & 15)) * 32 + (d >> 2))] = qn[i][d] * ecum[i];
+            // k'^T: A[m = d][kk = i] -> [d / 32][(d % 32) / 16][lane (i % 4, d % 16)][i / 4]
+            ws[kWsK + ((((d >> 5) * 2 + ((d >> 4) & 1)) * 64 + (i & 3) * 16 + (d & 15)) * 16 + (i >> 2))] =
+                kn[i][d] * expf(clast - cum[i]);
         }
         if (tid == 0) a.chunk_cdec[c * kHv + h] = expf(clast);
     }
@@ -180,15 +204,14 @@ __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
             for (int j = 0; j < i; ++j) acc = fmaf(-ut[i][j], X[j][col], acc);
             X[i][col] = acc;
         }
-        float* dst = ws + (isk ? kWsKcd : kWsNv);
-        for (int i = 0; i < kC; ++i) dst[i * 128 + col] = X[i][col];
+        if (isk) {      // kcd: A[m = i][k = col] -> [i / 16][lane (col % 4, i % 16)][col / 4]
+            for (int i = 0; i < kC; ++i)
+                ws[kWsKcd + (((i >> 4) * 64 + (col & 3) * 16 + (i & 15)) * 32 + (col >> 2))] = X[i][col];
+        } else {        // nv: C layout of slice col / 16 -> [slice][i / 16][lane ((i % 16) / 4, col % 16)][i % 4]
+            for (int i = 0; i < kC; ++i)
+                ws[kWsNv + ((((col >> 4) * 4 + (i >> 4)) * 64 + ((i & 15) >> 2) * 16 + (col & 15)) * 4 + (i & 3))] = X[i][col];
+        }
     }
-}
-
-// MFMA f32 16x16x4: lane l supplies A[l%16][l/16] and B[l/16][l%16] and holds
-// D[4 (l/16) + r][l%16], r = 0..3.
-__device__ __forceinline__ q35_f32x4 mfma4(float av, float bv, q35_f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, c, 0, 0, 0);
 }
 
 __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
@@ -206,55 +229,83 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
     __syncthreads();
 
     const int mr = ln & 15, kq = ln >> 4;          // A row / k-quad of this lane
-    for (int c = 0; c < nchunks; ++c) {
+    // this wave's A operands of one chunk, in registers: kcd and q' rows 16w + mr (k = 4ks + kq),
+    // intra row 16w + mr (j = 4ks + kq), k'^T rows 32w + 16 half + mr (i = 4ks + kq), and nv
+    struct Ops { float kcd[32], qp[32], in[16], kp[2][16], nv[4], cd; };
+    auto load_ops = [&](int c, Ops& o) {
         const float* ws = a.chunk_ws + ((size_t)c * kHv + h) * kCWs;
+        o.cd = a.chunk_cdec[c * kHv + h];
+        const q35_f32x4* pk = (const q35_f32x4*)(ws + kWsKcd + (wv * 64 + ln) * 32);
+        const q35_f32x4* pq = (const q35_f32x4*)(ws + kWsQ + (wv * 64 + ln) * 32);
+        const q35_f32x4* pi = (const q35_f32x4*)(ws + kWsIntra + (wv * 64 + ln) * 16);
+        const q35_f32x4* pp0 = (const q35_f32x4*)(ws + kWsK + ((wv * 2 + 0) * 64 + ln) * 16);
+        const q35_f32x4* pp1 = (const q35_f32x4*)(ws + kWsK + ((wv * 2 + 1) * 64 + ln) * 16);
+        const q35_f32x4 nv4 = *(const q35_f32x4*)(ws + kWsNv + ((blockIdx.y * 4 + wv) * 64 + ln) * 4);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            const q35_f32x4 x = pk[v], y = pq[v];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { o.kcd[4 * v + e] = x[e]; o.qp[4 * v + e] = y[e]; }
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const q35_f32x4 x = pi[v], y = pp0[v], z = pp1[v];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { o.in[4 * v + e] = x[e]; o.kp[0][4 * v + e] = y[e]; o.kp[1][4 * v + e] = z[e]; }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o.nv[r] = nv4[r];
+    };
+    Ops cur_ops, nxt_ops;
+    load_ops(0, cur_ops);
+    for (int c = 0; c < nchunks; ++c) {
         const int t0 = c * kC;
+        // next chunk's operands (unconditional, clamped: no branch splits the wait counts)
+        load_ops(min(c + 1, nchunks - 1), nxt_ops);
+        // B fragments of S, shared by phases 1 and 2 (all waves read S before the barrier)
+        float sf[32];
+#pragma unroll
+        for (int ks = 0; ks < 32; ++ks) sf[ks] = S[ks * 4 + kq][mr];
         // phase 1: v_new = nv - kcd S   (wave w: rows 16w .. 16w+15)
         {
             q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            const float* kcd = ws + kWsKcd + (wv * 16 + mr) * 128;
-#pragma unroll 8
-            for (int ks = 0; ks < 32; ++ks) acc = mfma4(kcd[ks * 4 + kq], S[ks * 4 + kq][mr], acc);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = wv * 16 + 4 * kq + r;
-                vn[row][mr] = ws[kWsNv + row * 128 + n0 + mr] - acc[r];
-            }
+            for (int ks = 0; ks < 32; ++ks) acc = mfma4(cur_ops.kcd[ks], sf[ks], acc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) vn[wv * 16 + 4 * kq + r][mr] = cur_ops.nv[r] - acc[r];
         }
         __syncthreads();
+        float vf[16];       // B fragments of v_new, shared by phases 2 and 3
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) vf[ks] = vn[ks * 4 + kq][mr];
         // phase 2: o = q' S + intra v_new
         {
             q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            const float* qp = ws + kWsQ + (wv * 16 + mr) * 128;
-#pragma unroll 8
-            for (int ks = 0; ks < 32; ++ks) acc = mfma4(qp[ks * 4 + kq], S[ks * 4 + kq][mr], acc);
-            const float* in = ws + kWsIntra + (wv * 16 + mr) * kC;
-#pragma unroll 8
-            for (int ks = 0; ks < 16; ++ks) acc = mfma4(in[ks * 4 + kq], vn[ks * 4 + kq][mr], acc);
+#pragma unroll
+            for (int ks = 0; ks < 32; ++ks) acc = mfma4(cur_ops.qp[ks], sf[ks], acc);
+#pragma unroll
+            for (int ks = 0; ks < 16; ++ks) acc = mfma4(cur_ops.in[ks], vf[ks], acc);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = wv * 16 + 4 * kq + r;
                 if (t0 + row < a.T) a.o[(size_t)(t0 + row) * 2048 + h * 128 + n0 + mr] = acc[r];
             }
         }
-        __syncthreads();
-        // phase 3: S = e^cum_63 S + k'^T v_new   (wave w: state rows 32w .. 32w+31)
-        {
-            const float cd = a.chunk_cdec[c * kHv + h];
+        // phase 3: S = e^cum_63 S + k'^T v_new   (wave w: its own state rows 32w .. 32w+31;
+        // no other wave reads S after the barrier above)
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const int m0 = wv * 32 + half * 16;
-                q35_f32x4 acc;
+        for (int half = 0; half < 2; ++half) {
+            const int m0 = wv * 32 + half * 16;
+            q35_f32x4 acc;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[r] = S[m0 + 4 * kq + r][mr] * cd;
-                const float* kp = ws + kWsK + m0 + mr;          // k'^T [m][i] = k'[i][m]
-#pragma unroll 8
-                for (int ks = 0; ks < 16; ++ks) acc = mfma4(kp[(ks * 4 + kq) * 128], vn[ks * 4 + kq][mr], acc);
+            for (int r = 0; r < 4; ++r) acc[r] = S[m0 + 4 * kq + r][mr] * cur_ops.cd;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) S[m0 + 4 * kq + r][mr] = acc[r];
-            }
+            for (int ks = 0; ks < 16; ++ks) acc = mfma4(cur_ops.kp[half][ks], vf[ks], acc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) S[m0 + 4 * kq + r][mr] = acc[r];
         }
-        __syncthreads();
+        __syncthreads();    // S complete and v_new consumed before the next chunk
+        cur_ops = nxt_ops;
     }
     for (int e = tid; e < 128 * 16; e += 256) Sout[(e >> 4) * 128 + n0 + (e & 15)] = S[e >> 4][e & 15];
 }
