@@ -192,18 +192,47 @@ __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
         if (tid == 0) a.chunk_cdec[c * kHv + h] = expf(clast);
     }
     __syncthreads();
-    // ---- forward substitution in place, one column per thread: tid < 128 -> nv (in vv),
-    // else kcd (in qn, right-hand side beta k~ e^cum)
+    // ---- (I + ut) X = R for R = beta v (X in vv) and R = beta k~ e^cum (X in qn), blocked by
+    // 16 rows: R_b -= ut[b, <b] X[<b] on MFMA (wave w: 4 of the 16 column tiles of [vv | qn]),
+    // then the 16-row unit-lower solve of block b, one column per thread, in registers
     {
+        for (int e = tid; e < kC * 128; e += 256) {
+            const int i = e >> 7, d = e & 127;
+            vv[i][d] = vv[i][d] * bl[i];
+            qn[i][d] = (kn[i][d] * bl[i]) * ecum[i];
+        }
+        const int wv = tid >> 6, ln = tid & 63, mr = ln & 15, kq = ln >> 4;
         const int col = tid & 127;
         const bool isk = tid >= 128;
-        float(*X)[129] = isk ? qn : vv;
-        for (int i = 0; i < kC; ++i) {
-            float acc = isk ? (kn[i][col] * bl[i]) * ecum[i] : vv[i][col] * bl[i];
-#pragma unroll 4
-            for (int j = 0; j < i; ++j) acc = fmaf(-ut[i][j], X[j][col], acc);
-            X[i][col] = acc;
+        for (int bb = 0; bb < 4; ++bb) {
+            __syncthreads();
+            if (bb > 0) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int ntile = wv * 4 + t;                  // 0..7 -> vv, 8..15 -> qn
+                    float(*Xt)[129] = ntile < 8 ? vv : qn;
+                    const int n = (ntile & 7) * 16 + mr;
+                    q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                    for (int ks = 0; ks < bb * 4; ++ks)
+                        acc = mfma4(ut[bb * 16 + mr][ks * 4 + kq], Xt[ks * 4 + kq][n], acc);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) Xt[bb * 16 + 4 * kq + r][n] -= acc[r];
+                }
+                __syncthreads();
+            }
+            float(*X)[129] = isk ? qn : vv;
+            float x[16];
+#pragma unroll
+            for (int ii = 0; ii < 16; ++ii) x[ii] = X[bb * 16 + ii][col];
+#pragma unroll
+            for (int ii = 1; ii < 16; ++ii)
+#pragma unroll
+                for (int jj = 0; jj < ii; ++jj) x[ii] = fmaf(-ut[bb * 16 + ii][bb * 16 + jj], x[jj], x[ii]);
+#pragma unroll
+            for (int ii = 0; ii < 16; ++ii) X[bb * 16 + ii][col] = x[ii];
         }
+        __syncthreads();
+        float(*X)[129] = isk ? qn : vv;
         if (isk) {      // kcd: A[m = i][k = col] -> [i / 16][lane (col % 4, i % 16)][col / 4]
             for (int i = 0; i < kC; ++i)
                 ws[kWsKcd + (((i >> 4) * 64 + (col & 3) * 16 + (i & 15)) * 32 + (col >> 2))] = X[i][col];
