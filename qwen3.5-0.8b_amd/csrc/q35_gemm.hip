@@ -136,15 +136,24 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
 
     const q35_bf16x8* wp = (const q35_bf16x8*)(a.W + ((size_t)nt * KB + kb) * 4096) + lane;
     q35_bf16x8 wf[8];
+    auto load_w = [&] {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) wf[s] = __builtin_nontemporal_load(wp + s * 64);
+        for (int s = 0; s < 8; ++s) wf[s] = __builtin_nontemporal_load(wp + s * 64);
+    };
+    // batch 1 with a producer: the producer's own loads go first (the vector-memory counter
+    // completes in order, so its arithmetic then overlaps the weight stream instead of
+    // waiting behind it)
+    const bool direct = AM != kAPlain && a.M == 1;
+    if (!direct) load_w();
     // residual rows of the epilogue, loaded now so their latency overlaps the k-block work
-    float xr[4] = {0.f, 0.f, 0.f, 0.f};
-    if (EM == kEResidual && wv == 0) {
+    // (unconditional loads from clamped rows: a branch per load would make the compiler wait
+    // for every outstanding load at the join)
+    uint16_t xr[4] = {0, 0, 0, 0};      // raw bits: converted only in the epilogue (every wave
+    if (EM == kEResidual) {              // loads them: no branch, so no wait at a join)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int row = mt * 16 + 4 * g + r;
-            if (row < a.M) xr[r] = bf2f(a.xres[(size_t)row * kHidden + nt * 16 + (lane & 15)]);
+            const int row = min(mt * 16 + 4 * g + r, a.M - 1);
+            xr[r] = a.xres[(size_t)row * kHidden + nt * 16 + (lane & 15)];
         }
     }
 
@@ -162,41 +171,59 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
         // of the row-0 lanes (g, s) = chunk 8g + s are gathered with wave shuffles -- no LDS
         // round trip, no block barrier.
         const int c = lane & 31;
-        float rs = 0.f;
-        q35_u32x4 xc, wc;     // kANormX: this lane's x chunk and norm weights, loaded with the row
+        const int k0 = kb * 256 + c * 8;
+        q35_u32x4 mine;
         if (AM == kANormX) {
-            const uint16_t* xr = (const uint16_t*)a.X;
+            const uint16_t* xr0 = (const uint16_t*)a.X;
             uint2 v[4];
 #pragma unroll
-            for (int w = 0; w < 4; ++w) v[w] = *(const uint2*)(xr + 4 * (64 * w + lane));
-            xc = *(const q35_u32x4*)(xr + kb * 256 + c * 8);
-            wc = *(const q35_u32x4*)(a.aux_w + kb * 256 + c * 8);
+            for (int w = 0; w < 4; ++w) v[w] = *(const uint2*)(xr0 + 4 * (64 * w + lane));
+            const q35_u32x4 xc = *(const q35_u32x4*)(xr0 + k0);
+            const q35_u32x4 wc = *(const q35_u32x4*)(a.aux_w + k0);
+            asm volatile("" ::: "memory");     // keep the producer's loads ahead of W
+            load_w();
+            __builtin_amdgcn_sched_barrier(0);   // ... and its arithmetic behind W's issue
             float wsum[4];
 #pragma unroll
             for (int w = 0; w < 4; ++w)
                 wsum[w] = wave_sum(quad_ss(__uint_as_float(v[w].x << 16), __uint_as_float(v[w].x & 0xffff0000u),
                                            __uint_as_float(v[w].y << 16), __uint_as_float(v[w].y & 0xffff0000u)));
-            rs = hidden_rsqrt((wsum[0] + wsum[1]) + (wsum[2] + wsum[3]));
-        } else if (AM == kAGatedNorm) {
-            // lane L sums quarter L/16 (64 contiguous o values); chunk c is in head c/16,
-            // whose quarters are 2(c/16) and 2(c/16)+1
-            const float q = half_head_ss((const float*)a.X + kb * 256 + (lane >> 4) * 64);
-            const int h2 = (c >> 4) * 32;
-            rs = head_rsqrt(__shfl(q, h2, 64), __shfl(q, h2 + 16, 64));
-        }
-        q35_u32x4 mine;
-        if (AM == kANormX) {      // produce_a<kANormX> on the preloaded chunk
+            const float rs = hidden_rsqrt((wsum[0] + wsum[1]) + (wsum[2] + wsum[3]));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < 4; ++i) {      // produce_a<kANormX> on the preloaded chunk
                 const uint32_t lo = f2bf(norm_elem(__uint_as_float(xc[i] << 16), rs, __uint_as_float(wc[i] << 16)));
                 const uint32_t hi = f2bf(norm_elem(__uint_as_float(xc[i] & 0xffff0000u), rs, __uint_as_float(wc[i] & 0xffff0000u)));
                 mine[i] = lo | (hi << 16);
             }
-        } else {
-            mine = produce_a<AM>(a, 0, kb * 256 + c * 8, rs);
+        } else if (AM == kASiluMul) {         // produce_a<kASiluMul> on preloaded g, u
+            const q35_u32x4 gq = *(const q35_u32x4*)((const uint16_t*)a.X + k0);
+            const q35_u32x4 uq = *(const q35_u32x4*)((const uint16_t*)a.X2 + k0);
+            asm volatile("" ::: "memory");     // keep the producer's loads ahead of W
+            load_w();
+            __builtin_amdgcn_sched_barrier(0);   // ... and its arithmetic behind W's issue
+            mine = silu_mul8(gq, uq);
+        } else {                               // kAGatedNorm: produce_a on preloaded o, z, w
+            // lane L sums quarter L/16 (64 contiguous o values); chunk c is in head c/16,
+            // whose quarters are 2(c/16) and 2(c/16)+1
+            const float* po = (const float*)a.X;
+            float qv[64];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) *(float4*)&qv[4 * i] = *(const float4*)(po + kb * 256 + (lane >> 4) * 64 + 4 * i);
+            float ov[8];
+            *(float4*)&ov[0] = *(const float4*)(po + k0);
+            *(float4*)&ov[4] = *(const float4*)(po + k0 + 4);
+            const q35_u32x4 zz = *(const q35_u32x4*)((const uint16_t*)a.X2 + k0);
+            const q35_u32x4 ww = *(const q35_u32x4*)(a.aux_w + (k0 & 127));
+            asm volatile("" ::: "memory");     // keep the producer's loads ahead of W
+            load_w();
+            __builtin_amdgcn_sched_barrier(0);   // ... and its arithmetic behind W's issue
+            const float q = half_head_ss_regs(qv);
+            const int h2 = (c >> 4) * 32;
+            const float rs = head_rsqrt(__shfl(q, h2, 64), __shfl(q, h2 + 16, 64));
+            mine = gated8(ov, zz, ww, rs);
         }
         if (AM == kANormX && a.hout && blockIdx.x == 0 && lane < 32)
-            *(q35_u32x4*)(a.hout + kb * 256 + c * 8) = mine;
+            *(q35_u32x4*)(a.hout + k0) = mine;
         const bool row0 = (lane & 15) == 0;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
@@ -272,7 +299,7 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = mt * 16 + 4 * g + r;
-            if (row < a.M) a.xres[(size_t)row * kHidden + nt * 16 + (lane & 15)] = f2bf(xr[r] + rbf(sum[r]));
+            if (row < a.M) a.xres[(size_t)row * kHidden + nt * 16 + (lane & 15)] = f2bf(bf2f(xr[r]) + rbf(sum[r]));
         }
         return;
     }
