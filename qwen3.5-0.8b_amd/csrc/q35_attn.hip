@@ -57,15 +57,16 @@ __global__ void __launch_bounds__(256) attn_prep(AttnArgs a) {
     if (isq) {
         a.q[((size_t)r * kNq + hh) * 256 + d] = out;
     } else {
-        const size_t off = lane * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + slot) * 256 + d;
-        a.kc[off] = f2bf(out);
-        a.vc[off] = pr[kAttnVOff + j * 256 + d];
+        const size_t base = lane * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256;
+        a.kc[base + kv_tiled_offset(slot, d)] = f2bf(out);
+        a.vc[base + (size_t)slot * 256 + d] = pr[kAttnVOff + j * 256 + d];
     }
 }
 
 // Scores on MFMA: a wave takes 16 cache slots per v_mfma_f32_16x16x32_bf16 chain with the
-// K rows as the A operand (step s of lane (slot t, group g) carries dims s*32 + g*8 .. +8,
-// so each load instruction reads 64 contiguous bytes of 16 slots) and B = [q_hi(4 heads) |
+// K rows as the A operand (step s of lane (slot t, group g) carries dims s*32 + g*8 .. +8;
+// the K cache is stored in exactly that order, q35_common.h kv_tiled_offset, so each load
+// instruction reads one contiguous KiB) and B = [q_hi(4 heads) |
 // q_lo(4 heads) | 0], q_hi = bf16(q), q_lo = bf16(q - q_hi), so s = C[t][h] + C[t][h+4]
 // carries q to ~2^-16 relative. A chunk = 4 waves x 64 slots.
 //
@@ -94,15 +95,16 @@ __device__ __forceinline__ void load_q_frags(const AttnArgs& a, int r, int j, ui
 
 // Scores of chunk c (slots c*256 .. +256, masked beyond `slot`) -> dst[h * dst_stride + t],
 // chunk stats (max, sum e^(s - max)) -> stats[h * stats_stride + 2c .. +1]. Contains barriers.
-// K fragments of sub-tile st of 64-slot slice q for this lane (slot clamped to `slot`:
-// masked later).
+// K fragments of sub-tile st of 64-slot slice q for this lane: K tile 4q + st of the tiled
+// cache, step s = one contiguous KiB (the tile index is clamped to `slot`'s tile; slots past
+// `slot` are masked later).
 __device__ __forceinline__ void load_k_sub(const AttnArgs& a, int lrow, int j, int q, int st, int slot,
                                            q35_u32x4* kf) {
     const int lane = threadIdx.x & 63;
-    const int t = min(q * 64 + st * 16 + (lane & 15), slot);
-    const uint16_t* kp = a.kc + lrow * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + t) * 256 + (lane >> 4) * 8;
+    const int tile = min(q * 4 + st, slot >> 4);
+    const uint16_t* kp = a.kc + lrow * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256 + (size_t)tile * 4096 + lane * 8;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) kf[s] = __builtin_nontemporal_load((const q35_u32x4*)(kp + s * 32));
+    for (int s = 0; s < 8; ++s) kf[s] = __builtin_nontemporal_load((const q35_u32x4*)(kp + s * 512));
 }
 
 __device__ __forceinline__ void load_k_slice(const AttnArgs& a, int lrow, int j, int q, int slot,

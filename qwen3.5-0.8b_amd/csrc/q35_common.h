@@ -47,6 +47,14 @@ constexpr int attn_slot(int l) { return l / 4; }
 // Element (n, k): tile (n/16, k/256); g = (k%256)/64; s = (k%64)/8; e = k%8.
 constexpr int kTileN = 16;
 constexpr int kTileK = 256;
+// K cache of one (lane, layer, kv head): 16-slot tiles in MFMA fragment order, so a score
+// step's operand (16 slots x 32 dims) is one contiguous KiB: tile slot/16, step d/32, lane
+// ((d/8) % 4) * 16 + slot % 16, element d % 8. Regions are padded to whole tiles.
+__host__ __device__ inline size_t kv_tiled_offset(int slot, int d) {
+    return (size_t)(slot >> 4) * 4096 + (d >> 5) * 512 + ((((d >> 3) & 3) << 4) | (slot & 15)) * 8 + (d & 7);
+}
+__host__ __device__ inline int kv_cap_padded(int cap) { return (cap + 15) & ~15; }
+
 __host__ __device__ inline size_t tiled_offset(int n, int k, int K) {
     int nt = n >> 4, kb = k >> 8, kk = k & 255;
     int g = kk >> 6, s = (kk >> 3) & 7, e = kk & 7;

@@ -83,6 +83,7 @@ struct LayerW {
 
 struct q35_state {
     int lanes = 0, cap = 0, mtp_cap = 0, nslots = 2, mtp_k = 0;
+    int capT = 0, mtp_capT = 0;   // K/V region strides: capacities padded to whole 16-slot K tiles
     float* S = nullptr;      // [lanes][nslots][18][16][128][128]
     float* win = nullptr;    // [lanes][nslots][18][3][6144]
     uint16_t *kc = nullptr, *vc = nullptr;    // [lanes][6][2][cap][256]
@@ -93,8 +94,8 @@ struct q35_state {
     std::vector<int> prefix, mtp_len, cur;
     long long S_lane() const { return (long long)nslots * kGdnLayers * kSLayer; }
     long long W_lane() const { return (long long)nslots * kGdnLayers * 18432; }
-    long long kv_lane() const { return (long long)kAttnLayers * 2 * cap * 256; }
-    long long mkv_lane() const { return (long long)2 * mtp_cap * 256; }
+    long long kv_lane() const { return (long long)kAttnLayers * 2 * capT * 256; }
+    long long mkv_lane() const { return (long long)2 * mtp_capT * 256; }
 };
 
 struct q35_engine {
@@ -491,7 +492,7 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
                      e->proj + kGdnZOff, kGdnInRows, w.gnorm, small ? kEResidual : -1, e->x);
         } else {
             attention_layer(e, w, R, s->kc, s->vc, s->kv_lane(),
-                            (long long)attn_slot(l) * 2 * s->cap * 256, s->cap);
+                            (long long)attn_slot(l) * 2 * s->capT * 256, s->capT);
         }
         mlp_layer(e, w, R);
         const bool lastl = l + 1 == e->n_layers;
@@ -542,7 +543,7 @@ void mtp_draft_pass(q35_engine* e, q35_state* s, int n, const uint16_t* hsrc) {
         gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, nullptr, 0);
         HCK(launch_addnorm(4, nullptr, nullptr, e->x, nullptr, e->kpart, 2048 / 256, e->M.norm_in, e->h, n, e->st));
     }
-    attention_layer(e, e->M, n, s->mkc, s->mvc, s->mkv_lane(), 0, s->mtp_cap);
+    attention_layer(e, e->M, n, s->mkc, s->mvc, s->mkv_lane(), 0, s->mtp_capT);
     mlp_layer(e, e->M, n);
     finish_norm(e, n, e->mtp_norm, e->nrm);
 }
@@ -681,6 +682,7 @@ int q35_state_alloc(q35_engine* e, int lanes, int cap, int mtp_k, int mtp_cap, q
         REQ(cap <= e->max_ctx && mtp_cap <= e->max_ctx, Q35_ERR_CAP, "cap exceeds engine max_ctx");
         auto* s = new q35_state();
         s->lanes = lanes; s->cap = cap; s->mtp_cap = mtp_cap; s->mtp_k = mtp_k;
+        s->capT = kv_cap_padded(cap); s->mtp_capT = kv_cap_padded(mtp_cap);
         s->nslots = mtp_k > 0 ? mtp_k + 2 : 2;
         s->S = dalloc<float>((size_t)lanes * s->S_lane());
         s->win = dalloc<float>((size_t)lanes * s->W_lane());
@@ -752,9 +754,9 @@ int q35_state_seed(q35_engine* e, q35_state* s, uint64_t seed, int prefix_len) {
             HCK(hipMemsetAsync(s->win + l * s->W_lane(), 0, s->W_lane() * 4, e->st));
             for (int a = 0; a < kAttnLayers; ++a)
                 for (int j = 0; j < kNkv; ++j) {
-                    size_t off = l * s->kv_lane() + ((size_t)(a * 2 + j) * s->cap) * 256;
+                    size_t off = l * s->kv_lane() + ((size_t)(a * 2 + j) * s->capT) * 256;
                     std::string tag = std::to_string(l) + "." + std::to_string(a) + "." + std::to_string(j);
-                    HCK(launch_gen_normal_plain(stream_key(seed, "state.k." + tag), s1, (long long)prefix_len * 256, s->kc + off, e->st));
+                    HCK(launch_gen_normal_kv_tiled(stream_key(seed, "state.k." + tag), s1, prefix_len, s->kc + off, e->st));
                     HCK(launch_gen_normal_plain(stream_key(seed, "state.v." + tag), s1, (long long)prefix_len * 256, s->vc + off, e->st));
                 }
             s->prefix[l] = prefix_len; s->mtp_len[l] = 0; s->cur[l] = 0;
@@ -786,16 +788,38 @@ static void state_io(q35_engine* e, q35_state* s, int lane, int which, int n_slo
         cp(s->S + lane * s->S_lane() + (long long)cur * kGdnLayers * kSLayer, 0, (size_t)kGdnLayers * kSLayer * 4);
     } else if (which == 1) {
         cp(s->win + lane * s->W_lane() + (long long)cur * kGdnLayers * 18432, 0, (size_t)kGdnLayers * 18432 * 4);
-    } else if (which == 2 || which == 3) {
-        REQ(n_slots >= 0 && n_slots <= s->cap, Q35_ERR_ARG, "n_slots out of range");
-        uint16_t* base = (which == 2 ? s->kc : s->vc) + lane * s->kv_lane();
-        for (int a = 0; a < kAttnLayers * 2; ++a)
-            cp(base + (size_t)a * s->cap * 256, (size_t)a * n_slots * 512, (size_t)n_slots * 512);
-    } else if (which == 4 || which == 5) {
-        REQ(s->mtp_cap > 0 && n_slots >= 0 && n_slots <= s->mtp_cap, Q35_ERR_ARG, "n_slots out of range");
-        uint16_t* base = (which == 4 ? s->mkc : s->mvc) + lane * s->mkv_lane();
-        for (int a = 0; a < 2; ++a)
-            cp(base + (size_t)a * s->mtp_cap * 256, (size_t)a * n_slots * 512, (size_t)n_slots * 512);
+    } else if (which >= 2 && which <= 5) {
+        // K / V caches: [heads][n_slots][256] bf16 row-major on the host. V is stored that way;
+        // K is stored in 16-slot tiles (kv_tiled_offset) and converted here.
+        const bool mtp = which >= 4, isk = which == 2 || which == 4;
+        const int cap = mtp ? s->mtp_cap : s->cap, capT = mtp ? s->mtp_capT : s->capT;
+        const int heads = mtp ? 2 : kAttnLayers * 2;
+        REQ(!mtp || s->mtp_cap > 0, Q35_ERR_ARG, "state has no MTP cache");
+        REQ(n_slots >= 0 && n_slots <= cap, Q35_ERR_ARG, "n_slots out of range");
+        REQ((size_t)heads * n_slots * 512 <= bytes, Q35_ERR_ARG, "host buffer too small");
+        uint16_t* base = (mtp ? (isk ? s->mkc : s->mvc) : (isk ? s->kc : s->vc)) +
+                         lane * (mtp ? s->mkv_lane() : s->kv_lane());
+        if (!isk) {
+            for (int a = 0; a < heads; ++a)
+                cp(base + (size_t)a * capT * 256, (size_t)a * n_slots * 512, (size_t)n_slots * 512);
+        } else if (n_slots > 0) {
+            const int nt = (n_slots + 15) / 16;
+            std::vector<uint16_t> tiles((size_t)nt * 4096);
+            uint16_t* h = (uint16_t*)host;
+            for (int a = 0; a < heads; ++a) {
+                uint16_t* dev = base + (size_t)a * capT * 256;
+                if (write) {   // keep the padding slots of the last tile as they are on the device
+                    copy_sync(e, tiles.data(), dev, tiles.size() * 2, hipMemcpyDeviceToHost);
+                    for (int t = 0; t < n_slots; ++t)
+                        for (int d = 0; d < 256; ++d) tiles[kv_tiled_offset(t, d)] = h[((size_t)a * n_slots + t) * 256 + d];
+                    copy_sync(e, dev, tiles.data(), tiles.size() * 2, hipMemcpyHostToDevice);
+                } else {
+                    copy_sync(e, tiles.data(), dev, tiles.size() * 2, hipMemcpyDeviceToHost);
+                    for (int t = 0; t < n_slots; ++t)
+                        for (int d = 0; d < 256; ++d) h[((size_t)a * n_slots + t) * 256 + d] = tiles[kv_tiled_offset(t, d)];
+                }
+            }
+        }
     } else {
         throw Q35Error(Q35_ERR_ARG, "unknown state tensor");
     }

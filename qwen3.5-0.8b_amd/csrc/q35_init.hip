@@ -57,6 +57,20 @@ hipError_t launch_gen_normal_tiled(uint64_t key, float scale, int N, int K, int 
     hipLaunchKernelGGL(gen_normal_tiled, dim3(4096), dim3(256), 0, st, key, scale, N, K, row_off_dst, dst);
     return hipGetLastError();
 }
+// K cache seeding: element i = slot * 256 + d of the stream (the same values as a row-major
+// fill) stored at the tiled position of (slot, d).
+__global__ void gen_normal_kv_tiled(uint64_t key, float scale, long long n, uint16_t* dst) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i < n; i += (long long)gridDim.x * blockDim.x)
+        dst[kv_tiled_offset((int)(i >> 8), (int)(i & 255))] = f2bf(normal_at(key, (uint64_t)i, scale));
+}
+
+hipError_t launch_gen_normal_kv_tiled(uint64_t key, float scale, int n_slots, uint16_t* dst, hipStream_t st) {
+    if (n_slots <= 0) return hipSuccess;
+    hipLaunchKernelGGL(gen_normal_kv_tiled, dim3(4096), dim3(256), 0, st, key, scale, (long long)n_slots * 256, dst);
+    return hipGetLastError();
+}
+
 hipError_t launch_gen_normal_plain(uint64_t key, float scale, long long n, uint16_t* dst, hipStream_t st) {
     hipLaunchKernelGGL(gen_normal_plain, dim3(4096), dim3(256), 0, st, key, scale, n, dst);
     return hipGetLastError();
