@@ -366,7 +366,14 @@ __global__ void __launch_bounds__(256) attn_fused(AttnArgs a, int lds_slots) {
     float(*red)[2][256] = (float(*)[2][256])ubuf;
     __shared__ float p[4][kPart];
     __shared__ float ml[4][2];
-    const int r = blockIdx.x, j = blockIdx.y, tid = threadIdx.x;
+    // Block order: the T rows of one lane read the same K/V, so they run as consecutive
+    // blocks of one XCD (blocks go round-robin to the 8 XCDs) and share its L2 stream:
+    // (lane group, kv head) pair p -> XCD p % 8, blocks 8 ((p / 8) T + t) + p % 8.
+    const int T = a.T, tid = threadIdx.x;
+    const int xcd = blockIdx.x & 7, kk = blockIdx.x >> 3;
+    const int pr = (kk / T) * 8 + xcd;
+    if (pr >= (a.R / T) * kNkv) return;
+    const int j = pr % kNkv, r = (pr / kNkv) * T + kk % T;
     const int slot = a.rm.slot[r];
     const int lrow = a.rm.lane[r];
     const int nch = slot / kChunk + 1, nparts = slot / kPart + 1;
@@ -410,7 +417,9 @@ hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
     const int lds_slots = (a.cap + 63) / 64 * 64;
     const size_t lds = (size_t)(4 * lds_slots + 4 * 8 * a.max_chunks) * 4;
     if (a.R >= 64 && lds <= 96 * 1024) {
-        hipLaunchKernelGGL(attn_fused, dim3(a.R, kNkv), dim3(256), lds, st, a, lds_slots);
+        if (a.T < 1 || a.R % a.T) return hipErrorInvalidValue;
+        const int pairs = a.R / a.T * kNkv;
+        hipLaunchKernelGGL(attn_fused, dim3((pairs + 7) / 8 * a.T * 8), dim3(256), lds, st, a, lds_slots);
     } else {
         hipLaunchKernelGGL(attn_scores, dim3(a.R, kNkv, a.max_chunks * 4), dim3(64), 0, st, a);
         hipLaunchKernelGGL(attn_pv, dim3(a.R, kNkv, a.max_chunks * 2), dim3(256), 0, st, a);

@@ -396,7 +396,7 @@ void gemm(q35_engine* e, const uint16_t* W, int N, int K, int M, const void* X, 
 inline bool small_rows(int R) { return R <= 16; }
 
 void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16_t* vc,
-                     long long kv_lane, long long layer_off, int cap) {
+                     long long kv_lane, long long layer_off, int cap, int T = 1) {
     if (small_rows(R))
         gemm(e, w.W_in, kAttnInRows, kHidden, R, e->x, kHidden, e->proj, kAttnInRows, kANormX, nullptr, 0, w.norm_in);
     else
@@ -408,7 +408,7 @@ void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16
     a.q = e->q; a.sc = e->sc; a.sc_ld = e->sc_ld; a.stats = e->stats; a.part = e->part;
     a.max_chunks = (cap + 255) / 256;
     REQ(a.max_chunks <= e->max_chunks, Q35_ERR_CAP, "cache capacity exceeds engine max_ctx");
-    a.out = e->aout; a.R = R; a.inv_freq = e->inv_freq;
+    a.out = e->aout; a.R = R; a.T = T; a.inv_freq = e->inv_freq;
     HCK(launch_attn_prep(a, e->st));
     {
         KTimer kt(e, kFamAttn);      // the attention core alone (scores, softmax, P.V, gate)
@@ -492,7 +492,7 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
                      e->proj + kGdnZOff, kGdnInRows, w.gnorm, small ? kEResidual : -1, e->x);
         } else {
             attention_layer(e, w, R, s->kc, s->vc, s->kv_lane(),
-                            (long long)attn_slot(l) * 2 * s->capT * 256, s->capT);
+                            (long long)attn_slot(l) * 2 * s->capT * 256, s->capT, T);
         }
         mlp_layer(e, w, R);
         const bool lastl = l + 1 == e->n_layers;

@@ -111,6 +111,7 @@ struct AttnArgs {
     int max_chunks;
     uint16_t* out;         // [R][2048] gated attention output (input of o_proj)
     int R;
+    int T;                 // rows per lane (a lane's rows are consecutive; MTP verify: k + 1)
     const float* inv_freq; // [32] f32 rope inverse frequencies
 };
 hipError_t launch_attn_prep(const AttnArgs& a, hipStream_t st);   // q/k norm + rope, cache append
