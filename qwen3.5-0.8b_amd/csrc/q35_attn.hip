@@ -202,6 +202,88 @@ __global__ void __launch_bounds__(64) attn_scores(AttnArgs a) {
                        a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 8, (size_t)a.max_chunks * 8);
 }
 
+// attn_prep's per-head arithmetic for one wave: lane holds d = lane + 64 w (w = 0..3); the
+// sum of squares folds each 64-element quarter with a wave sum and then (q0 + q1) + (q2 + q3),
+// block_sum256a's tree, so the result is bit-identical to the 256-thread kernel.
+__device__ __forceinline__ void head_norm_rope_wave(const AttnArgs& a, const uint16_t* src,
+                                                    const uint16_t* normw, int pos, float* out) {
+    const int lane = threadIdx.x & 63;
+    float x[4], ssq[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) x[w] = bf2f(src[lane + 64 * w]);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) ssq[w] = wave_sum(x[w] * x[w]);
+    const float rs = rsqrtf(((ssq[0] + ssq[1]) + (ssq[2] + ssq[3])) * (1.0f / 256.0f) + kEps);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) out[w] = rbf(__fmul_rn(__fmul_rn(x[w], rs), 1.0f + bf2f(normw[lane + 64 * w])));
+    // rope on dims 0..63 (pairs d, d +- 32): quarter 0 holds them, the partner is lane ^ 32
+    const float partner = xor32(out[0]);
+    const int i = lane & 31;
+    const float ang = __fmul_rn((float)pos, a.inv_freq[i]);
+    const float c = cosf(ang), sn = sinf(ang);
+    const float rot = lane < 32 ? -partner : partner;
+    out[0] = __fadd_rn(__fmul_rn(out[0], c), __fmul_rn(rot, sn));
+}
+
+// The split path with one row per lane (batch-1 decode): attn_prep folded into the slice
+// score kernel. Every block makes its 4 q heads itself; the block whose slice holds the new
+// slot also makes the new K row, appends K and V to the cache and patches its own K fragments
+// for that slot (its global load may still hold the previous contents).
+__global__ void __launch_bounds__(64) attn_scores_prep(AttnArgs a) {
+    __shared__ uint16_t qb[16][256];
+    __shared__ uint16_t knew[256];
+    const int r = blockIdx.x, j = blockIdx.y, q = blockIdx.z;
+    const int slot = a.rm.slot[r];
+    if (q * 64 > slot) return;
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const int lrow = a.rm.lane[r], pos = a.rm.pos[r];
+    q35_u32x4 qf[8], kf[4][8];
+    load_k_slice(a, lrow, j, q, slot, kf);
+    const uint16_t* pr = a.proj + (size_t)r * kAttnInRows;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float o[4];
+        head_norm_rope_wave(a, pr + (4 * j + i) * 512, a.q_norm, pos, o);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int d = lane + 64 * w;
+            const uint16_t hi = f2bf(o[w]);
+            qb[i][d] = hi;
+            qb[4 + i][d] = f2bf(o[w] - bf2f(hi));
+            qb[8 + i][d] = 0;
+            qb[12 + i][d] = 0;
+        }
+    }
+    const bool own = q == (slot >> 6);
+    if (own) {
+        float o[4];
+        head_norm_rope_wave(a, pr + kAttnKOff + j * 256, a.k_norm, pos, o);
+        const size_t base = lrow * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int d = lane + 64 * w;
+            const uint16_t kb = f2bf(o[w]);
+            knew[d] = kb;
+            a.kc[base + kv_tiled_offset(slot, d)] = kb;
+            a.vc[base + (size_t)slot * 256 + d] = pr[kAttnVOff + j * 256 + d];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[s] = *(const q35_u32x4*)&qb[n][s * 32 + g * 8];
+    if (own && n == (slot & 15)) {
+        const int st = (slot >> 4) - q * 4;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            if (t == st) {
+#pragma unroll
+                for (int s = 0; s < 8; ++s) kf[t][s] = *(const q35_u32x4*)&knew[s * 32 + g * 8];
+            }
+    }
+    score_slice<false>(a, lrow, j, q, slot, qf, kf, 0, a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld, a.sc_ld,
+                       a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 8, (size_t)a.max_chunks * 8);
+}
+
 // P.V over one 128-slot part: thread (dg, tg) owns dims dg*8..+8 for slots tg*16..+16 of
 // the part (16-byte V loads, issued before the softmax bookkeeping); the 8 slot groups are
 // summed in order (pairs in a wave by a lane swap, then the 4 waves through LDS).
@@ -406,8 +488,16 @@ hipError_t attn_init() {
     return hipFuncSetAttribute((const void*)attn_fused, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
 }
 
+static size_t fused_lds(const AttnArgs& a) {
+    return (size_t)(4 * ((a.cap + 63) / 64 * 64) + 4 * 8 * a.max_chunks) * 4;
+}
+static bool use_fused(const AttnArgs& a) { return a.R >= 64 && fused_lds(a) <= 96 * 1024; }
+// one row per lane on the split path: the prep runs inside the slice score kernel
+static bool prep_in_scores(const AttnArgs& a) { return !use_fused(a) && a.T == 1; }
+
 hipError_t launch_attn_prep(const AttnArgs& a, hipStream_t st) {
     if (a.R <= 0 || a.max_chunks <= 0) return hipErrorInvalidValue;
+    if (prep_in_scores(a)) return hipSuccess;
     hipLaunchKernelGGL(attn_prep, dim3(a.R, kNq + kNkv), dim3(256), 0, st, a);
     return hipGetLastError();
 }
@@ -415,13 +505,16 @@ hipError_t launch_attn_prep(const AttnArgs& a, hipStream_t st) {
 hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
     if (a.R <= 0 || a.max_chunks <= 0) return hipErrorInvalidValue;
     const int lds_slots = (a.cap + 63) / 64 * 64;
-    const size_t lds = (size_t)(4 * lds_slots + 4 * 8 * a.max_chunks) * 4;
-    if (a.R >= 64 && lds <= 96 * 1024) {
+    const size_t lds = fused_lds(a);
+    if (use_fused(a)) {
         if (a.T < 1 || a.R % a.T) return hipErrorInvalidValue;
         const int pairs = a.R / a.T * kNkv;
         hipLaunchKernelGGL(attn_fused, dim3((pairs + 7) / 8 * a.T * 8), dim3(256), lds, st, a, lds_slots);
     } else {
-        hipLaunchKernelGGL(attn_scores, dim3(a.R, kNkv, a.max_chunks * 4), dim3(64), 0, st, a);
+        if (prep_in_scores(a))
+            hipLaunchKernelGGL(attn_scores_prep, dim3(a.R, kNkv, a.max_chunks * 4), dim3(64), 0, st, a);
+        else
+            hipLaunchKernelGGL(attn_scores, dim3(a.R, kNkv, a.max_chunks * 4), dim3(64), 0, st, a);
         hipLaunchKernelGGL(attn_pv, dim3(a.R, kNkv, a.max_chunks * 2), dim3(256), 0, st, a);
         hipLaunchKernelGGL(attn_combine, dim3(a.R, kNq), dim3(256), 0, st, a);
     }
