@@ -29,16 +29,16 @@ S_BYTES = 18 * 16 * 128 * 128 * 4
 WIN_BYTES = 18 * 3 * 6144 * 4
 KV_BYTES_PER_SLOT = 6 * 2 * 2 * 256 * 2   # K and V, 6 layers, 2 kv heads
 FAM = {"gemm": 1, "lm_head": 2, "gdn": 3, "attn": 4}
-KERNEL_NAMES = {"attn": "attn_fused", "gdn": "gdn_persist", "lm_head": "gemm_large_m<kEArgmax> (tied lm_head)",
+KERNEL_NAMES = {"attn": "attn_fused", "gdn": "gdn_persist", "lm_head": "gemm_lmhead<8, 2> (tied lm_head)",
                 "gemm": "projection / MLP GEMMs"}
 DOMINANT = "attn"           # largest share of the batch-256 step
 # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled by what
 # the same counter reads for a 1 GiB copy (FETCH x2.0, WRITE x1.0); the runs and the
 # calibration are in profiles/hbm_traffic_decode_b256_ctx4096.md.
 MEASURED_TRAFFIC = {
-    ("attn", 256, 4096): (1057562.5 * 2.0 + 1024.0 * 1.0) * 1024,                        # attn_fused
-    ("gdn", 256, 4096): (143107.0 * 2.0 + 283683.3 * 1.0) * 1024,                         # gdn_persist
-    ("lm_head", 256, 4096): (269641.3 * 2.0 + 31040.7 * 1.0) * 1024,                      # gemm_large_m<kEArgmax>
+    ("attn", 256, 4096): (1058422.4 * 2.0 + 1024.0 * 1.0) * 1024,                        # attn_fused
+    ("gdn", 256, 4096): (143107.0 * 2.0 + 283680.9 * 1.0) * 1024,                         # gdn_persist
+    ("lm_head", 256, 4096): (255558.8 * 2.0 + 38848.7 * 1.0) * 1024,                      # gemm_lmhead<8, 2>
 }
 
 

@@ -72,6 +72,34 @@ __device__ __forceinline__ q35_u32x4 produce_a(const GemmArgs& a, int m, int k0,
 
 __device__ __forceinline__ q35_bf16x8 as_bf(q35_u32x4 v) { return *(q35_bf16x8*)&v; }
 
+// (max, lowest index) over the 16 lanes of a DPP row; every lane ends with the result. The
+// combine is exact and commutative, so the pairing order (quad swaps, then the half-row and
+// row mirrors) gives the same winner as any other reduction order.
+__device__ __forceinline__ void argmax16_step(float& v, int& idx, int ctrl) {
+    float v2;
+    int i2;
+    if (ctrl == 0xB1) {
+        v2 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
+        i2 = __builtin_amdgcn_update_dpp(0, idx, 0xB1, 0xf, 0xf, false);
+    } else if (ctrl == 0x4E) {
+        v2 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
+        i2 = __builtin_amdgcn_update_dpp(0, idx, 0x4E, 0xf, 0xf, false);
+    } else if (ctrl == 0x141) {
+        v2 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
+        i2 = __builtin_amdgcn_update_dpp(0, idx, 0x141, 0xf, 0xf, false);
+    } else {
+        v2 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));
+        i2 = __builtin_amdgcn_update_dpp(0, idx, 0x140, 0xf, 0xf, false);
+    }
+    if (v2 > v || (v2 == v && i2 < idx)) { v = v2; idx = i2; }
+}
+__device__ __forceinline__ void argmax16(float& v, int& idx) {
+    argmax16_step(v, idx, 0xB1);    // quad_perm [1,0,3,2]
+    argmax16_step(v, idx, 0x4E);    // quad_perm [2,3,0,1]
+    argmax16_step(v, idx, 0x141);   // row_half_mirror: quad 0 <-> quad 1, 2 <-> 3
+    argmax16_step(v, idx, 0x140);   // row_mirror: half 0 <-> half 1
+}
+
 // Epilogue of one 16x16 tile: lane holds D[row0 + 4*(lane/16) + r][col0 + lane%16].
 template <int EM>
 __device__ __forceinline__ void epilogue(const GemmArgs& a, q35_f32x4 sum, int nt, int row0, int lane) {
@@ -101,19 +129,15 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, q35_f32x4 sum, int n
     } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            int row = row0 + 4 * g + r;
+            const int row = row0 + 4 * g + r;
             float v = rbf(sum[r]);
-            if (row < a.M && a.logits) a.logits[(size_t)row * a.ldl + col] = v;
+            // 32-bit element offsets (logits < 2^31 elements): no 64-bit products to keep live
+            if (row < a.M && a.logits) a.logits[(unsigned)(row * a.ldl + col)] = v;
             int idx = col;
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) {
-                float v2 = __shfl_xor(v, o, 64);
-                int i2 = __shfl_xor(idx, o, 64);
-                if (v2 > v || (v2 == v && i2 < idx)) { v = v2; idx = i2; }
-            }
+            argmax16(v, idx);
             if ((lane & 15) == 0 && row < a.M) {
-                a.part_val[(size_t)row * a.ldp + nt] = v;
-                a.part_idx[(size_t)row * a.ldp + nt] = idx;
+                a.part_val[(unsigned)(row * a.ldp + nt)] = v;
+                a.part_idx[(unsigned)(row * a.ldp + nt)] = idx;
             }
         }
     }
@@ -434,6 +458,143 @@ __global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
     for (int mt = 0; mt < MT; ++mt) epilogue<EM>(a, sum[mt], nt, row0 + mt * 16, lane);
 }
 
+// ---------------------------------------------------------------- tied lm_head, batched lanes
+// K = 1024 (the hidden size), argmax epilogue, M <= 512. Persistent blocks of NW waves,
+// about one per CU: a block stages its 64 A rows (64 x 1024 bf16 = 128 KiB) in LDS once, in
+// MFMA fragment order, and then walks a stream of column units; each wave computes a 64-row x
+// (16 NTW)-column tile per unit, so each A fragment read from LDS feeds NTW MFMAs and each
+// weight fragment feeds 4 (one per 16-row tile). The 8 NTW weight fragments of one k-block
+// live in a rolling register buffer: the slot of (column tile n, step s) is refilled with
+// the next k-block's (or the next unit's first k-block's) fragment right after its last
+// use, so the weight stream stays one k-block ahead of the MFMAs without a second buffer.
+// Used as <8, 2>: two waves per SIMD hide the weight-stream latency (275 us for M = 256 on
+// MI355X against 400 us for the 64 x 256 tiled kernel, whose waves each re-read the whole A
+// tile from LDS; <4, 4> at one wave per SIMD: 420 us). The row blocks of one column stream
+// sit on one XCD and share each weight unit through its L2.
+// Reduction order = the canonical one above (chain per k-block from zero, summed in order).
+int g_lmhead_persist = 1;
+void set_lmhead_persist(int on) { g_lmhead_persist = on; }
+constexpr int kLmKB = kHidden / 256;
+constexpr int kLmLds = 4 * kLmKB * 8 * 64 * 16;          // 128 KiB of A fragments
+
+template <int NW, int NTW>
+__global__ void __launch_bounds__(64 * NW) gemm_lmhead(GemmArgs a, int mb) {
+    extern __shared__ q35_u32x4 dyn_lds[];
+    q35_u32x4(*As)[kLmKB * 8][64] = (q35_u32x4(*)[kLmKB * 8][64])dyn_lds;   // [mt][kb*8+s][slot]
+    constexpr int NT = 64 * NW;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar addressing
+    // blocks b, b + 8, ... run on XCD b % 8; the mb row blocks of one column stream take
+    // consecutive slots there, so a weight unit is fetched from HBM once per XCD
+    const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
+    const int rb = k % mb;
+    const int streams = gridDim.x / mb;                      // a multiple of 8
+    const int stream = (k / mb) * 8 + xcd;
+    const int row0 = rb * 64;
+    const int nunits = a.N / (16 * NTW);                     // wave units of NTW column tiles
+    const int ustride = streams * NW;
+    int u = stream * NW + wv;
+
+    // weight fragment (unit, column tile n, k-block, step s): one lane-contiguous KiB, read
+    // with buffer loads -- scalar resource + uniform scalar byte offset + the lane's 16-byte
+    // offset, so no 64-bit address is held per fragment (the weight matrix is < 4 GiB)
+    const __amdgpu_buffer_rsrc_t wres =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.W, 0, (int)((size_t)a.N * kHidden * 2), 0x00020000);
+    const int voff = lane * 16;
+    auto wload = [&](int unit, int n, int kb, int s) {
+        const int so = (((unit * NTW + n) * kLmKB + kb) * 512 + s * 64) * 16;
+        // cached: the other row blocks of this column stream on the XCD re-read it from L2
+        q35_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(wres, voff, so, 0);
+        return *(q35_bf16x8*)&v;
+    };
+    const int u0 = min(u, nunits - 1);
+    q35_bf16x8 wf[NTW][8];
+#pragma unroll
+    for (int n = 0; n < NTW; ++n)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) wf[n][s] = wload(u0, n, 0, s);
+
+    // stage A: chunk c = row * 32 + kk of a k-block (8 elements each); zero rows beyond M
+#pragma unroll
+    for (int kb = 0; kb < kLmKB; ++kb) {
+        constexpr int CPT = 2048 / NT;
+        q35_u32x4 v[CPT];
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * NT;
+            const int row = c >> 5, kk = c & 31;
+            const int m = min(row0 + row, a.M - 1);
+            v[i] = *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + kb * 256 + kk * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + i * NT;
+            const int row = c >> 5, kk = c & 31;
+            const q35_u32x4 z = {0u, 0u, 0u, 0u};
+            As[row >> 4][kb * 8 + (kk & 7)][lds_swz(kk & 7, kk >> 3, row & 15)] = row0 + row < a.M ? v[i] : z;
+        }
+        __builtin_amdgcn_sched_barrier(0);     // one k-block of staging registers at a time
+    }
+    __syncthreads();
+
+    int sw[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) sw[s] = lds_swz(s, lane >> 4, lane & 15);
+    for (; u < nunits; u += ustride) {
+        const int un = min(u + ustride, nunits - 1);         // next unit (clamped: a reload)
+        q35_f32x4 sum[4][NTW];
+        q35_u32x4 af[4], an[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) an[mt] = As[mt][0][sw[0]];
+#pragma unroll
+        for (int kb = 0; kb < kLmKB; ++kb) {
+            q35_f32x4 c[4][NTW];
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) af[mt] = an[mt];
+                // the next step's A fragments are read while this step's MFMAs run
+                const int kn = s < 7 ? kb : kb + 1, sn = (s + 1) & 7;
+                if (kn < kLmKB) {
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) an[mt] = As[mt][kn * 8 + sn][sw[sn]];
+                }
+                __builtin_amdgcn_sched_barrier(0);   // those reads go out before the MFMAs
+#pragma unroll
+                for (int n = 0; n < NTW; ++n) {
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt)
+                        c[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            as_bf(af[mt]), wf[n][s], s == 0 ? (q35_f32x4){0.f, 0.f, 0.f, 0.f} : c[mt][n], 0, 0, 0);
+                    wf[n][s] = kb + 1 < kLmKB ? wload(u, n, kb + 1, s) : wload(un, n, 0, s);
+                }
+                // keep the refills where they are issued (the scheduler would otherwise sink
+                // them next to their use a k-block later and wait on each)
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int n = 0; n < NTW; ++n) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sum[mt][n][r] = kb == 0 ? c[mt][n][r] : sum[mt][n][r] + c[mt][n][r];
+                    asm volatile("" : "+a"(sum[mt][n]));   // running sums wait in AGPRs: the
+                }                                           // VGPRs hold the weight stream
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int n = 0; n < NTW; ++n) {
+                // opaque per unit, so the row offsets are not hoisted out of the unit loop
+                // (kept live across it they would spill, and a spill reload drains the stream)
+                int r0 = row0 + mt * 16;
+                asm volatile("" : "+s"(r0));
+                epilogue<kEArgmax>(a, sum[mt][n], u * NTW + n, r0, lane);
+                __builtin_amdgcn_sched_barrier(0);   // one tile's temporaries at a time
+            }
+    }
+}
+
 // Final argmax over the per-tile partials of each row: lowest id among the maxima.
 __global__ void __launch_bounds__(1024) argmax_rows(const float* pv, const int* pi, int ldp, int n,
                                                     int* out_tok, float* out_val) {
@@ -479,6 +640,20 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
     const int gz = EM == kEPartial ? KB : 1;
     // 64-row tiles: more blocks in flight (W tiles are re-read from L2 by the M tiles)
     const int nb = EM == kESiluMul ? (a.N / 32 + 1) / 2 : (a.N / 16 + 3) / 4, mb = (a.M + 63) / 64;
+    const int mbk = (a.M + 63) / 64;
+    if (EM == kEArgmax && a.K == kHidden && a.N % 64 == 0 && mbk <= 8 && g_lmhead_persist) {
+        // persistent blocks with A resident in LDS: mbk row blocks x (256 / mbk) column
+        // streams, one block per CU (the 128 KiB of A fragments allow no second)
+        const int streams = max(8, 256 / mbk / 8 * 8);
+        if (g_lmhead_persist == 2)
+            hipLaunchKernelGGL((gemm_lmhead<4, 4>), dim3(mbk * streams), dim3(256), kLmLds, st, a, mbk);
+        else if (g_lmhead_persist == 3)
+            hipLaunchKernelGGL((gemm_lmhead<16, 1>), dim3(mbk * streams), dim3(1024), kLmLds, st, a, mbk);
+
+        else
+            hipLaunchKernelGGL((gemm_lmhead<8, 2>), dim3(mbk * streams), dim3(512), kLmLds, st, a, mbk);
+        return;
+    }
     if (EM == kEArgmax) {
         // tied lm_head (N = 248,320): 16 waves x 16 columns share each staged A tile, so the
         // A rows are re-read from L2 by 4x fewer blocks (measured best of 64x64, 128x128, 64x256)
@@ -528,6 +703,8 @@ hipError_t gemm_init() {
     Q35_ATTR(kAGatedNorm, kEStore) Q35_ATTR(kAGatedNorm, kEPartial) Q35_ATTR(kAGatedNorm, kEResidual)
     Q35_ATTR(kANormX, kEStore) Q35_ATTR(kANormX, kEArgmax)
 #undef Q35_ATTR
+    if (hipFuncSetAttribute((const void*)gemm_lmhead<8, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, kLmLds) != hipSuccess)
+        return hipGetLastError();
     return hipSuccess;
 }
 

@@ -80,6 +80,28 @@ def test_config1_lm_head_argmax(eng, oracle_weights):
     assert (lg[:16].double() - ref).abs().max().item() < 0.06
 
 
+@pytest.mark.parametrize("M", [17, 100, 250, 256])
+def test_lm_head_persistent_equals_tiled(eng, M):
+    """The persistent lm_head kernel (A resident in LDS, 64 x 32 wave tiles) and the 64 x 256
+    tiled kernel follow the same reduction order: identical logits and tokens, including a
+    ragged last row block (M = 17, 100, 250)."""
+    import torch
+    print(f"lm_head persistent vs tiled M={M}", flush=True)
+    g = torch.Generator().manual_seed(M)
+    X = torch.randn(M, 1024, generator=g).to(torch.bfloat16).cuda()
+    out = {}
+    for p in (0, 1):
+        eng.set_option("lmhead_persist", p)
+        tok = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+        lg = torch.full((M, 248320), float("nan"), dtype=torch.float32, device="cuda")
+        eng.op_lm_head_argmax(X.data_ptr(), M, tok.data_ptr(), lg.data_ptr())
+        eng.sync()
+        out[p] = (tok.cpu(), lg.cpu())
+    eng.set_option("lmhead_persist", 1)
+    assert torch.equal(out[0][0], out[1][0])
+    assert torch.equal(out[0][1], out[1][1])
+
+
 @pytest.mark.parametrize("B", [1, 64, 1024])
 def test_config2_gdn_step(eng, oracle_weights, B):
     import torch
