@@ -1081,6 +1081,11 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
         } else if (n == "gdn_chunked") {
             HCK(hipStreamSynchronize(e->st));
             e->gdn_chunked = value ? 1 : 0;
+        } else if (n == "gemm_pre") {            // process-wide kernel choice; drops captured steps
+            HCK(hipStreamSynchronize(e->st));
+            set_gemm_pre(value ? 1 : 0);
+            for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
+            e->graphs.clear();
         } else if (n == "lmhead_persist") {      // process-wide kernel choice; drops captured steps
             HCK(hipStreamSynchronize(e->st));
             set_lmhead_persist(value ? 1 : 0);

@@ -16,6 +16,8 @@
 // Kernels (all follow the order above):
 //   gemm_small_m   one 16-row tile; wave w of a block owns k-block w (M <= 16, batch 1);
 //                  with a producer the wave builds its A tile cooperatively in LDS
+//   gemm_pre       K = 1024 at M > 16: 32-row blocks, every load issued up front (A by LDS-DMA)
+//   gemm_lmhead    tied lm_head at 16 < M <= 512: persistent, A resident in LDS
 //   gemm_large_m   4 waves x 16 columns, 64 rows per block; the A tile of each k-block is
 //                  staged once in LDS in MFMA fragment order, the next k-block's loads in
 //                  flight meanwhile (batched lanes);
@@ -458,6 +460,147 @@ __global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
     for (int mt = 0; mt < MT; ++mt) epilogue<EM>(a, sum[mt], nt, row0 + mt * 16, lane);
 }
 
+// ---------------------------------------------------------------- K = 1024, batched lanes
+// Same column tiles, block order and epilogues as gemm_large_m<EM, MT, 4>, for K = 1024 (the
+// hidden size: every input projection and gate|up), used with MT = 2 (32-row blocks). All of
+// a block's loads are issued before its first MFMA: per k-block, the A fragments go straight
+// into LDS with global_load_lds (layout below) and each wave's 8 weight fragments into
+// registers. The k-blocks are then consumed in order, each after an explicit wait for its own
+// loads (the vector-memory counter completes in order) and a raw barrier: one L2/HBM round
+// trip per block instead of one per k-block. The LDS fragment reads and the weight loads are
+// inline asm, so the compiler's wait insertion (which cannot order LDS-DMA against other
+// loads) adds no wait for all loads; every wait is explicit and tied to the registers it
+// guards. At 256 lanes: gate|up 17.1 us (pipelined kernel 18.2), attention qkv 11.9 (14.8).
+constexpr int kPreKB = kHidden / 256;
+int g_gemm_pre = 1;
+void set_gemm_pre(int on) { g_gemm_pre = on; }
+
+template <int MT> constexpr int pre_lds_bytes() { return kPreKB * MT * 8 * 64 * 16; }
+
+template <int EM, int MT>
+__global__ void __launch_bounds__(256) gemm_pre(GemmArgs a) {
+    extern __shared__ q35_u32x4 dyn_lds[];
+    q35_u32x4(*As)[MT][512] = (q35_u32x4(*)[MT][512])dyn_lds;          // [kb][mt][group * 64 + slot]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    constexpr int NW = 4, HW = 2;
+    const int mb = (a.M + MT * 16 - 1) / (MT * 16);
+    const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
+    const int nblk = (idx / mb) * 8 + xcd;
+    const int half = a.N / 32;
+    const int jg = nblk * HW + (wv % HW);
+    if (EM == kESiluMul ? nblk * HW >= half : nblk * NW >= a.N / 16) return;   // whole block
+    const int nt = EM == kESiluMul ? (wv < HW ? jg : half + jg) : nblk * NW + wv;
+    const bool nvalid = EM == kESiluMul ? jg < half : nt < a.N / 16;
+    const int ntc = nvalid ? nt : 0;          // invalid waves load a valid tile and store nothing
+    const int row0 = (idx % mb) * MT * 16;
+
+    // LDS layout per (k-block, m-tile): 8 KiB groups (g, h) = (k-group, row half), slot
+    // row_lo * 8 + (s ^ row_lo) of a group holds A[row h*8 + row_lo][k-group g, step s]. One
+    // DMA instruction fills one group: lane j = row_lo * 8 + sx reads chunk s = sx ^ row_lo of
+    // its row, so the 64 lanes read 8 whole 128-byte lines; the XOR spreads the MFMA reads
+    // (fixed s, rows row_lo = 0..7) over distinct bank groups.
+    const int g = lane >> 4;
+    const int jrow = lane >> 3, jchunk = (lane & 7) ^ (lane >> 3);
+    // weight tile base (wave-uniform, scalar registers) and the lane's byte offset
+    const uint16_t* wbase = a.W + (size_t)ntc * kPreKB * 4096;
+    const unsigned wvoff = lane * 16;
+    q35_u32x4 wf[kPreKB][8];
+    constexpr int GPW = MT * 8 / NW;          // (mt, g, h) groups per wave per k-block
+#pragma unroll
+    for (int kb = 0; kb < kPreKB; ++kb) {
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) {
+            const int grp = wv * GPW + i, mt = grp >> 3, gg = (grp >> 1) & 3, h = grp & 1;
+            const int m = min(row0 + mt * 16 + h * 8 + jrow, a.M - 1);   // rows >= M feed rows >= M only
+            __builtin_amdgcn_global_load_lds(
+                (const void*)((const uint16_t*)a.X + (size_t)m * a.ldx + kb * 256 + gg * 64 + jchunk * 8),
+                (__attribute__((address_space(3))) void*)&As[kb][mt][(gg * 2 + h) * 64], 16, 0, 0);
+        }
+        // weight fragments through inline asm as well (with LDS-DMA and ordinary loads both
+        // pending the compiler treats the counter as out of order and waits for zero); cached
+        // loads: the other row blocks of this column block re-read the tile from L2
+        const uint16_t* wk0 = wbase + kb * 4096;
+        const uint16_t* wk1 = wk0 + 2048;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "=v"(wf[kb][s]) : "v"(wvoff), "s"(wk0), "n"(s * 1024) : "memory");
+#pragma unroll
+        for (int s = 4; s < 8; ++s)
+            asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "=v"(wf[kb][s]) : "v"(wvoff), "s"(wk1), "n"((s - 4) * 1024) : "memory");
+        __builtin_amdgcn_sched_barrier(0);     // issue order = k-block order (the waits below count it)
+    }
+    // LDS byte offsets of this lane's fragment (row r16 = lane & 15, k-group g) at each step s
+    unsigned soff[8];
+    {
+        const int r16 = lane & 15, h = r16 >> 3, rl = r16 & 7;
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            soff[s] = (unsigned)(size_t)(__attribute__((address_space(3))) const void*)&As[0][0][(g * 2 + h) * 64 + rl * 8 + (s ^ rl)];
+    }
+    q35_f32x4 sum[MT];
+#pragma unroll
+    for (int kb = 0; kb < kPreKB; ++kb) {
+        // this k-block's loads are the oldest (GPW + 8) * (kPreKB - kb) still counted
+        // (tied to this k-block's weight registers, so no use of them moves above the wait)
+#define Q35_PRE_WAIT(N)                                                                          \
+    asm volatile("s_waitcnt vmcnt(%8)"                                                          \
+                 : "+v"(wf[kb][0]), "+v"(wf[kb][1]), "+v"(wf[kb][2]), "+v"(wf[kb][3]),           \
+                   "+v"(wf[kb][4]), "+v"(wf[kb][5]), "+v"(wf[kb][6]), "+v"(wf[kb][7])            \
+                 : "n"(N) : "memory")
+        if (kb == 0) Q35_PRE_WAIT((GPW + 8) * 3);
+        if (kb == 1) Q35_PRE_WAIT((GPW + 8) * 2);
+        if (kb == 2) Q35_PRE_WAIT(GPW + 8);
+        if (kb == 3) Q35_PRE_WAIT(0);
+#undef Q35_PRE_WAIT
+        __builtin_amdgcn_s_barrier();          // every wave's share of the A groups has landed
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            // the fragment reads are inline asm: the compiler cannot tell which LDS-DMA they
+            // depend on and would otherwise wait for every outstanding load (vmcnt(0)) first
+            q35_u32x4 af[8];
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+                asm volatile("ds_read_b128 %0, %1" : "=v"(af[s]) : "v"(soff[s] + (unsigned)((kb * MT + mt) * 8192)) : "memory");
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(af[0]), "+v"(af[1]), "+v"(af[2]), "+v"(af[3]), "+v"(af[4]), "+v"(af[5]), "+v"(af[6]), "+v"(af[7]));
+            q35_f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(af[s]), as_bf(wf[kb][s]), c, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sum[mt][r] = kb == 0 ? c[r] : sum[mt][r] + c[r];
+        }
+    }
+    if (EM == kESiluMul) {
+        // up waves hand bf16(u) to the gate waves through LDS (after every wave's last read)
+        float* ub = (float*)dyn_lds;                             // [HW][MT][4][64]
+        __syncthreads();
+        if (wv >= HW && nvalid) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ub[(((wv - HW) * MT + mt) * 4 + r) * 64 + lane] = rbf(sum[mt][r]);
+        }
+        __syncthreads();
+        if (wv >= HW || !nvalid) return;
+        const int col = jg * 16 + (lane & 15);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = row0 + mt * 16 + 4 * g + r;
+                const float u = ub[((wv * MT + mt) * 4 + r) * 64 + lane];
+                if (row < a.M) a.Y[(size_t)row * a.ldy + col] = f2bf(__fmul_rn(rbf(silu_f(rbf(sum[mt][r]))), u));
+            }
+        return;
+    }
+    if (!nvalid) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) epilogue<EM>(a, sum[mt], nt, row0 + mt * 16, lane);
+}
+
 // ---------------------------------------------------------------- tied lm_head, batched lanes
 // K = 1024 (the hidden size), argmax epilogue, M <= 512. Persistent blocks of NW waves,
 // about one per CU: a block stages its 64 A rows (64 x 1024 bf16 = 128 KiB) in LDS once, in
@@ -645,13 +788,7 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
         // persistent blocks with A resident in LDS: mbk row blocks x (256 / mbk) column
         // streams, one block per CU (the 128 KiB of A fragments allow no second)
         const int streams = max(8, 256 / mbk / 8 * 8);
-        if (g_lmhead_persist == 2)
-            hipLaunchKernelGGL((gemm_lmhead<4, 4>), dim3(mbk * streams), dim3(256), kLmLds, st, a, mbk);
-        else if (g_lmhead_persist == 3)
-            hipLaunchKernelGGL((gemm_lmhead<16, 1>), dim3(mbk * streams), dim3(1024), kLmLds, st, a, mbk);
-
-        else
-            hipLaunchKernelGGL((gemm_lmhead<8, 2>), dim3(mbk * streams), dim3(512), kLmLds, st, a, mbk);
+        hipLaunchKernelGGL((gemm_lmhead<8, 2>), dim3(mbk * streams), dim3(512), kLmLds, st, a, mbk);
         return;
     }
     if (EM == kEArgmax) {
@@ -659,6 +796,13 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
         // A rows are re-read from L2 by 4x fewer blocks (measured best of 64x64, 128x128, 64x256)
         const int nb16 = (a.N / 16 + 15) / 16;
         hipLaunchKernelGGL((gemm_large_m<EM, 4, 16>), dim3((nb16 + 7) / 8 * 8 * mb, 1, gz), dim3(1024), 0, st, a);
+        return;
+    }
+    if ((EM == kEStore || EM == kESiluMul) && a.K == kHidden && g_gemm_pre) {
+        // 32-row blocks (64 KiB of A fragments: two blocks per CU); 64-row blocks (128 KiB,
+        // one per CU) measured 10-35 % slower
+        const int mb2 = (a.M + 31) / 32;
+        hipLaunchKernelGGL((gemm_pre<EM, 2>), dim3((nb + 7) / 8 * 8 * mb2), dim3(256), pre_lds_bytes<2>(), st, a);
         return;
     }
     hipLaunchKernelGGL((gemm_large_m<EM, 4, 4>), dim3((nb + 7) / 8 * 8 * mb, 1, gz), dim3(256), 0, st, a);
@@ -703,7 +847,9 @@ hipError_t gemm_init() {
     Q35_ATTR(kAGatedNorm, kEStore) Q35_ATTR(kAGatedNorm, kEPartial) Q35_ATTR(kAGatedNorm, kEResidual)
     Q35_ATTR(kANormX, kEStore) Q35_ATTR(kANormX, kEArgmax)
 #undef Q35_ATTR
-    if (hipFuncSetAttribute((const void*)gemm_lmhead<8, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, kLmLds) != hipSuccess)
+    if (hipFuncSetAttribute((const void*)gemm_lmhead<8, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, kLmLds) != hipSuccess ||
+        hipFuncSetAttribute((const void*)gemm_pre<kEStore, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<2>()) != hipSuccess ||
+        hipFuncSetAttribute((const void*)gemm_pre<kESiluMul, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<2>()) != hipSuccess)
         return hipGetLastError();
     return hipSuccess;
 }

@@ -33,6 +33,7 @@ struct GemmArgs {
 };
 // One-time kernel attribute setup (dynamic LDS above 64 KiB for the batch-1 producers).
 hipError_t gemm_init();
+void set_gemm_pre(int on);         // batched K = 1024 GEMMs: all loads up front (1) or k-block pipelined (0)
 void set_lmhead_persist(int on);   // tied lm_head at batched lanes: persistent kernel (1) or 64 x 256 tiles (0)
 hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st);
 hipError_t launch_argmax(const float* pv, const int* pi, int ldp, int n, int rows, int* tok,

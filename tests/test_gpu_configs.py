@@ -102,6 +102,31 @@ def test_lm_head_persistent_equals_tiled(eng, M):
     assert torch.equal(out[0][1], out[1][1])
 
 
+
+@pytest.mark.parametrize("N", [1024, 5120, 7168, 8704])
+def test_k1024_gemm_forms_identical(eng, N):
+    """Batched K = 1024 projections: the all-loads-up-front kernel (32-row blocks, A fragments
+    DMA'd into LDS) and the k-block pipelined kernel give identical bits, for ragged (M = 17,
+    200) and full (M = 256) row counts."""
+    import torch
+    print(f"k1024 gemm forms N={N}", flush=True)
+    g = torch.Generator().manual_seed(N)
+    W = (torch.randn(N, 1024, generator=g) * 0.02).to(torch.bfloat16).cuda()
+    Wt = torch.empty_like(W)
+    eng.op_tile_weight(W.data_ptr(), N, 1024, Wt.data_ptr())
+    for M in (17, 200, 256):
+        X = torch.randn(M, 1024, generator=g).to(torch.bfloat16).cuda()
+        out = {}
+        for p in (0, 1):
+            eng.set_option("gemm_pre", p)
+            Y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+            eng.op_gemm(Wt.data_ptr(), N, 1024, X.data_ptr(), M, Y.data_ptr())
+            eng.sync()
+            out[p] = Y.cpu()
+        eng.set_option("gemm_pre", 1)
+        assert not torch.isnan(out[0].float()).any()
+        assert torch.equal(out[0], out[1]), M
+
 @pytest.mark.parametrize("B", [1, 64, 1024])
 def test_config2_gdn_step(eng, oracle_weights, B):
     import torch
