@@ -103,6 +103,7 @@ struct q35_engine {
     int n_layers = kLayers;          // diagnostic: run only the first n layers of a body
     int kprof = 0;                   // kernel family timed with HIP events (0 = off)
     int gdn_chunked = 1;             // prompt waves of one lane use the chunked GDN form
+    int b1_partials = 1;             // one-row bodies: 1024-wide GEMVs leave k-block chains
     float *gchunk = nullptr, *gcdec = nullptr;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> kev;
     size_t kev_used = 0;
@@ -395,10 +396,58 @@ void gemm(q35_engine* e, const uint16_t* W, int N, int K, int M, const void* X, 
 // RMSNorm in the consuming GEMM's A operand, so no add+norm launches remain.
 inline bool small_rows(int R) { return R <= 16; }
 
+// One-row bodies (a batch-1 decode step, a one-token prompt): the 1024-wide GEMVs (out_proj,
+// o_proj, down) run one wave per (column tile, k-block) and leave their k-block chains in
+// e->kpart (8x or 14x the blocks of the residual-epilogue form, whose 64 blocks use a quarter
+// of the CUs); the next norm GEMM folds them into the residual row (kANormXP) and writes the
+// new row to the other buffer of a pair; the final add+norm folds the last layer's chains.
+inline bool b1_partials(const q35_engine* e, int R, int T, bool ckpt) {
+    return e->b1_partials && R == 1 && T == 1 && !ckpt;
+}
+struct B1Res {
+    uint16_t* cur;     // residual row as of the last fold
+    uint16_t* alt;     // receives the next fold
+    int pend = 0;      // k-block chains pending in e->kpart
+};
+
+// RMSNorm GEMM of the residual row: folds pending chains first (one-row bodies).
+void norm_gemm(q35_engine* e, B1Res* rr, const uint16_t* W, int N, int R, uint16_t* Y, int ldy,
+               const uint16_t* normw) {
+    if (!rr) {
+        gemm(e, W, N, kHidden, R, e->x, kHidden, Y, ldy, kANormX, nullptr, 0, normw);
+        return;
+    }
+    GemmArgs a{};
+    a.W = W; a.N = N; a.K = kHidden; a.M = 1; a.X = rr->cur; a.ldx = kHidden;
+    a.aux_w = normw; a.Y = Y; a.ldy = ldy;
+    int amode = kANormX;
+    if (rr->pend) {
+        amode = kANormXP;
+        a.kpart = e->kpart; a.kpb = rr->pend; a.xres = rr->alt;
+        std::swap(rr->cur, rr->alt);
+        rr->pend = 0;
+    }
+    KTimer kt(e, kFamGemm);
+    HCK(launch_gemm(a, amode, kEStore, e->st));
+}
+
+// A 1024-wide output projection feeding the residual: epilogue add (<= 16 rows), k-block
+// chains for the next fold (one-row bodies) or chains for the add+norm kernel (batched).
+void resid_gemm(q35_engine* e, B1Res* rr, const uint16_t* W, int K, int R, const void* X, int ldx,
+                int amode = kAPlain, const void* X2 = nullptr, int ldx2 = 0, const uint16_t* aux = nullptr) {
+    if (rr) {
+        REQ(rr->pend == 0, Q35_ERR_STATE, "unfolded k-block chains");
+        gemm(e, W, kHidden, K, R, X, ldx, nullptr, 0, amode, X2, ldx2, aux, kEPartial);
+        rr->pend = K / 256;
+    } else {
+        gemm(e, W, kHidden, K, R, X, ldx, nullptr, 0, amode, X2, ldx2, aux, small_rows(R) ? kEResidual : -1, e->x);
+    }
+}
+
 void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16_t* vc,
-                     long long kv_lane, long long layer_off, int cap, int T = 1) {
+                     long long kv_lane, long long layer_off, int cap, int T = 1, B1Res* rr = nullptr) {
     if (small_rows(R))
-        gemm(e, w.W_in, kAttnInRows, kHidden, R, e->x, kHidden, e->proj, kAttnInRows, kANormX, nullptr, 0, w.norm_in);
+        norm_gemm(e, rr, w.W_in, kAttnInRows, R, e->proj, kAttnInRows, w.norm_in);
     else
         gemm(e, w.W_in, kAttnInRows, kHidden, R, e->h, kHidden, e->proj, kAttnInRows);
     AttnArgs a{};
@@ -414,18 +463,14 @@ void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16
         KTimer kt(e, kFamAttn);      // the attention core alone (scores, softmax, P.V, gate)
         HCK(launch_attn_core(a, e->st));
     }
-    if (small_rows(R))
-        gemm(e, w.W_out, kHidden, 2048, R, e->aout, 2048, nullptr, 0, kAPlain, nullptr, 0, nullptr, kEResidual, e->x);
-    else
-        gemm(e, w.W_out, kHidden, 2048, R, e->aout, 2048, nullptr, 0);
+    resid_gemm(e, rr, w.W_out, 2048, R, e->aout, 2048);
 }
 
 // MLP sub-block; on the batched path it leaves chains that `finish_norm` folds in.
-void mlp_layer(q35_engine* e, const LayerW& w, int R) {
+void mlp_layer(q35_engine* e, const LayerW& w, int R, B1Res* rr = nullptr) {
     if (small_rows(R)) {
-        gemm(e, w.W_gu, kGuRows, kHidden, R, e->x, kHidden, e->gu, kGuRows, kANormX, nullptr, 0, w.norm_post);
-        gemm(e, w.W_down, kHidden, kFF, R, e->gu, kGuRows, nullptr, 0, kASiluMul, e->gu + kFF, kGuRows,
-             nullptr, kEResidual, e->x);
+        norm_gemm(e, rr, w.W_gu, kGuRows, R, e->gu, kGuRows, w.norm_post);
+        resid_gemm(e, rr, w.W_down, kFF, R, e->gu, kGuRows, kASiluMul, e->gu + kFF, kGuRows);
         return;
     }
     HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, 2048 / 256, w.norm_post, e->h, R, e->st));
@@ -457,13 +502,15 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
     const int nl = R / T;
     const int cs = nl <= 8 ? 8 : nl <= 32 ? 4 : nl <= 64 ? 2 : 1;
     const bool small = small_rows(R);
+    B1Res res{e->x, e->h};          // e->h is unused by small bodies
+    B1Res* rr = b1_partials(e, R, T, ckpt) ? &res : nullptr;
     HCK(launch_addnorm(0, e->tok_dev, e->E, e->x, nullptr, nullptr, 0, e->L[0].norm_in, small ? nullptr : e->h,
                        R, e->st));
     for (int l = 0; l < e->n_layers; ++l) {
         const LayerW& w = e->L[l];
         if (!is_attn_layer(l)) {
             if (small)
-                gemm(e, w.W_in, kGdnInRows, kHidden, R, e->x, kHidden, e->proj, kGdnInRows, kANormX, nullptr, 0, w.norm_in);
+                norm_gemm(e, rr, w.W_in, kGdnInRows, R, e->proj, kGdnInRows, w.norm_in);
             else
                 gemm(e, w.W_in, kGdnInRows, kHidden, R, e->h, kHidden, e->proj, kGdnInRows);
             GdnArgs g{};
@@ -488,17 +535,19 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
             if (fused_norm)
                 gemm(e, w.W_out, kHidden, 2048, R, e->prod, 2048, nullptr, 0);
             else
-                gemm(e, w.W_out, kHidden, 2048, R, e->o, 2048, nullptr, 0, kAGatedNorm,
-                     e->proj + kGdnZOff, kGdnInRows, w.gnorm, small ? kEResidual : -1, e->x);
+                resid_gemm(e, rr, w.W_out, 2048, R, e->o, 2048, kAGatedNorm, e->proj + kGdnZOff, kGdnInRows, w.gnorm);
         } else {
             attention_layer(e, w, R, s->kc, s->vc, s->kv_lane(),
-                            (long long)attn_slot(l) * 2 * s->capT * 256, s->capT, T);
+                            (long long)attn_slot(l) * 2 * s->capT * 256, s->capT, T, rr);
         }
-        mlp_layer(e, w, R);
+        mlp_layer(e, w, R, rr);
         const bool lastl = l + 1 == e->n_layers;
         const uint16_t* nw = lastl ? e->final_norm : e->L[l + 1].norm_in;
         finish_norm(e, R, nw, lastl ? e->nrm : e->h);
     }
+    // one-row body: the last layer's chains and the final norm in one add+norm launch; the
+    // normed row is in e->nrm, so the caller's lm_head takes no norm weight
+    if (rr) HCK(launch_addnorm(3, nullptr, nullptr, rr->cur, nullptr, e->kpart, rr->pend, e->final_norm, e->nrm, 1, e->st));
 }
 
 // lm_head + argmax over rows [row0, row0 + M); tokens into e->tok_dev[0..M). After a
@@ -854,7 +903,8 @@ int q35_prefill(q35_engine* e, q35_state* s, int lane, const int32_t* ids, int n
             s->cur[lane] = (s->cur[lane] + 1) % s->nslots;
             done += T;
             if (done == n) {
-                lm_head(e, T - 1, 1, logits != nullptr, small_rows(T) ? e->final_norm : nullptr);
+                lm_head(e, T - 1, 1, logits != nullptr,
+                        small_rows(T) && !b1_partials(e, T, T, false) ? e->final_norm : nullptr);
                 save_hlast(e, s, {T - 1}, {lane});
             }
         }
@@ -887,7 +937,8 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
         upload_cur(e, s);
         auto step = [&] {
             body_kernels(e, s, n, 1, false);
-            lm_head(e, 0, n, out_logits != nullptr, small_rows(n) ? e->final_norm : nullptr);
+            lm_head(e, 0, n, out_logits != nullptr,
+                    small_rows(n) && !b1_partials(e, n, 1, false) ? e->final_norm : nullptr);
             HCK(launch_copy_rows(e->nrm, e->ridx_src, s->hlast, e->ridx_dst, n, kHidden, e->st));
         };
         if (e->use_graph && e->kprof == 0) {
@@ -1084,6 +1135,11 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
         } else if (n == "gemm_pre") {            // process-wide kernel choice; drops captured steps
             HCK(hipStreamSynchronize(e->st));
             set_gemm_pre(value ? 1 : 0);
+            for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
+            e->graphs.clear();
+        } else if (n == "b1_partials") {         // drops captured steps
+            HCK(hipStreamSynchronize(e->st));
+            e->b1_partials = value ? 1 : 0;
             for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
             e->graphs.clear();
         } else if (n == "lmhead_persist") {      // process-wide kernel choice; drops captured steps

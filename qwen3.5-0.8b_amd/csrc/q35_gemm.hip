@@ -32,6 +32,9 @@
 //   kAGatedNorm y = bf16(w * (o * rsqrt(mean_head(o^2)+eps)) * silu(z)), per 128-wide
 //               head, o f32, z bf16                    (specimpl.py:142-147, 304-305)
 //   kANormX     h = rmsnorm_zc(x) of the residual row (specimpl.py:135-139), batch-1 only
+//   kANormXP    one row: x' = bf16(x + bf16(sum of the producing GEMM's k-block chains in
+//               k-block order)) -- the residual add of specimpl.py:445-448 -- then h =
+//               rmsnorm_zc(x'); block 0 writes x' to xres (the next residual row)
 // Epilogues: kEStore (bf16 rows), kEPartial (one f32 k-block chain), kEResidual (batch-1:
 // x <- bf16(x + bf16(sum)), the residual add of specimpl.py:445-448) and kEArgmax
 // (bf16-rounded logits, per-tile max with the lowest index, optional f32 logits copy).
@@ -50,6 +53,8 @@ __device__ __forceinline__ q35_u32x4 produce_a(const GemmArgs& a, int m, int k0,
         q35_u32x4 g = *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + k0);
         q35_u32x4 u = *(const q35_u32x4*)((const uint16_t*)a.X2 + (size_t)m * a.ldx2 + k0);
         return silu_mul8(g, u);
+    } else if (AM == kANormXP) {          // one row only: produced in the direct path
+        return (q35_u32x4){0u, 0u, 0u, 0u};
     } else if (AM == kANormX) {
         q35_u32x4 x = *(const q35_u32x4*)((const uint16_t*)a.X + (size_t)m * a.ldx + k0);
         q35_u32x4 w = *(const q35_u32x4*)(a.aux_w + k0);
@@ -217,6 +222,51 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
             const float rs = hidden_rsqrt((wsum[0] + wsum[1]) + (wsum[2] + wsum[3]));
 #pragma unroll
             for (int i = 0; i < 4; ++i) {      // produce_a<kANormX> on the preloaded chunk
+                const uint32_t lo = f2bf(norm_elem(__uint_as_float(xc[i] << 16), rs, __uint_as_float(wc[i] << 16)));
+                const uint32_t hi = f2bf(norm_elem(__uint_as_float(xc[i] & 0xffff0000u), rs, __uint_as_float(wc[i] & 0xffff0000u)));
+                mine[i] = lo | (hi << 16);
+            }
+        } else if (AM == kANormXP) {
+            // this GEMM has K = 1024, so wave kb owns columns 256 kb .. +255: lane L folds the
+            // quad q = 64 kb + L (columns 4q .. 4q+3) -- the add+norm kernel's quad -- and the
+            // four waves exchange their square sums (same reduction tree)
+            const uint16_t* xr0 = (const uint16_t*)a.X;
+            const int q0 = 256 * kb + 4 * lane;
+            const uint2 xq = *(const uint2*)(xr0 + q0);
+            float4 d[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j)     // unconditional clamped loads: no wait at a join
+                d[j] = *(const float4*)(a.kpart + (size_t)min(j, a.kpb - 1) * kHidden + q0);
+            const q35_u32x4 wc = *(const q35_u32x4*)(a.aux_w + k0);
+            asm volatile("" ::: "memory");     // keep the producer's loads ahead of W
+            load_w();
+            __builtin_amdgcn_sched_barrier(0);   // ... and its arithmetic behind W's issue
+            float4 dsum = d[0];
+#pragma unroll
+            for (int j = 1; j < 16; ++j)
+                if (j < a.kpb) { dsum.x = dsum.x + d[j].x; dsum.y = dsum.y + d[j].y; dsum.z = dsum.z + d[j].z; dsum.w = dsum.w + d[j].w; }
+            const float xv0[4] = {__uint_as_float(xq.x << 16), __uint_as_float(xq.x & 0xffff0000u),
+                                  __uint_as_float(xq.y << 16), __uint_as_float(xq.y & 0xffff0000u)};
+            const float cv[4] = {dsum.x, dsum.y, dsum.z, dsum.w};
+            uint32_t o[4];
+            float xn[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { o[i] = f2bf(xv0[i] + rbf(cv[i])); xn[i] = bf2f((uint16_t)o[i]); }
+            const uint2 pk = {o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+            if (blockIdx.x == 0) *(uint2*)(a.xres + q0) = pk;
+            __shared__ float wred[16];
+            const float ws = wave_sum(quad_ss(xn[0], xn[1], xn[2], xn[3]));
+            if (lane == 0) wred[kb] = ws;
+            __syncthreads();
+            const float rs = hidden_rsqrt((wred[0] + wred[1]) + (wred[2] + wred[3]));
+            // chunk c = columns 256 kb + 8c .. +7 = the quads of lanes 2c and 2c + 1
+            q35_u32x4 xc;
+            xc[0] = (uint32_t)__shfl((int)pk.x, 2 * c, 64);
+            xc[1] = (uint32_t)__shfl((int)pk.y, 2 * c, 64);
+            xc[2] = (uint32_t)__shfl((int)pk.x, 2 * c + 1, 64);
+            xc[3] = (uint32_t)__shfl((int)pk.y, 2 * c + 1, 64);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {      // produce_a<kANormX> on x'
                 const uint32_t lo = f2bf(norm_elem(__uint_as_float(xc[i] << 16), rs, __uint_as_float(wc[i] << 16)));
                 const uint32_t hi = f2bf(norm_elem(__uint_as_float(xc[i] & 0xffff0000u), rs, __uint_as_float(wc[i] & 0xffff0000u)));
                 mine[i] = lo | (hi << 16);
@@ -820,7 +870,7 @@ static hipError_t launch_am_em(const GemmArgs& a, hipStream_t st) {
             hipLaunchKernelGGL((gemm_small_m<AM, EM>), dim3(a.N / 16, 1, 1), dim3(64 * KB), lds, st, a);
         return hipGetLastError();
     }
-    if (EM == kEResidual || AM == kANormX) return hipErrorInvalidValue;   // batch-1 forms only
+    if (EM == kEResidual || AM == kANormX || AM == kANormXP) return hipErrorInvalidValue;   // batch-1 forms only
     if (AM != kAPlain) {
         // produce A once into a.prod (bf16 [M][K]), then the plain batched GEMM
         if (!a.prod) return hipErrorInvalidValue;
@@ -845,7 +895,7 @@ hipError_t gemm_init() {
                             big) != hipSuccess) return hipGetLastError();
     Q35_ATTR(kASiluMul, kEStore) Q35_ATTR(kASiluMul, kEPartial) Q35_ATTR(kASiluMul, kEResidual)
     Q35_ATTR(kAGatedNorm, kEStore) Q35_ATTR(kAGatedNorm, kEPartial) Q35_ATTR(kAGatedNorm, kEResidual)
-    Q35_ATTR(kANormX, kEStore) Q35_ATTR(kANormX, kEArgmax)
+    Q35_ATTR(kANormX, kEStore) Q35_ATTR(kANormX, kEArgmax) Q35_ATTR(kANormXP, kEStore)
 #undef Q35_ATTR
     if (hipFuncSetAttribute((const void*)gemm_lmhead<8, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, kLmLds) != hipSuccess ||
         hipFuncSetAttribute((const void*)gemm_pre<kEStore, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<2>()) != hipSuccess ||
@@ -859,6 +909,9 @@ hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st) 
     if (emode == kEPartial && (!a.kpart || a.K / 256 > 16)) return hipErrorInvalidValue;
     if (emode == kEResidual && (!a.xres || a.N != kHidden)) return hipErrorInvalidValue;
     if (amode == kANormX && a.K != kHidden) return hipErrorInvalidValue;
+    if (amode == kANormXP && (a.K != kHidden || a.M != 1 || !a.kpart || !a.xres || a.kpb < 1 ||
+                              a.kpb > 16 || emode != kEStore))
+        return hipErrorInvalidValue;
 #define Q35_AM(EMV)                                                          \
     if (amode == kAPlain) return launch_am_em<kAPlain, EMV>(a, st);          \
     if (amode == kASiluMul) return launch_am_em<kASiluMul, EMV>(a, st);      \
@@ -866,6 +919,7 @@ hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st) 
     return hipErrorInvalidValue;
     if (emode == kEStore) {
         if (amode == kANormX) return launch_am_em<kANormX, kEStore>(a, st);
+        if (amode == kANormXP) return launch_am_em<kANormXP, kEStore>(a, st);
         Q35_AM(kEStore)
     }
     if (emode == kEPartial) { Q35_AM(kEPartial) }

@@ -6,7 +6,7 @@
 
 namespace q35 {
 
-enum { kAPlain = 0, kASiluMul = 1, kAGatedNorm = 2, kANormX = 3 };
+enum { kAPlain = 0, kASiluMul = 1, kAGatedNorm = 2, kANormX = 3, kANormXP = 4 };
 enum { kEStore = 0, kEArgmax = 1, kEPartial = 2, kEResidual = 3, kESiluMul = 4 };
 // kESiluMul (batched lanes): N = 2F columns [gate | up]; each block pairs gate tiles with the
 // matching up tiles and stores act = bf16(bf16(silu(bf16 g)) * bf16 u) into Y [M][F].
@@ -30,6 +30,7 @@ struct GemmArgs {
     uint16_t* prod;        // M > 16 with a producer: bf16 [M][K] staging of the produced A
     uint16_t* xres;        // kEResidual: residual rows [M][1024], x <- bf16(x + bf16(sum))
     uint16_t* hout;        // kANormX (optional): the normalised rows [M][1024] are written here
+    int kpb;               // kANormXP: k-block chains of the producing GEMM pending in kpart
 };
 // One-time kernel attribute setup (dynamic LDS above 64 KiB for the batch-1 producers).
 hipError_t gemm_init();

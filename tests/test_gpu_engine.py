@@ -237,6 +237,35 @@ def test_graph_replay_equals_eager(eng):
     assert np.array_equal(res[0][2], res[1][2])
 
 
+def test_one_row_partials_equal_epilogue_add(eng):
+    """One-row bodies: the 1024-wide GEMVs leaving k-block chains that the next norm GEMM folds
+    into the residual (and the final add+norm) give the same bits as the residual add in the
+    GEMV epilogue: tokens, full logits and state, for a one-token prompt and decode steps."""
+    from oracle.weights import lane_prompt_ids
+    from qwen35 import State
+    ids = lane_prompt_ids(3, 0, 9)
+    res = {}
+    for mode in (0, 1):
+        eng.set_option("b1_partials", mode)
+        st = State(eng, 1, 512)
+        y, lg0 = st.prefill(0, ids[:1], logits=True)
+        st.prefill(0, ids[1:])
+        toks, lgs = [], [lg0]
+        t = int(y)
+        for _ in range(4):
+            out, lg = st.decode_step([t], logits=True)
+            t = int(out[0])
+            toks.append(t)
+            lgs.append(lg[0])
+        res[mode] = (int(y), toks, lgs, st.read(0, "S"), st.read(0, "k", 16))
+        st.close()
+    eng.set_option("b1_partials", 1)
+    assert res[0][0] == res[1][0] and res[0][1] == res[1][1]
+    for a, b in zip(res[0][2], res[1][2]):
+        assert np.array_equal(a, b)
+    assert np.array_equal(res[0][3], res[1][3]) and np.array_equal(res[0][4], res[1][4])
+
+
 @pytest.mark.parametrize("P", [4096, 9000, 32768])
 def test_seeded_state_decode(oracle_weights, P):
     """The benchmark's seeded workload: lanes with N(0,0.1) GDN state and N(0,1) K/V over P
