@@ -17,7 +17,7 @@
 //   gemm_small_m   one 16-row tile; wave w of a block owns k-block w (M <= 16, batch 1);
 //                  with a producer the wave builds its A tile cooperatively in LDS
 //   gemm_pre       K = 1024 at M > 16: 32-row blocks, every load issued up front (A by LDS-DMA)
-//   gemm_lmhead    tied lm_head at 16 < M <= 512: persistent, A resident in LDS
+//   gemm_lmhead    tied lm_head at M > 16: persistent, A resident in LDS
 //   gemm_large_m   4 waves x 16 columns, 64 rows per block; the A tile of each k-block is
 //                  staged once in LDS in MFMA fragment order, the next k-block's loads in
 //                  flight meanwhile (batched lanes);
@@ -652,7 +652,7 @@ __global__ void __launch_bounds__(256) gemm_pre(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------- tied lm_head, batched lanes
-// K = 1024 (the hidden size), argmax epilogue, M <= 512. Persistent blocks of NW waves,
+// K = 1024 (the hidden size), argmax epilogue, launches of M <= 512. Persistent blocks of NW waves,
 // about one per CU: a block stages its 64 A rows (64 x 1024 bf16 = 128 KiB) in LDS once, in
 // MFMA fragment order, and then walks a stream of column units; each wave computes a 64-row x
 // (16 NTW)-column tile per unit, so each A fragment read from LDS feeds NTW MFMAs and each
@@ -833,12 +833,23 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
     const int gz = EM == kEPartial ? KB : 1;
     // 64-row tiles: more blocks in flight (W tiles are re-read from L2 by the M tiles)
     const int nb = EM == kESiluMul ? (a.N / 32 + 1) / 2 : (a.N / 16 + 3) / 4, mb = (a.M + 63) / 64;
-    const int mbk = (a.M + 63) / 64;
-    if (EM == kEArgmax && a.K == kHidden && a.N % 64 == 0 && mbk <= 8 && g_lmhead_persist) {
+    if (EM == kEArgmax && a.K == kHidden && a.N % 64 == 0 && g_lmhead_persist) {
         // persistent blocks with A resident in LDS: mbk row blocks x (256 / mbk) column
-        // streams, one block per CU (the 128 KiB of A fragments allow no second)
-        const int streams = max(8, 256 / mbk / 8 * 8);
-        hipLaunchKernelGGL((gemm_lmhead<8, 2>), dim3(mbk * streams), dim3(512), kLmLds, st, a, mbk);
+        // streams, one block per CU (the 128 KiB of A fragments allow no second). Above 512
+        // rows (MTP verify: 3 rows per lane) in launches of at most 256 rows: rows are
+        // independent, and one pass with more row blocks than CUs would run a second partial
+        // wave of blocks.
+        for (int r0 = 0; r0 < a.M; r0 += a.M > 512 ? 256 : a.M) {
+            GemmArgs c = a;
+            c.M = min(a.M - r0, a.M > 512 ? 256 : a.M);
+            c.X = (const uint16_t*)a.X + (size_t)r0 * a.ldx;
+            if (a.logits) c.logits = a.logits + (size_t)r0 * a.ldl;
+            c.part_val = a.part_val + (size_t)r0 * a.ldp;
+            c.part_idx = a.part_idx + (size_t)r0 * a.ldp;
+            const int mbk = (c.M + 63) / 64;
+            const int streams = max(8, 256 / mbk / 8 * 8);
+            hipLaunchKernelGGL((gemm_lmhead<8, 2>), dim3(mbk * streams), dim3(512), kLmLds, st, c, mbk);
+        }
         return;
     }
     if (EM == kEArgmax) {

@@ -103,6 +103,29 @@ def test_lm_head_persistent_equals_tiled(eng, M):
 
 
 
+
+def test_lm_head_persistent_row_chunks():
+    """Above 512 rows (MTP verify at 256 lanes: 768 rows) the persistent lm_head runs in
+    launches of 256 rows; tokens and logits equal the tiled kernel's, row offsets included."""
+    import torch
+    from qwen35 import Engine
+    e = Engine(max_rows=768, max_ctx=64, seed=0)
+    try:
+        M = 700
+        X = torch.randn(M, 1024, generator=torch.Generator().manual_seed(700)).to(torch.bfloat16).cuda()
+        out = {}
+        for p in (0, 1):
+            e.set_option("lmhead_persist", p)
+            tok = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+            lg = torch.full((M, 248320), float("nan"), dtype=torch.float32, device="cuda")
+            e.op_lm_head_argmax(X.data_ptr(), M, tok.data_ptr(), lg.data_ptr())
+            e.sync()
+            out[p] = (tok.cpu(), lg.cpu())
+        assert torch.equal(out[0][0], out[1][0])
+        assert torch.equal(out[0][1], out[1][1])
+    finally:
+        e.close()
+
 @pytest.mark.parametrize("N", [1024, 5120, 7168, 8704])
 def test_k1024_gemm_forms_identical(eng, N):
     """Batched K = 1024 projections: the all-loads-up-front kernel (32-row blocks, A fragments
