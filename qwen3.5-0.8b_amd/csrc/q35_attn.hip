@@ -16,6 +16,8 @@
 //   attn_combine (row, q head)      sum of the parts in order, bf16, times bf16(sigmoid(gate))
 // The k cache holds bf16(k post-rope); the reference's torch path keeps it in f32, so
 // k's rotated dims carry one extra bf16 rounding here (the cache layout is bf16 by design).
+#include <algorithm>
+
 #include "q35_common.h"
 #include "q35_kernels.h"
 
@@ -449,13 +451,19 @@ __global__ void __launch_bounds__(256) attn_fused(AttnArgs a, int lds_slots) {
     __shared__ float p[4][kPart];
     __shared__ float ml[4][2];
     // Block order: the T rows of one lane read the same K/V, so they run as consecutive
-    // blocks of one XCD (blocks go round-robin to the 8 XCDs) and share its L2 stream:
-    // (lane group, kv head) pair p -> XCD p % 8, blocks 8 ((p / 8) T + t) + p % 8.
+    // blocks of one XCD (blocks go round-robin to the 8 XCDs) and share its L2 stream. With
+    // fewer (lane, kv head) pairs than XCDs (a prompt wave of one lane) each pair's rows are
+    // cut into `nseg` contiguous segments of `seg` rows so that every XCD gets a segment:
+    // virtual pair v -> XCD v % 8, blocks 8 ((v / 8) seg + i) + v % 8.
     const int T = a.T, tid = threadIdx.x;
+    const int npairs = (a.R / T) * kNkv;
+    const int nseg = max(1, 8 / npairs), seg = (T + nseg - 1) / nseg;
     const int xcd = blockIdx.x & 7, kk = blockIdx.x >> 3;
-    const int pr = (kk / T) * 8 + xcd;
-    if (pr >= (a.R / T) * kNkv) return;
-    const int j = pr % kNkv, r = (pr / kNkv) * T + kk % T;
+    const int v = (kk / seg) * 8 + xcd;
+    if (v >= npairs * nseg) return;
+    const int pr = v / nseg, t = (v % nseg) * seg + kk % seg;
+    if (t >= T) return;
+    const int j = pr % kNkv, r = (pr / kNkv) * T + t;
     const int slot = a.rm.slot[r];
     const int lrow = a.rm.lane[r];
     const int nch = slot / kChunk + 1, nparts = slot / kPart + 1;
@@ -509,7 +517,8 @@ hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
     if (use_fused(a)) {
         if (a.T < 1 || a.R % a.T) return hipErrorInvalidValue;
         const int pairs = a.R / a.T * kNkv;
-        hipLaunchKernelGGL(attn_fused, dim3((pairs + 7) / 8 * a.T * 8), dim3(256), lds, st, a, lds_slots);
+        const int nseg = std::max(1, 8 / pairs), seg = (a.T + nseg - 1) / nseg;
+        hipLaunchKernelGGL(attn_fused, dim3((pairs * nseg + 7) / 8 * seg * 8), dim3(256), lds, st, a, lds_slots);
     } else {
         if (prep_in_scores(a))
             hipLaunchKernelGGL(attn_scores_prep, dim3(a.R, kNkv, a.max_chunks * 4), dim3(64), 0, st, a);
