@@ -99,6 +99,28 @@ def run_decode(eng, B: int, ctx: int, steps: int, warmup: int, kprof: str | None
     return wall, ev_ms / 1e3, kt
 
 
+def run_prefill(eng, n: int, reps: int = 2):
+    """Prompt of n random ids into one lane (waves of eng.max_rows rows; the GDN layers take the
+    chunked form, config 2's T = 4096 case). Returns the best of `reps` timed passes."""
+    import numpy as np
+    from qwen35 import State
+    ids = np.random.default_rng(0).integers(0, 248320, n).astype(np.int32)
+    st = State(eng, 1, n + 64)
+    st.prefill(0, ids[:64])            # warm: kernels loaded, graphs of the decode path untouched
+    st.reset()
+    best = None
+    for _ in range(reps):
+        eng.sync()
+        t0 = time.perf_counter()
+        st.prefill(0, ids)
+        eng.sync()
+        dt = time.perf_counter() - t0
+        st.reset()
+        best = dt if best is None else min(best, dt)
+    st.close()
+    return {"tokens": n, "ms": round(best * 1e3, 2), "tok_s": round(n / best, 1), "wave_rows": eng.max_rows}
+
+
 def run_mtp(eng, B: int, ctx: int, rounds: int, warmup: int):
     """Config 4: B seeded lanes at context ctx, each round = 2 MTP drafts + a 3-row verify with
     greedy accept and rollback (q35_mtp_round). Returns emitted tokens/s and accept stats."""
@@ -162,6 +184,7 @@ def main():
     ap.add_argument("--kprof-steps", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mtp-rounds", type=int, default=5, help="config 4 (MTP k=2) rounds; 0 skips it")
+    ap.add_argument("--prefill-len", type=int, default=4096, help="one-lane prompt prefill length; 0 skips it")
     ap.add_argument("--eager", action="store_true", help="launch kernels eagerly (no hipGraph)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run one 1 GiB device-to-device torch copy first (counter calibration: "
@@ -214,6 +237,7 @@ def main():
                                   "mfma_frac": round(tf / MFMA_PEAK, 4)})
     roof = rooflines.get(DOMINANT) or (next(iter(rooflines.values())) if rooflines else None)
     mtp = run_mtp(eng, B, L, args.mtp_rounds, 1) if args.mtp_rounds > 0 else None
+    pre = run_prefill(eng, args.prefill_len) if 0 < args.prefill_len <= eng.max_ctx - 64 else None
     cpu = None
     if not args.no_cpu:
         tps, thr, n = cpu_baseline(L)
@@ -231,7 +255,7 @@ def main():
            "batch1": {"tok_s": round(args.b1_steps / wall1, 2), "ms_per_step": round(ms1, 4),
                       "hbm_gbs": round(gbs1, 1), "hbm_frac": round(gbs1 / HBM_PEAK, 4),
                       "bytes_per_token": step_bytes(1, L)},
-           "mtp_k2": mtp, "roofline": roof,
+           "mtp_k2": mtp, "prefill": pre, "roofline": roof,
            "kernel_rooflines": {k: v for k, v in rooflines.items() if k != DOMINANT}, "cpu_baseline": cpu}
     print(json.dumps(out))
 
