@@ -90,7 +90,6 @@ struct q35_state {
     uint16_t *mkc = nullptr, *mvc = nullptr;  // [lanes][2][mtp_cap][256]
     uint16_t* hlast = nullptr;                // [lanes][1024] post-final-norm row of the last body
     int* cur_dev = nullptr;                   // [lanes]
-    int* h_cur = nullptr;                     // [lanes] pinned staging of `cur` for the upload
     std::vector<int> prefix, mtp_len, cur;
     long long S_lane() const { return (long long)nslots * kGdnLayers * kSLayer; }
     long long W_lane() const { return (long long)nslots * kGdnLayers * 18432; }
@@ -130,6 +129,8 @@ struct q35_engine {
     std::map<std::string, hipGraphExec_t> graphs;   // captured decode steps
     // pinned staging
     int *h_tok, *h_lane, *h_pos, *h_slot, *h_out, *h_src, *h_dst, *hin = nullptr;
+    int* h_cur = nullptr;            // pinned staging of a state's `cur` for its upload
+    int h_cur_cap = 0;               // (one engine buffer, sized for the largest state)
 };
 
 namespace {
@@ -375,8 +376,8 @@ void upload_idx(q35_engine* e, int n) {
 // `cur` goes through pinned staging: the host advances s->cur right after enqueueing a
 // body, so the copy must not read the live vector. Callers drain the stream before a body.
 void upload_cur(q35_engine* e, q35_state* s) {
-    for (int i = 0; i < s->lanes; ++i) s->h_cur[i] = s->cur[i];
-    HCK(hipMemcpyAsync(s->cur_dev, s->h_cur, s->lanes * sizeof(int), hipMemcpyHostToDevice, e->st));
+    for (int i = 0; i < s->lanes; ++i) e->h_cur[i] = s->cur[i];
+    HCK(hipMemcpyAsync(s->cur_dev, e->h_cur, s->lanes * sizeof(int), hipMemcpyHostToDevice, e->st));
 }
 
 // Y != nullptr: bf16 store; Y == nullptr: k-block chains to e->kpart (summed by the next
@@ -647,7 +648,7 @@ int q35_destroy(q35_engine* e) {
                       e->sc, e->stats, e->part, e->pval, e->pidx, e->prod, e->din, e->inv_freq,
                       e->logits_dev, e->kpart, e->gchunk, e->gcdec};
         for (void* p : ds) if (p) hipFree(p);
-        void* hs[] = {e->hin, e->h_out};
+        void* hs[] = {e->hin, e->h_out, e->h_cur};
         for (void* p : hs) if (p) hipHostFree(p);
         hipEventDestroy(e->ev0);
         hipEventDestroy(e->ev1);
@@ -743,7 +744,12 @@ int q35_state_alloc(q35_engine* e, int lanes, int cap, int mtp_k, int mtp_cap, q
         }
         s->hlast = dalloc<uint16_t>((size_t)lanes * kHidden);
         s->cur_dev = dalloc<int>(lanes);
-        s->h_cur = halloc<int>(lanes);
+        if (lanes > e->h_cur_cap) {      // no body is in flight: callers drain the stream
+            HCK(hipStreamSynchronize(e->st));
+            if (e->h_cur) HCK(hipHostFree(e->h_cur));
+            e->h_cur = halloc<int>(lanes);
+            e->h_cur_cap = lanes;
+        }
         s->prefix.assign(lanes, 0);
         s->mtp_len.assign(lanes, 0);
         s->cur.assign(lanes, 0);
@@ -771,7 +777,6 @@ int q35_state_free(q35_engine* e, q35_state* s) {
         }
         void* ds[] = {s->S, s->win, s->kc, s->vc, s->mkc, s->mvc, s->hlast, s->cur_dev};
         for (void* p : ds) if (p) hipFree(p);
-        if (s->h_cur) hipHostFree(s->h_cur);
         delete s;
     });
 }
