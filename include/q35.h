@@ -50,6 +50,18 @@ int q35_init_random(q35_engine* e, uint64_t seed);
 /* Load one tensor given in checkpoint layout and dtype bf16 (row-major, the reference's
  * names, e.g. "model.language_model.layers.0.mlp.gate_proj.weight"); engine/loader.cpp:478. */
 int q35_load_tensor(q35_engine* e, const char* name, const uint16_t* host_bf16, size_t n_elems);
+/* Load a checkpoint given as the bytes of its .safetensors file (replaces specimpl.Weights,
+ * speccheck/specimpl.py:60-127, and the engine's loader, engine/loader.cpp:478): the
+ * model.visual.* tensors are skipped, every other tensor must be one of the 335 text-tower
+ * and MTP tensors with its checkpoint shape, stored as BF16, F16 or F32 (cast to bf16 with
+ * round-to-nearest-even, as torch's .to(torch.bfloat16)); the file must hold 488 tensors, 153
+ * of them vision (the reference's G0 gate). The tied lm_head reads the embedding. Nothing is
+ * written unless the whole file passes. n_loaded / n_skipped (nullable) receive 335 / 153. */
+int q35_load_safetensors(q35_engine* e, const void* file_bytes, size_t n_bytes, int32_t* n_loaded,
+                         int32_t* n_skipped);
+/* Parse and validate a .safetensors container without an engine (no GPU work): tensor count
+ * and how many are model.visual.* (the same header checks as q35_load_safetensors). */
+int q35_safetensors_scan(const void* file_bytes, size_t n_bytes, int32_t* n_tensors, int32_t* n_vision);
 /* Read a tensor back in checkpoint layout (tests). */
 int q35_read_tensor(q35_engine* e, const char* name, uint16_t* host_bf16, size_t n_elems);
 

@@ -19,6 +19,7 @@
 #include "../../include/q35.h"
 #include "q35_common.h"
 #include "q35_kernels.h"
+#include "q35_safetensors.h"
 
 using namespace q35;
 
@@ -598,6 +599,33 @@ void mtp_draft_pass(q35_engine* e, q35_state* s, int n, const uint16_t* hsrc) {
     finish_norm(e, n, e->mtp_norm, e->nrm);
 }
 
+// One tensor in checkpoint layout (bf16 bits) into its placement: plain tensors are copied,
+// matrices tiled into their combined GEMM operand.
+void load_one(q35_engine* e, const std::string& name, const uint16_t* host, size_t n) {
+    auto it = e->reg.find(name);
+    REQ(it != e->reg.end(), Q35_ERR_ARG, "unknown tensor " + name);
+    const Placement& p = it->second;
+    REQ(n == (size_t)p.rows * p.cols, Q35_ERR_ARG, "element count mismatch: " + name);
+    if (p.tiled) {
+        uint16_t* tmp = dalloc<uint16_t>(n);
+        copy_sync(e, tmp, host, n * 2, hipMemcpyHostToDevice);
+        HCK(launch_tile(tmp, p.rows, p.cols, p.base, p.row_off, 0, e->st));
+        HCK(hipStreamSynchronize(e->st));
+        HCK(hipFree(tmp));
+    } else {
+        copy_sync(e, p.base, host, n * 2, hipMemcpyHostToDevice);
+    }
+}
+
+// The checkpoint's shape of a registered tensor: [rows, K] for matrices, [n] for vectors,
+// [6144, 1, 4] for the depthwise conv weights (specimpl.py:92-127, the G1 shape table).
+bool shape_ok(const Placement& p, const std::string& name, const std::vector<int64_t>& sh) {
+    if (p.tiled) return sh.size() == 2 && sh[0] == p.rows && sh[1] == p.cols;
+    if (name.size() > 13 && name.compare(name.size() - 13, 13, "conv1d.weight") == 0)
+        return sh.size() == 3 && sh[0] == kConvCh && sh[1] == 1 && sh[2] == 4;
+    return sh.size() == 1 && sh[0] == p.rows;
+}
+
 int guard(const std::function<void()>& f) {
     try {
         f();
@@ -688,20 +716,55 @@ int q35_init_random(q35_engine* e, uint64_t seed) {
 int q35_load_tensor(q35_engine* e, const char* name, const uint16_t* host, size_t n) {
     return guard([&] {
         REQ(e && name && host, Q35_ERR_ARG, "null argument");
-        auto it = e->reg.find(name);
-        REQ(it != e->reg.end(), Q35_ERR_ARG, std::string("unknown tensor ") + name);
-        const Placement& p = it->second;
-        REQ(n == (size_t)p.rows * p.cols, Q35_ERR_ARG, "element count mismatch");
-        if (p.tiled) {
-            uint16_t* tmp = dalloc<uint16_t>(n);
-            copy_sync(e, tmp, host, n * 2, hipMemcpyHostToDevice);
-            HCK(launch_tile(tmp, p.rows, p.cols, p.base, p.row_off, 0, e->st));
-            HCK(hipStreamSynchronize(e->st));
-            HCK(hipFree(tmp));
-        } else {
-            copy_sync(e, p.base, host, n * 2, hipMemcpyHostToDevice);
+        load_one(e, name, host, n);
+        e->weights_ready = true;
+    });
+}
+
+int q35_safetensors_scan(const void* file, size_t n, int32_t* n_tensors, int32_t* n_vision) {
+    return guard([&] {
+        REQ(file && n_tensors && n_vision, Q35_ERR_ARG, "null argument");
+        std::vector<StTensor> ts;
+        std::string err;
+        REQ(parse_safetensors(file, n, ts, err), Q35_ERR_ARG, "safetensors: " + err);
+        int vis = 0;
+        for (const auto& t : ts) vis += t.name.rfind("model.visual.", 0) == 0;
+        *n_tensors = (int32_t)ts.size();
+        *n_vision = vis;
+    });
+}
+
+int q35_load_safetensors(q35_engine* e, const void* file, size_t n, int32_t* n_loaded, int32_t* n_skipped) {
+    return guard([&] {
+        REQ(e && file, Q35_ERR_ARG, "null argument");
+        std::vector<StTensor> ts;
+        std::string err;
+        REQ(parse_safetensors(file, n, ts, err), Q35_ERR_ARG, "safetensors: " + err);
+        // the reference loader's gate (specimpl.py:60-62, 88-91): 488 tensors, the 153
+        // model.visual.* ones skipped, 335 loaded. Everything is checked before the first
+        // tensor is written, so a refused file leaves the engine's weights as they were.
+        std::vector<const StTensor*> keep;
+        int skipped = 0;
+        for (const auto& t : ts) {
+            if (t.name.rfind("model.visual.", 0) == 0) { ++skipped; continue; }
+            auto it = e->reg.find(t.name);
+            REQ(it != e->reg.end(), Q35_ERR_ARG, "unknown tensor " + t.name);
+            REQ(shape_ok(it->second, t.name, t.shape), Q35_ERR_ARG, "shape mismatch: " + t.name);
+            REQ(t.dtype == "BF16" || t.dtype == "F32" || t.dtype == "F16", Q35_ERR_ARG,
+                "tensor " + t.name + " has dtype " + t.dtype + " (BF16, F16 or F32 expected)");
+            keep.push_back(&t);
+        }
+        REQ(ts.size() == 488 && skipped == 153 && keep.size() == e->reg.size(), Q35_ERR_ARG,
+            "expected 488 tensors (153 vision, 335 text tower + MTP), found " + std::to_string(ts.size()) +
+                " (" + std::to_string(skipped) + " vision)");
+        std::vector<uint16_t> bits;
+        for (const StTensor* t : keep) {      // casts as Tensor.to(torch.bfloat16) (specimpl.py:84)
+            REQ(to_bf16(*t, bits, err), Q35_ERR_ARG, err);
+            load_one(e, t->name, bits.data(), bits.size());
         }
         e->weights_ready = true;
+        if (n_loaded) *n_loaded = (int32_t)keep.size();
+        if (n_skipped) *n_skipped = skipped;
     });
 }
 

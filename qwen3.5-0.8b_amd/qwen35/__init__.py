@@ -6,7 +6,7 @@ include/q35.h. There is no CPU fallback: if the HIP library is missing or no GPU
 visible, every entry point raises.
 """
 from .engine import (EOS_IDS, VOCAB, Engine, EngineError, Forward, State, greedy_mtp,
-                     lib_path, load_library)
+                     lib_path, load_library, safetensors_scan)
 
 __all__ = ["Engine", "EngineError", "Forward", "State", "greedy_mtp", "load_library",
-           "lib_path", "VOCAB", "EOS_IDS"]
+           "lib_path", "safetensors_scan", "VOCAB", "EOS_IDS"]

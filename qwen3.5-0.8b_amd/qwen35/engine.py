@@ -36,6 +36,9 @@ _SIGS = {
     "q35_init_random": ([C.c_void_p, C.c_uint64], C.c_int),
     "q35_load_tensor": ([C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t], C.c_int),
     "q35_read_tensor": ([C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t], C.c_int),
+    "q35_load_safetensors": ([C.c_void_p, C.c_void_p, C.c_size_t, C.POINTER(C.c_int32), C.POINTER(C.c_int32)],
+                             C.c_int),
+    "q35_safetensors_scan": ([C.c_void_p, C.c_size_t, C.POINTER(C.c_int32), C.POINTER(C.c_int32)], C.c_int),
     "q35_state_alloc": ([C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_void_p)], C.c_int),
     "q35_state_free": ([C.c_void_p, C.c_void_p], C.c_int),
     "q35_state_reset": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int], C.c_int),
@@ -91,6 +94,16 @@ def _p(a: np.ndarray):
     return a.ctypes.data_as(C.c_void_p)
 
 
+def safetensors_scan(data: bytes | np.ndarray) -> tuple[int, int]:
+    """(tensors, vision tensors) of a .safetensors container, validated by the library's parser
+    without an engine or a GPU (q35_safetensors_scan); raises EngineError on a malformed file."""
+    b = np.frombuffer(data, dtype=np.uint8) if isinstance(data, (bytes, bytearray)) else data
+    nt, nv = C.c_int32(), C.c_int32()
+    _ck(load_library().q35_safetensors_scan(C.c_void_p(b.ctypes.data) if b.size else None, b.size,
+                                            C.byref(nt), C.byref(nv)))
+    return nt.value, nv.value
+
+
 class Engine:
     """Weights + scratch + stream (WeightStore / DecodeScratch of the reference)."""
 
@@ -112,6 +125,21 @@ class Engine:
     def load_tensor(self, name: str, bits: np.ndarray):
         b = np.ascontiguousarray(bits, dtype=np.uint16)
         _ck(load_library().q35_load_tensor(self.h, name.encode(), _p(b), b.size))
+
+    def load_checkpoint(self, model_dir) -> tuple[int, int]:
+        """Weights from the checkpoint directory's .safetensors file, as specimpl.Weights
+        (speccheck/specimpl.py:70-86) loads it: the first *.safetensors found, vision tensors
+        skipped, everything cast to bf16. The file is memory-mapped and parsed by the library
+        (q35_load_safetensors). Returns (loaded, skipped) = (335, 153)."""
+        path = next(Path(model_dir).glob("*.safetensors"))
+        buf = np.memmap(path, dtype=np.uint8, mode="r")
+        loaded, skipped = C.c_int32(), C.c_int32()
+        try:
+            _ck(load_library().q35_load_safetensors(self.h, C.c_void_p(buf.ctypes.data), buf.size,
+                                                    C.byref(loaded), C.byref(skipped)))
+        finally:
+            del buf
+        return loaded.value, skipped.value
 
     def read_tensor(self, name: str, n: int) -> np.ndarray:
         out = np.empty(n, dtype=np.uint16)
