@@ -1,0 +1,105 @@
+"""The resident session protocol (decode_run --session, engine/decode_run.cpp:1760-1790,
+2436-2680) over the engine: replies and their order, greedy tokens identical to a plain
+Forward over the same transcript across turns (the pending-sample rule: a budget-ended turn
+drops its unshown sample, the next feed carries only the caller's ids), argument errors that
+do not poison, an engine error that poisons until `reset`, the opt-in logits dump, and the
+stdin/stdout entry point in a child process."""
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+@pytest.fixture(scope="module")
+def eng():
+    from qwen35 import Engine
+    e = Engine(max_rows=64, max_ctx=512, seed=0, use_graph=True)
+    yield e
+    e.close()
+
+
+def test_session_turns_match_forward(eng, tmp_path):
+    from oracle.weights import lane_prompt_ids
+    from qwen35 import Forward, State
+    from qwen35.session import Session
+    out = []
+    s = Session(eng, 512, str(tmp_path))
+    emit = out.append
+    assert s.ready_line() == "READY cap=512"
+    ids1 = [int(t) for t in lane_prompt_ids(9, 0, 12)]
+    ids2 = [int(t) for t in lane_prompt_ids(9, 1, 5)]
+
+    s.handle("gen 3", emit)
+    assert out[-1].startswith("ERROR gen with no sampled token")
+    s.handle("feed " + " ".join(map(str, ids1)), emit)
+    assert out[-1] == f"FED n=12 prefix_len=12"
+    n0 = len(out)
+    s.handle("dump 14", emit)
+    assert out[-1] == f"DUMP armed=1 min=14 max=14 dir={tmp_path}"
+    s.handle("gen 5", emit)
+    lines = out[n0 + 1:]
+    gens = [l for l in lines if l.startswith("GEN ")]
+    assert [int(l.split()[2]) for l in gens] == [11, 12, 13, 14, 15]
+    toks = [int(l.split()[1]) for l in gens]
+    assert lines[-1] == "END steps=5 stop=0 prefix_len=17"
+    dumps = [l for l in lines if l.startswith("DUMP seq=")]
+    assert len(dumps) == 1 and " kind=step pos=14 " in dumps[0]
+    row = np.fromfile(tmp_path / dumps[0].split("file=")[1], dtype=np.float32)
+    assert row.size == 248320 and int(np.argmax(row)) == toks[3]   # the row at 14 decides "GEN <id> 14"
+    s.handle("dump off", emit)
+    assert out[-1] == "DUMP armed=0 written=1"
+
+    ref = Forward(eng, State(eng, 1, 512)).greedy(ids1, 4, stop_on_eos=False)
+    assert toks == ref[:5]
+
+    s.handle("gen 1", emit)                   # the budget-ended turn left no pending sample
+    assert out[-1].startswith("ERROR gen with no sampled token")
+    s.handle("feed " + " ".join(map(str, ids2)), emit)
+    assert out[-1] == "FED n=5 prefix_len=22"
+    s.handle("gen 3", emit)
+    toks2 = [int(l.split()[1]) for l in out[-4:-1]]
+    assert out[-1] == "END steps=3 stop=0 prefix_len=25"
+    ref2 = Forward(eng, State(eng, 1, 512)).greedy(ids1 + toks + ids2, 2, stop_on_eos=False)
+    assert toks2 == ref2[:3]
+    s.handle("stats", emit)
+    assert out[-1] == "PREFIX p=25 sampled=-1 stopped=0"
+
+    s.handle("gen x", emit)
+    s.handle("feed 1 2", emit)                # argument errors above did not poison
+    assert out[-1] == "FED n=2 prefix_len=27"
+    s.handle("feed 999999999", emit)          # out-of-range id: the engine refuses -> poisoned
+    assert out[-1].startswith("ERROR ")
+    s.handle("gen 1", emit)
+    assert out[-1].startswith("ERROR session is poisoned")
+    s.handle("reset", emit)
+    assert out[-1] == "RESET prefix_len=0"
+    s.handle("feed " + " ".join(map(str, ids1)), emit)
+    s.handle("gen 2", emit)
+    assert [int(l.split()[1]) for l in out[-3:-1]] == toks[:2]
+    s.handle("frobnicate", emit)
+    assert out[-1].startswith("ERROR unknown command 'frobnicate'")
+    assert s.handle("quit", emit) is False and out[-1] == "BYE"
+    s.close()
+
+
+def test_session_stdin_stdout():
+    cmds = "feed 11 22 33\ngen 3\nstats\nquit\n"
+    env = dict(os.environ)
+    env["PYTHONPATH"] = f"{ROOT}:{ROOT / 'qwen3.5-0.8b_amd'}"
+    r = subprocess.run([sys.executable, "-m", "qwen35.session", "--cap", "256", "--max-rows", "64"],
+                       input=cmds, capture_output=True, text=True, timeout=180, env=env)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [l for l in r.stdout.splitlines() if l]
+    assert lines[0] == "READY cap=256"
+    assert lines[1] == "FED n=3 prefix_len=3"
+    assert [l.split()[0] for l in lines[2:6]] == ["GEN", "GEN", "GEN", "END"]
+    assert lines[5] == "END steps=3 stop=0 prefix_len=6"
+    assert lines[6] == "PREFIX p=6 sampled=-1 stopped=0"
+    assert lines[7] == "BYE"
