@@ -79,6 +79,17 @@ int q35_state_prefix_len(q35_engine* e, q35_state* s, int lane, int32_t* out);
 int q35_state_read(q35_engine* e, q35_state* s, int lane, int which, int n_slots, void* host, size_t bytes);
 int q35_state_write(q35_engine* e, q35_state* s, int lane, int which, int n_slots, const void* host, size_t bytes);
 
+/* Prefix reuse and preempt / resume (specification/08-state-management.md §08.3-08.4: the
+ * tuple is stored and restored verbatim, no recompute). q35_state_copy_lane forks lane
+ * src_lane's tuple -- its current GDN S and conv window, K/V slots [0, prefix_len), the MTP
+ * cache, the last post-final-norm row and prefix_len -- device-to-device into dst_lane (of
+ * the same or another state of this engine; the destination's capacity must hold it). The
+ * snapshot is one contiguous host blob of the same tuple (q35_state_snapshot with host ==
+ * NULL reports its size in *bytes_needed); q35_state_restore writes it back into any lane. */
+int q35_state_copy_lane(q35_engine* e, q35_state* src, int src_lane, q35_state* dst, int dst_lane);
+int q35_state_snapshot(q35_engine* e, q35_state* s, int lane, void* host, size_t bytes, size_t* bytes_needed);
+int q35_state_restore(q35_engine* e, q35_state* s, int lane, const void* host, size_t bytes);
+
 /* Prompt of one lane (prefill_wave, engine/prefill.cpp:63 / specimpl.py:457-464): the
  * tokens are consumed in waves of at most max_rows rows; *y0 = greedy id after the last
  * prompt token; logits (nullable) receives that row's 248320 bf16-valued logits. */

@@ -942,6 +942,132 @@ static void state_io(q35_engine* e, q35_state* s, int lane, int which, int n_slo
     }
 }
 
+// ---- whole-tuple copies: prefix reuse and preempt / resume (specification/08-state-management.md
+// §08.3-08.4: the tuple S, conv window, KV[0..P), prefix_len is stored and restored verbatim)
+// One lane's tuple, in the lane's current GDN slot: device-to-device into another lane.
+static void copy_lane(q35_engine* e, q35_state* src, int sl, q35_state* dst, int dl) {
+    check_lane(src, sl);
+    check_lane(dst, dl);
+    const int P = src->prefix[sl], M = src->mtp_len[sl];
+    REQ(P <= dst->cap, Q35_ERR_CAP, "prefix exceeds the destination lane's cache capacity");
+    REQ(dst->mtp_cap == 0 || M <= dst->mtp_cap, Q35_ERR_CAP, "MTP cache exceeds the destination's");
+    if (src == dst && sl == dl) return;
+    auto d2d = [&](void* d, const void* s_, size_t nb) {
+        if (nb) HCK(hipMemcpyAsync(d, s_, nb, hipMemcpyDeviceToDevice, e->st));
+    };
+    const long long sS = (long long)kGdnLayers * kSLayer, sW = (long long)kGdnLayers * 18432;
+    d2d(dst->S + dl * dst->S_lane() + dst->cur[dl] * sS, src->S + sl * src->S_lane() + src->cur[sl] * sS, sS * 4);
+    d2d(dst->win + dl * dst->W_lane() + dst->cur[dl] * sW, src->win + sl * src->W_lane() + src->cur[sl] * sW, sW * 4);
+    // K: whole 16-slot tiles (the slots past P of the last tile are never read before written)
+    const size_t ktile = (size_t)(P + 15) / 16 * 4096 * 2, vrows = (size_t)P * 512;
+    for (int a = 0; a < kAttnLayers * 2; ++a) {
+        d2d(dst->kc + dl * dst->kv_lane() + (size_t)a * dst->capT * 256,
+            src->kc + sl * src->kv_lane() + (size_t)a * src->capT * 256, ktile);
+        d2d(dst->vc + dl * dst->kv_lane() + (size_t)a * dst->capT * 256,
+            src->vc + sl * src->kv_lane() + (size_t)a * src->capT * 256, vrows);
+    }
+    const int Mc = dst->mtp_cap > 0 && src->mtp_cap > 0 ? M : 0;
+    for (int a = 0; a < 2 && Mc > 0; ++a) {
+        d2d(dst->mkc + dl * dst->mkv_lane() + (size_t)a * dst->mtp_capT * 256,
+            src->mkc + sl * src->mkv_lane() + (size_t)a * src->mtp_capT * 256, (size_t)(Mc + 15) / 16 * 4096 * 2);
+        d2d(dst->mvc + dl * dst->mkv_lane() + (size_t)a * dst->mtp_capT * 256,
+            src->mvc + sl * src->mkv_lane() + (size_t)a * src->mtp_capT * 256, (size_t)Mc * 512);
+    }
+    d2d(dst->hlast + (size_t)dl * kHidden, src->hlast + (size_t)sl * kHidden, kHidden * 2);
+    HCK(hipStreamSynchronize(e->st));
+    dst->prefix[dl] = P;
+    dst->mtp_len[dl] = Mc;
+}
+
+// Snapshot blob: a header, then S f32 [18][16][128][128], window f32 [18][3][6144], K and V
+// bf16 [12][P][256] (row layout), MTP K and V bf16 [2][M][256], last hidden row bf16 [1024].
+struct SnapHeader {
+    char magic[8];               // "Q35SNAP1"
+    int32_t prefix_len, mtp_len, gdn_layers, attn_layers;
+    int64_t bytes;               // whole blob
+    int32_t reserved[8];
+};
+
+static size_t snap_bytes(int P, int M) {
+    return sizeof(SnapHeader) + (size_t)kGdnLayers * kSLayer * 4 + (size_t)kGdnLayers * 18432 * 4 +
+           2 * (size_t)kAttnLayers * 2 * P * 512 + 2 * (size_t)2 * M * 512 + kHidden * 2;
+}
+
+static void snapshot_lane(q35_engine* e, q35_state* s, int lane, void* host, size_t bytes, size_t* need) {
+    check_lane(s, lane);
+    const int P = s->prefix[lane], M = s->mtp_cap > 0 ? s->mtp_len[lane] : 0;
+    const size_t n = snap_bytes(P, M);
+    if (need) *need = n;
+    if (!host) return;
+    REQ(bytes >= n, Q35_ERR_ARG, "host buffer too small for the snapshot");
+    SnapHeader h{};
+    std::memcpy(h.magic, "Q35SNAP1", 8);
+    h.prefix_len = P; h.mtp_len = M; h.gdn_layers = kGdnLayers; h.attn_layers = kAttnLayers; h.bytes = (int64_t)n;
+    char* p = (char*)host;
+    std::memcpy(p, &h, sizeof h);
+    size_t off = sizeof h;
+    const size_t nS = (size_t)kGdnLayers * kSLayer * 4, nW = (size_t)kGdnLayers * 18432 * 4;
+    const size_t nKV = (size_t)kAttnLayers * 2 * P * 512, nM = (size_t)2 * M * 512;
+    state_io(e, s, lane, 0, 0, p + off, nS, false); off += nS;
+    state_io(e, s, lane, 1, 0, p + off, nW, false); off += nW;
+    state_io(e, s, lane, 2, P, p + off, nKV, false); off += nKV;
+    state_io(e, s, lane, 3, P, p + off, nKV, false); off += nKV;
+    if (M > 0) {
+        state_io(e, s, lane, 4, M, p + off, nM, false); off += nM;
+        state_io(e, s, lane, 5, M, p + off, nM, false); off += nM;
+    }
+    copy_sync(e, p + off, s->hlast + (size_t)lane * kHidden, kHidden * 2, hipMemcpyDeviceToHost);
+}
+
+static void restore_lane(q35_engine* e, q35_state* s, int lane, const void* host, size_t bytes) {
+    check_lane(s, lane);
+    REQ(bytes >= sizeof(SnapHeader), Q35_ERR_ARG, "snapshot too short");
+    SnapHeader h;
+    std::memcpy(&h, host, sizeof h);
+    REQ(std::memcmp(h.magic, "Q35SNAP1", 8) == 0 && h.gdn_layers == kGdnLayers && h.attn_layers == kAttnLayers,
+        Q35_ERR_ARG, "not a snapshot of this engine's state layout");
+    const int P = h.prefix_len, M = h.mtp_len;
+    REQ(P >= 0 && M >= 0 && h.bytes == (int64_t)snap_bytes(P, M) && bytes >= (size_t)h.bytes, Q35_ERR_ARG,
+        "snapshot size does not match its header");
+    REQ(P <= s->cap, Q35_ERR_CAP, "snapshot prefix exceeds the lane's cache capacity");
+    REQ(M == 0 || M <= s->mtp_cap, Q35_ERR_CAP, "snapshot MTP cache exceeds the state's");
+    char* p = (char*)host;
+    size_t off = sizeof h;
+    const size_t nS = (size_t)kGdnLayers * kSLayer * 4, nW = (size_t)kGdnLayers * 18432 * 4;
+    const size_t nKV = (size_t)kAttnLayers * 2 * P * 512, nM = (size_t)2 * M * 512;
+    state_io(e, s, lane, 0, 0, p + off, nS, true); off += nS;
+    state_io(e, s, lane, 1, 0, p + off, nW, true); off += nW;
+    state_io(e, s, lane, 2, P, p + off, nKV, true); off += nKV;
+    state_io(e, s, lane, 3, P, p + off, nKV, true); off += nKV;
+    if (M > 0) {
+        state_io(e, s, lane, 4, M, p + off, nM, true); off += nM;
+        state_io(e, s, lane, 5, M, p + off, nM, true); off += nM;
+    }
+    copy_sync(e, s->hlast + (size_t)lane * kHidden, p + off, kHidden * 2, hipMemcpyHostToDevice);
+    s->prefix[lane] = P;
+    s->mtp_len[lane] = s->mtp_cap > 0 ? M : 0;
+}
+
+int q35_state_copy_lane(q35_engine* e, q35_state* src, int src_lane, q35_state* dst, int dst_lane) {
+    return guard([&] {
+        REQ(e && src && dst, Q35_ERR_ARG, "null argument");
+        HCK(hipStreamSynchronize(e->st));
+        copy_lane(e, src, src_lane, dst, dst_lane);
+    });
+}
+int q35_state_snapshot(q35_engine* e, q35_state* s, int lane, void* host, size_t bytes, size_t* bytes_needed) {
+    return guard([&] {
+        REQ(e && s && (host || bytes_needed), Q35_ERR_ARG, "null argument");
+        snapshot_lane(e, s, lane, host, bytes, bytes_needed);
+    });
+}
+int q35_state_restore(q35_engine* e, q35_state* s, int lane, const void* host, size_t bytes) {
+    return guard([&] {
+        REQ(e && s && host, Q35_ERR_ARG, "null argument");
+        restore_lane(e, s, lane, host, bytes);
+    });
+}
+
 int q35_state_read(q35_engine* e, q35_state* s, int lane, int which, int n_slots, void* host, size_t bytes) {
     return guard([&] { state_io(e, s, lane, which, n_slots, host, bytes, false); });
 }

@@ -46,6 +46,10 @@ _SIGS = {
     "q35_state_prefix_len": ([C.c_void_p, C.c_void_p, C.c_int, C.POINTER(C.c_int32)], C.c_int),
     "q35_state_read": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_size_t], C.c_int),
     "q35_state_write": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_size_t], C.c_int),
+    "q35_state_copy_lane": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int], C.c_int),
+    "q35_state_snapshot": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t)],
+                           C.c_int),
+    "q35_state_restore": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_size_t], C.c_int),
     "q35_prefill": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.POINTER(C.c_int32), C.c_void_p], C.c_int),
     "q35_decode_step": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "q35_mtp_draft": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int,
@@ -247,6 +251,25 @@ class State:
             pass
 
     # ---- engine calls over this state
+    def copy_lane(self, lane: int, dst: "State", dst_lane: int):
+        """Fork this lane's whole tuple (S, conv window, KV[0, P), MTP cache, last hidden row,
+        P) into dst's lane, device to device: prefix reuse (specification/08-state-management.md
+        §08.3)."""
+        _ck(load_library().q35_state_copy_lane(self.eng.h, self.h, lane, dst.h, dst_lane))
+
+    def snapshot(self, lane: int) -> np.ndarray:
+        """The lane's tuple as one contiguous host blob (preempt, §08.4)."""
+        n = C.c_size_t()
+        _ck(load_library().q35_state_snapshot(self.eng.h, self.h, lane, None, 0, C.byref(n)))
+        buf = np.empty(n.value, np.uint8)
+        _ck(load_library().q35_state_snapshot(self.eng.h, self.h, lane, _p(buf), buf.size, C.byref(n)))
+        return buf
+
+    def restore(self, lane: int, blob: np.ndarray):
+        """Write a snapshot back into a lane (resume, §08.4)."""
+        b = np.ascontiguousarray(blob, dtype=np.uint8)
+        _ck(load_library().q35_state_restore(self.eng.h, self.h, lane, _p(b), b.size))
+
     def prefill(self, lane: int, ids, logits: bool = False):
         ids = _i32(ids)
         y0 = C.c_int32()
