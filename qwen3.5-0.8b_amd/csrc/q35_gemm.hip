@@ -153,9 +153,14 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, q35_f32x4 sum, int n
 // ---------------------------------------------------------------- small M
 // kEStore / kEArgmax: grid (N/16, ceil(M/16)); block = KB waves, wave w owns k-block w.
 // kEPartial: grid (N/16, ceil(M/16), KB); one wave per block, storing its k-block chain.
-template <int AM, int EM>
-__global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
-    const int nt = blockIdx.x;
+// TPB > 1 (one row with a norm producer, kEStore): each block takes TPB adjacent column tiles,
+// so the producer's per-block work (the norm, or the fold of the residual's k-block chains --
+// 57 KiB of chain reads per block, more than its weight tile) is shared by TPB tiles; every
+// wave runs TPB MFMA chains on the same A fragments. Used with TPB = 2 for N >= 4096
+// (batch 1: 1,171 -> 1,209 tok/s; TPB = 4, a quarter of the blocks: 1,168).
+template <int AM, int EM, int TPB = 1>
+__global__ void __launch_bounds__(TPB > 1 ? 256 : 1024) gemm_small_m(GemmArgs a) {   // TPB > 1: K = 1024, 4 waves
+    const int nt = blockIdx.x * TPB;
     const int mt = blockIdx.y;
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
@@ -166,10 +171,12 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
     const bool mvalid = m < a.M;
 
     const q35_bf16x8* wp = (const q35_bf16x8*)(a.W + ((size_t)nt * KB + kb) * 4096) + lane;
-    q35_bf16x8 wf[8];
+    q35_bf16x8 wf[TPB][8];
     auto load_w = [&] {
 #pragma unroll
-        for (int s = 0; s < 8; ++s) wf[s] = __builtin_nontemporal_load(wp + s * 64);
+        for (int t = 0; t < TPB; ++t)
+#pragma unroll
+            for (int s = 0; s < 8; ++s) wf[t][s] = __builtin_nontemporal_load(wp + (size_t)t * KB * 512 + s * 64);
     };
     // batch 1 with a producer: the producer's own loads go first (the vector-memory counter
     // completes in order, so its arithmetic then overlaps the weight stream instead of
@@ -354,20 +361,25 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
 #pragma unroll
         for (int s = 0; s < 8; ++s) af[s] = As[s][lane];
     }
-    q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    q35_f32x4 acc[TPB];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(af[s]), wf[s], acc, 0, 0, 0);
+    for (int t = 0; t < TPB; ++t) {
+        acc[t] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(af[s]), wf[t][s], acc[t], 0, 0, 0);
+    }
     if (EM == kEPartial) {
-        epilogue<EM>(a, acc, nt, mt * 16, lane);
+        epilogue<EM>(a, acc[0], nt, mt * 16, lane);
         return;
     }
-    __shared__ q35_f32x4 part[16][64];
-    part[wv][lane] = acc;
+    __shared__ q35_f32x4 part[TPB][16][64];
+#pragma unroll
+    for (int t = 0; t < TPB; ++t) part[t][wv][lane] = acc[t];
     __syncthreads();
-    if (wv != 0) return;
-    q35_f32x4 sum = part[0][lane];
+    if (wv >= TPB) return;                 // wave t sums tile t's k-block chains in order
+    q35_f32x4 sum = part[wv][0][lane];
     for (int w = 1; w < KB; ++w) {
-        q35_f32x4 p = part[w][lane];
+        q35_f32x4 p = part[wv][w][lane];
 #pragma unroll
         for (int r = 0; r < 4; ++r) sum[r] = sum[r] + p[r];
     }
@@ -379,7 +391,7 @@ __global__ void __launch_bounds__(1024) gemm_small_m(GemmArgs a) {
         }
         return;
     }
-    epilogue<EM>(a, sum, nt, mt * 16, lane);
+    epilogue<EM>(a, sum, nt + wv, mt * 16, lane);
 }
 
 // Elementwise A producer for batched launches: Y[m][k] = produce_a(m, k) (bf16), so the
@@ -522,6 +534,8 @@ __global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
 // loads) adds no wait for all loads; every wait is explicit and tied to the registers it
 // guards. At 256 lanes: gate|up 17.1 us (pipelined kernel 18.2), attention qkv 11.9 (14.8).
 constexpr int kPreKB = kHidden / 256;
+int g_gemv_tpb = 2;
+void set_gemv_tpb(int v) { g_gemv_tpb = v; }
 int g_gemm_pre = 1;
 void set_gemm_pre(int on) { g_gemm_pre = on; }
 
@@ -877,6 +891,9 @@ static hipError_t launch_am_em(const GemmArgs& a, hipStream_t st) {
         const size_t lds = AM == kAPlain ? 0 : (size_t)waves * (512 * 16 + 64 * 4);
         if (EM == kEPartial)
             hipLaunchKernelGGL((gemm_small_m<AM, EM>), dim3(a.N / 16, 1, KB), dim3(64), lds, st, a);
+        else if ((AM == kANormX || AM == kANormXP) && EM == kEStore && a.M == 1 && g_gemv_tpb == 2 &&
+                 a.N % 32 == 0 && a.N >= 4096 && KB == 4)
+            hipLaunchKernelGGL((gemm_small_m<AM, EM, 2>), dim3(a.N / 32, 1, 1), dim3(64 * KB), 0, st, a);
         else
             hipLaunchKernelGGL((gemm_small_m<AM, EM>), dim3(a.N / 16, 1, 1), dim3(64 * KB), lds, st, a);
         return hipGetLastError();
