@@ -140,7 +140,13 @@ int q35_sync(q35_engine* e);
  * since the option was set or last read, and resets them. */
 int q35_kprof_read(q35_engine* e, float* total_ms, int* launches);
 /* Options: "layers" (diagnostic: bodies run only the first n of the 24 layers, the final
- * norm then applies to that layer's output), "graph" (0/1). */
+ * norm then applies to that layer's output), "graph" (0/1: capture decode steps), "kprof"
+ * (above), "gdn_chunked" (0/1: chunked GDN form for prompt waves of >= 64 rows). Kernel-form
+ * switches, each bit-identical to its alternative and kept for A/B measurement, dropping the
+ * engine's captured steps when set: "b1_partials" (this engine: one-row bodies leave k-block
+ * chains for the next norm GEMV) and, process-wide (every engine of the process), "gemv_tpb"
+ * (1/2 column tiles per block of the one-row norm GEMVs), "gemm_pre" (batched K = 1024 GEMMs
+ * issue all loads up front), "lmhead_persist" (persistent lm_head at batched lanes). */
 int q35_set_option(q35_engine* e, const char* name, int value);
 /* Copy the current content of a named scratch buffer ("x", "h", "nrm", "delta", "proj",
  * "o", "gu", "aout", "q") to host, after the stream drains (diagnostics and tests). */

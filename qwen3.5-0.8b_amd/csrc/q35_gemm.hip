@@ -534,9 +534,9 @@ __global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
 // loads) adds no wait for all loads; every wait is explicit and tied to the registers it
 // guards. At 256 lanes: gate|up 17.1 us (pipelined kernel 18.2), attention qkv 11.9 (14.8).
 constexpr int kPreKB = kHidden / 256;
-int g_gemv_tpb = 2;
+static int g_gemv_tpb = 2;
 void set_gemv_tpb(int v) { g_gemv_tpb = v; }
-int g_gemm_pre = 1;
+static int g_gemm_pre = 1;
 void set_gemm_pre(int on) { g_gemm_pre = on; }
 
 template <int MT> constexpr int pre_lds_bytes() { return kPreKB * MT * 8 * 64 * 16; }
@@ -679,7 +679,7 @@ __global__ void __launch_bounds__(256) gemm_pre(GemmArgs a) {
 // tile from LDS; <4, 4> at one wave per SIMD: 420 us). The row blocks of one column stream
 // sit on one XCD and share each weight unit through its L2.
 // Reduction order = the canonical one above (chain per k-block from zero, summed in order).
-int g_lmhead_persist = 1;
+static int g_lmhead_persist = 1;
 void set_lmhead_persist(int on) { g_lmhead_persist = on; }
 constexpr int kLmKB = kHidden / 256;
 constexpr int kLmLds = 4 * kLmKB * 8 * 64 * 16;          // 128 KiB of A fragments
