@@ -146,7 +146,10 @@ int q35_kprof_read(q35_engine* e, float* total_ms, int* launches);
  * engine's captured steps when set: "b1_partials" (this engine: one-row bodies leave k-block
  * chains for the next norm GEMV) and, process-wide (every engine of the process), "gemv_tpb"
  * (1/2 column tiles per block of the one-row norm GEMVs), "gemm_pre" (batched K = 1024 GEMMs
- * issue all loads up front), "lmhead_persist" (persistent lm_head at batched lanes). */
+ * issue all loads up front), "lmhead_persist" (persistent lm_head at batched lanes). Not
+ * bit-identical, a different rounding point within the stated tolerance: "attn_prompt"
+ * (process-wide; 1: prompt waves of one lane with >= 64 rows use the flash-form MFMA
+ * attention kernel, 0: the one-row kernels). */
 int q35_set_option(q35_engine* e, const char* name, int value);
 /* Copy the current content of a named scratch buffer ("x", "h", "nrm", "delta", "proj",
  * "o", "gu", "aout", "q") to host, after the stream drains (diagnostics and tests). */

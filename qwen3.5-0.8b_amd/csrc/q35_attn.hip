@@ -17,6 +17,7 @@
 // The k cache holds bf16(k post-rope); the reference's torch path keeps it in f32, so
 // k's rotated dims carry one extra bf16 rounding here (the cache layout is bf16 by design).
 #include <algorithm>
+#include <type_traits>
 
 #include "q35_common.h"
 #include "q35_kernels.h"
@@ -492,8 +493,263 @@ __global__ void __launch_bounds__(256) attn_fused(AttnArgs a, int lds_slots) {
     for (int i = 0; i < 4; ++i) a.out[(size_t)r * 2048 + (4 * j + i) * 256 + tid] = gated_out(a, r, 4 * j + i, tid, acc[i]);
 }
 
+// ---------------------------------------------------------------- prompt waves (flash form)
+// A prompt wave of one lane (T >= 64 rows at consecutive slots): all of its rows read the
+// same K/V, so a block takes 16 rows x the 4 q heads of one kv head (64 query columns) and
+// streams the lane's K/V once for all of them, with both products on MFMA:
+//   S^T = K Q^T   A = the K cache's fragments (16 slots x 32 dims per step), B = q as bf16 hi
+//                 (8 steps) plus its lo part on the rotated dims 0..63 (2 steps): the
+//                 decode path's split of the f32 post-rope q; wave w owns columns
+//                 (row 4w + n/4, head n%4) and streams every K tile itself
+//   online softmax per column over 64-slot tiles (running max and sum in f32, e^(s - m)
+//                 rounded to bf16 as the P.V operand)
+//   O = P V       A = P straight from the S^T accumulators (lane (column, g) holds slots
+//                 4g + r of each 16-slot sub-tile: the MFMA's k index is taken in that order),
+//                 B = V columns read from LDS with ds_read_b64_tr_b16 (a 16-lane group reads
+//                 4 slots x 16 dims and receives them transposed), V tiles staged in LDS by
+//                 all 4 waves with 16-byte chunks XOR-swizzled by slot
+// The softmax normalisation comes last (O / l), so the bf16 rounding of the weights happens
+// before it rather than after as on the decode path (speccheck/specimpl.py:385-392 rounds
+// the normalised weights): same math, different rounding point -- prompt logits stay within
+// the engine-vs-oracle tolerance, not bit-equal to the one-row kernels.
+constexpr int kPrRows = 16;
+typedef short q35_s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int pr_swz(int t, int c) { return c ^ ((t & 15) << 1); }   // c: 16-byte chunk 0..31
+
+static int g_attn_prompt = 1;
+void set_attn_prompt(int on) { g_attn_prompt = on; }
+
+constexpr int kPrLds = 4 * 64 * 256 * 2;     // K and V tiles, double-buffered: 128 KiB
+
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 q35_bf16x2;
+// two f32 -> packed bf16 (round to nearest even, v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+    const q35_bf16x2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t pr_lds[];
+    uint16_t(*kt)[64 * 256] = (uint16_t(*)[64 * 256])pr_lds;
+    uint16_t(*vt)[64 * 256] = (uint16_t(*)[64 * 256])(pr_lds + 2 * 64 * 256);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int T = a.T, ngrp = (T + kPrRows - 1) / kPrRows;
+    // XCDs 0-3 take kv head 0 and 4-7 kv head 1: each XCD's L2 holds one head's K/V stream
+    const int xcd = blockIdx.x & 7, j = xcd >> 2;
+    const int grp = (blockIdx.x >> 3) * 4 + (xcd & 3);
+    if (grp >= ngrp) return;
+    const int r0 = grp * kPrRows;
+    const int lrow = a.rm.lane[0];
+    const int smax = a.rm.slot[min(r0 + kPrRows, T) - 1];
+    const int qrow = min(r0 + 4 * wv + (n >> 2), T - 1);
+    const int qslot = a.rm.slot[qrow];
+    const int wslot = a.rm.slot[min(r0 + 4 * wv, T - 1)];     // the wave's smallest slot
+    const size_t kvbase = lrow * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256;
+
+    // q fragments of column n: dims s*32 + g*8 .. +8
+    q35_u32x4 qhi[8], qlo[2];
+    {
+        const float* qp = a.q + ((size_t)qrow * kNq + 4 * j + (n & 3)) * 256 + g * 8;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const float4 x0 = *(const float4*)(qp + s * 32), x1 = *(const float4*)(qp + s * 32 + 4);
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            uint16_t h[8], l[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                h[e] = f2bf(xs[e]);
+                l[e] = f2bf(xs[e] - bf2f(h[e]));
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qhi[s][e] = (uint32_t)h[2 * e] | ((uint32_t)h[2 * e + 1] << 16);
+            if (s < 2) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qlo[s][e] = (uint32_t)l[2 * e] | ((uint32_t)l[2 * e + 1] << 16);
+            }
+        }
+    }
+    const int ntiles = smax / 64 + 1;
+    // K and V tiles (64 slots) reach LDS by direct-to-LDS loads (global_load_lds: lane i of
+    // an instruction fills the 16-byte slot i of a 1 KiB run), issued one tile ahead: K in its
+    // cache layout (four 16-slot MFMA tiles, 32 KiB contiguous), V with each row's 16-byte
+    // chunks XOR-swizzled by slot. Cached loads: the 12 blocks of a kv head on one XCD read
+    // the same tiles and all but the first hit that XCD's L2. Slots past the group's last are
+    // clamped to it (K: scores masked; V: weights zero, values finite). The wave's 8 K and 8 V
+    // runs per tile are its only vector-memory loads in the loop, so "s_waitcnt vmcnt(0)"
+    // at the top of a tile waits for exactly that tile's data; every LDS read below is
+    // inline asm, which keeps the compiler from waiting on the prefetch in flight.
+    auto issue_tiles = [&](int it, int buf) {
+        const int t0 = it * 64;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int run = wv * 8 + i;                   // 1 KiB run of the 32 KiB tile
+            const int tile = min(it * 4 + (run >> 3), smax >> 4);
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(a.kc + kvbase + (size_t)tile * 4096 + (run & 7) * 512 + lane * 8),
+                (__attribute__((address_space(3))) void*)&kt[buf][run * 512], 16, 0, 0);
+            const int row = 2 * run + (lane >> 5), pos = lane & 31;
+            const int slot = min(t0 + row, smax);
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(a.vc + kvbase + (size_t)slot * 256 + pr_swz(row, pos) * 8),
+                (__attribute__((address_space(3))) void*)&vt[buf][run * 512], 16, 0, 0);
+        }
+    };
+    issue_tiles(0, 0);
+
+    float m_run = -INFINITY, l_run = 0.f;
+    q35_f32x4 o[16];
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) o[dt] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
+    // LDS byte offsets: K fragment (sub-tile st, step s) at st*8192 + s*1024 + lane*16; V
+    // transposed reads: source lane n of group g points at slot (4g + n/4) + 16c + 32ks of
+    // the tile, dims 16 dt + 4 (n % 4) .. +4 (chunk 2 dt + (n % 4) / 2, swizzled by slot)
+    const unsigned kb0 = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&kt[0][0] + lane * 16;
+    const unsigned vb0 = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&vt[0][0];
+    const int trow = 4 * g + (n >> 2);
+    unsigned voff[2][2][16];      // [ks][c][dt]
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int dt = 0; dt < 16; ++dt) {
+                const int row = 32 * ks + 16 * c + trow;
+                const int ch = 2 * dt + ((n & 3) >> 1);
+                voff[ks][c][dt] = vb0 + (unsigned)(row * 512 + pr_swz(row, ch) * 16 + (n & 1) * 8);
+            }
+
+    for (int it = 0; it < ntiles; ++it) {
+        const int t0 = it * 64, buf = it & 1;
+        // this tile's loads have landed (the only ones in flight), and every wave is done
+        // with the other buffer (tile it - 1) before it is refilled
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (it + 1 < ntiles) issue_tiles(it + 1, buf ^ 1);
+        const unsigned kbase = kb0 + (unsigned)(buf * 64 * 256 * 2);
+        float sv[4][4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            q35_u32x4 kf[8];
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kf[s]) : "v"(kbase), "n"(st * 8192 + s * 1024) : "memory");
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3]), "+v"(kf[4]), "+v"(kf[5]), "+v"(kf[6]), "+v"(kf[7]));
+            q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&kf[s], *(q35_bf16x8*)&qhi[s], acc, 0, 0, 0);
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&kf[s], *(q35_bf16x8*)&qlo[s], acc, 0, 0, 0);
+            // scores in the log2 domain: s / 16 * log2(e)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sv[st][r] = acc[r] * (0.0625f * 1.4426950408889634f);
+        }
+        if (t0 + 63 > wslot) {            // a tile crossing the diagonal of some column of the wave
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (t0 + st * 16 + 4 * g + r > qslot) sv[st][r] = -INFINITY;
+        }
+        // online softmax of column n over this tile
+        float mt = -INFINITY;
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sv[st][r]);
+        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+        mt = fmaxf(mt, xor32(mt));
+        const float mnew = fmaxf(m_run, mt);      // finite: slot 0 is in every column's first tile
+        const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);   // exp2(-inf) = 0 on the first tile
+        // P as the A operand, bf16 (k = g*8 + e <-> slot 32 ks + 16 (e / 4) + 4g + e % 4); the
+        // running sum adds the rounded weights that P.V uses
+        q35_u32x4 pa[2];
+        float ps = 0.f;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            float pv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pv[r] = __builtin_amdgcn_exp2f(sv[st][r] - mnew);   // masked: 0
+            const uint32_t w0 = pk_bf16(pv[0], pv[1]), w1 = pk_bf16(pv[2], pv[3]);
+            pa[st >> 1][2 * (st & 1)] = w0;
+            pa[st >> 1][2 * (st & 1) + 1] = w1;
+            ps += (__uint_as_float(w0 << 16) + __uint_as_float(w0 & 0xffff0000u)) +
+                  (__uint_as_float(w1 << 16) + __uint_as_float(w1 & 0xffff0000u));
+        }
+        ps += __shfl_xor(ps, 16, 64);
+        ps += xor32(ps);
+        l_run = l_run * alpha + ps;
+        m_run = mnew;
+        // rescale O rows 4g + r by their columns' alpha -- only when some column's max moved
+        if (__any(alpha != 1.f)) {
+            float ar[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+            for (int dt = 0; dt < 16; ++dt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[dt][r] *= ar[r];
+        }
+        // P.V: V fragments 8 d-tiles at a time (16 transposed reads, one wait, 8 MFMAs)
+        const unsigned vbuf = (unsigned)(buf * 64 * 256 * 2);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int dh = 0; dh < 2; ++dh) {
+                uint2 v0[8], v1[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v0[u]) : "v"(voff[ks][0][8 * dh + u] + vbuf) : "memory");
+                    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v1[u]) : "v"(voff[ks][1][8 * dh + u] + vbuf) : "memory");
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)"
+                             : "+v"(v0[0]), "+v"(v0[1]), "+v"(v0[2]), "+v"(v0[3]), "+v"(v0[4]), "+v"(v0[5]), "+v"(v0[6]), "+v"(v0[7]),
+                               "+v"(v1[0]), "+v"(v1[1]), "+v"(v1[2]), "+v"(v1[3]), "+v"(v1[4]), "+v"(v1[5]), "+v"(v1[6]), "+v"(v1[7]));
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    q35_u32x4 b = {v0[u].x, v0[u].y, v1[u].x, v1[u].y};
+                    o[8 * dh + u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&pa[ks], *(q35_bf16x8*)&b,
+                                                                           o[8 * dh + u], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // O / l, bf16, times bf16(sigmoid(gate)): lane (n, g) holds row 4 wv + g, head r, dims 16 dt + n
+    const int row = r0 + 4 * wv + g;
+    float lr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lr[r] = __shfl(l_run, 4 * g + r, 64);
+    if (row < T) {
+        // every gate value loaded before the first store (a store to out could alias proj,
+        // which would otherwise serialize each load behind the previous store)
+        const uint16_t* pr = a.proj + (size_t)row * kAttnInRows + 256 + n;
+        uint16_t gv[4][16];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int dt = 0; dt < 16; ++dt) gv[r][dt] = pr[(4 * j + r) * 512 + 16 * dt];
+        uint16_t* po = a.out + (size_t)row * 2048 + 4 * j * 256 + n;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+            for (int dt = 0; dt < 16; ++dt) {
+                const float ov = rbf(o[dt][r] / lr[r]);
+                const float gt = rbf(sigmoid_f(bf2f(gv[r][dt])));
+                po[r * 256 + 16 * dt] = f2bf(ov * gt);
+            }
+        }
+    }
+}
+
 hipError_t attn_init() {
-    return hipFuncSetAttribute((const void*)attn_fused, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+    const hipError_t e = hipFuncSetAttribute((const void*)attn_fused, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute((const void*)attn_prompt, hipFuncAttributeMaxDynamicSharedMemorySize, kPrLds);
 }
 
 static size_t fused_lds(const AttnArgs& a) {
@@ -514,7 +770,11 @@ hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
     if (a.R <= 0 || a.max_chunks <= 0) return hipErrorInvalidValue;
     const int lds_slots = (a.cap + 63) / 64 * 64;
     const size_t lds = fused_lds(a);
-    if (use_fused(a)) {
+    if (g_attn_prompt && a.T >= 64 && a.R == a.T) {
+        // one lane's prompt wave: 16 rows per block, kv head by XCD half
+        const int ngrp = (a.T + kPrRows - 1) / kPrRows;
+        hipLaunchKernelGGL(attn_prompt, dim3((ngrp + 3) / 4 * 8), dim3(256), kPrLds, st, a);
+    } else if (use_fused(a)) {
         if (a.T < 1 || a.R % a.T) return hipErrorInvalidValue;
         const int pairs = a.R / a.T * kNkv;
         const int nseg = std::max(1, 8 / pairs), seg = (a.T + nseg - 1) / nseg;

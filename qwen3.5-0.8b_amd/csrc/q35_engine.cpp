@@ -1326,6 +1326,11 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
         } else if (n == "gdn_chunked") {
             HCK(hipStreamSynchronize(e->st));
             e->gdn_chunked = value ? 1 : 0;
+        } else if (n == "attn_prompt") {         // process-wide kernel choice; drops captured steps
+            HCK(hipStreamSynchronize(e->st));
+            set_attn_prompt(value ? 1 : 0);
+            for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
+            e->graphs.clear();
         } else if (n == "gemv_tpb") {            // process-wide kernel choice; drops captured steps
             REQ(value == 1 || value == 2, Q35_ERR_ARG, "gemv_tpb is 1 or 2");
             HCK(hipStreamSynchronize(e->st));

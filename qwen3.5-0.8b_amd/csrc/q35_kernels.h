@@ -121,6 +121,7 @@ struct AttnArgs {
 hipError_t launch_attn_prep(const AttnArgs& a, hipStream_t st);   // q/k norm + rope, cache append
 hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st);   // scores, softmax, P.V, gate
 hipError_t attn_init();   // one-time kernel attribute setup
+void set_attn_prompt(int on);  // prompt waves of >= 64 rows: flash-form MFMA kernel (1) or the one-row kernels (0)
 
 // Synthetic init (portable stream, see q35_init.hip).
 hipError_t launch_gen_normal_tiled(uint64_t key, float scale, int N, int K, int row_off_dst,
