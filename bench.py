@@ -185,6 +185,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mtp-rounds", type=int, default=5, help="config 4 (MTP k=2) rounds; 0 skips it")
     ap.add_argument("--prefill-len", type=int, default=4096, help="one-lane prompt prefill length; 0 skips it")
+    ap.add_argument("--prefill-rows", type=int, default=2048, help="prompt wave rows (the engine's max_rows)")
     ap.add_argument("--eager", action="store_true", help="launch kernels eagerly (no hipGraph)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run one 1 GiB device-to-device torch copy first (counter calibration: "
@@ -206,7 +207,7 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    eng = Engine(max_rows=max(3 * B, 64), max_ctx=L + max(args.steps, args.b1_steps) + args.warmup + 64, seed=0,
+    eng = Engine(max_rows=max(3 * B, 64, args.prefill_rows), max_ctx=L + max(args.steps, args.b1_steps) + args.warmup + 64, seed=0,
                  use_graph=not args.eager)
     # timed value: graph replay, no per-kernel events
     wall, ev_s, _ = run_decode(eng, B, L, args.steps, args.warmup, None)

@@ -178,18 +178,38 @@ __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
             }
     }
     __syncthreads();
-    // ---- q' = q~ e^cum and k' = k~ e^(cum_63 - cum) in operand order (before the solve reuses qn)
+    // ---- q' = q~ e^cum and k' = k~ e^(cum_63 - cum) in operand order (before the solve reuses qn).
+    // The workspace is written as whole 16-byte vectors, consecutive threads on consecutive
+    // vectors: each thread gathers the vector's 4 elements from LDS.
+    if (tid < kC) ut[tid][kC] = expf(cum[kC - 1] - cum[tid]);      // e^(cum_63 - cum_i), column kC spare
+    __syncthreads();
     {
-        const float clast = cum[kC - 1];
-        for (int e = tid; e < kC * 128; e += 256) {
-            const int i = e >> 7, d = e & 127;
-            // q': A[m = i][k = d] -> [i / 16][lane (d % 4, i % 16)][d / 4]
-            ws[kWsQ + (((i >> 4) * 64 + (d & 3) * 16 + (i & 15)) * 32 + (d >> 2))] = qn[i][d] * ecum[i];
-            // k'^T: A[m = d][kk = i] -> [d / 32][(d % 32) / 16][lane (i % 4, d % 16)][i / 4]
-            ws[kWsK + ((((d >> 5) * 2 + ((d >> 4) & 1)) * 64 + (i & 3) * 16 + (d & 15)) * 16 + (i >> 2))] =
-                kn[i][d] * expf(clast - cum[i]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int u = tid + 256 * k;
+            // q': A[m = i][k = d] -> [i / 16][lane (d % 4, i % 16)][d / 4]; vector u = (lane slot, d/4 quad)
+            {
+                const int q = u & 7, ln = (u >> 3) & 63, i = (u >> 9) * 16 + (ln & 15), dq = ln >> 4;
+                float4 v;
+                v.x = qn[i][16 * q + dq] * ecum[i];
+                v.y = qn[i][16 * q + 4 + dq] * ecum[i];
+                v.z = qn[i][16 * q + 8 + dq] * ecum[i];
+                v.w = qn[i][16 * q + 12 + dq] * ecum[i];
+                *(float4*)&ws[kWsQ + 4 * u] = v;
+            }
+            // k'^T: A[m = d][kk = i] -> [d / 16][lane (i % 4, d % 16)][i / 4]; vector u = (lane slot, i/4 quad)
+            {
+                const int q = u & 3, ln = (u >> 2) & 63, d = (u >> 8) * 16 + (ln & 15), iq = ln >> 4;
+                float4 v;
+                const int i0 = 16 * q + iq;
+                v.x = kn[i0][d] * ut[i0][kC];
+                v.y = kn[i0 + 4][d] * ut[i0 + 4][kC];
+                v.z = kn[i0 + 8][d] * ut[i0 + 8][kC];
+                v.w = kn[i0 + 12][d] * ut[i0 + 12][kC];
+                *(float4*)&ws[kWsK + 4 * u] = v;
+            }
         }
-        if (tid == 0) a.chunk_cdec[c * kHv + h] = expf(clast);
+        if (tid == 0) a.chunk_cdec[c * kHv + h] = expf(cum[kC - 1]);
     }
     __syncthreads();
     // ---- (I + ut) X = R for R = beta v (X in vv) and R = beta k~ e^cum (X in qn), blocked by
@@ -232,13 +252,29 @@ __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
             for (int ii = 0; ii < 16; ++ii) X[bb * 16 + ii][col] = x[ii];
         }
         __syncthreads();
-        float(*X)[129] = isk ? qn : vv;
-        if (isk) {      // kcd: A[m = i][k = col] -> [i / 16][lane (col % 4, i % 16)][col / 4]
-            for (int i = 0; i < kC; ++i)
-                ws[kWsKcd + (((i >> 4) * 64 + (col & 3) * 16 + (i & 15)) * 32 + (col >> 2))] = X[i][col];
-        } else {        // nv: C layout of slice col / 16 -> [slice][i / 16][lane ((i % 16) / 4, col % 16)][i % 4]
-            for (int i = 0; i < kC; ++i)
-                ws[kWsNv + ((((col >> 4) * 4 + (i >> 4)) * 64 + ((i & 15) >> 2) * 16 + (col & 15)) * 4 + (i & 3))] = X[i][col];
+        // 16-byte vectors gathered from LDS, consecutive threads on consecutive vectors
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int u = tid + 256 * k;
+            {   // kcd: A[m = i][k = col] -> [i / 16][lane (col % 4, i % 16)][col / 4]
+                const int q = u & 7, ln = (u >> 3) & 63, i = (u >> 9) * 16 + (ln & 15), cq = ln >> 4;
+                float4 v;
+                v.x = qn[i][16 * q + cq];
+                v.y = qn[i][16 * q + 4 + cq];
+                v.z = qn[i][16 * q + 8 + cq];
+                v.w = qn[i][16 * q + 12 + cq];
+                *(float4*)&ws[kWsKcd + 4 * u] = v;
+            }
+            {   // nv: C layout of slice col / 16 -> [slice][i / 16][lane ((i % 16) / 4, col % 16)][i % 4]
+                const int ln = u & 63, ib = (u >> 6) & 3, sl = u >> 8;
+                const int i0 = ib * 16 + (ln >> 4) * 4, cl = sl * 16 + (ln & 15);
+                float4 v;
+                v.x = vv[i0][cl];
+                v.y = vv[i0 + 1][cl];
+                v.z = vv[i0 + 2][cl];
+                v.w = vv[i0 + 3][cl];
+                *(float4*)&ws[kWsNv + 4 * u] = v;
+            }
         }
     }
 }
