@@ -527,7 +527,7 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
             const bool chunked = e->gdn_chunked && !small && nl == 1 && T >= 64 && !ckpt;
             const bool fused_norm = !small && cs == 1 && !chunked;   // whole-head blocks: norm in the GDN kernel
             if (fused_norm) { g.y = e->prod; g.gnorm = w.gnorm; }
-            g.chunk_ws = e->gchunk; g.chunk_cdec = e->gcdec;
+            g.chunk_ws = e->gchunk; g.chunk_cdec = e->gcdec; g.conv_u = e->gu;   // gu is free until the MLP
             {
                 KTimer kt(e, kFamGdn);
                 if (chunked) HCK(launch_gdn_chunked(g, e->st));

@@ -1,9 +1,12 @@
 // GatedDeltaNet over a prompt wave of one lane in the chunked (UT-transform) form, chunk 64
 // (speccheck/specimpl.py:187-235; the reference engine's gdn_chunk_prefill,
-// engine/kernels_gdn.cpp:488). Two kernels:
+// engine/kernels_gdn.cpp:488). Three kernels:
 //
-//   gdn_chunk_prep  grid (chunk, head): causal conv + bf16 SiLU, L2 norms and gates with the
-//                   recurrent kernel's arithmetic; then, within the chunk, the decay prefix
+//   gdn_chunk_conv  grid (16-row run, 256 channels): causal conv + bf16 SiLU of every (row,
+//                   channel) of the wave with the recurrent kernel's arithmetic -> conv_u, and
+//                   the conv window after the wave
+//   gdn_chunk_prep  grid (chunk, head): L2 norms and gates with the recurrent kernel's
+//                   arithmetic; then, within the chunk, the decay prefix
 //                   cum_i = g_0 + .. + g_i, the pairwise-decayed products
 //                   ut = (beta k~) k~^T (strictly lower) and intra = q~ k~^T (lower), the two
 //                   unit-lower-triangular solves (I + ut) nv = beta v and
@@ -40,72 +43,73 @@ __device__ __forceinline__ q35_f32x4 mfma4(float av, float bv, q35_f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, c, 0, 0, 0);
 }
 
+constexpr int kConvRows = 16;
+
+__global__ void __launch_bounds__(256) gdn_chunk_conv(GdnArgs a) {
+    const int ch = blockIdx.y * 256 + threadIdx.x;       // 0..6143: q | k | v channels
+    const int t0 = blockIdx.x * kConvRows;
+    const int n = min(kConvRows, a.T - t0);
+    const int lane = a.lane[0];
+    const int cur = a.cur ? a.cur[lane] : 0;
+    const float* Win = a.win + lane * a.W_lane + a.W_layer + cur * a.W_slot;
+    const uint2 cpk = *(const uint2*)(a.conv_w + (size_t)ch * 4);
+    const float cw0 = __uint_as_float(cpk.x << 16), cw1 = __uint_as_float(cpk.x & 0xffff0000u);
+    const float cw2 = __uint_as_float(cpk.y << 16), cw3 = __uint_as_float(cpk.y & 0xffff0000u);
+    // raw rows t0-3 .. t0-1: earlier rows of the wave, or the lane's window before it
+    auto raw = [&](int t) -> float {
+        return t >= 0 ? bf2f(a.proj[(size_t)t * kGdnInRows + ch]) : Win[(t + 3) * 6144 + ch];
+    };
+    float w0 = raw(t0 - 3), w1 = raw(t0 - 2), w2 = raw(t0 - 1);
+    uint16_t xr[kConvRows];
+#pragma unroll
+    for (int i = 0; i < kConvRows; ++i) xr[i] = a.proj[(size_t)min(t0 + i, a.T - 1) * kGdnInRows + ch];
+    uint16_t* u = a.conv_u + (size_t)t0 * 6144 + ch;
+#pragma unroll
+    for (int i = 0; i < kConvRows; ++i) {
+        if (i < n) {
+            const float x = bf2f(xr[i]);
+            float v = 0.f;
+            v = v + w0 * cw0; v = v + w1 * cw1; v = v + w2 * cw2; v = v + x * cw3;
+            u[(size_t)i * 6144] = f2bf(silu_f(rbf(v)));
+            w0 = w1; w1 = w2; w2 = x;
+        }
+    }
+    if (t0 + kConvRows >= a.T) {      // the run holding the wave's last row: window after the wave
+        float* Wo = a.win + lane * a.W_lane + a.W_layer + ((cur + 1) % a.nslots) * a.W_slot;
+        Wo[ch] = w0; Wo[6144 + ch] = w1; Wo[12288 + ch] = w2;
+    }
+}
+
 __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
     const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
     const int t0 = c * kC;
     const int nrow = min(kC, a.T - t0);
-    const int lane = a.lane[0];
-    const int cur = a.cur ? a.cur[lane] : 0;
-    const float* Win = a.win + lane * a.W_lane + a.W_layer + cur * a.W_slot;
 
     __shared__ float qn[kC][129], kn[kC][129], vv[kC][129];
     __shared__ float ut[kC][kC + 1];
     __shared__ float gl[kC], bl[kC], cum[kC], ecum[kC];
 
-    // ---- causal conv + SiLU: tid < 128 -> q channel (and v channel), else k channel
+    // ---- post-conv SiLU values (gdn_chunk_conv) of the head's q, k and v channels as 16-byte
+    // runs: 64 rows x 48 runs of 8 channels, 12 per thread; rows past the wave are zero
     {
-        const int cqk = tid < 128 ? h * 128 + tid : 2048 + h * 128 + (tid - 128);
-        const int cv = 4096 + h * 128 + tid;
-        const bool hasv = tid < 128;
-        const uint2 cpk = *(const uint2*)(a.conv_w + (size_t)cqk * 4);
-        const float cw0 = __uint_as_float(cpk.x << 16), cw1 = __uint_as_float(cpk.x & 0xffff0000u);
-        const float cw2 = __uint_as_float(cpk.y << 16), cw3 = __uint_as_float(cpk.y & 0xffff0000u);
-        float vw0 = 0.f, vw1 = 0.f, vw2 = 0.f, vw3 = 0.f;
-        if (hasv) {
-            const uint2 d = *(const uint2*)(a.conv_w + (size_t)cv * 4);
-            vw0 = __uint_as_float(d.x << 16); vw1 = __uint_as_float(d.x & 0xffff0000u);
-            vw2 = __uint_as_float(d.y << 16); vw3 = __uint_as_float(d.y & 0xffff0000u);
-        }
-        // raw rows t0-3 .. t0-1: earlier rows of the wave, or the lane's window before it
-        auto raw = [&](int t, int ch) -> float {
-            return t >= 0 ? bf2f(a.proj[(size_t)t * kGdnInRows + ch]) : Win[(t + 3) * 6144 + ch];
-        };
-        float w0 = raw(t0 - 3, cqk), w1 = raw(t0 - 2, cqk), w2 = raw(t0 - 1, cqk);
-        float v0 = 0.f, v1 = 0.f, v2 = 0.f;
-        if (hasv) { v0 = raw(t0 - 3, cv); v1 = raw(t0 - 2, cv); v2 = raw(t0 - 1, cv); }
-        // every row's raw value first (rows past the wave read the last row and are masked)
-        uint16_t xr[kC], xvr[kC];
+        q35_u32x4 xr[12];
 #pragma unroll
-        for (int i = 0; i < kC; ++i) {
-            const uint16_t* pr = a.proj + (size_t)min(t0 + i, a.T - 1) * kGdnInRows;
-            xr[i] = pr[cqk];
-            xvr[i] = hasv ? pr[cv] : (uint16_t)0;
+        for (int k = 0; k < 12; ++k) {
+            const int id = tid + 256 * k, row = id / 48, cc = id % 48;
+            const int ch = (cc >> 4) * 2048 + h * 128 + (cc & 15) * 8;
+            xr[k] = *(const q35_u32x4*)(a.conv_u + (size_t)min(t0 + row, a.T - 1) * 6144 + ch);
         }
 #pragma unroll
-        for (int i = 0; i < kC; ++i) {
-            float uq = 0.f, uvv = 0.f;
-            if (i < nrow) {
-                const float x = bf2f(xr[i]);
-                float u = 0.f;
-                u = u + w0 * cw0; u = u + w1 * cw1; u = u + w2 * cw2; u = u + x * cw3;
-                uq = rbf(silu_f(rbf(u)));
-                w0 = w1; w1 = w2; w2 = x;
-                if (hasv) {
-                    const float xv = bf2f(xvr[i]);
-                    float uv = 0.f;
-                    uv = uv + v0 * vw0; uv = uv + v1 * vw1; uv = uv + v2 * vw2; uv = uv + xv * vw3;
-                    uvv = rbf(silu_f(rbf(uv)));
-                    v0 = v1; v1 = v2; v2 = xv;
-                }
+        for (int k = 0; k < 12; ++k) {
+            const int id = tid + 256 * k, row = id / 48, cc = id % 48;
+            float(*dst)[129] = cc < 16 ? qn : cc < 32 ? kn : vv;
+            const int d0 = (cc & 15) * 8;
+            const bool ok = row < nrow;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                dst[row][d0 + 2 * e] = ok ? __uint_as_float(xr[k][e] << 16) : 0.f;
+                dst[row][d0 + 2 * e + 1] = ok ? __uint_as_float(xr[k][e] & 0xffff0000u) : 0.f;
             }
-            if (tid < 128) qn[i][tid] = uq; else kn[i][tid - 128] = uq;
-            if (hasv) vv[i][tid] = uvv;
-        }
-        // the chunk holding the wave's last row writes the window after the wave
-        if (t0 + kC >= a.T) {
-            float* Wo = a.win + lane * a.W_lane + a.W_layer + ((cur + 1) % a.nslots) * a.W_slot;
-            Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2;
-            if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
         }
     }
     // ---- gates (rows past the wave: g = 0, beta = 0)
@@ -378,6 +382,8 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
 hipError_t launch_gdn_chunked(const GdnArgs& a, hipStream_t st) {
     if (a.nlanes != 1 || a.T < 1 || a.ckpt || !a.chunk_ws || !a.chunk_cdec) return hipErrorInvalidValue;
     const int nchunks = (a.T + kC - 1) / kC;
+    if (!a.conv_u) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gdn_chunk_conv, dim3((a.T + kConvRows - 1) / kConvRows, 6144 / 256), dim3(256), 0, st, a);
     hipLaunchKernelGGL(gdn_chunk_prep, dim3(nchunks, kHv), dim3(256), 0, st, a);
     hipLaunchKernelGGL(gdn_chunk_scan, dim3(kHv, 8), dim3(256), 0, st, a, nchunks);
     return hipGetLastError();

@@ -84,9 +84,11 @@ struct GdnArgs {
     // y[r][h*128 + j] = bf16(w[j] * (o * rsqrt(mean_head(o^2) + eps)) * silu(z)), bf16 [R][2048]
     uint16_t* y;
     const uint16_t* gnorm;     // [128]
-    // Chunked prompt form (one lane, no checkpoints): per-(chunk, head) workspace and decays
+    // Chunked prompt form (one lane, no checkpoints): per-(chunk, head) workspace and decays,
+    // and the wave's post-conv SiLU values [T][6144] bf16
     float* chunk_ws;
     float* chunk_cdec;
+    uint16_t* conv_u;
 };
 hipError_t launch_gdn(const GdnArgs& a, int col_slices, hipStream_t st);
 // Chunked (UT-transform, chunk 64) form over the T rows of one lane: same state/window slot
