@@ -20,6 +20,8 @@
 //
 // The state is read from slot cur and written to slot (cur + 1) % nslots, the conv window
 // likewise, exactly as the recurrent kernel does for a wave without checkpoints.
+#include <type_traits>
+
 #include "q35_common.h"
 #include "q35_kernels.h"
 
@@ -300,7 +302,8 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
     const int mr = ln & 15, kq = ln >> 4;          // A row / k-quad of this lane
     // this wave's A operands of one chunk, in registers: kcd and q' rows 16w + mr (k = 4ks + kq),
     // intra row 16w + mr (j = 4ks + kq), k'^T rows 32w + 16 half + mr (i = 4ks + kq), and nv
-    struct Ops { float kcd[32], qp[32], in[16], kp[2][16], nv[4], cd; };
+    // (16-byte vectors loaded straight into the set: no copy waits for the data before its use)
+    struct Ops { q35_f32x4 kcd[8], qp[8], in[4], kp[2][4], nv; float cd; };
     auto load_ops = [&](int c, Ops& o) {
         const float* ws = a.chunk_ws + ((size_t)c * kHv + h) * kCWs;
         o.cd = a.chunk_cdec[c * kHv + h];
@@ -309,28 +312,24 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
         const q35_f32x4* pi = (const q35_f32x4*)(ws + kWsIntra + (wv * 64 + ln) * 16);
         const q35_f32x4* pp0 = (const q35_f32x4*)(ws + kWsK + ((wv * 2 + 0) * 64 + ln) * 16);
         const q35_f32x4* pp1 = (const q35_f32x4*)(ws + kWsK + ((wv * 2 + 1) * 64 + ln) * 16);
-        const q35_f32x4 nv4 = *(const q35_f32x4*)(ws + kWsNv + ((blockIdx.y * 4 + wv) * 64 + ln) * 4);
+        o.nv = *(const q35_f32x4*)(ws + kWsNv + ((blockIdx.y * 4 + wv) * 64 + ln) * 4);
 #pragma unroll
-        for (int v = 0; v < 8; ++v) {
-            const q35_f32x4 x = pk[v], y = pq[v];
+        for (int v = 0; v < 8; ++v) { o.kcd[v] = pk[v]; o.qp[v] = pq[v]; }
 #pragma unroll
-            for (int e = 0; e < 4; ++e) { o.kcd[4 * v + e] = x[e]; o.qp[4 * v + e] = y[e]; }
-        }
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const q35_f32x4 x = pi[v], y = pp0[v], z = pp1[v];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) { o.in[4 * v + e] = x[e]; o.kp[0][4 * v + e] = y[e]; o.kp[1][4 * v + e] = z[e]; }
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o.nv[r] = nv4[r];
+        for (int v = 0; v < 4; ++v) { o.in[v] = pi[v]; o.kp[0][v] = pp0[v]; o.kp[1][v] = pp1[v]; }
     };
-    Ops cur_ops, nxt_ops;
-    load_ops(0, cur_ops);
-    for (int c = 0; c < nchunks; ++c) {
+    // a ring of three operand sets: chunk c's loads are issued two chunks ahead (one chunk of
+    // compute does not cover the workspace's load latency); the ring index is static (the
+    // chunk loop is unrolled by 3)
+    Ops ops[3];
+    load_ops(0, ops[0]);
+    load_ops(min(1, nchunks - 1), ops[1]);
+    auto step = [&](int c, auto par) {
+        constexpr int P = decltype(par)::value;
+        Ops& cur_ops = ops[P];
         const int t0 = c * kC;
-        // next chunk's operands (unconditional, clamped: no branch splits the wait counts)
-        load_ops(min(c + 1, nchunks - 1), nxt_ops);
+        // operands two chunks ahead (unconditional, clamped: no branch splits the wait counts)
+        load_ops(min(c + 2, nchunks - 1), ops[(P + 2) % 3]);
         // B fragments of S, shared by phases 1 and 2 (all waves read S before the barrier)
         float sf[32];
 #pragma unroll
@@ -339,7 +338,7 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
         {
             q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 32; ++ks) acc = mfma4(cur_ops.kcd[ks], sf[ks], acc);
+            for (int ks = 0; ks < 32; ++ks) acc = mfma4(cur_ops.kcd[ks >> 2][ks & 3], sf[ks], acc);
 #pragma unroll
             for (int r = 0; r < 4; ++r) vn[wv * 16 + 4 * kq + r][mr] = cur_ops.nv[r] - acc[r];
         }
@@ -351,9 +350,9 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
         {
             q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 32; ++ks) acc = mfma4(cur_ops.qp[ks], sf[ks], acc);
+            for (int ks = 0; ks < 32; ++ks) acc = mfma4(cur_ops.qp[ks >> 2][ks & 3], sf[ks], acc);
 #pragma unroll
-            for (int ks = 0; ks < 16; ++ks) acc = mfma4(cur_ops.in[ks], vf[ks], acc);
+            for (int ks = 0; ks < 16; ++ks) acc = mfma4(cur_ops.in[ks >> 2][ks & 3], vf[ks], acc);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = wv * 16 + 4 * kq + r;
@@ -369,12 +368,16 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[r] = S[m0 + 4 * kq + r][mr] * cur_ops.cd;
 #pragma unroll
-            for (int ks = 0; ks < 16; ++ks) acc = mfma4(cur_ops.kp[half][ks], vf[ks], acc);
+            for (int ks = 0; ks < 16; ++ks) acc = mfma4(cur_ops.kp[half][ks >> 2][ks & 3], vf[ks], acc);
 #pragma unroll
             for (int r = 0; r < 4; ++r) S[m0 + 4 * kq + r][mr] = acc[r];
         }
         __syncthreads();    // S complete and v_new consumed before the next chunk
-        cur_ops = nxt_ops;
+    };
+    for (int c = 0; c < nchunks; c += 3) {
+        step(c, std::integral_constant<int, 0>{});
+        if (c + 1 < nchunks) step(c + 1, std::integral_constant<int, 1>{});
+        if (c + 2 < nchunks) step(c + 2, std::integral_constant<int, 2>{});
     }
     for (int e = tid; e < 128 * 16; e += 256) Sout[(e >> 4) * 128 + n0 + (e & 15)] = S[e >> 4][e & 15];
 }
