@@ -95,3 +95,34 @@ def test_prompt_attention_vs_float64(eng, pre, n):
               flush=True)
         assert np.isfinite(aout).all()
         assert (d <= 2 * ulp + REL_W * mag).all() and d.mean() <= MEAN_D, (mode, d.max(), d.mean())
+
+
+def test_prompt_attention_long_context_sampled_rows():
+    """A 2,048-row wave after a 2,000-slot prefix (contexts up to 4,048 slots: 64 K/V tiles,
+    the online softmax rescaling across many tiles), checked on 48 sampled rows (every head)
+    against the same float64 restatement and bound."""
+    from oracle.weights import lane_prompt_ids
+    from qwen35 import Engine, State
+    eng = Engine(max_rows=2048, max_ctx=4160, seed=0)
+    try:
+        pre, n = 2000, 2048
+        st = State(eng, 1, 4160)
+        st.prefill(0, lane_prompt_ids(9, 0, pre))
+        st.prefill(0, lane_prompt_ids(9, 1, n))
+        q = eng.read_scratch("q", (n, 8, 256), np.float32)
+        aout = _u16f(eng.read_scratch("aout", (n, 2048), np.uint16)).reshape(n, 8, 256)
+        proj = eng.read_scratch("proj", (n, 5120), np.uint16)
+        K = _u16f(st.read(0, "k", pre + n)[5])
+        V = _u16f(st.read(0, "v", pre + n)[5])
+        st.close()
+    finally:
+        eng.close()
+    gate = _u16f(proj[:, :4096].reshape(n, 8, 512)[:, :, 256:])
+    rows = np.unique(np.concatenate([[0, 1, 15, 16, 63, 64, n - 1], np.random.default_rng(5).integers(0, n, 41)]))
+    ref, mag = _reference(q[rows], K, V, gate[rows], [pre + int(r) for r in rows])
+    got = aout[rows]
+    d = np.abs(got - ref)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -40))) - 7)
+    print(f"  long context: {rows.size} rows, max |d| {d.max():.3g}, mean |d| {d.mean():.3g}", flush=True)
+    assert np.isfinite(got).all()
+    assert (d <= 2 * ulp + REL_W * mag).all() and d.mean() <= MEAN_D, (d.max(), d.mean())
