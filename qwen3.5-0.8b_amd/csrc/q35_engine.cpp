@@ -475,7 +475,7 @@ void mlp_layer(q35_engine* e, const LayerW& w, int R, B1Res* rr = nullptr) {
         resid_gemm(e, rr, w.W_down, kFF, R, e->gu, kGuRows, kASiluMul, e->gu + kFF, kGuRows);
         return;
     }
-    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, 2048 / 256, w.norm_post, e->h, R, e->st));
+    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(R, 2048), w.norm_post, e->h, R, e->st));
     // gate|up GEMM with the SwiGLU product in its epilogue: act [R][3584] -> plain down GEMM
     gemm(e, w.W_gu, kGuRows, kHidden, R, e->h, kHidden, e->gu, kFF, kAPlain, nullptr, 0, nullptr, kESiluMul);
     gemm(e, w.W_down, kHidden, kFF, R, e->gu, kFF, nullptr, 0);
@@ -484,7 +484,7 @@ void mlp_layer(q35_engine* e, const LayerW& w, int R, B1Res* rr = nullptr) {
 // Batched path: fold the down-projection chains into x and normalise for the next consumer.
 void finish_norm(q35_engine* e, int R, const uint16_t* nw, uint16_t* out) {
     if (small_rows(R)) return;
-    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, kFF / 256, nw, out, R, e->st));
+    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(R, kFF), nw, out, R, e->st));
 }
 
 // Runs the 24-layer body over R = nl * T rows (rows of one lane consecutive) and leaves the
@@ -592,7 +592,7 @@ void mtp_draft_pass(q35_engine* e, q35_state* s, int n, const uint16_t* hsrc) {
         gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, e->x, kHidden);
     } else {
         gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, nullptr, 0);
-        HCK(launch_addnorm(4, nullptr, nullptr, e->x, nullptr, e->kpart, 2048 / 256, e->M.norm_in, e->h, n, e->st));
+        HCK(launch_addnorm(4, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(n, 2048), e->M.norm_in, e->h, n, e->st));
     }
     attention_layer(e, e->M, n, s->mkc, s->mvc, s->mkv_lane(), 0, s->mtp_capT);
     mlp_layer(e, e->M, n);
@@ -1329,6 +1329,12 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
         } else if (n == "attn_prompt") {         // process-wide kernel choice; drops captured steps
             HCK(hipStreamSynchronize(e->st));
             set_attn_prompt(value ? 1 : 0);
+            for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
+            e->graphs.clear();
+        } else if (n == "partial_rows") {         // process-wide kernel choice; drops captured steps
+            REQ(value >= 17, Q35_ERR_ARG, "partial_rows must exceed the 16-row batch-1 path");
+            HCK(hipStreamSynchronize(e->st));
+            set_partial_rows(value);
             for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
             e->graphs.clear();
         } else if (n == "gemv_tpb") {            // process-wide kernel choice; drops captured steps

@@ -443,8 +443,11 @@ __global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
     const bool nvalid = EM == kESiluMul ? jg < half : nt < a.N / 16;
     const int row0 = (idx % mb) * MT * 16;
     const int KB = a.K >> 8;
-    const int kb0 = EM == kEPartial ? blockIdx.z : 0;
-    const int kb1 = EM == kEPartial ? blockIdx.z + 1 : KB;
+    // kEPartial: one k-block chain per block (grid z = KB), or -- grid z = 1, enough row
+    // blocks to fill the chip -- every chain summed in order in the block and stored as chain 0
+    const bool zsplit = EM == kEPartial && gridDim.z > 1;
+    const int kb0 = zsplit ? blockIdx.z : 0;
+    const int kb1 = zsplit ? blockIdx.z + 1 : KB;
     q35_f32x4 sum[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) sum[i] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
@@ -841,10 +844,16 @@ __global__ void __launch_bounds__(1024) argmax_rows(const float* pv, const int* 
     }
 }
 
+// kEPartial GEMMs with at least this many rows sum all k-block chains in the block (one chain
+// left for the add+norm) instead of one block per chain
+static int g_partial_rows = 1024;
+void set_partial_rows(int m) { g_partial_rows = m; }
+int gemm_partial_chains(int M, int K) { return M > 16 && M >= g_partial_rows ? 1 : K / 256; }
+
 template <int EM>
 static void launch_large(const GemmArgs& a, hipStream_t st) {
     const int KB = a.K / 256;
-    const int gz = EM == kEPartial ? KB : 1;
+    const int gz = EM == kEPartial ? (a.M >= g_partial_rows ? 1 : KB) : 1;
     // 64-row tiles: more blocks in flight (W tiles are re-read from L2 by the M tiles)
     const int nb = EM == kESiluMul ? (a.N / 32 + 1) / 2 : (a.N / 16 + 3) / 4, mb = (a.M + 63) / 64;
     if (EM == kEArgmax && a.K == kHidden && a.N % 64 == 0 && g_lmhead_persist) {

@@ -34,7 +34,9 @@ struct GemmArgs {
 };
 // One-time kernel attribute setup (dynamic LDS above 64 KiB for the batch-1 producers).
 hipError_t gemm_init();
-void set_gemv_tpb(int v);          // one-row norm GEMVs (N >= 4096): column tiles per block, 1 or 2
+void set_gemv_tpb(int v);
+void set_partial_rows(int m);     // batched kEPartial GEMMs with M >= m leave one (summed) chain
+int gemm_partial_chains(int M, int K);   // k-block chains a batched kEPartial GEMM leaves in kpart          // one-row norm GEMVs (N >= 4096): column tiles per block, 1 or 2
 void set_gemm_pre(int on);         // batched K = 1024 GEMMs: all loads up front (1) or k-block pipelined (0)
 void set_lmhead_persist(int on);   // tied lm_head at batched lanes: persistent kernel (1) or 64 x 256 tiles (0)
 hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st);
