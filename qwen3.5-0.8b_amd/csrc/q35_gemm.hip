@@ -422,7 +422,7 @@ __device__ __forceinline__ int lds_swz(int s, int g, int r16) {
     return g * 16 + (r16 ^ ((s + 8 * (g & 1)) & 15));
 }
 
-template <int EM, int MT, int NW>
+template <int EM, int MT, int NW, bool FULLK = false>
 __global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
     __shared__ q35_u32x4 As[MT][8][64];
     constexpr int NT = 64 * NW;                    // threads
@@ -443,11 +443,10 @@ __global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
     const bool nvalid = EM == kESiluMul ? jg < half : nt < a.N / 16;
     const int row0 = (idx % mb) * MT * 16;
     const int KB = a.K >> 8;
-    // kEPartial: one k-block chain per block (grid z = KB), or -- grid z = 1, enough row
-    // blocks to fill the chip -- every chain summed in order in the block and stored as chain 0
-    const bool zsplit = EM == kEPartial && gridDim.z > 1;
-    const int kb0 = zsplit ? blockIdx.z : 0;
-    const int kb1 = zsplit ? blockIdx.z + 1 : KB;
+    // kEPartial: one k-block chain per block (grid z = KB), or -- FULLK, enough row blocks to
+    // fill the chip -- every chain summed in order in the block and stored as chain 0
+    const int kb0 = EM == kEPartial && !FULLK ? blockIdx.z : 0;
+    const int kb1 = EM == kEPartial && !FULLK ? blockIdx.z + 1 : KB;
     q35_f32x4 sum[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) sum[i] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
@@ -889,7 +888,10 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
         hipLaunchKernelGGL((gemm_pre<EM, 2>), dim3((nb + 7) / 8 * 8 * mb2), dim3(256), pre_lds_bytes<2>(), st, a);
         return;
     }
-    hipLaunchKernelGGL((gemm_large_m<EM, 4, 4>), dim3((nb + 7) / 8 * 8 * mb, 1, gz), dim3(256), 0, st, a);
+    if (EM == kEPartial && gz == 1)
+        hipLaunchKernelGGL((gemm_large_m<EM, 4, 4, true>), dim3((nb + 7) / 8 * 8 * mb, 1, 1), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((gemm_large_m<EM, 4, 4>), dim3((nb + 7) / 8 * 8 * mb, 1, gz), dim3(256), 0, st, a);
 }
 
 template <int AM, int EM>

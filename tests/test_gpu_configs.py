@@ -43,11 +43,13 @@ def test_config1_projection_sweep(eng, name, N, K):
     X = torch.randn(256, K, generator=g).to(torch.bfloat16)
     Wd = W.cuda()
     Wt = torch.empty_like(Wd)
+    torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
     eng.op_tile_weight(Wd.data_ptr(), N, K, Wt.data_ptr())
     outs = {}
     for B in (1, 16, 256):
         Xd = X[:B].contiguous().cuda()
         Y = torch.empty(B, N, dtype=torch.bfloat16, device="cuda")
+        torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
         eng.op_gemm(Wt.data_ptr(), N, K, Xd.data_ptr(), B, Y.data_ptr())
         eng.sync()
         outs[B] = Y.cpu()
@@ -68,6 +70,7 @@ def test_config1_lm_head_argmax(eng, oracle_weights):
     for B in (1, 16, 256):
         tok = torch.empty(B, dtype=torch.int32, device="cuda")
         lg = torch.empty(B, 248320, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
         eng.op_lm_head_argmax(X[:B].contiguous().cuda().data_ptr(), B, tok.data_ptr(), lg.data_ptr())
         eng.sync()
         res[B] = (tok.cpu(), lg.cpu())
@@ -94,6 +97,7 @@ def test_lm_head_persistent_equals_tiled(eng, M):
         eng.set_option("lmhead_persist", p)
         tok = torch.full((M,), -1, dtype=torch.int32, device="cuda")
         lg = torch.full((M, 248320), float("nan"), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
         eng.op_lm_head_argmax(X.data_ptr(), M, tok.data_ptr(), lg.data_ptr())
         eng.sync()
         out[p] = (tok.cpu(), lg.cpu())
@@ -118,6 +122,7 @@ def test_lm_head_persistent_row_chunks():
             e.set_option("lmhead_persist", p)
             tok = torch.full((M,), -1, dtype=torch.int32, device="cuda")
             lg = torch.full((M, 248320), float("nan"), dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
             e.op_lm_head_argmax(X.data_ptr(), M, tok.data_ptr(), lg.data_ptr())
             e.sync()
             out[p] = (tok.cpu(), lg.cpu())
@@ -136,6 +141,7 @@ def test_k1024_gemm_forms_identical(eng, N):
     g = torch.Generator().manual_seed(N)
     W = (torch.randn(N, 1024, generator=g) * 0.02).to(torch.bfloat16).cuda()
     Wt = torch.empty_like(W)
+    torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
     eng.op_tile_weight(W.data_ptr(), N, 1024, Wt.data_ptr())
     for M in (17, 200, 256):
         X = torch.randn(M, 1024, generator=g).to(torch.bfloat16).cuda()
@@ -143,6 +149,7 @@ def test_k1024_gemm_forms_identical(eng, N):
         for p in (0, 1):
             eng.set_option("gemm_pre", p)
             Y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+            torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
             eng.op_gemm(Wt.data_ptr(), N, 1024, X.data_ptr(), M, Y.data_ptr())
             eng.sync()
             out[p] = Y.cpu()
@@ -169,6 +176,7 @@ def test_config2_gdn_step(eng, oracle_weights, B):
     o = torch.empty(B, 2048, dtype=torch.float32, device="cuda")
     dproj = proj.cuda()
     cw, al, db = conv_w.contiguous().cuda(), A_log.contiguous().cuda(), dt_bias.contiguous().cuda()
+    torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
     eng.op_gdn_step(dproj.data_ptr(), cw.data_ptr(), al.data_ptr(), db.data_ptr(), dS2.data_ptr(),
                     dW2.data_ptr(), o.data_ptr(), B)
     S1, W1, o = dS2[:, 1].cpu(), dW2[:, 1].cpu(), o.cpu()

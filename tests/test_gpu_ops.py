@@ -33,7 +33,9 @@ def test_gemm_vs_float64(eng, N, K, M):
     Wd, Xd = W.cuda(), X.cuda()
     Wt = torch.empty_like(Wd)
     Y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
     eng.op_tile_weight(Wd.data_ptr(), N, K, Wt.data_ptr())
+    torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
     eng.op_gemm(Wt.data_ptr(), N, K, Xd.data_ptr(), M, Y.data_ptr())
     eng.sync()
     ref = X.double() @ W.double().t()
@@ -45,6 +47,7 @@ def test_gemm_vs_float64(eng, N, K, M):
     assert (excess <= acc).all(), (excess - acc).max().item()
     # row independence: row 0 alone gives the same bits
     Y1 = torch.empty(1, N, dtype=torch.bfloat16, device="cuda")
+    torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
     eng.op_gemm(Wt.data_ptr(), N, K, Xd[-1:].contiguous().data_ptr(), 1, Y1.data_ptr())
     eng.sync()
     assert torch.equal(Y1.cpu(), Y[-1:].cpu())
@@ -58,6 +61,7 @@ def test_lm_head_argmax(eng, oracle_weights):
     X[3] = X[2]
     tok = torch.empty(5, dtype=torch.int32, device="cuda")
     lg = torch.empty(5, 248320, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
     eng.op_lm_head_argmax(X.cuda().data_ptr(), 5, tok.data_ptr(), lg.data_ptr())
     eng.sync()
     lg = lg.cpu()
