@@ -146,7 +146,9 @@ int q35_kprof_read(q35_engine* e, float* total_ms, int* launches);
  * engine's captured steps when set: "b1_partials" (this engine: one-row bodies leave k-block
  * chains for the next norm GEMV) and, process-wide (every engine of the process), "gemv_tpb"
  * (1/2 column tiles per block of the one-row norm GEMVs), "gemm_pre" (batched K = 1024 GEMMs
- * issue all loads up front), "lmhead_persist" (persistent lm_head at batched lanes). Not
+ * issue all loads up front), "lmhead_persist" (persistent lm_head at batched lanes),
+ * "partial_rows" (>= 17: batched out/o/down GEMMs with at least this many rows sum their
+ * k-block chains in the block, one chain for the add+norm; default 1,024). Not
  * bit-identical, a different rounding point within the stated tolerance: "attn_prompt"
  * (process-wide; 1: prompt waves of one lane with >= 64 rows use the flash-form MFMA
  * attention kernel, 0: the one-row kernels). */
