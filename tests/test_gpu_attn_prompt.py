@@ -8,10 +8,13 @@ the projection rows. Cases: one-wave prompts whose row count is and is not a mul
 
 Tolerance (stated): the kernel rounds the unnormalised weights e^(s - m) to bf16 and divides
 by the sum afterwards, the reference rounds the normalised weights, so each weight carries
-a different bf16 rounding (each <= 2^-9 relative, so the two differ by <= 2^-8 of the
-weight) and the bf16 output may land one rounding step away: every element within 2 bf16
-ulps of the reference value plus 2^-8 sum_t p_t |v_t| sigmoid(gate) (the weight-rounding
-bound), and mean |d| <= 2^-10 (measured ~4.5e-4 on outputs up to ~5). The one-row kernels
+a different bf16 rounding: the kernel's weight bf16(e_t) / sum_s bf16(e_s) is off the exact
+softmax weight by at most 2^-9 for its own rounding plus 2^-9 for the normaliser's (a
+weighted mean of the same roundings), the reference's by 2^-9 -- 3 x 2^-9 of each weight
+apart -- and the bf16 output may land one rounding step away: every element within 2 bf16
+ulps of the reference value plus 3 x 2^-9 sum_t p_t |v_t| sigmoid(gate) (the weight-rounding
+bound, which decides outputs that cancel to near zero), and mean |d| <= 2^-10 (measured
+~4.5e-4 on outputs up to ~5). The one-row kernels
 meet the same bound on the same inputs (checked in the test; they round like the
 reference, mean |d| ~1e-6), and the full-model prompt logits
 stay within the engine-vs-oracle tolerance (test_chunked_prefill_vs_oracle_chunk_form runs
@@ -21,7 +24,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-REL_W, MEAN_D = 2.0 ** -8, 2.0 ** -10
+REL_W, MEAN_D = 3 * 2.0 ** -9, 2.0 ** -10
 
 
 def _bf(a):
@@ -125,4 +128,32 @@ def test_prompt_attention_long_context_sampled_rows():
     ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -40))) - 7)
     print(f"  long context: {rows.size} rows, max |d| {d.max():.3g}, mean |d| {d.mean():.3g}", flush=True)
     assert np.isfinite(got).all()
+    assert (d <= 2 * ulp + REL_W * mag).all() and d.mean() <= MEAN_D, (d.max(), d.mean())
+
+
+def test_prompt_attention_full_odd_capacity():
+    """A lane whose capacity (1,000 slots: not a multiple of the 64-slot tiles) is filled by
+    one 999-row wave: the last K/V tile is partial and the padded tail of the cache is never
+    read into a weight; every row checked."""
+    from oracle.weights import lane_prompt_ids
+    from qwen35 import Engine, State
+    eng = Engine(max_rows=1024, max_ctx=1024, seed=0)
+    try:
+        n = 999
+        st = State(eng, 1, 1000)
+        st.prefill(0, lane_prompt_ids(10, 0, n))
+        q = eng.read_scratch("q", (n, 8, 256), np.float32)
+        aout = _u16f(eng.read_scratch("aout", (n, 2048), np.uint16)).reshape(n, 8, 256)
+        proj = eng.read_scratch("proj", (n, 5120), np.uint16)
+        K = _u16f(st.read(0, "k", n)[5])
+        V = _u16f(st.read(0, "v", n)[5])
+        st.close()
+    finally:
+        eng.close()
+    gate = _u16f(proj[:, :4096].reshape(n, 8, 512)[:, :, 256:])
+    ref, mag = _reference(q, K, V, gate, list(range(n)))
+    d = np.abs(aout - ref)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -40))) - 7)
+    print(f"  odd capacity: max |d| {d.max():.3g}, mean |d| {d.mean():.3g}", flush=True)
+    assert np.isfinite(aout).all()
     assert (d <= 2 * ulp + REL_W * mag).all() and d.mean() <= MEAN_D, (d.max(), d.mean())
