@@ -21,11 +21,15 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I", str(SRC), "-I", str(PKG.parent / "include")]
+# MFMA accumulators in architectural VGPRs: without it the compiler keeps loop-carried
+# accumulators in AGPRs and copies them to VGPRs and back around every VALU touch of them
+# (the prompt attention's online-softmax rescale: ~190 v_accvgpr moves per K/V tile)
+FILE_FLAGS = {"q35_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.name + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd = [HIPCC, *FLAGS, "-x", "hip", "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -515,12 +515,15 @@ __global__ void __launch_bounds__(256) attn_fused(AttnArgs a, int lds_slots) {
 constexpr int kPrRows = 16;
 typedef short q35_s16x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ int pr_swz(int t, int c) { return c ^ ((t & 15) << 1); }   // c: 16-byte chunk 0..31
+// V tile rows in LDS: 32 16-byte chunks + 2 pad chunks (544 B): transposed reads of 4 rows x
+// 32 B per 16-lane group land on distinct banks, and every read address is one lane base plus
+// an immediate offset
+constexpr int kPrVRow = 34, kPrVBuf = 64 * kPrVRow * 16;    // 16-byte slots per row; bytes per V tile
 
 static int g_attn_prompt = 1;
 void set_attn_prompt(int on) { g_attn_prompt = on; }
 
-constexpr int kPrLds = 4 * 64 * 256 * 2;     // K and V tiles, double-buffered: 128 KiB
+constexpr int kPrLds = 2 * 64 * 256 * 2 + 2 * kPrVBuf;   // K and V tiles, double-buffered: 132 KiB
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 q35_bf16x2;
 // two f32 -> packed bf16 (round to nearest even, v_cvt_pk_bf16_f32)
@@ -532,7 +535,7 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
 __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t pr_lds[];
     uint16_t(*kt)[64 * 256] = (uint16_t(*)[64 * 256])pr_lds;
-    uint16_t(*vt)[64 * 256] = (uint16_t(*)[64 * 256])(pr_lds + 2 * 64 * 256);
+    uint16_t* vt = pr_lds + 2 * 64 * 256;                          // [2][64 rows][kPrVRow slots]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int T = a.T, ngrp = (T + kPrRows - 1) / kPrRows;
@@ -573,8 +576,8 @@ __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
     const int ntiles = smax / 64 + 1;
     // K and V tiles (64 slots) reach LDS by direct-to-LDS loads (global_load_lds: lane i of
     // an instruction fills the 16-byte slot i of a 1 KiB run), issued one tile ahead: K in its
-    // cache layout (four 16-slot MFMA tiles, 32 KiB contiguous), V with each row's 16-byte
-    // chunks XOR-swizzled by slot. Cached loads: the 12 blocks of a kv head on one XCD read
+    // cache layout (four 16-slot MFMA tiles, 32 KiB contiguous), V as padded rows of kPrVRow
+    // slots (34 runs; a pad slot takes a copy of the row's chunk 0). Cached loads: the 12 blocks of a kv head on one XCD read
     // the same tiles and all but the first hit that XCD's L2. Slots past the group's last are
     // clamped to it (K: scores masked; V: weights zero, values finite). The wave's 8 K and 8 V
     // runs per tile are its only vector-memory loads in the loop, so "s_waitcnt vmcnt(0)"
@@ -589,11 +592,17 @@ __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
             __builtin_amdgcn_global_load_lds(
                 (const void*)(a.kc + kvbase + (size_t)tile * 4096 + (run & 7) * 512 + lane * 8),
                 (__attribute__((address_space(3))) void*)&kt[buf][run * 512], 16, 0, 0);
-            const int row = 2 * run + (lane >> 5), pos = lane & 31;
-            const int slot = min(t0 + row, smax);
-            __builtin_amdgcn_global_load_lds(
-                (const void*)(a.vc + kvbase + (size_t)slot * 256 + pr_swz(row, pos) * 8),
-                (__attribute__((address_space(3))) void*)&vt[buf][run * 512], 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 9; ++i) {
+            const int run = 4 * i + wv;                   // 64-slot run of the padded V tile
+            if (run < 64 * kPrVRow / 64) {
+                const int sl = run * 64 + lane, row = sl / kPrVRow, pos = sl % kPrVRow;
+                const int slot = min(t0 + row, smax);
+                __builtin_amdgcn_global_load_lds(
+                    (const void*)(a.vc + kvbase + (size_t)slot * 256 + (pos < 32 ? pos : 0) * 8),
+                    (__attribute__((address_space(3))) void*)(vt + buf * (kPrVBuf / 2) + run * 512), 16, 0, 0);
+            }
         }
     };
     issue_tiles(0, 0);
@@ -603,22 +612,12 @@ __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt) o[dt] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
     // LDS byte offsets: K fragment (sub-tile st, step s) at st*8192 + s*1024 + lane*16; V
-    // transposed reads: source lane n of group g points at slot (4g + n/4) + 16c + 32ks of
-    // the tile, dims 16 dt + 4 (n % 4) .. +4 (chunk 2 dt + (n % 4) / 2, swizzled by slot)
+    // transposed reads: source lane n of group g points at row (4g + n/4) + 16c + 32ks of the
+    // tile, dims 16 dt + 4 (n % 4) .. +4: the lane's base (row 4g + n/4, its 8 bytes of the
+    // d-tile's 32) plus the immediate (16c + 32ks) * 544 + 32 dt
     const unsigned kb0 = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&kt[0][0] + lane * 16;
-    const unsigned vb0 = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&vt[0][0];
-    const int trow = 4 * g + (n >> 2);
-    unsigned voff[2][2][16];      // [ks][c][dt]
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int dt = 0; dt < 16; ++dt) {
-                const int row = 32 * ks + 16 * c + trow;
-                const int ch = 2 * dt + ((n & 3) >> 1);
-                voff[ks][c][dt] = vb0 + (unsigned)(row * 512 + pr_swz(row, ch) * 16 + (n & 1) * 8);
-            }
+    const unsigned vlane = (unsigned)(size_t)(__attribute__((address_space(3))) void*)vt +
+                           (unsigned)((4 * g + (n >> 2)) * kPrVRow * 16 + (n & 3) * 8);
 
     for (int it = 0; it < ntiles; ++it) {
         const int t0 = it * 64, buf = it & 1;
@@ -696,7 +695,7 @@ __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
                 for (int r = 0; r < 4; ++r) o[dt][r] *= ar[r];
         }
         // P.V: V fragments 8 d-tiles at a time (16 transposed reads, one wait, 8 MFMAs)
-        const unsigned vbuf = (unsigned)(buf * 64 * 256 * 2);
+        const unsigned vb = vlane + (unsigned)(buf * kPrVBuf);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
@@ -704,8 +703,10 @@ __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
                 uint2 v0[8], v1[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v0[u]) : "v"(voff[ks][0][8 * dh + u] + vbuf) : "memory");
-                    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v1[u]) : "v"(voff[ks][1][8 * dh + u] + vbuf) : "memory");
+                    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v0[u])
+                                 : "v"(vb), "n"((32 * ks) * kPrVRow * 16 + 32 * (8 * dh + u)) : "memory");
+                    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v1[u])
+                                 : "v"(vb), "n"((32 * ks + 16) * kPrVRow * 16 + 32 * (8 * dh + u)) : "memory");
                 }
                 asm volatile("s_waitcnt lgkmcnt(0)"
                              : "+v"(v0[0]), "+v"(v0[1]), "+v"(v0[2]), "+v"(v0[3]), "+v"(v0[4]), "+v"(v0[5]), "+v"(v0[6]), "+v"(v0[7]),
