@@ -119,6 +119,14 @@ int q35_mtp_draft(q35_engine* e, q35_state* s, const int32_t* lanes, int n, cons
 int q35_mtp_round(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* cur,
                   int k, int32_t* emit, int32_t* n_emit, int64_t* stats);
 
+/* The same round with the session driver's stop rule (mtpaccept::session_body,
+ * engine/mtp_accept.h:422-431, engine/mtp_accept.cpp:585-600): when an accepted draft equals
+ * `stop` (>= 0; 248046 in the session), the accepted prefix ends before it, so that token
+ * is the lane's last emit and stays pending (printed, never fed) -- the state ends where the
+ * transcript does, as after a plain step that sampled it. stop < 0 is q35_mtp_round. */
+int q35_mtp_round_stop(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* cur,
+                       int k, int32_t stop, int32_t* emit, int32_t* n_emit, int64_t* stats);
+
 /* Per-op entry points on caller device buffers (benchmark and parity harness). */
 /* Y[M][N] = X[M][K] . W^T with W in checkpoint row-major layout, tiled into scratch first
  * by q35_op_tile_weight. */

@@ -1205,6 +1205,14 @@ int q35_mtp_draft(q35_engine* e, q35_state* s, const int32_t* lanes, int n, cons
 
 int q35_mtp_round(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* cur,
                   int k, int32_t* emit, int32_t* n_emit, int64_t* stats) {
+    return q35_mtp_round_stop(e, s, lanes, n, cur, k, -1, emit, n_emit, stats);
+}
+
+// stop >= 0: an accepted draft equal to `stop` ends the accepted prefix (the target row before
+// it chose the same token, so it is emitted as the bonus and left pending, never fed): the
+// session driver's stop cut, engine/mtp_accept.cpp:585-600
+int q35_mtp_round_stop(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* cur,
+                       int k, int32_t stop, int32_t* emit, int32_t* n_emit, int64_t* stats) {
     return guard([&] {
         REQ(e && s && cur && emit && n_emit, Q35_ERR_ARG, "null argument");
         REQ(k >= 1 && k <= s->mtp_k, Q35_ERR_STATE, "k exceeds the state's MTP slots");
@@ -1242,7 +1250,7 @@ int q35_mtp_round(q35_engine* e, q35_state* s, const int32_t* lanes, int n, cons
         for (int i = 0; i < n; ++i) {
             const int* tgt = e->h_out + i * T;
             int a = 0;
-            while (a < k && drafts[i][a] == tgt[a]) ++a;
+            while (a < k && drafts[i][a] == tgt[a] && drafts[i][a] != stop) ++a;
             int m = 0;
             for (int j = 0; j < a; ++j) emit[i * (k + 1) + m++] = drafts[i][j];
             emit[i * (k + 1) + m++] = tgt[a];

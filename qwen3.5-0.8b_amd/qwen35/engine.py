@@ -56,6 +56,8 @@ _SIGS = {
                        C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "q35_mtp_round": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
                        C.c_void_p, C.c_void_p], C.c_int),
+    "q35_mtp_round_stop": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int32,
+                            C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "q35_op_tile_weight": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p], C.c_int),
     "q35_op_gemm": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p], C.c_int),
     "q35_op_gdn_step": ([C.c_void_p] * 8 + [C.c_int], C.c_int),
@@ -299,15 +301,17 @@ class State:
                                          _p(pos), step, _p(out), _p(xd), _p(lg) if logits else None))
         return out, xd, lg
 
-    def mtp_round(self, cur, k: int, lanes=None, stats: np.ndarray | None = None):
+    def mtp_round(self, cur, k: int, lanes=None, stats: np.ndarray | None = None, stop: int = -1):
+        """One speculative round per lane; stop >= 0 applies the session's stop cut (an
+        accepted draft equal to it ends the lane's emits and stays pending)."""
         c = _i32(cur)
         n = c.size
         ln = _i32(lanes) if lanes is not None else None
         emit = np.zeros((n, k + 1), np.int32)
         ne = np.zeros(n, np.int32)
         st = stats if stats is not None else np.zeros(4, np.int64)
-        _ck(load_library().q35_mtp_round(self.eng.h, self.h, _p(ln) if ln is not None else None, n, _p(c), k,
-                                         _p(emit), _p(ne), _p(st)))
+        _ck(load_library().q35_mtp_round_stop(self.eng.h, self.h, _p(ln) if ln is not None else None, n, _p(c),
+                                              k, stop, _p(emit), _p(ne), _p(st)))
         return [list(emit[i, :ne[i]]) for i in range(n)]
 
 

@@ -19,6 +19,19 @@ prints `READY cap=<n>`, then answers one command per stdin line:
 Token ids only: rendering and tokenizing the chat is the caller's side (engine/chat.py). A
 failure inside a step poisons the session until `reset` (the state may be half-advanced);
 argument errors do not.
+
+With `--mtp-k K` (K >= 1; the reference's session runs accept rounds at k = 2 by default,
+engine/decode_run.cpp:162-187) `gen` advances by speculative rounds instead of single steps,
+as mtpaccept::session_body does (engine/mtp_accept.cpp:530-660): a round feeds the pending
+sample plus K drafts and prints the accepted drafts, the bonus becoming the next pending
+sample; it runs only when the turn can print all K + 1 of its tokens and the lane has room
+for K + 1 more slots, else the step is a plain one ("ROUND-SKIP reason=budget_tail" /
+"context_limit"); an accepted stop token ends the round's emits and stays pending (the stop
+cut). Greedy rounds are lossless, so the GEN lines are those of the plain session; each
+round adds an "ACCEPT ..." line and a turn that ran rounds ends with "MTPSTAT ...". While a
+logits dump is armed, steps are plain (one priced row per printed token). The drafter's own
+K/V cache is kept across feeds (the reference clears it at a feed); that changes which
+drafts are proposed, never the tokens printed.
 """
 from __future__ import annotations
 
@@ -38,10 +51,13 @@ class Session:
     """One lane's session state machine; `handle` runs one command line and passes every
     output line to `emit` as soon as it exists (GEN lines stream)."""
 
-    def __init__(self, eng: Engine, cap: int = DEFAULT_CAP, out_dir: str | None = None):
+    def __init__(self, eng: Engine, cap: int = DEFAULT_CAP, out_dir: str | None = None, mtp_k: int = 0):
         self.eng = eng
         self.cap = cap
-        self.state = State(eng, 1, cap)
+        self.mtp_k = mtp_k
+        self.state = State(eng, 1, cap, mtp_k=mtp_k, mtp_cap=cap if mtp_k else 0)
+        self.rounds = 0
+        self.turn = np.zeros(4, np.int64)     # drafted, accepted, bonus, verified rows this turn
         self.sampled = -1            # the last sample handed to the caller and not yet consumed
         self.stopped = False
         self.poisoned = False
@@ -115,6 +131,7 @@ class Session:
                 self._dump(emit, "feed", row, p - 1)
             elif cmd == "gen":
                 emitted, stop, cur = 0, False, self.sampled
+                self.turn[:] = 0
                 while emitted < budget:
                     emit(f"GEN {cur} {self.state.prefix_len(0) - 1}")
                     emitted += 1
@@ -122,6 +139,25 @@ class Session:
                         stop = True
                         break
                     want = self._armed()
+                    if self.mtp_k and not want:
+                        k, p = self.mtp_k, self.state.prefix_len(0)
+                        rows = k + 1
+                        if p + rows > self.cap:
+                            emit(f"ROUND-SKIP reason=context_limit anchor={p} cap={self.cap} rows={rows}")
+                        elif budget - emitted < rows:
+                            emit(f"ROUND-SKIP reason=budget_tail anchor={p} budget_left={budget - emitted} rows={rows}")
+                        else:
+                            em = [int(t) for t in self.state.mtp_round([cur], k, [0], self.turn, STOP_TOKEN)[0]]
+                            self.rounds += 1
+                            a = len(em) - 1
+                            emit(f"ACCEPT round={self.rounds} anchor={p} fed={cur} k={k} n_accepted={a} "
+                                 f"emitted={len(em)} pos={p}->{self.state.prefix_len(0)}")
+                            for i, t in enumerate(em[:-1]):    # the accepted drafts (fed, so shown now)
+                                emit(f"GEN {t} {p + i}")
+                                emitted += 1
+                            cur = em[-1]
+                            continue
+                    
                     out = self.state.decode_step([cur], logits=want)
                     tok, lg = (out if want else (out, None))
                     cur = int(tok[0])
@@ -130,6 +166,10 @@ class Session:
                 # sample was never shown, so it is dropped and the caller closes the turn
                 self.sampled = cur if stop else -1
                 self.stopped = stop
+                if self.turn[2]:
+                    d, acc, rounds = int(self.turn[0]), int(self.turn[1]), int(self.turn[2])
+                    emit(f"MTPSTAT rounds={rounds} drafted={d} accepted={acc} "
+                         f"accept_rate={acc / d:.4f} tokens_per_round={(acc + rounds) / rounds:.4f}")
                 emit(f"END steps={emitted} stop={int(stop)} prefix_len={self.state.prefix_len(0)}")
             elif cmd == "stats":
                 emit(f"PREFIX p={self.state.prefix_len(0)} sampled={self.sampled} stopped={int(self.stopped)}")
@@ -172,12 +212,13 @@ def main(argv=None) -> int:
     ap.add_argument("--max-rows", type=int, default=512, help="rows per prompt wave")
     ap.add_argument("--out", help="directory for opt-in logits dumps")
     ap.add_argument("--graph", type=int, default=1, help="capture decode steps in hipGraphs")
+    ap.add_argument("--mtp-k", type=int, default=2, help="drafts per speculative round; 0: plain steps")
     a = ap.parse_args(argv)
     eng = Engine(max_rows=a.max_rows, max_ctx=a.cap, seed=None if a.checkpoint else a.seed, use_graph=bool(a.graph))
     if a.checkpoint:
         n, sk = eng.load_checkpoint(a.checkpoint)
         print(f"LOADED tensors={n} skipped={sk}", flush=True)
-    s = Session(eng, a.cap, a.out)
+    s = Session(eng, a.cap, a.out, mtp_k=a.mtp_k)
 
     def emit(line: str):
         print(line, flush=True)

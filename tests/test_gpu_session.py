@@ -96,10 +96,84 @@ def test_session_stdin_stdout():
     r = subprocess.run([sys.executable, "-m", "qwen35.session", "--cap", "256", "--max-rows", "64"],
                        input=cmds, capture_output=True, text=True, timeout=180, env=env)
     assert r.returncode == 0, r.stderr[-2000:]
-    lines = [l for l in r.stdout.splitlines() if l]
+    # the CLI runs k = 2 rounds by default: drop their diagnostic lines (budget 3 < k + 1 rows
+    # skips every round here, so the tokens come from plain steps)
+    diag = ("ROUND-SKIP ", "ACCEPT ", "MTPSTAT ")
+    lines = [l for l in r.stdout.splitlines() if l and not l.startswith(diag)]
+    assert r.stdout.count("ROUND-SKIP reason=budget_tail") == 3
     assert lines[0] == "READY cap=256"
     assert lines[1] == "FED n=3 prefix_len=3"
     assert [l.split()[0] for l in lines[2:6]] == ["GEN", "GEN", "GEN", "END"]
     assert lines[5] == "END steps=3 stop=0 prefix_len=6"
     assert lines[6] == "PREFIX p=6 sampled=-1 stopped=0"
     assert lines[7] == "BYE"
+
+
+def test_session_mtp_rounds_match_plain(tmp_path, monkeypatch):
+    """`gen` by speculative rounds (k = 2) prints the GEN/FED/END lines of the plain session
+    over several turns, including accepted drafts and the stop cut. Random weights make the
+    drafter disagree always, so the final norms are reshaped to keep one hidden dimension d
+    (1 + w = 0 elsewhere) and two embedding rows get large entries in d: every greedy pick
+    (target and draft) is then 248046 (the stop token) or 1000 by the sign of x_d. With a
+    positive norm factor at d the picks repeat (a fed 1000 adds -8 to x_d): drafts are
+    accepted, mostly whole rounds. With a negative factor for the target its picks
+    alternate (1000, then the stop token); the drafter's factor takes both signs. A third
+    run with the stop cut switched off (stop = -1 passed to the round) must print a
+    different transcript for some setting: an accepted stop draft then sits mid-round, so
+    the cut was exercised and mattered."""
+    from oracle.weights import lane_prompt_ids
+    from qwen35 import Engine, State
+    from qwen35.session import STOP_TOKEN, Session
+    d = 7
+    keep = ("GEN ", "FED ", "END ")
+    feeds = [lane_prompt_ids(11, t, n) for t, n in enumerate((8, 3, 2, 4, 1, 5, 2, 6))]
+    eng = Engine(max_rows=64, max_ctx=512, seed=0, use_graph=True)
+
+    def norm_w(factor_bits):
+        w = np.full(1024, 0xBF80, np.uint16)          # bf16 -1.0: 1 + w = 0
+        w[d] = factor_bits
+        return w
+
+    def run(k):
+        out = []
+        s = Session(eng, 512, str(tmp_path), mtp_k=k)
+        for ids in feeds:
+            s.handle("feed " + " ".join(str(int(t)) for t in ids), out.append)
+            s.handle("gen 24", out.append)
+        s.close()
+        return out
+
+    try:
+        emb = "model.language_model.embed_tokens.weight"
+        E = eng.read_tensor(emb, 248320 * 1024).reshape(248320, 1024)
+        E[STOP_TOKEN, d] = 0x4100                       # bf16 8.0
+        E[1000, d] = 0xC100                             # bf16 -8.0
+        eng.load_tensor(emb, E.reshape(-1))
+        del E
+        cut_mattered, accepted = False, 0
+        # (target, drafter) factor 1 + w at d: bf16 bits of w = 3.0 (factor 4) or -5.0 (-4)
+        for tgt_bits, mtp_bits in ((0x4040, 0x4040), (0xC0A0, 0x4040), (0xC0A0, 0xC0A0)):
+            eng.load_tensor("model.language_model.norm.weight", norm_w(tgt_bits))
+            eng.load_tensor("mtp.norm.weight", norm_w(mtp_bits))
+            plain_log, spec_log = run(0), run(2)
+            orig = State.mtp_round
+            monkeypatch.setattr(State, "mtp_round", lambda self, cur, k, lanes=None, stats=None, stop=-1:
+                                orig(self, cur, k, lanes, stats, -1))
+            nocut = [l for l in run(2) if l.startswith(keep)]
+            monkeypatch.undo()
+            plain = [l for l in plain_log if l.startswith(keep)]
+            spec = [l for l in spec_log if l.startswith(keep)]
+            acc = [l for l in spec_log if l.startswith("ACCEPT ")]
+            n_acc = [int(l.split("n_accepted=")[1].split()[0]) for l in acc]
+            stops = sum(l.startswith("END ") and " stop=1 " in l for l in plain)
+            print(f"mtp session (norm bits {tgt_bits:#x}, {mtp_bits:#x}): {len(acc)} rounds, accepted per round "
+                  f"{n_acc}, {stops} stopped turns; without the cut the transcript differs: {nocut != plain}",
+                  flush=True)
+            assert not any(l.startswith("ERROR") for l in plain_log + spec_log)
+            assert spec == plain
+            assert len(acc) > 0 and any(l.startswith("MTPSTAT ") for l in spec_log)
+            cut_mattered |= nocut != plain
+            accepted += sum(n_acc)
+        assert cut_mattered and accepted > 0
+    finally:
+        eng.close()
