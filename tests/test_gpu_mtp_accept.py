@@ -1,0 +1,76 @@
+"""MTP rounds that accept drafts (mtpaccept::accept_round, engine/mtp_accept.cpp:89; greedy
+accept + rollback of speccheck/mtp.py:150-177) at 8 lanes. Random-init drafts never agree
+with the target, so the final norms are reshaped to keep one hidden dimension d (1 + w = 0
+elsewhere) and two embedding rows get large entries in d: every greedy pick is then token
+248046 or 1000 by the sign of x_d, and the drafter agrees with the target often. Two
+settings: norm factors +4 / +4 (picks repeat: whole rounds accepted) and -4 / -4 (the
+target's picks alternate). Checked per lane against a plain State fed the same tokens one
+step at a time: every emitted token is the plain step's argmax, and after the rounds the
+GDN state S, the conv window and the K/V rows of both states are bit-identical (the verify
+rows and the kept state slot are those of plain steps: the rollback picked the right
+slot and prefix)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+D, STOP = 7, 248046
+
+
+def _norm_w(bits):
+    w = np.full(1024, 0xBF80, np.uint16)          # bf16 -1.0: 1 + w = 0
+    w[D] = bits
+    return w
+
+
+def test_mtp_rounds_with_accepts_match_plain_steps():
+    from oracle.weights import lane_prompt_ids
+    from qwen35 import Engine, State
+    eng = Engine(max_rows=64, max_ctx=512, seed=0)
+    try:
+        emb = "model.language_model.embed_tokens.weight"
+        E = eng.read_tensor(emb, 248320 * 1024).reshape(248320, 1024)
+        E[STOP, D] = 0x4100                          # bf16 8.0
+        E[1000, D] = 0xC100                          # bf16 -8.0
+        eng.load_tensor(emb, E.reshape(-1))
+        del E
+        lanes = 8
+        total = np.zeros(4, np.int64)
+        hist = {}
+        for bits in (0x4040, 0xC0A0):                # w[d] = 3.0 (factor 4), -5.0 (factor -4)
+            eng.load_tensor("model.language_model.norm.weight", _norm_w(bits))
+            eng.load_tensor("mtp.norm.weight", _norm_w(bits))
+            spec = State(eng, lanes, 256, mtp_k=2, mtp_cap=256)
+            plain = State(eng, lanes, 256)
+            cur = []
+            for i in range(lanes):
+                ids = lane_prompt_ids(30 + i, 0, 5 + 3 * i)
+                y = spec.prefill(i, ids)
+                assert plain.prefill(i, ids) == y
+                cur.append(int(y))
+            for r in range(6):
+                stats = np.zeros(4, np.int64)
+                print(f"mtp accept: norm bits {bits:#x}, round {r}", flush=True)
+                em = spec.mtp_round(cur, 2, list(range(lanes)), stats)
+                total += stats
+                for i in range(lanes):
+                    e = [int(t) for t in em[i]]
+                    hist[len(e) - 1] = hist.get(len(e) - 1, 0) + 1
+                    fed = [cur[i]] + e[:-1]
+                    for j, t in enumerate(fed):
+                        got = int(plain.decode_step([t], [i])[0])
+                        assert got == e[j], (bits, r, i, j)
+                    cur[i] = e[-1]
+                    assert spec.prefix_len(i) == plain.prefix_len(i)
+            for i in range(lanes):
+                P = plain.prefix_len(i)
+                for which in ("S", "win"):
+                    assert np.array_equal(spec.read(i, which), plain.read(i, which)), (bits, i, which)
+                for which in ("k", "v"):
+                    assert np.array_equal(spec.read(i, which, P), plain.read(i, which, P)), (bits, i, which)
+            spec.close()
+            plain.close()
+        print(f"mtp accept: accepted per round histogram {hist}, stats {total.tolist()}", flush=True)
+        assert hist.get(2, 0) > 0 and hist.get(0, 0) > 0
+    finally:
+        eng.close()
