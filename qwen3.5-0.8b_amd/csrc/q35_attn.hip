@@ -507,7 +507,7 @@ __global__ void __launch_bounds__(256) attn_fused(AttnArgs a, int lds_slots) {
 //                 4g + r of each 16-slot sub-tile: the MFMA's k index is taken in that order),
 //                 B = V columns read from LDS with ds_read_b64_tr_b16 (a 16-lane group reads
 //                 4 slots x 16 dims and receives them transposed), V tiles staged in LDS by
-//                 all 4 waves with 16-byte chunks XOR-swizzled by slot
+//                 all 4 waves as padded 544-byte rows
 // The softmax normalisation comes last (O / l), so the bf16 rounding of the weights happens
 // before it rather than after as on the decode path (speccheck/specimpl.py:385-392 rounds
 // the normalised weights): same math, different rounding point -- prompt logits stay within
