@@ -132,6 +132,14 @@ struct q35_engine {
     int *h_tok, *h_lane, *h_pos, *h_slot, *h_out, *h_src, *h_dst, *hin = nullptr;
     int* h_cur = nullptr;            // pinned staging of a state's `cur` for its upload
     int h_cur_cap = 0;               // (one engine buffer, sized for the largest state)
+    // Row metadata on the device (token, lane, position, slot, row indices; a state's `cur`)
+    // changes only by the uploads below, which bump meta_epoch, and by a decode step, which
+    // advances positions, slots and `cur` on the device and leaves its sampled tokens in the
+    // token row. The next decode step of the same state and lanes, fed exactly those tokens
+    // with the host's prefix and `cur` still at the values the step left, needs no upload.
+    uint64_t meta_epoch = 0, fast_epoch = ~0ull;
+    const void* fast_s = nullptr;
+    std::vector<int> fast_lanes, fast_prefix, fast_cur, fast_tok;
 };
 
 namespace {
@@ -366,17 +374,20 @@ void ensure_logits(q35_engine* e, int rows) {
 // Row metadata must already be staged in e->h_lane/h_pos/h_slot/h_tok for R rows.
 // One copy of the metadata block from tok through region `upto` (rows [0, n) of it).
 void upload_meta(q35_engine* e, int upto, int n) {
+    ++e->meta_epoch;
     HCK(hipMemcpyAsync(e->din, e->hin, ((size_t)upto * e->R + n) * sizeof(int), hipMemcpyHostToDevice, e->st));
 }
 void upload_rows(q35_engine* e, int R) { upload_meta(e, 3, R); }   // tok, lane, pos, slot
 // src / dst row indices only (tok_dev may hold device-written tokens): one copy
 void upload_idx(q35_engine* e, int n) {
+    ++e->meta_epoch;
     HCK(hipMemcpyAsync(e->ridx_src, e->h_src, ((size_t)e->R + n) * sizeof(int), hipMemcpyHostToDevice, e->st));
 }
 
 // `cur` goes through pinned staging: the host advances s->cur right after enqueueing a
 // body, so the copy must not read the live vector. Callers drain the stream before a body.
 void upload_cur(q35_engine* e, q35_state* s) {
+    ++e->meta_epoch;
     for (int i = 0; i < s->lanes; ++i) e->h_cur[i] = s->cur[i];
     HCK(hipMemcpyAsync(s->cur_dev, e->h_cur, s->lanes * sizeof(int), hipMemcpyHostToDevice, e->st));
 }
@@ -790,6 +801,7 @@ int q35_read_tensor(q35_engine* e, const char* name, uint16_t* host, size_t n) {
 
 int q35_state_alloc(q35_engine* e, int lanes, int cap, int mtp_k, int mtp_cap, q35_state** out) {
     return guard([&] {
+        if (e) ++e->meta_epoch;           // a state buffer may reuse a freed address
         REQ(e && out, Q35_ERR_ARG, "null argument");
         REQ(lanes > 0 && cap > 0 && mtp_k >= 0 && mtp_k <= 4 && mtp_cap >= 0, Q35_ERR_ARG, "bad state shape");
         REQ(cap <= e->max_ctx && mtp_cap <= e->max_ctx, Q35_ERR_CAP, "cap exceeds engine max_ctx");
@@ -828,6 +840,7 @@ int q35_state_alloc(q35_engine* e, int lanes, int cap, int mtp_k, int mtp_cap, q
 
 int q35_state_free(q35_engine* e, q35_state* s) {
     return guard([&] {
+        if (e) ++e->meta_epoch;           // a state buffer may reuse a freed address
         if (!s) return;
         if (e) {
             hipStreamSynchronize(e->st);
@@ -1127,13 +1140,21 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
         }
         REQ(e->weights_ready, Q35_ERR_STATE, "weights not initialised");
         for (int i = 0; i < n; ++i) { e->h_src[i] = i; e->h_dst[i] = ls[i]; }
-        upload_meta(e, 5, n);        // tok, lane, pos, slot, src, dst in one copy
-        upload_cur(e, s);
+        bool fast = e->fast_s == (const void*)s && e->fast_epoch == e->meta_epoch && (int)e->fast_lanes.size() == n;
+        for (int i = 0; fast && i < n; ++i)
+            fast = e->fast_lanes[i] == ls[i] && e->fast_tok[i] == tokens[i] &&
+                   e->fast_prefix[i] == s->prefix[ls[i]] && e->fast_cur[i] == s->cur[ls[i]];
+        e->fast_s = nullptr;                 // re-armed only when this step completes
+        if (!fast) {
+            upload_meta(e, 5, n);        // tok, lane, pos, slot, src, dst in one copy
+            upload_cur(e, s);
+        }
         auto step = [&] {
             body_kernels(e, s, n, 1, false);
             lm_head(e, 0, n, out_logits != nullptr,
                     small_rows(n) && !b1_partials(e, n, 1, false) ? e->final_norm : nullptr);
-            HCK(launch_copy_rows(e->nrm, e->ridx_src, s->hlast, e->ridx_dst, n, kHidden, e->st));
+            HCK(launch_copy_rows_advance(e->nrm, e->ridx_src, s->hlast, e->ridx_dst, n, kHidden, e->rpos, e->rslot,
+                                         e->rlane, s->cur_dev, s->nslots, e->st));
         };
         if (e->use_graph && e->kprof == 0) {
             if (out_logits) ensure_logits(e, n);
@@ -1167,6 +1188,13 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
         if (out_logits) HCK(hipMemcpyAsync(out_logits, e->logits_dev, (size_t)n * kVocab * 4, hipMemcpyDeviceToHost, e->st));
         HCK(hipStreamSynchronize(e->st));
         for (int i = 0; i < n; ++i) out_tok[i] = e->h_out[i];
+        e->fast_lanes.assign(ls.begin(), ls.begin() + n);
+        e->fast_tok.assign(out_tok, out_tok + n);
+        e->fast_prefix.resize(n);
+        e->fast_cur.resize(n);
+        for (int i = 0; i < n; ++i) { e->fast_prefix[i] = s->prefix[ls[i]]; e->fast_cur[i] = s->cur[ls[i]]; }
+        e->fast_epoch = e->meta_epoch;
+        e->fast_s = s;
     });
 }
 

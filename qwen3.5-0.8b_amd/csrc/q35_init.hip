@@ -112,6 +112,34 @@ __global__ void copy_rows_kernel(const uint16_t* src, const int* src_rows, uint1
     for (int k = threadIdx.x; k < width; k += blockDim.x) d[k] = s[k];
 }
 
+// copy_rows_kernel plus the decode step's metadata advance for row i (one row per lane): the
+// row's position and slot move to the next one and its lane's state slot index turns over,
+// so that the next decode step of the same lanes finds its metadata on the device (the
+// sampled token is already in place: the argmax writes it to the token row)
+__global__ void copy_rows_advance_kernel(const uint16_t* src, const int* src_rows, uint16_t* dst,
+                                         const int* dst_rows, int width, int* pos, int* slot,
+                                         const int* lane, int* cur, int nslots) {
+    const int i = blockIdx.x;
+    const uint16_t* s = src + (size_t)src_rows[i] * width;
+    uint16_t* d = dst + (size_t)dst_rows[i] * width;
+    for (int k = threadIdx.x; k < width; k += blockDim.x) d[k] = s[k];
+    if (threadIdx.x == 0) {
+        pos[i] += 1;
+        slot[i] += 1;
+        const int l = lane[i];
+        cur[l] = (cur[l] + 1) % nslots;
+    }
+}
+
+hipError_t launch_copy_rows_advance(const uint16_t* src, const int* src_rows, uint16_t* dst, const int* dst_rows,
+                                    int n, int width, int* pos, int* slot, const int* lane, int* cur, int nslots,
+                                    hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(copy_rows_advance_kernel, dim3(n), dim3(256), 0, st, src, src_rows, dst, dst_rows, width,
+                       pos, slot, lane, cur, nslots);
+    return hipGetLastError();
+}
+
 hipError_t launch_copy_rows(const uint16_t* src, const int* src_rows, uint16_t* dst, const int* dst_rows,
                             int n, int width, hipStream_t st) {
     if (n <= 0) return hipSuccess;

@@ -140,5 +140,8 @@ hipError_t launch_tile(const uint16_t* src, int N, int K, uint16_t* dst, int row
                        hipStream_t st);
 hipError_t launch_copy_rows(const uint16_t* src, const int* src_rows, uint16_t* dst, const int* dst_rows,
                             int n, int width, hipStream_t st);
+hipError_t launch_copy_rows_advance(const uint16_t* src, const int* src_rows, uint16_t* dst, const int* dst_rows,
+                                    int n, int width, int* pos, int* slot, const int* lane, int* cur, int nslots,
+                                    hipStream_t st);
 
 }  // namespace q35
