@@ -196,10 +196,10 @@ def test_config2_gdn_step(eng, oracle_weights, B):
         assert (o[b] - ro.reshape(-1)).abs().max().item() <= 1e-4 * ro.abs().max().item() + 1e-7, b
 
 
-@pytest.mark.parametrize("B,L", [(32, 1024), (256, 1024), (32, 8192), (256, 8192)])
+@pytest.mark.parametrize("B,L", [(32, 1024), (256, 1024), (32, 8192), (256, 8192), (32, 32768), (256, 32768)])
 def test_config3_attention_batched(oracle_weights, B, L):
     """BASELINE config 3 at batched lanes: B lanes of seeded state (N(0,1) bf16 K/V over L
-    slots, N(0,0.1) GDN state) take one decode step. B = 256 at L = 1024 runs the fused
+    slots, N(0,0.1) GDN state) take one decode step (L up to 32,768, config 3's largest). B = 256 at L = 1024 runs the fused
     per-lane attention kernel, the other cases the split slice/part kernels. Checked: lanes 0
     and B-1 against the oracle holding the same state (engine tolerances), and every checked
     lane's logits bit-identical to the same lane decoded alone (single-row path)."""
