@@ -1,4 +1,4 @@
-"""Decode throughput of the MI355X Qwen3.5-0.8B engine (BASELINE.json metric).
+"""Decode throughput of the MI355X Qwen3.5-0.8B engine (decode tok/s at batch 1 and 256, ctx 4096, with the HBM roofline fraction).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 256] [--ctx 4096]
 

@@ -133,7 +133,7 @@ int q35_mtp_round_stop(q35_engine* e, q35_state* s, const int32_t* lanes, int n,
 int q35_op_tile_weight(q35_engine* e, const uint16_t* w_rowmajor_dev, int N, int K, uint16_t* w_tiled_dev);
 int q35_op_gemm(q35_engine* e, const uint16_t* w_tiled_dev, int N, int K, const uint16_t* x_dev,
                 int M, uint16_t* y_dev);
-/* One GatedDeltaNet decode step for B independent lanes (the layer's
+/* One GatedDeltaNet decode step for B independent lanes (benchmark config 2; the layer's
  * conv + gates + L2 norms + delta rule, engine/kernels_gdn.cpp:35-536): proj [B][8224] bf16
  * (qkv 6144 | z 2048 | b 16 | a 16), conv_w [6144][4] bf16, A_log / dt_bias [16] bf16;
  * S2 [B][2][16][128][128] f32 and W2 [B][2][3][6144] f32 hold the input state in slot 0 and

@@ -7,7 +7,7 @@ speccheck/mtp.py:64-77 / specification/01-weights-and-shapes.md:71-84 for `mtp.*
 Every tensor is loaded as bf16, as specimpl's `Weights(dtype=torch.bfloat16)` does by
 default (specimpl.py:70-85, keep_f32_scalars=False).
 
-Init: matrices, embedding and conv N(0,0.02); RMSNorm weights and
+Init (benchmark config 0): matrices, embedding and conv N(0,0.02); RMSNorm weights and
 the gated-norm weight 1.0; A_log = log U(1,16); dt_bias ~ U(-1,1). Stream ids are
 fnv1a64(name); see prng.c for the stream definition.
 """

@@ -1,5 +1,5 @@
-"""Chunked (UT-transform, chunk 64) GatedDeltaNet prompt path (SURVEY row a13;
-speccheck/specimpl.py:187-235) against the recurrent path of the same engine and against the
+"""Chunked (UT-transform, chunk 64) GatedDeltaNet prompt path
+(speccheck/specimpl.py:187-235) against the recurrent path of the same engine and against the
 oracle's own chunk form (oracle/model.py gdn_chunk_scan).
 
 Tolerances (stated and checked):

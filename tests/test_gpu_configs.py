@@ -1,4 +1,4 @@
-"""BASELINE.json parity configs on the GPU, op by op through the C ABI.
+"""The benchmark's parity configs on the GPU, op by op through the C ABI.
 
 config 1: every decode projection shape at batch 1, 16 and 256 (W ~ N(0,0.02), x ~ N(0,1)
           bf16), plus the tied lm_head with argmax. Bar: within one bf16 rounding plus the f32
@@ -198,7 +198,7 @@ def test_config2_gdn_step(eng, oracle_weights, B):
 
 @pytest.mark.parametrize("B,L", [(32, 1024), (256, 1024), (32, 8192), (256, 8192), (32, 32768), (256, 32768)])
 def test_config3_attention_batched(oracle_weights, B, L):
-    """BASELINE config 3 at batched lanes: B lanes of seeded state (N(0,1) bf16 K/V over L
+    """Benchmark config 3 at batched lanes: B lanes of seeded state (N(0,1) bf16 K/V over L
     slots, N(0,0.1) GDN state) take one decode step (L up to 32,768, config 3's largest). B = 256 at L = 1024 runs the fused
     per-lane attention kernel, the other cases the split slice/part kernels. Checked: lanes 0
     and B-1 against the oracle holding the same state (engine tolerances), and every checked

@@ -269,7 +269,7 @@ def test_one_row_partials_equal_epilogue_add(eng):
 @pytest.mark.parametrize("P", [4096, 9000, 32768, 131072])
 def test_seeded_state_decode(oracle_weights, P):
     """The benchmark's seeded workload: lanes with N(0,0.1) GDN state and N(0,1) K/V over P
-    slots (P = 9000, 32768 and 131072: up to 512 score chunks and 1024 P.V parts, 4x BASELINE config 3's
+    slots (P = 9000, 32768 and 131072: up to 512 score chunks and 1024 P.V parts, 4x benchmark config 3's
     longest context) decode one step like the oracle
     holding the same state (oracle/seeded.py)."""
     import torch

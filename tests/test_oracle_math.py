@@ -1,6 +1,6 @@
 """Pins oracle/model.py's functions against float64 brute force (oracle/ref64.py),
 closed forms and invariants, chosen so that a dropped term, a swapped operand or a wrong
-index fails (specification/03-05; SURVEY-listed invariants)."""
+index fails (specification/03-05 and their stated invariants)."""
 import numpy as np
 import torch
 import torch.nn.functional as F
