@@ -18,13 +18,25 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 }
 
 // One row per block, 256 threads x 4 elements.
-__global__ void __launch_bounds__(256) addnorm_kernel(int mode, const int* tok, const uint16_t* E,
+// The mode is a template argument: with a run-time mode the compiler waited for the residual
+// row's load at the mode branch, before issuing the chain loads (two round trips instead of one).
+template <int mode>
+__global__ void __launch_bounds__(256) addnorm_kernel(const int* tok, const uint16_t* E,
                                                       uint16_t* x, const uint16_t* delta,
                                                       const float* kpart, int kblocks,
                                                       const uint16_t* w, uint16_t* h) {
     __shared__ float red[4];
     const int r = blockIdx.x;
     const int k = threadIdx.x * 4;
+    // every load first: the GEMM k-block chains, then the residual row, then the norm weight
+    float4 d[16];
+    if (mode == 3 || mode == 4) {
+        const size_t stride = (size_t)gridDim.x * kHidden;
+#pragma unroll
+        for (int kb = 0; kb < 16; ++kb)
+            if (kb < kblocks) d[kb] = *(const float4*)(kpart + kb * stride + (size_t)r * kHidden + k);
+    }
+    const uint2 wv = h ? *(const uint2*)(w + k) : make_uint2(0u, 0u);
     float xv[4];
     uint16_t* xr = x + (size_t)r * kHidden + k;
     if (mode == 0) {
@@ -45,11 +57,6 @@ __global__ void __launch_bounds__(256) addnorm_kernel(int mode, const int* tok, 
                 dv[2] = __uint_as_float(d.y << 16); dv[3] = __uint_as_float(d.y & 0xffff0000u);
             } else {
                 // GEMM k-block chains summed in k-block order, rounded once to bf16
-                const size_t stride = (size_t)gridDim.x * kHidden;
-                float4 d[16];
-#pragma unroll
-                for (int kb = 0; kb < 16; ++kb)
-                    if (kb < kblocks) d[kb] = *(const float4*)(kpart + kb * stride + (size_t)r * kHidden + k);
                 float4 c = d[0];
 #pragma unroll
                 for (int kb = 1; kb < 16; ++kb)
@@ -70,7 +77,6 @@ __global__ void __launch_bounds__(256) addnorm_kernel(int mode, const int* tok, 
     float ss = quad_ss(xv[0], xv[1], xv[2], xv[3]);
     ss = block_sum256(ss, red);
     const float rs = hidden_rsqrt(ss);
-    uint2 wv = *(const uint2*)(w + k);
     float wf[4] = {__uint_as_float(wv.x << 16), __uint_as_float(wv.x & 0xffff0000u),
                    __uint_as_float(wv.y << 16), __uint_as_float(wv.y & 0xffff0000u)};
     uint16_t o[4];
@@ -117,8 +123,16 @@ hipError_t launch_addnorm(int mode, const int* tok, const uint16_t* E, uint16_t*
                           const uint16_t* delta, const float* kpart, int kblocks,
                           const uint16_t* w, uint16_t* h, int rows, hipStream_t st) {
     if (rows <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(addnorm_kernel, dim3(rows), dim3(256), 0, st, mode, tok, E, x, delta, kpart,
-                       kblocks, w, h);
+#define Q35_ADDNORM(M) hipLaunchKernelGGL(addnorm_kernel<M>, dim3(rows), dim3(256), 0, st, tok, E, x, delta, kpart, kblocks, w, h)
+    switch (mode) {
+        case 0: Q35_ADDNORM(0); break;
+        case 1: Q35_ADDNORM(1); break;
+        case 2: Q35_ADDNORM(2); break;
+        case 3: Q35_ADDNORM(3); break;
+        case 4: Q35_ADDNORM(4); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef Q35_ADDNORM
     return hipGetLastError();
 }
 
