@@ -150,16 +150,15 @@ int q35_kprof_read(q35_engine* e, float* total_ms, int* launches);
 /* Options: "layers" (diagnostic: bodies run only the first n of the 24 layers, the final
  * norm then applies to that layer's output), "graph" (0/1: capture decode steps), "kprof"
  * (above), "gdn_chunked" (0/1: chunked GDN form for prompt waves of >= 64 rows). Kernel-form
- * switches, each bit-identical to its alternative and kept for A/B measurement, dropping the
- * engine's captured steps when set: "b1_partials" (this engine: one-row bodies leave k-block
- * chains for the next norm GEMV) and, process-wide (every engine of the process), "gemv_tpb"
- * (1/2 column tiles per block of the one-row norm GEMVs), "gemm_pre" (batched K = 1024 GEMMs
- * issue all loads up front), "lmhead_persist" (persistent lm_head at batched lanes),
- * "partial_rows" (>= 17: batched out/o/down GEMMs with at least this many rows sum their
- * k-block chains in the block, one chain for the add+norm; default 1,024). Not
- * bit-identical, a different rounding point within the stated tolerance: "attn_prompt"
- * (process-wide; 1: prompt waves of one lane with >= 64 rows use the flash-form MFMA
- * attention kernel, 0: the one-row kernels). */
+ * switches of this engine only (each engine holds its own; setting one drops the engine's
+ * captured steps), each bit-identical to its alternative and kept for A/B measurement:
+ * "b1_partials" (one-row bodies leave k-block chains for the next norm GEMV), "gemv_tpb" (1/2
+ * column tiles per block of the one-row norm GEMVs), "gemm_pre" (batched K = 1024 GEMMs issue
+ * all loads up front), "lmhead_persist" (persistent lm_head at batched lanes), "partial_rows"
+ * (>= 17: batched out/o/down GEMMs with at least this many rows sum their k-block chains in
+ * the block, one chain for the add+norm; default 1,024). Not bit-identical, a different
+ * rounding point within the stated tolerance: "attn_prompt" (1: prompt waves of one lane with
+ * >= 64 rows use the flash-form MFMA attention kernel, 0: the one-row kernels). */
 int q35_set_option(q35_engine* e, const char* name, int value);
 /* Copy the current content of a named scratch buffer ("x", "h", "nrm", "delta", "proj",
  * "o", "gu", "aout", "q") to host, after the stream drains (diagnostics and tests). */

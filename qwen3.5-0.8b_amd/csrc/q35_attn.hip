@@ -520,8 +520,6 @@ typedef short q35_s16x4 __attribute__((ext_vector_type(4)));
 // an immediate offset
 constexpr int kPrVRow = 34, kPrVBuf = 64 * kPrVRow * 16;    // 16-byte slots per row; bytes per V tile
 
-static int g_attn_prompt = 1;
-void set_attn_prompt(int on) { g_attn_prompt = on; }
 
 constexpr int kPrLds = 2 * 64 * 256 * 2 + 2 * kPrVBuf;   // K and V tiles, double-buffered: 132 KiB
 
@@ -771,7 +769,7 @@ hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
     if (a.R <= 0 || a.max_chunks <= 0) return hipErrorInvalidValue;
     const int lds_slots = (a.cap + 63) / 64 * 64;
     const size_t lds = fused_lds(a);
-    if (g_attn_prompt && a.T >= 64 && a.R == a.T) {
+    if (a.prompt_flash && a.T >= 64 && a.R == a.T) {
         // one lane's prompt wave: 16 rows per block, kv head by XCD half
         const int ngrp = (a.T + kPrRows - 1) / kPrRows;
         hipLaunchKernelGGL(attn_prompt, dim3((ngrp + 3) / 4 * 8), dim3(256), kPrLds, st, a);

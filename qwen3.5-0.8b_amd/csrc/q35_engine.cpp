@@ -104,6 +104,7 @@ struct q35_engine {
     int kprof = 0;                   // kernel family timed with HIP events (0 = off)
     int gdn_chunked = 1;             // prompt waves of one lane use the chunked GDN form
     int b1_partials = 1;             // one-row bodies: 1024-wide GEMVs leave k-block chains
+    KernelForms forms;               // this engine's kernel-form choices (q35_set_option)
     float *gchunk = nullptr, *gcdec = nullptr;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> kev;
     size_t kev_used = 0;
@@ -137,6 +138,8 @@ struct q35_engine {
     // advances positions, slots and `cur` on the device and leaves its sampled tokens in the
     // token row. The next decode step of the same state and lanes, fed exactly those tokens
     // with the host's prefix and `cur` still at the values the step left, needs no upload.
+    // Every other call that changes a state's host prefix / cur or the device rows (reset,
+    // seed, lane copy, restore, MTP rounds, allocation and release) bumps meta_epoch too.
     uint64_t meta_epoch = 0, fast_epoch = ~0ull;
     const void* fast_s = nullptr;
     std::vector<int> fast_lanes, fast_prefix, fast_cur, fast_tok;
@@ -400,7 +403,7 @@ void gemm(q35_engine* e, const uint16_t* W, int N, int K, int M, const void* X, 
     GemmArgs a{};
     a.W = W; a.N = N; a.K = K; a.M = M; a.X = X; a.ldx = ldx; a.X2 = X2; a.ldx2 = ldx2;
     a.aux_w = aux; a.Y = Y; a.ldy = ldy;
-    a.kpart = e->kpart; a.prod = e->prod; a.xres = xres;
+    a.kpart = e->kpart; a.prod = e->prod; a.xres = xres; a.forms = e->forms;
     KTimer kt(e, kFamGemm);
     HCK(launch_gemm(a, amode, emode >= 0 ? emode : (Y ? kEStore : kEPartial), e->st));
 }
@@ -432,7 +435,7 @@ void norm_gemm(q35_engine* e, B1Res* rr, const uint16_t* W, int N, int R, uint16
     }
     GemmArgs a{};
     a.W = W; a.N = N; a.K = kHidden; a.M = 1; a.X = rr->cur; a.ldx = kHidden;
-    a.aux_w = normw; a.Y = Y; a.ldy = ldy;
+    a.aux_w = normw; a.Y = Y; a.ldy = ldy; a.forms = e->forms;
     int amode = kANormX;
     if (rr->pend) {
         amode = kANormXP;
@@ -470,7 +473,7 @@ void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16
     a.q = e->q; a.sc = e->sc; a.sc_ld = e->sc_ld; a.stats = e->stats; a.part = e->part;
     a.max_chunks = (cap + 255) / 256;
     REQ(a.max_chunks <= e->max_chunks, Q35_ERR_CAP, "cache capacity exceeds engine max_ctx");
-    a.out = e->aout; a.R = R; a.T = T; a.inv_freq = e->inv_freq;
+    a.out = e->aout; a.R = R; a.T = T; a.inv_freq = e->inv_freq; a.prompt_flash = e->forms.attn_prompt;
     HCK(launch_attn_prep(a, e->st));
     {
         KTimer kt(e, kFamAttn);      // the attention core alone (scores, softmax, P.V, gate)
@@ -486,7 +489,7 @@ void mlp_layer(q35_engine* e, const LayerW& w, int R, B1Res* rr = nullptr) {
         resid_gemm(e, rr, w.W_down, kFF, R, e->gu, kGuRows, kASiluMul, e->gu + kFF, kGuRows);
         return;
     }
-    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(R, 2048), w.norm_post, e->h, R, e->st));
+    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(R, 2048, e->forms), w.norm_post, e->h, R, e->st));
     // gate|up GEMM with the SwiGLU product in its epilogue: act [R][3584] -> plain down GEMM
     gemm(e, w.W_gu, kGuRows, kHidden, R, e->h, kHidden, e->gu, kFF, kAPlain, nullptr, 0, nullptr, kESiluMul);
     gemm(e, w.W_down, kHidden, kFF, R, e->gu, kFF, nullptr, 0);
@@ -495,7 +498,7 @@ void mlp_layer(q35_engine* e, const LayerW& w, int R, B1Res* rr = nullptr) {
 // Batched path: fold the down-projection chains into x and normalise for the next consumer.
 void finish_norm(q35_engine* e, int R, const uint16_t* nw, uint16_t* out) {
     if (small_rows(R)) return;
-    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(R, kFF), nw, out, R, e->st));
+    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(R, kFF, e->forms), nw, out, R, e->st));
 }
 
 // Runs the 24-layer body over R = nl * T rows (rows of one lane consecutive) and leaves the
@@ -569,6 +572,7 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
 void lm_head(q35_engine* e, int row0, int M, bool want_logits, const uint16_t* normw = nullptr) {
     GemmArgs a{};
     a.W = e->E; a.N = kVocab; a.K = kHidden; a.M = M; a.X = e->nrm + (size_t)row0 * kHidden; a.ldx = kHidden;
+    a.forms = e->forms;
     const int amode = kAPlain;
     if (normw)   // one small norm launch: cheaper than normalising in each of the 15,520 blocks
         HCK(launch_addnorm(2, nullptr, nullptr, e->x + (size_t)row0 * kHidden, nullptr, nullptr, 0, normw,
@@ -603,7 +607,7 @@ void mtp_draft_pass(q35_engine* e, q35_state* s, int n, const uint16_t* hsrc) {
         gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, e->x, kHidden);
     } else {
         gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, nullptr, 0);
-        HCK(launch_addnorm(4, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(n, 2048), e->M.norm_in, e->h, n, e->st));
+        HCK(launch_addnorm(4, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(n, 2048, e->forms), e->M.norm_in, e->h, n, e->st));
     }
     attention_layer(e, e->M, n, s->mkc, s->mvc, s->mkv_lane(), 0, s->mtp_capT);
     mlp_layer(e, e->M, n);
@@ -861,6 +865,7 @@ int q35_state_reset(q35_engine* e, q35_state* s, const int32_t* lanes, int n) {
     return guard([&] {
         REQ(e && s, Q35_ERR_ARG, "null argument");
         HCK(hipStreamSynchronize(e->st));
+        ++e->meta_epoch;                 // host prefix / cur change: the next step uploads
         for (int i = 0; i < (lanes ? n : s->lanes); ++i) {
             int l = lanes ? lanes[i] : i;
             check_lane(s, l);
@@ -876,6 +881,7 @@ int q35_state_seed(q35_engine* e, q35_state* s, uint64_t seed, int prefix_len) {
     return guard([&] {
         REQ(e && s, Q35_ERR_ARG, "null argument");
         REQ(prefix_len >= 0 && prefix_len < s->cap, Q35_ERR_CAP, "prefix_len must leave room in the cache");
+        ++e->meta_epoch;
         const float s01 = (float)(0.1 / 65536.0), s1 = (float)(1.0 / 65536.0);
         for (int l = 0; l < s->lanes; ++l) {
             float* S0 = s->S + l * s->S_lane();   // slot 0
@@ -1065,6 +1071,7 @@ int q35_state_copy_lane(q35_engine* e, q35_state* src, int src_lane, q35_state* 
     return guard([&] {
         REQ(e && src && dst, Q35_ERR_ARG, "null argument");
         HCK(hipStreamSynchronize(e->st));
+        ++e->meta_epoch;
         copy_lane(e, src, src_lane, dst, dst_lane);
     });
 }
@@ -1077,6 +1084,7 @@ int q35_state_snapshot(q35_engine* e, q35_state* s, int lane, void* host, size_t
 int q35_state_restore(q35_engine* e, q35_state* s, int lane, const void* host, size_t bytes) {
     return guard([&] {
         REQ(e && s && host, Q35_ERR_ARG, "null argument");
+        ++e->meta_epoch;
         restore_lane(e, s, lane, host, bytes);
     });
 }
@@ -1245,6 +1253,7 @@ int q35_mtp_round_stop(q35_engine* e, q35_state* s, const int32_t* lanes, int n,
         REQ(e && s && cur && emit && n_emit, Q35_ERR_ARG, "null argument");
         REQ(k >= 1 && k <= s->mtp_k, Q35_ERR_STATE, "k exceeds the state's MTP slots");
         REQ(n > 0 && n * (k + 1) <= e->R, Q35_ERR_CAP, "rows exceed max_rows");
+        ++e->meta_epoch;                 // drafts and the verify body rewrite the row metadata
         std::vector<int> ls(n), P(n);
         for (int i = 0; i < n; ++i) {
             ls[i] = lanes ? lanes[i] : i;
@@ -1337,7 +1346,7 @@ int q35_op_lm_head_argmax(q35_engine* e, const uint16_t* x, int M, int32_t* tok,
     return guard([&] {
         REQ(e && x && tok && M > 0 && M <= e->R, Q35_ERR_ARG, "bad lm_head call");
         GemmArgs a{};
-        a.W = e->E; a.N = kVocab; a.K = kHidden; a.M = M; a.X = x; a.ldx = kHidden;
+        a.W = e->E; a.N = kVocab; a.K = kHidden; a.M = M; a.X = x; a.ldx = kHidden; a.forms = e->forms;
         a.logits = logits; a.ldl = kVocab;
         a.part_val = e->pval; a.part_idx = e->pidx; a.ldp = kVocab / 16;
         HCK(launch_gemm(a, kAPlain, kEArgmax, e->st));
@@ -1362,36 +1371,18 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
         } else if (n == "gdn_chunked") {
             HCK(hipStreamSynchronize(e->st));
             e->gdn_chunked = value ? 1 : 0;
-        } else if (n == "attn_prompt") {         // process-wide kernel choice; drops captured steps
+        } else if (n == "b1_partials" || n == "attn_prompt" || n == "partial_rows" || n == "gemv_tpb" ||
+                   n == "gemm_pre" || n == "lmhead_persist") {
+            // kernel-form switches of this engine: captured steps hold the old forms
+            REQ(n != "partial_rows" || value >= 17, Q35_ERR_ARG, "partial_rows must exceed the 16-row batch-1 path");
+            REQ(n != "gemv_tpb" || value == 1 || value == 2, Q35_ERR_ARG, "gemv_tpb is 1 or 2");
             HCK(hipStreamSynchronize(e->st));
-            set_attn_prompt(value ? 1 : 0);
-            for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
-            e->graphs.clear();
-        } else if (n == "partial_rows") {         // process-wide kernel choice; drops captured steps
-            REQ(value >= 17, Q35_ERR_ARG, "partial_rows must exceed the 16-row batch-1 path");
-            HCK(hipStreamSynchronize(e->st));
-            set_partial_rows(value);
-            for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
-            e->graphs.clear();
-        } else if (n == "gemv_tpb") {            // process-wide kernel choice; drops captured steps
-            REQ(value == 1 || value == 2, Q35_ERR_ARG, "gemv_tpb is 1 or 2");
-            HCK(hipStreamSynchronize(e->st));
-            set_gemv_tpb(value);
-            for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
-            e->graphs.clear();
-        } else if (n == "gemm_pre") {            // process-wide kernel choice; drops captured steps
-            HCK(hipStreamSynchronize(e->st));
-            set_gemm_pre(value ? 1 : 0);
-            for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
-            e->graphs.clear();
-        } else if (n == "b1_partials") {         // drops captured steps
-            HCK(hipStreamSynchronize(e->st));
-            e->b1_partials = value ? 1 : 0;
-            for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
-            e->graphs.clear();
-        } else if (n == "lmhead_persist") {      // process-wide kernel choice; drops captured steps
-            HCK(hipStreamSynchronize(e->st));
-            set_lmhead_persist(value ? 1 : 0);
+            if (n == "b1_partials") e->b1_partials = value ? 1 : 0;
+            else if (n == "attn_prompt") e->forms.attn_prompt = value ? 1 : 0;
+            else if (n == "partial_rows") e->forms.partial_rows = value;
+            else if (n == "gemv_tpb") e->forms.gemv_tpb = value;
+            else if (n == "gemm_pre") e->forms.gemm_pre = value ? 1 : 0;
+            else e->forms.lmhead_persist = value ? 1 : 0;
             for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
             e->graphs.clear();
         } else {

@@ -536,10 +536,6 @@ __global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
 // loads) adds no wait for all loads; every wait is explicit and tied to the registers it
 // guards. At 256 lanes: gate|up 17.1 us (pipelined kernel 18.2), attention qkv 11.9 (14.8).
 constexpr int kPreKB = kHidden / 256;
-static int g_gemv_tpb = 2;
-void set_gemv_tpb(int v) { g_gemv_tpb = v; }
-static int g_gemm_pre = 1;
-void set_gemm_pre(int on) { g_gemm_pre = on; }
 
 template <int MT> constexpr int pre_lds_bytes() { return kPreKB * MT * 8 * 64 * 16; }
 
@@ -681,8 +677,6 @@ __global__ void __launch_bounds__(256) gemm_pre(GemmArgs a) {
 // tile from LDS; <4, 4> at one wave per SIMD: 420 us). The row blocks of one column stream
 // sit on one XCD and share each weight unit through its L2.
 // Reduction order = the canonical one above (chain per k-block from zero, summed in order).
-static int g_lmhead_persist = 1;
-void set_lmhead_persist(int on) { g_lmhead_persist = on; }
 constexpr int kLmKB = kHidden / 256;
 constexpr int kLmLds = 4 * kLmKB * 8 * 64 * 16;          // 128 KiB of A fragments
 
@@ -843,19 +837,17 @@ __global__ void __launch_bounds__(1024) argmax_rows(const float* pv, const int* 
     }
 }
 
-// kEPartial GEMMs with at least this many rows sum all k-block chains in the block (one chain
-// left for the add+norm) instead of one block per chain
-static int g_partial_rows = 1024;
-void set_partial_rows(int m) { g_partial_rows = m; }
-int gemm_partial_chains(int M, int K) { return M > 16 && M >= g_partial_rows ? 1 : K / 256; }
+// kEPartial GEMMs with at least forms.partial_rows rows sum all k-block chains in the block
+// (one chain left for the add+norm) instead of one block per chain
+int gemm_partial_chains(int M, int K, const KernelForms& f) { return M > 16 && M >= f.partial_rows ? 1 : K / 256; }
 
 template <int EM>
 static void launch_large(const GemmArgs& a, hipStream_t st) {
     const int KB = a.K / 256;
-    const int gz = EM == kEPartial ? (a.M >= g_partial_rows ? 1 : KB) : 1;
+    const int gz = EM == kEPartial ? (a.M >= a.forms.partial_rows ? 1 : KB) : 1;
     // 64-row tiles: more blocks in flight (W tiles are re-read from L2 by the M tiles)
     const int nb = EM == kESiluMul ? (a.N / 32 + 1) / 2 : (a.N / 16 + 3) / 4, mb = (a.M + 63) / 64;
-    if (EM == kEArgmax && a.K == kHidden && a.N % 64 == 0 && g_lmhead_persist) {
+    if (EM == kEArgmax && a.K == kHidden && a.N % 64 == 0 && a.forms.lmhead_persist) {
         // persistent blocks with A resident in LDS: mbk row blocks x (256 / mbk) column
         // streams, one block per CU (the 128 KiB of A fragments allow no second). Above 512
         // rows (MTP verify: 3 rows per lane) in launches of at most 256 rows: rows are
@@ -881,7 +873,7 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
         hipLaunchKernelGGL((gemm_large_m<EM, 4, 16>), dim3((nb16 + 7) / 8 * 8 * mb, 1, gz), dim3(1024), 0, st, a);
         return;
     }
-    if ((EM == kEStore || EM == kESiluMul) && a.K == kHidden && g_gemm_pre) {
+    if ((EM == kEStore || EM == kESiluMul) && a.K == kHidden && a.forms.gemm_pre) {
         // 32-row blocks (64 KiB of A fragments: two blocks per CU); 64-row blocks (128 KiB,
         // one per CU) measured 10-35 % slower
         const int mb2 = (a.M + 31) / 32;
@@ -902,7 +894,7 @@ static hipError_t launch_am_em(const GemmArgs& a, hipStream_t st) {
         const size_t lds = AM == kAPlain ? 0 : (size_t)waves * (512 * 16 + 64 * 4);
         if (EM == kEPartial)
             hipLaunchKernelGGL((gemm_small_m<AM, EM>), dim3(a.N / 16, 1, KB), dim3(64), lds, st, a);
-        else if ((AM == kANormX || AM == kANormXP) && EM == kEStore && a.M == 1 && g_gemv_tpb == 2 &&
+        else if ((AM == kANormX || AM == kANormXP) && EM == kEStore && a.M == 1 && a.forms.gemv_tpb == 2 &&
                  a.N % 32 == 0 && a.N >= 4096 && KB == 4)
             hipLaunchKernelGGL((gemm_small_m<AM, EM, 2>), dim3(a.N / 32, 1, 1), dim3(64 * KB), 0, st, a);
         else

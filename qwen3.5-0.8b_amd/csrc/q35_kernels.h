@@ -11,6 +11,17 @@ enum { kEStore = 0, kEArgmax = 1, kEPartial = 2, kEResidual = 3, kESiluMul = 4 }
 // kESiluMul (batched lanes): N = 2F columns [gate | up]; each block pairs gate tiles with the
 // matching up tiles and stores act = bf16(bf16(silu(bf16 g)) * bf16 u) into Y [M][F].
 
+// Kernel-form choices of one engine (q35_set_option), each bit-identical to its alternative
+// except attn_prompt (a different rounding point within the stated tolerance). They travel
+// with the launch arguments, so engines of one process never see each other's settings.
+struct KernelForms {
+    int gemv_tpb = 2;          // one-row norm GEMVs (N >= 4096): column tiles per block, 1 or 2
+    int gemm_pre = 1;          // batched K = 1024 GEMMs: all loads up front (1) or k-block pipelined (0)
+    int lmhead_persist = 1;    // tied lm_head at batched lanes: persistent kernel (1) or 64 x 256 tiles (0)
+    int partial_rows = 1024;   // batched kEPartial GEMMs with M >= this leave one (summed) chain
+    int attn_prompt = 1;       // prompt waves of >= 64 rows: flash-form MFMA kernel (1) or one-row kernels (0)
+};
+
 struct GemmArgs {
     const uint16_t* W;     // tiled [N/16][K/256] x 8 KiB
     int N, K, M;
@@ -31,14 +42,12 @@ struct GemmArgs {
     uint16_t* xres;        // kEResidual: residual rows [M][1024], x <- bf16(x + bf16(sum))
     uint16_t* hout;        // kANormX (optional): the normalised rows [M][1024] are written here
     int kpb;               // kANormXP: k-block chains of the producing GEMM pending in kpart
+    KernelForms forms;
 };
 // One-time kernel attribute setup (dynamic LDS above 64 KiB for the batch-1 producers).
 hipError_t gemm_init();
-void set_gemv_tpb(int v);
-void set_partial_rows(int m);     // batched kEPartial GEMMs with M >= m leave one (summed) chain
-int gemm_partial_chains(int M, int K);   // k-block chains a batched kEPartial GEMM leaves in kpart          // one-row norm GEMVs (N >= 4096): column tiles per block, 1 or 2
-void set_gemm_pre(int on);         // batched K = 1024 GEMMs: all loads up front (1) or k-block pipelined (0)
-void set_lmhead_persist(int on);   // tied lm_head at batched lanes: persistent kernel (1) or 64 x 256 tiles (0)
+// k-block chains a batched kEPartial GEMM leaves in kpart
+int gemm_partial_chains(int M, int K, const KernelForms& f);
 hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st);
 hipError_t launch_argmax(const float* pv, const int* pi, int ldp, int n, int rows, int* tok,
                          float* val, hipStream_t st);
@@ -121,11 +130,11 @@ struct AttnArgs {
     int R;
     int T;                 // rows per lane (a lane's rows are consecutive; MTP verify: k + 1)
     const float* inv_freq; // [32] f32 rope inverse frequencies
+    int prompt_flash;      // KernelForms::attn_prompt of the calling engine
 };
 hipError_t launch_attn_prep(const AttnArgs& a, hipStream_t st);   // q/k norm + rope, cache append
 hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st);   // scores, softmax, P.V, gate
 hipError_t attn_init();   // one-time kernel attribute setup
-void set_attn_prompt(int on);  // prompt waves of >= 64 rows: flash-form MFMA kernel (1) or the one-row kernels (0)
 
 // Synthetic init (portable stream, see q35_init.hip).
 hipError_t launch_gen_normal_tiled(uint64_t key, float scale, int N, int K, int row_off_dst,

@@ -157,3 +157,28 @@ def test_prompt_attention_full_odd_capacity():
     print(f"  odd capacity: max |d| {d.max():.3g}, mean |d| {d.mean():.3g}", flush=True)
     assert np.isfinite(aout).all()
     assert (d <= 2 * ulp + REL_W * mag).all() and d.mean() <= MEAN_D, (d.max(), d.mean())
+
+
+def test_kernel_forms_are_per_engine(eng):
+    """A kernel-form switch set on one engine leaves another engine of the process alone: the
+    second engine's prompt logits keep the bits of its own (flash-form) kernel."""
+    from oracle.weights import lane_prompt_ids
+    from qwen35 import Engine, State
+    ids = lane_prompt_ids(8, 2, 96)
+
+    def run(e):
+        st = State(e, 1, 256)
+        y, lg = st.prefill(0, ids, logits=True)
+        st.close()
+        return y, lg
+
+    y1, l1 = run(eng)
+    other = Engine(max_rows=512, max_ctx=2048, seed=0)
+    try:
+        other.set_option("attn_prompt", 0)
+        y0, l0 = run(other)
+        y2, l2 = run(eng)
+    finally:
+        other.close()
+    assert y1 == y2 and np.array_equal(l1, l2)
+    assert not np.array_equal(l0, l1)    # the one-row kernels round the weights differently

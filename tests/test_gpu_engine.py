@@ -85,19 +85,83 @@ def test_teacher_forced_logits(eng, oracle_run):
     assert not mism, mism
 
 
-def test_free_running_greedy(eng, oracle_run):
+def test_teacher_forced_vs_reference_golden(eng, golden):
+    """The engine against the reference's own bits (tests/golden/config0_greedy.npz, written by
+    speccheck/specimpl.py:496-517 in the build container): the prompt, then the reference's 64
+    greedy tokens fed back (teacher forcing), so every one of the 65 logits rows is the row the
+    reference priced.
+      * logits at the reference's top-32 ids of every row within LOGIT_MAX of its values, mean
+        |d| over all rows within LOGIT_MEAN; logits0 / logits64 (the first 4,096 vocabulary
+        entries of rows 0 and 64) the same
+      * argmax == the reference's token on every row whose reference top-1/top-2 gap exceeds
+        GAP, and on every row whose gap exceeds twice that row's measured max |d| over the
+        top-32 ids (no plausible rounding difference could reorder such a row); rows that
+        pass neither are named as near-ties"""
+    from qwen35 import State, Forward
+    g = golden["config0_greedy"]
+    ids = [int(t) for t in g["prompt"]]
+    gold = [int(t) for t in g["tokens"]]
+    top_i, top_v = g["top_i"], g["top_v"]
+    st = State(eng, 1, 512)
+    f = Forward(eng, st)
+    y0, lg = f.prefill(ids, logits=True)
+    rows, toks = [lg], [y0]
+    for s in range(64):
+        t, lg = f.decode(gold[s], logits=True)
+        rows.append(lg)
+        toks.append(t)
+    st.close()
+    maxes, means, skipped, bad = [], [], [], []
+    for r in range(65):
+        d = np.abs(rows[r][top_i[r]] - top_v[r])
+        maxes.append(float(d.max()))
+        means.append(float(d.mean()))
+        gap = float(top_v[r][0] - top_v[r][1])
+        assert toks[r] == int(np.flatnonzero(rows[r] == rows[r].max())[0])   # lowest id of the max
+        if gap > GAP or gap > 2 * d.max():
+            if toks[r] != gold[r]:
+                bad.append((r, toks[r], gold[r], gap, float(d.max())))
+        else:
+            skipped.append((r, round(gap, 4), round(float(d.max()), 4)))
+        print(f"row {r:2d}: max|d|={d.max():.4f} mean|d|={d.mean():.5f} gap={gap:.4f} "
+              f"{'ok' if toks[r] == gold[r] else 'differs'}", flush=True)
+    d0 = np.abs(rows[0][:4096] - g["logits0"])
+    d64 = np.abs(rows[64][:4096] - g["logits64"])
+    print(f"top-32 over 65 rows: max|d|={max(maxes):.4f} mean|d|={np.mean(means):.5f}; "
+          f"logits0 max {d0.max():.4f} mean {d0.mean():.5f}; logits64 max {d64.max():.4f} "
+          f"mean {d64.mean():.5f}; near-ties not checked (row, gap, max|d|): {skipped}", flush=True)
+    assert not bad, bad
+    assert max(maxes) <= LOGIT_MAX and np.mean(means) <= LOGIT_MEAN
+    for d in (d0, d64):
+        assert d.max() <= LOGIT_MAX and d.mean() <= LOGIT_MEAN
+
+
+def _golden_near_tie(golden, r):
+    """Row r of the reference's config-0 run is a near-tie: its top-1/top-2 gap is at most GAP
+    (two correct bf16 implementations may order it differently)."""
+    tv = golden["config0_greedy"]["top_v"][r]
+    return float(tv[0] - tv[1]) <= GAP
+
+
+def test_free_running_greedy(eng, oracle_run, golden):
+    """Free-running greedy ids equal the reference's 65 golden ids up to the first divergence,
+    and that divergence (if any) is at a row that the reference itself prices as a near-tie;
+    the same rule against this host's oracle run."""
     from qwen35 import State, Forward
     ids, toks, rows, _ = oracle_run
+    gold = [int(t) for t in golden["config0_greedy"]["tokens"]]
     st = State(eng, 1, 512)
     got = Forward(eng, st).greedy(ids, 64, stop_on_eos=False)
-    agree = 0
-    while agree < len(got) and got[agree] == toks[agree]:
-        agree += 1
-    print(f"free-running greedy: {agree}/65 identical before first divergence", flush=True)
+    st.close()
+    agree = next((i for i, (a, b) in enumerate(zip(got, gold)) if a != b), 65)
+    print(f"free-running greedy: {agree}/65 identical to the reference's golden ids", flush=True)
     if agree < 65:
-        ref = rows[agree]
-        top2 = np.sort(ref)[-2:]
-        assert top2[1] - top2[0] <= GAP, (agree, top2)
+        assert _golden_near_tie(golden, agree), (agree, golden["config0_greedy"]["top_v"][agree][:2])
+    agree_h = next((i for i, (a, b) in enumerate(zip(got, toks)) if a != b), 65)
+    print(f"free-running greedy: {agree_h}/65 identical to this host's oracle run", flush=True)
+    if agree_h < 65:
+        top2 = np.sort(rows[agree_h])[-2:]
+        assert top2[1] - top2[0] <= GAP, (agree_h, top2)
 
 
 def test_gdn_state_after_prompt(eng, oracle_weights, golden):
@@ -178,12 +242,18 @@ def test_mtp_k2_lossless_and_oracle(eng, golden):
     plain = Forward(eng, State(eng, 1, 512)).greedy(ids, len(out) - 1, stop_on_eos=False)
     assert out == plain[:len(out)]
     assert stats["drafted"] == 2 * stats["bonus"]
-    n = min(len(out), len(g["batch_tokens"]))
-    agree = 0
-    while agree < n and out[agree] == int(g["batch_tokens"][agree]):
-        agree += 1
-    print(f"mtp k=2: {agree}/{n} ids agree with the reference's greedy_mtp; stats {stats}", flush=True)
-    assert agree >= 1
+    # the reference's greedy_mtp (batched and sequential verify) emits the plain greedy ids,
+    # so its ids are golden config-0 rows: the engine's rounds equal them up to the first
+    # divergence, which must be at a row the reference prices as a near-tie
+    for key in ("batch_tokens", "steps_tokens"):
+        ref = [int(t) for t in g[key]]
+        n = min(len(out), len(ref))
+        agree = next((i for i in range(n) if out[i] != ref[i]), n)
+        print(f"mtp k=2: {agree}/{n} ids equal the reference's greedy_mtp ({key}); stats {stats}", flush=True)
+        if agree < n:
+            assert _golden_near_tie(golden, agree), (key, agree)
+        else:
+            assert n == min(len(out), 17)
 
 
 def test_mtp_draft_vs_oracle(eng, oracle_weights, golden):

@@ -4,20 +4,22 @@ so the next step of the same state and lanes, fed exactly those tokens, skips th
 upload. Checked against steps that always upload (the same sequence with a step of another
 state in between, which invalidates the device copy): same tokens and bit-identical logits,
 across greedy runs, a fed token other than the sampled one (teacher forcing), a change of
-the lane set, a reset lane and a prefill in between."""
+the lane set, a reset lane, a prefill, an MTP round, a lane copy and a snapshot restore in
+between, with captured (graph) and eager steps."""
 import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
 
 
-def test_device_metadata_fast_path_matches_uploads():
+@pytest.mark.parametrize("graph", [True, False])
+def test_device_metadata_fast_path_matches_uploads(graph):
     from oracle.weights import lane_prompt_ids
     from qwen35 import Engine, State
-    eng = Engine(max_rows=64, max_ctx=512, seed=0, use_graph=True)
+    eng = Engine(max_rows=64, max_ctx=512, seed=0, use_graph=graph)
     try:
-        a = State(eng, 4, 256)                 # consecutive steps: device metadata reused
-        b = State(eng, 4, 256)                 # same work, another state's step in between
+        a = State(eng, 4, 256, mtp_k=2, mtp_cap=128)   # consecutive steps: device metadata reused
+        b = State(eng, 4, 256, mtp_k=2, mtp_cap=128)   # same work, another state's step in between
         other = State(eng, 1, 64)
         other.prefill(0, [5, 6, 7])
         o_tok = [9]
@@ -34,12 +36,36 @@ def test_device_metadata_fast_path_matches_uploads():
         script += [(None, [0, 1, 3])] * 3
         script += [("prefill", None)]
         script += [(None, [0, 1, 2, 3])] * 4
+        script += [("snap1", None)]
+        script += [("mtp01", None)]
+        script += [(None, [0, 1, 2, 3])] * 3
+        script += [("copy0to3", None)]
+        script += [(None, [0, 1, 2, 3])] * 3
+        script += [("restore1", None)]
+        script += [(None, [0, 1, 2, 3])] * 3
         last = {}
         for st, interleave in ((a, False), (b, True)):
             out = []
             prev = {i: None for i in range(4)}
+            snap = None
             for k, (toks, lanes) in enumerate(script):
-                print(f"step meta: {'upload' if interleave else 'device'} step {k}", flush=True)
+                print(f"step meta: graph={graph} {'upload' if interleave else 'device'} step {k} {toks}", flush=True)
+                if toks == "snap1":
+                    snap = (st.snapshot(1), prev[1])
+                    continue
+                if toks == "restore1":
+                    st.restore(1, snap[0])
+                    prev[1] = snap[1]
+                    continue
+                if toks == "copy0to3":
+                    st.copy_lane(0, st, 3)
+                    prev[3] = prev[0]
+                    continue
+                if toks == "mtp01":
+                    em = st.mtp_round([prev[0], prev[1]], 2, [0, 1])
+                    prev[0], prev[1] = int(em[0][-1]), int(em[1][-1])
+                    out.append((em, None))
+                    continue
                 if toks == "reset2":
                     st.reset([2])
                     continue
@@ -58,7 +84,7 @@ def test_device_metadata_fast_path_matches_uploads():
             last[interleave] = out
         for (ta, la), (tb, lb) in zip(last[False], last[True]):
             assert ta == tb
-            assert np.array_equal(la, lb)
+            assert (la is None and lb is None) or np.array_equal(la, lb)
         for st in (a, b, other):
             st.close()
     finally:
