@@ -96,6 +96,14 @@ int q35_state_restore(q35_engine* e, q35_state* s, int lane, const void* host, s
 int q35_prefill(q35_engine* e, q35_state* s, int lane, const int32_t* ids, int n, int32_t* y0,
                 float* logits);
 
+/* The same prompt with every row priced (prefill_wave with PrefillLogits::kAll,
+ * engine/prefill.h:46-58,116-118, the reference's byte-identity gate mode): sampled[i] = greedy
+ * id (lowest id on ties) of prompt row i, top_logit[i] (nullable) = that id's bf16-valued
+ * logit, logits (nullable) = [n][248320] f32. The state advances exactly as q35_prefill's
+ * (same waves, same kernels); the extra cost is one lm_head pass per row. */
+int q35_prefill_all(q35_engine* e, q35_state* s, int lane, const int32_t* ids, int n, int32_t* sampled,
+                    float* top_logit, float* logits);
+
 /* One greedy decode step for n lanes (decode_step, engine/decode_step.h:582): lane
  * lanes[i] (or i when lanes is NULL) consumes tokens[i]; out_tok[i] = argmax (lowest id on
  * ties) of the bf16 logits; out_logits (nullable) is [n][248320]. */
@@ -140,6 +148,21 @@ int q35_op_gemm(q35_engine* e, const uint16_t* w_tiled_dev, int N, int K, const 
  * receive the new state in slot 1; o [B][2048] f32 (before the gated norm). */
 int q35_op_gdn_step(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w, const uint16_t* A_log,
                     const uint16_t* dt_bias, float* S2, float* W2, float* o, int B);
+/* The same step with the layer's gated RMSNorm (engine/kernels_gdn.cpp:525, specimpl.py:142-147,
+ * 304-305): y [B][2048] bf16 = bf16(w * (o * rsqrt(mean_head(o^2) + 1e-6)) * silu(z)) per
+ * 128-wide head, with gnorm [128] bf16, made where the engine makes it for B lanes: in the
+ * recurrence's epilogue for B > 64 (form 0: the persistent kernel; form 1: the non-persistent
+ * whole-head kernel of the MTP verify path), by the out_proj GEMM's batched A producer for
+ * B <= 64 (form 1: the whole-head kernel's epilogue instead). B <= max_rows. */
+int q35_op_gdn_step_norm(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w, const uint16_t* A_log,
+                         const uint16_t* dt_bias, const uint16_t* gnorm, float* S2, float* W2, float* o,
+                         uint16_t* y, int B, int form);
+/* Y[M][N] = A . W^T with A made by one of the GEMM's A producers from X (and X2): amode 0 A = X
+ * (bf16 [M][K]); 1 SwiGLU A = bf16(bf16(silu(X)) * X2) (X, X2 bf16 [M][K]); 2 gated RMSNorm
+ * A = bf16(aux_w * (X * rsqrt(mean_head(X^2) + 1e-6)) * silu(X2)) (X f32 [M][K], X2 bf16 z,
+ * aux_w [128]). M <= 16 uses the one-row GEMM's in-register producer, M > 16 the batched one. */
+int q35_op_gemm_a(q35_engine* e, const uint16_t* w_tiled_dev, int N, int K, int amode, const void* x_dev, int ldx,
+                  const void* x2_dev, int ldx2, const uint16_t* aux_dev, int M, uint16_t* y_dev);
 int q35_op_lm_head_argmax(q35_engine* e, const uint16_t* x_dev, int M, int32_t* tok_dev, float* logits_dev);
 int q35_sync(q35_engine* e);
 /* Live per-kernel timing: with option "kprof" = family (1 projection/MLP GEMMs, 2 lm_head

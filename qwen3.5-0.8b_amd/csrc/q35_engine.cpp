@@ -128,6 +128,7 @@ struct q35_engine {
     int sc_ld = 0, max_chunks = 0;
     float* logits_dev = nullptr;
     int logits_rows = 0;
+    float* topv_dev = nullptr;       // [R] the argmax's logit value per row (all-rows prefill)
     std::map<std::string, hipGraphExec_t> graphs;   // captured decode steps
     // pinned staging
     int *h_tok, *h_lane, *h_pos, *h_slot, *h_out, *h_src, *h_dst, *hin = nullptr;
@@ -335,6 +336,7 @@ void alloc_scratch(q35_engine* e) {
     e->pval = dalloc<float>(R * (size_t)(kVocab / 16));
     e->pidx = dalloc<int>(R * (size_t)(kVocab / 16));
     e->kpart = dalloc<float>(R * 16 * kHidden);
+    e->topv_dev = dalloc<float>(R);
     e->gchunk = dalloc<float>(gdn_chunk_ws_floats(R));
     e->gcdec = dalloc<float>((size_t)((R + 63) / 64) * kHv);
     e->prod = dalloc<uint16_t>(R * kFF);
@@ -569,7 +571,8 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
 // lm_head + argmax over rows [row0, row0 + M); tokens into e->tok_dev[0..M). After a
 // batched body the normed rows are in e->nrm; after a batch-1 body (`normw` given) the
 // final RMSNorm of the residual rows is applied first.
-void lm_head(q35_engine* e, int row0, int M, bool want_logits, const uint16_t* normw = nullptr) {
+void lm_head(q35_engine* e, int row0, int M, bool want_logits, const uint16_t* normw = nullptr,
+             float* top_val = nullptr) {
     GemmArgs a{};
     a.W = e->E; a.N = kVocab; a.K = kHidden; a.M = M; a.X = e->nrm + (size_t)row0 * kHidden; a.ldx = kHidden;
     a.forms = e->forms;
@@ -583,7 +586,7 @@ void lm_head(q35_engine* e, int row0, int M, bool want_logits, const uint16_t* n
         KTimer kt(e, kFamLmHead);
         HCK(launch_gemm(a, amode, kEArgmax, e->st));
     }
-    HCK(launch_argmax(e->pval, e->pidx, kVocab / 16, kVocab / 16, M, e->tok_dev, nullptr, e->st));
+    HCK(launch_argmax(e->pval, e->pidx, kVocab / 16, kVocab / 16, M, e->tok_dev, top_val, e->st));
 }
 
 void save_hlast(q35_engine* e, q35_state* s, const std::vector<int>& src_rows, const std::vector<int>& lanes) {
@@ -689,7 +692,7 @@ int q35_destroy(q35_engine* e) {
         e->graphs.clear();
         void* ds[] = {e->blob, e->x, e->h, e->delta, e->nrm, e->proj, e->gu, e->aout, e->cat, e->o, e->q,
                       e->sc, e->stats, e->part, e->pval, e->pidx, e->prod, e->din, e->inv_freq,
-                      e->logits_dev, e->kpart, e->gchunk, e->gcdec};
+                      e->logits_dev, e->kpart, e->gchunk, e->gcdec, e->topv_dev};
         for (void* p : ds) if (p) hipFree(p);
         void* hs[] = {e->hin, e->h_out, e->h_cur};
         for (void* p : hs) if (p) hipHostFree(p);
@@ -1096,38 +1099,67 @@ int q35_state_write(q35_engine* e, q35_state* s, int lane, int which, int n_slot
     return guard([&] { state_io(e, s, lane, which, n_slots, const_cast<void*>(host), bytes, true); });
 }
 
-int q35_prefill(q35_engine* e, q35_state* s, int lane, const int32_t* ids, int n, int32_t* y0, float* logits) {
-    return guard([&] {
-        REQ(e && s && ids && y0, Q35_ERR_ARG, "null argument");
-        REQ(n > 0, Q35_ERR_ARG, "empty prompt");
-        check_lane(s, lane);
-        REQ(s->prefix[lane] + n <= s->cap, Q35_ERR_CAP, "prompt exceeds the lane's cache capacity");
-        for (int i = 0; i < n; ++i) check_tok(ids[i]);
-        int done = 0;
-        while (done < n) {
-            const int T = std::min(e->R, n - done);
-            HCK(hipStreamSynchronize(e->st));
-            for (int t = 0; t < T; ++t) {
-                e->h_tok[t] = ids[done + t];
-                e->h_lane[t] = lane;
-                e->h_pos[t] = s->prefix[lane] + t;
-                e->h_slot[t] = s->prefix[lane] + t;
-            }
-            body(e, s, T, T, false);
-            s->prefix[lane] += T;
-            s->cur[lane] = (s->cur[lane] + 1) % s->nslots;
-            done += T;
-            if (done == n) {
-                lm_head(e, T - 1, 1, logits != nullptr,
-                        small_rows(T) && !b1_partials(e, T, T, false) ? e->final_norm : nullptr);
-                save_hlast(e, s, {T - 1}, {lane});
+// The wave loop of a prompt (prefill_wave, engine/prefill.cpp:63). all_rows: every row of every
+// wave is priced (PrefillLogits::kAll, engine/prefill.h:46-58): its argmax into sampled[], its
+// top logit into top[] and its logits into logits[] (nullable), in lm_head launches of at most
+// kAllChunk rows; otherwise only the prompt's last row (*sampled, logits nullable).
+constexpr int kAllChunk = 256;
+void prefill_waves(q35_engine* e, q35_state* s, int lane, const int32_t* ids, int n, bool all_rows,
+                   int32_t* sampled, float* top, float* logits) {
+    REQ(e && s && ids && sampled, Q35_ERR_ARG, "null argument");
+    REQ(n > 0, Q35_ERR_ARG, "empty prompt");
+    check_lane(s, lane);
+    REQ(s->prefix[lane] + n <= s->cap, Q35_ERR_CAP, "prompt exceeds the lane's cache capacity");
+    for (int i = 0; i < n; ++i) check_tok(ids[i]);
+    int done = 0;
+    while (done < n) {
+        const int T = std::min(e->R, n - done);
+        HCK(hipStreamSynchronize(e->st));
+        for (int t = 0; t < T; ++t) {
+            e->h_tok[t] = ids[done + t];
+            e->h_lane[t] = lane;
+            e->h_pos[t] = s->prefix[lane] + t;
+            e->h_slot[t] = s->prefix[lane] + t;
+        }
+        body(e, s, T, T, false);
+        s->prefix[lane] += T;
+        s->cur[lane] = (s->cur[lane] + 1) % s->nslots;
+        const uint16_t* normw = small_rows(T) && !b1_partials(e, T, T, false) ? e->final_norm : nullptr;
+        if (all_rows) {
+            // the body's tokens are consumed: lm_head leaves row r0 + i's id in tok_dev[i]
+            for (int r0 = 0; r0 < T; r0 += kAllChunk) {
+                const int M = std::min(kAllChunk, T - r0);
+                lm_head(e, r0, M, logits != nullptr, normw, e->topv_dev);
+                HCK(hipMemcpyAsync(sampled + done + r0, e->tok_dev, M * sizeof(int), hipMemcpyDeviceToHost, e->st));
+                if (top) HCK(hipMemcpyAsync(top + done + r0, e->topv_dev, M * sizeof(float), hipMemcpyDeviceToHost, e->st));
+                if (logits)
+                    HCK(hipMemcpyAsync(logits + (size_t)(done + r0) * kVocab, e->logits_dev, (size_t)M * kVocab * 4,
+                                       hipMemcpyDeviceToHost, e->st));
+                HCK(hipStreamSynchronize(e->st));
             }
         }
+        done += T;
+        if (done == n) {
+            if (!all_rows) lm_head(e, T - 1, 1, logits != nullptr, normw);
+            save_hlast(e, s, {T - 1}, {lane});
+        }
+    }
+    if (!all_rows) {
         HCK(hipMemcpyAsync(e->h_out, e->tok_dev, sizeof(int), hipMemcpyDeviceToHost, e->st));
         if (logits) HCK(hipMemcpyAsync(logits, e->logits_dev, (size_t)kVocab * 4, hipMemcpyDeviceToHost, e->st));
         HCK(hipStreamSynchronize(e->st));
-        *y0 = e->h_out[0];
-    });
+        *sampled = e->h_out[0];
+    }
+    HCK(hipStreamSynchronize(e->st));
+}
+
+int q35_prefill(q35_engine* e, q35_state* s, int lane, const int32_t* ids, int n, int32_t* y0, float* logits) {
+    return guard([&] { prefill_waves(e, s, lane, ids, n, false, y0, nullptr, logits); });
+}
+
+int q35_prefill_all(q35_engine* e, q35_state* s, int lane, const int32_t* ids, int n, int32_t* sampled,
+                    float* top_logit, float* logits) {
+    return guard([&] { prefill_waves(e, s, lane, ids, n, true, sampled, top_logit, logits); });
 }
 
 int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* tokens,
@@ -1318,27 +1350,66 @@ int q35_op_gemm(q35_engine* e, const uint16_t* wt, int N, int K, const uint16_t*
     });
 }
 
+// One GDN decode step of B lanes on caller buffers; y/gnorm (optional) receive the gated
+// RMSNorm output as the engine's path for B lanes makes it: whole-head blocks (B > 64) fuse it
+// into the recurrence's epilogue, column-sliced blocks (B <= 64) leave it to the out_proj
+// GEMM's A producer (produce_kernel here). form 1: the non-persistent whole-head kernel
+// (gdn_kernel<1>, the MTP verify path) instead of the persistent one.
+static void op_gdn(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w, const uint16_t* A_log,
+                   const uint16_t* dt_bias, const uint16_t* gnorm, float* S2, float* W2, float* o, uint16_t* y,
+                   int B, int form) {
+    REQ(e && proj && conv_w && A_log && dt_bias && S2 && W2 && o && B > 0, Q35_ERR_ARG, "bad gdn call");
+    REQ(B <= 65536 && (form == 0 || form == 1), Q35_ERR_ARG, "bad gdn call");
+    REQ(!y == !gnorm, Q35_ERR_ARG, "y and gnorm go together");
+    REQ(!y || B <= e->R, Q35_ERR_CAP, "B exceeds max_rows (the norm staging is engine scratch)");
+    // rows b = lanes b (T = 1); per lane two slots: 0 = input state, 1 = output state
+    std::vector<int> lanes(B);
+    for (int i = 0; i < B; ++i) lanes[i] = i;
+    int* dl = dalloc<int>(B);
+    copy_sync(e, dl, lanes.data(), B * sizeof(int), hipMemcpyHostToDevice);
+    GdnArgs g{};
+    g.proj = proj; g.o = o; g.conv_w = conv_w; g.A_log = A_log; g.dt_bias = dt_bias;
+    g.S = S2; g.S_lane = 2 * kSLayer; g.S_slot = kSLayer; g.S_layer = 0;
+    g.win = W2; g.W_lane = 2 * kWLayer; g.W_slot = kWLayer; g.W_layer = 0;
+    g.cur = nullptr; g.nslots = 2; g.ckpt = 0;
+    g.lane = dl; g.T = 1; g.nlanes = B;
+    const int cs = B <= 8 ? 8 : B <= 32 ? 4 : B <= 64 ? 2 : 1;
+    const bool whole = cs == 1 || form == 1;           // whole-head blocks: norm in the epilogue
+    if (whole && y) { g.y = y; g.gnorm = gnorm; }
+    if (cs == 1 && form == 0) HCK(launch_gdn_persist(g, e->st));
+    else HCK(launch_gdn(g, whole ? 1 : cs, e->st));
+    if (y && !whole) {
+        // the column-sliced path: the out_proj producer's arithmetic, staged to y
+        GemmArgs a{};
+        a.N = kHidden; a.K = 2048; a.M = B; a.X = o; a.ldx = 2048; a.X2 = proj + kGdnZOff; a.ldx2 = kGdnInRows;
+        a.aux_w = gnorm; a.prod = y; a.forms = e->forms;
+        HCK(launch_produce(a, kAGatedNorm, e->st));
+    }
+    HCK(hipStreamSynchronize(e->st));
+    HCK(hipFree(dl));
+}
+
 int q35_op_gdn_step(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w, const uint16_t* A_log,
                     const uint16_t* dt_bias, float* S2, float* W2, float* o, int B) {
+    return guard([&] { op_gdn(e, proj, conv_w, A_log, dt_bias, nullptr, S2, W2, o, nullptr, B, 0); });
+}
+
+int q35_op_gdn_step_norm(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w, const uint16_t* A_log,
+                         const uint16_t* dt_bias, const uint16_t* gnorm, float* S2, float* W2, float* o,
+                         uint16_t* y, int B, int form) {
+    return guard([&] { op_gdn(e, proj, conv_w, A_log, dt_bias, gnorm, S2, W2, o, y, B, form); });
+}
+
+int q35_op_gemm_a(q35_engine* e, const uint16_t* wt, int N, int K, int amode, const void* x, int ldx,
+                  const void* x2, int ldx2, const uint16_t* aux, int M, uint16_t* y) {
     return guard([&] {
-        REQ(e && proj && conv_w && A_log && dt_bias && S2 && W2 && o && B > 0, Q35_ERR_ARG, "bad gdn call");
-        REQ(B <= 65536, Q35_ERR_ARG, "B too large");
-        // rows b = lanes b (T = 1); per lane two slots: 0 = input state, 1 = output state
-        std::vector<int> lanes(B);
-        for (int i = 0; i < B; ++i) lanes[i] = i;
-        int* dl = dalloc<int>(B);
-        copy_sync(e, dl, lanes.data(), B * sizeof(int), hipMemcpyHostToDevice);
-        GdnArgs g{};
-        g.proj = proj; g.o = o; g.conv_w = conv_w; g.A_log = A_log; g.dt_bias = dt_bias;
-        g.S = S2; g.S_lane = 2 * kSLayer; g.S_slot = kSLayer; g.S_layer = 0;
-        g.win = W2; g.W_lane = 2 * kWLayer; g.W_slot = kWLayer; g.W_layer = 0;
-        g.cur = nullptr; g.nslots = 2; g.ckpt = 0;
-        g.lane = dl; g.T = 1; g.nlanes = B;
-        const int cs = B <= 8 ? 8 : B <= 32 ? 4 : B <= 64 ? 2 : 1;
-        if (cs == 1) HCK(launch_gdn_persist(g, e->st));
-        else HCK(launch_gdn(g, cs, e->st));
-        HCK(hipStreamSynchronize(e->st));
-        HCK(hipFree(dl));
+        REQ(e && wt && x && y && M > 0 && N % 16 == 0 && K % 256 == 0 && K <= 4096, Q35_ERR_ARG, "bad gemm shape");
+        REQ(amode == kAPlain || amode == kASiluMul || amode == kAGatedNorm, Q35_ERR_ARG, "amode is 0, 1 or 2");
+        REQ(amode == kAPlain || x2, Q35_ERR_ARG, "this producer needs x2");
+        REQ(amode != kAGatedNorm || (aux && K % 128 == 0), Q35_ERR_ARG, "gated norm needs its weight");
+        REQ(M <= 16 || amode == kAPlain || ((size_t)M * K <= (size_t)e->R * kFF), Q35_ERR_CAP,
+            "M x K exceeds the producer staging");
+        gemm(e, wt, N, K, M, x, ldx, y, N, amode, x2, ldx2, aux);
     });
 }
 

@@ -966,6 +966,17 @@ hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st) 
     return hipErrorInvalidValue;
 }
 
+hipError_t launch_produce(const GemmArgs& a, int amode, hipStream_t st) {
+    if (!a.prod || a.M <= 0 || a.K % 256) return hipErrorInvalidValue;
+    GemmArgs p = a;
+    p.Y = a.prod;
+    p.ldy = a.K;
+    if (amode == kASiluMul) hipLaunchKernelGGL((produce_kernel<kASiluMul>), dim3(a.M), dim3(256), 0, st, p);
+    else if (amode == kAGatedNorm) hipLaunchKernelGGL((produce_kernel<kAGatedNorm>), dim3(a.M), dim3(256), 0, st, p);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 hipError_t launch_argmax(const float* pv, const int* pi, int ldp, int n, int rows, int* tok,
                          float* val, hipStream_t st) {
     hipLaunchKernelGGL(argmax_rows, dim3(rows), dim3(1024), 0, st, pv, pi, ldp, n, tok, val);

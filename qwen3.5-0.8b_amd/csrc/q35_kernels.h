@@ -49,6 +49,9 @@ hipError_t gemm_init();
 // k-block chains a batched kEPartial GEMM leaves in kpart
 int gemm_partial_chains(int M, int K, const KernelForms& f);
 hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st);
+// The batched A producer alone: a.prod [M][K] bf16 = the producer's A operand (kASiluMul or
+// kAGatedNorm), as launch_gemm stages it for M > 16.
+hipError_t launch_produce(const GemmArgs& a, int amode, hipStream_t st);
 hipError_t launch_argmax(const float* pv, const int* pi, int ldp, int n, int rows, int* tok,
                          float* val, hipStream_t st);
 

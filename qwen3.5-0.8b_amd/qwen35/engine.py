@@ -51,6 +51,8 @@ _SIGS = {
                            C.c_int),
     "q35_state_restore": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_size_t], C.c_int),
     "q35_prefill": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.POINTER(C.c_int32), C.c_void_p], C.c_int),
+    "q35_prefill_all": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p,
+                         C.c_void_p], C.c_int),
     "q35_decode_step": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "q35_mtp_draft": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int,
                        C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
@@ -61,6 +63,9 @@ _SIGS = {
     "q35_op_tile_weight": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p], C.c_int),
     "q35_op_gemm": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p], C.c_int),
     "q35_op_gdn_step": ([C.c_void_p] * 8 + [C.c_int], C.c_int),
+    "q35_op_gdn_step_norm": ([C.c_void_p] * 10 + [C.c_int, C.c_int], C.c_int),
+    "q35_op_gemm_a": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
+                       C.c_int, C.c_void_p, C.c_int, C.c_void_p], C.c_int),
     "q35_op_lm_head_argmax": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p], C.c_int),
     "q35_sync": ([C.c_void_p], C.c_int),
     "q35_kprof_read": ([C.c_void_p, C.POINTER(C.c_float), C.POINTER(C.c_int)], C.c_int),
@@ -189,6 +194,17 @@ class Engine:
     def op_gdn_step(self, proj: int, conv_w: int, A_log: int, dt_bias: int, S2: int, W2: int, o: int, B: int):
         _ck(load_library().q35_op_gdn_step(self.h, *[C.c_void_p(p) for p in (proj, conv_w, A_log, dt_bias, S2, W2, o)], B))
 
+    def op_gdn_step_norm(self, proj: int, conv_w: int, A_log: int, dt_bias: int, gnorm: int, S2: int, W2: int,
+                         o: int, y: int, B: int, form: int = 0):
+        _ck(load_library().q35_op_gdn_step_norm(
+            self.h, *[C.c_void_p(p) for p in (proj, conv_w, A_log, dt_bias, gnorm, S2, W2, o, y)], B, form))
+
+    def op_gemm_a(self, wt_ptr: int, N: int, K: int, amode: int, x_ptr: int, ldx: int, x2_ptr: int, ldx2: int,
+                  aux_ptr: int, M: int, y_ptr: int):
+        _ck(load_library().q35_op_gemm_a(self.h, C.c_void_p(wt_ptr), N, K, amode, C.c_void_p(x_ptr), ldx,
+                                         C.c_void_p(x2_ptr) if x2_ptr else None, ldx2,
+                                         C.c_void_p(aux_ptr) if aux_ptr else None, M, C.c_void_p(y_ptr)))
+
     def op_lm_head_argmax(self, x_ptr: int, M: int, tok_ptr: int, logits_ptr: int = 0):
         _ck(load_library().q35_op_lm_head_argmax(self.h, C.c_void_p(x_ptr), M, C.c_void_p(tok_ptr),
                                                  C.c_void_p(logits_ptr) if logits_ptr else None))
@@ -279,6 +295,18 @@ class State:
         _ck(load_library().q35_prefill(self.eng.h, self.h, lane, _p(ids), ids.size, C.byref(y0),
                                        _p(lg) if logits else None))
         return (y0.value, lg) if logits else y0.value
+
+    def prefill_all(self, lane: int, ids, logits: bool = False):
+        """The prompt with every row priced (PrefillLogits::kAll, engine/prefill.h:46-58): per-row
+        greedy ids and top logit values, and optionally every row's logits [n][248320]."""
+        ids = _i32(ids)
+        n = ids.size
+        samp = np.empty(n, np.int32)
+        top = np.empty(n, np.float32)
+        lg = np.empty((n, VOCAB), np.float32) if logits else None
+        _ck(load_library().q35_prefill_all(self.eng.h, self.h, lane, _p(ids), n, _p(samp), _p(top),
+                                           _p(lg) if logits else None))
+        return (samp, top, lg) if logits else (samp, top)
 
     def decode_step(self, tokens, lanes=None, logits: bool = False):
         t = _i32(tokens)

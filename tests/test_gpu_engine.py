@@ -18,6 +18,9 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 LOGIT_MAX, LOGIT_MEAN, GAP = 0.375, 0.05, 0.375
+# against the reference's own rows (built in the same container as the golden vectors) the
+# spread is smaller than against the GPU host's oracle run: measured top-32 max |d| 0.1875
+GOLDEN_MAX = 0.25
 
 
 @pytest.fixture(scope="module")
@@ -90,7 +93,7 @@ def test_teacher_forced_vs_reference_golden(eng, golden):
     speccheck/specimpl.py:496-517 in the build container): the prompt, then the reference's 64
     greedy tokens fed back (teacher forcing), so every one of the 65 logits rows is the row the
     reference priced.
-      * logits at the reference's top-32 ids of every row within LOGIT_MAX of its values, mean
+      * logits at the reference's top-32 ids of every row within GOLDEN_MAX of its values, mean
         |d| over all rows within LOGIT_MEAN; logits0 / logits64 (the first 4,096 vocabulary
         entries of rows 0 and 64) the same
       * argmax == the reference's token on every row whose reference top-1/top-2 gap exceeds
@@ -131,9 +134,9 @@ def test_teacher_forced_vs_reference_golden(eng, golden):
           f"logits0 max {d0.max():.4f} mean {d0.mean():.5f}; logits64 max {d64.max():.4f} "
           f"mean {d64.mean():.5f}; near-ties not checked (row, gap, max|d|): {skipped}", flush=True)
     assert not bad, bad
-    assert max(maxes) <= LOGIT_MAX and np.mean(means) <= LOGIT_MEAN
+    assert max(maxes) <= GOLDEN_MAX and np.mean(means) <= LOGIT_MEAN
     for d in (d0, d64):
-        assert d.max() <= LOGIT_MAX and d.mean() <= LOGIT_MEAN
+        assert d.max() <= GOLDEN_MAX and d.mean() <= LOGIT_MEAN
 
 
 def _golden_near_tie(golden, r):
