@@ -31,10 +31,10 @@ KV_BYTES_PER_SLOT = 6 * 2 * 2 * 256 * 2   # K and V, 6 layers, 2 kv heads
 FAM = {"gemm": 1, "lm_head": 2, "gdn": 3, "attn": 4}
 KERNEL_NAMES = {"attn": "attn_fused", "gdn": "gdn_persist", "lm_head": "gemm_lmhead<8, 2> (tied lm_head)",
                 "gemm": "projection / MLP GEMMs"}
-DOMINANT = "attn"           # largest share of the batch-256 step
-# HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled by what
-# the same counter reads for a 1 GiB copy (FETCH x2.0, WRITE x1.0); the runs and the
-# calibration are in profiles/hbm_traffic_decode_b256_ctx4096.md.
+# HBM bytes per launch from an earlier rocprofv3 FETCH_SIZE / WRITE_SIZE run (not this run), each
+# scaled by what the same counter reads for a 1 GiB copy (FETCH x2.0, WRITE x1.0); the runs and
+# the calibration are in the file named by TRAFFIC_SOURCE.
+TRAFFIC_SOURCE = "profiles/hbm_traffic_decode_b256_ctx4096.md"
 MEASURED_TRAFFIC = {
     ("attn", 256, 4096): (1058422.4 * 2.0 + 1024.0 * 1.0) * 1024,                        # attn_fused
     ("gdn", 256, 4096): (143107.0 * 2.0 + 283680.9 * 1.0) * 1024,                         # gdn_persist
@@ -149,8 +149,71 @@ def run_mtp(eng, B: int, ctx: int, rounds: int, warmup: int):
     st.close()
     return {"tok_s": round(emitted / wall, 2), "ms_per_round": round(wall / rounds * 1e3, 3),
             "accept_rate": round(float(stats[1]) / max(int(stats[0]), 1), 4),
-            "tokens_per_round_per_lane": round(emitted / rounds / B, 3), "lanes": B, "k": 2,
-            "note": "random-init weights: the drafter almost never agrees with the target"}
+            "tokens_per_round_per_lane": round(emitted / rounds / B, 3), "lanes": B, "k": 2}
+
+
+def run_mtp_adaptive(eng, B: int, ctx: int, turns: int):
+    """Config 4 with the adaptive depth policy (engine/mtp_adaptive.h) per lane: every turn runs
+    each lane at its policy's depth (q35_mtp_adaptive_step). With random-init weights no draft
+    is accepted, so every lane demotes after 16 rounds and abandons after 24 more; reported are
+    the whole run's emitted tok/s and the steady state after abandonment."""
+    import numpy as np
+    import torch
+    from qwen35 import MtpPolicy, State
+    st = State(eng, B, ctx + 3 * turns + 16, mtp_k=2, mtp_cap=2 * turns + 16)
+    st.seed(1, ctx)
+    tok = st.decode_step(np.random.default_rng(1).integers(0, 248320, size=B).astype(np.int32))
+    pol = [MtpPolicy(2) for _ in range(B)]
+    eng.sync()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    emitted, t_abandon, e_abandon, depth_turns = 0, None, 0, {0: 0, 1: 0, 2: 0}
+    for t in range(turns):
+        em, dep = st.mtp_adaptive_step(tok, pol)
+        emitted += sum(len(e) for e in em)
+        for d in dep:
+            depth_turns[int(d)] += 1
+        tok = np.array([e[-1] for e in em], np.int32)
+        if t_abandon is None and (dep == 0).all():
+            t_abandon, e_abandon, n_abandon = time.perf_counter(), emitted, t
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    st.close()
+    steady = None
+    if t_abandon is not None and t_abandon < t0 + wall and turns - n_abandon > 1:
+        steady = round((emitted - e_abandon) / (t0 + wall - t_abandon), 2)
+    return {"tok_s_whole_run": round(emitted / wall, 2), "tok_s_after_abandon": steady, "turns": turns,
+            "lane_turns_at_depth": {str(k): v for k, v in depth_turns.items()}, "lanes": B}
+
+
+def run_mtp_accepting(eng, B: int, ctx: int, rounds: int, d: int = 7):
+    """MTP k = 2 rounds with weights reshaped so drafts accept (final norms keep one hidden
+    dimension d, embedding rows 248046 / 1000 get +-8 there: every greedy pick is one of the two
+    by the sign of x_d, as in the accept tests). The same work per round as run_mtp; the
+    weights are restored afterwards. Returns emitted tok/s, the plain step rate on the same
+    weights and the accept rate."""
+    import numpy as np
+    emb = "model.language_model.embed_tokens.weight"
+    names = (emb, "model.language_model.norm.weight", "mtp.norm.weight")
+    saved = {n: eng.read_tensor(n, 248320 * 1024 if n == emb else 1024) for n in names}
+    E = saved[emb].reshape(248320, 1024).copy()
+    E[248046, d] = 0x4100
+    E[1000, d] = 0xC100
+    nw = np.full(1024, 0xBF80, np.uint16)
+    nw[d] = 0x4040
+    try:
+        eng.load_tensor(emb, E.reshape(-1))
+        del E
+        for n in names[1:]:
+            eng.load_tensor(n, nw)
+        res = run_mtp(eng, B, ctx, rounds, 1)
+        wall, _, _ = run_decode(eng, B, ctx, rounds, 1, None)
+        res["plain_tok_s_same_weights"] = round(B * rounds / wall, 2)
+        res["speedup_vs_plain"] = round(res["tok_s"] / res["plain_tok_s_same_weights"], 4)
+        return res
+    finally:
+        for n in names:
+            eng.load_tensor(n, saved[n])
 
 
 def cpu_baseline(ctx: int, budget_s: float = 15.0):
@@ -184,6 +247,7 @@ def main():
     ap.add_argument("--kprof-steps", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mtp-rounds", type=int, default=5, help="config 4 (MTP k=2) rounds; 0 skips it")
+    ap.add_argument("--adaptive-turns", type=int, default=60, help="config 4 turns with the adaptive depth policy")
     ap.add_argument("--prefill-len", type=int, default=4096, help="one-lane prompt prefill length; 0 skips it")
     ap.add_argument("--prefill-rows", type=int, default=2048, help="prompt wave rows (the engine's max_rows)")
     ap.add_argument("--eager", action="store_true", help="launch kernels eagerly (no hipGraph)")
@@ -207,7 +271,9 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    eng = Engine(max_rows=max(3 * B, 64, args.prefill_rows), max_ctx=L + max(args.steps, args.b1_steps) + args.warmup + 64, seed=0,
+    eng = Engine(max_rows=max(3 * B, 64, args.prefill_rows),
+                 max_ctx=L + max(args.steps, args.b1_steps, 3 * args.adaptive_turns, 12 * args.mtp_rounds) + args.warmup + 64,
+                 seed=0,
                  use_graph=not args.eager)
     # timed value: graph replay, no per-kernel events
     wall, ev_s, _ = run_decode(eng, B, L, args.steps, args.warmup, None)
@@ -230,19 +296,33 @@ def main():
         ach = byt / (per_launch_ms / 1e3) / 1e9
         rooflines[kp] = {"kernel": KERNEL_NAMES[kp], "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK,
                          "unit": "GB/s", "frac": round(ach / HBM_PEAK, 4), "traffic": MEASURED_TRAFFIC.get((kp, B, L)),
+                         "traffic_source": TRAFFIC_SOURCE if (kp, B, L) in MEASURED_TRAFFIC else None,
                          "bytes_per_launch": int(byt), "avg_launch_us": round(per_launch_ms * 1e3, 2),
-                         "launches_per_step": launches_per_step}
+                         "launches_per_step": launches_per_step,
+                         "us_per_step": round(kt[0] / args.kprof_steps * 1e3, 2)}
         if kp in ("lm_head", "gemm"):   # also priced against dense bf16 MFMA
             tf = family_flops(kp, B) / launches_per_step / (per_launch_ms / 1e3) / 1e12
             rooflines[kp].update({"achieved_tflops": round(tf, 1), "mfma_peak_tflops": MFMA_PEAK,
                                   "mfma_frac": round(tf / MFMA_PEAK, 4)})
-    roof = rooflines.get(DOMINANT) or (next(iter(rooflines.values())) if rooflines else None)
-    mtp = run_mtp(eng, B, L, args.mtp_rounds, 1) if args.mtp_rounds > 0 else None
+    # the dominant kernel family: the largest measured share of the step
+    dominant = max(rooflines, key=lambda k: rooflines[k]["us_per_step"]) if rooflines else None
+    roof = rooflines.get(dominant)
+    mtp = None
+    if args.mtp_rounds > 0:
+        mtp = run_mtp(eng, B, L, args.mtp_rounds, 1)
+        mtp["round_cost_steps"] = round(mtp["ms_per_round"] / ms, 4)
+        m1 = run_mtp(eng, 1, L, 4 * args.mtp_rounds, 2)
+        m1["round_cost_steps"] = round(m1["ms_per_round"] / ms1, 4)
+        mtp = {"b%d" % B: mtp, "b1": m1,
+               "adaptive_b%d" % B: run_mtp_adaptive(eng, B, L, args.adaptive_turns),
+               "note": "random-init weights: the drafter almost never agrees with the target"}
+        mtp["accepting_b%d" % B] = run_mtp_accepting(eng, B, L, args.mtp_rounds)
+        mtp["accepting_b1"] = run_mtp_accepting(eng, 1, L, 4 * args.mtp_rounds)
     pre = run_prefill(eng, args.prefill_len) if 0 < args.prefill_len <= eng.max_ctx - 64 else None
     cpu = None
     if not args.no_cpu:
         tps, thr, n = cpu_baseline(L)
-        cpu = {"value": round(tps, 3), "unit": "tok/s", "cores": thr, "kind": "port",
+        cpu = {"value": round(tps, 3), "unit": "tok/s", "cores": thr, "nproc": len(os.sched_getaffinity(0)), "kind": "port",
                "sample": f"oracle (torch CPU restatement of speccheck/specimpl.py) greedy decode of lane 0 "
                          f"of this workload (seeded state, ctx {L}), batch 1, {n} tokens"}
     out = {"metric": "decode tok/s at batch 1 and 256 (ctx 4k); achieved HBM GB/s vs 8 TB/s peak",
@@ -257,7 +337,7 @@ def main():
                       "hbm_gbs": round(gbs1, 1), "hbm_frac": round(gbs1 / HBM_PEAK, 4),
                       "bytes_per_token": step_bytes(1, L)},
            "mtp_k2": mtp, "prefill": pre, "roofline": roof,
-           "kernel_rooflines": {k: v for k, v in rooflines.items() if k != DOMINANT}, "cpu_baseline": cpu}
+           "kernel_rooflines": {k: v for k, v in rooflines.items() if k != dominant}, "cpu_baseline": cpu}
     print(json.dumps(out))
 
 

@@ -135,6 +135,28 @@ int q35_mtp_round(q35_engine* e, q35_state* s, const int32_t* lanes, int n, cons
 int q35_mtp_round_stop(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* cur,
                        int k, int32_t stop, int32_t* emit, int32_t* n_emit, int64_t* stats);
 
+/* Adaptive speculation depth (mtpadapt::Tracker, engine/mtp_adaptive.h:1-254): one policy per
+ * request decides the depth of its next round -- 2, 1, or 0 (plain steps for the rest of the
+ * request) -- from the tokens its own rounds emitted: the window estimate is emitted tokens per
+ * step-equivalent over the last 32 rounds (a round at depth k billed cost_k plain steps; <= 0
+ * selects the reference's 1.58 / 1.90); after 16 rounds at k = 2 an estimate below 0.95 demotes
+ * to 1, after 24 rounds at k = 1 one below 0.90 abandons; the window clears on a change and
+ * there is no re-promotion. Host-only; no GPU work. */
+typedef struct q35_mtp_policy q35_mtp_policy;
+int q35_mtp_policy_create(int start_k, double cost_k1, double cost_k2, q35_mtp_policy** out);
+int q35_mtp_policy_free(q35_mtp_policy* p);
+int q35_mtp_policy_k(const q35_mtp_policy* p, int32_t* k);
+/* Feed one round (its depth and emitted token count). change (nullable, [3]) = {from, to, rounds
+ * seen} when the depth changed, else {-1, -1, -1}; est (nullable) = the window estimate. */
+int q35_mtp_policy_note(q35_mtp_policy* p, int k_round, int emitted, int32_t* change, double* est);
+/* One turn of n lanes at their policies' depths: lanes at depth 2 run one k = 2 round together,
+ * depth 1 one k = 1 round, depth 0 one plain decode step; every round's emitted count is fed to
+ * its lane's policy. emit [n][3] (unused entries -1), n_emit [n], depth (nullable) [n] = the depth
+ * each lane ran at; stop as in q35_mtp_round_stop; stats as in q35_mtp_round (rounds only). */
+int q35_mtp_adaptive_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* cur,
+                          q35_mtp_policy* const* pol, int32_t stop, int32_t* emit, int32_t* n_emit,
+                          int32_t* depth, int64_t* stats);
+
 /* Per-op entry points on caller device buffers (benchmark and parity harness). */
 /* Y[M][N] = X[M][K] . W^T with W in checkpoint row-major layout, tiled into scratch first
  * by q35_op_tile_weight. */

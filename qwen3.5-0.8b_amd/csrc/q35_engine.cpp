@@ -1336,6 +1336,48 @@ int q35_mtp_round_stop(q35_engine* e, q35_state* s, const int32_t* lanes, int n,
     });
 }
 
+// One decoding turn of n lanes, each at its own adaptive depth (engine/mtp_adaptive.h; the
+// reference drives one request per process, decode_run.cpp:4857-5010 / mtp_accept.cpp:525-640):
+// the lanes at depth 2 run one k = 2 round together, those at depth 1 one k = 1 round, the
+// abandoned ones one plain step; each round's emitted count is fed to its lane's policy.
+int q35_mtp_adaptive_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* cur,
+                          q35_mtp_policy* const* pol, int32_t stop, int32_t* emit, int32_t* n_emit,
+                          int32_t* depth, int64_t* stats) {
+    return guard([&] {
+        REQ(e && s && cur && pol && emit && n_emit, Q35_ERR_ARG, "null argument");
+        REQ(n > 0, Q35_ERR_ARG, "no lanes");
+        std::vector<int> grp[3];
+        for (int i = 0; i < n; ++i) {
+            REQ(pol[i], Q35_ERR_ARG, "null policy");
+            int32_t k = 0;
+            q35_mtp_policy_k(pol[i], &k);
+            REQ(k <= s->mtp_k, Q35_ERR_STATE, "policy depth exceeds the state's MTP slots");
+            grp[k].push_back(i);
+            if (depth) depth[i] = k;
+        }
+        for (int k = 2; k >= 0; --k) {
+            const int m = (int)grp[k].size();
+            if (!m) continue;
+            std::vector<int32_t> ls(m), cs(m), em((size_t)m * (k + 1)), ne(m);
+            for (int j = 0; j < m; ++j) { ls[j] = lanes ? lanes[grp[k][j]] : grp[k][j]; cs[j] = cur[grp[k][j]]; }
+            int rc;
+            if (k > 0) {
+                rc = q35_mtp_round_stop(e, s, ls.data(), m, cs.data(), k, stop, em.data(), ne.data(), stats);
+            } else {
+                rc = q35_decode_step(e, s, ls.data(), m, cs.data(), em.data(), nullptr);
+                for (int j = 0; j < m; ++j) ne[j] = 1;
+            }
+            if (rc) throw Q35Error(rc, g_err);
+            for (int j = 0; j < m; ++j) {
+                const int i = grp[k][j];
+                n_emit[i] = ne[j];
+                for (int t = 0; t < 3; ++t) emit[i * 3 + t] = t < ne[j] ? em[(size_t)j * (k + 1) + t] : -1;
+                if (k > 0) q35_mtp_policy_note(pol[i], k, ne[j], nullptr, nullptr);
+            }
+        }
+    });
+}
+
 int q35_op_tile_weight(q35_engine* e, const uint16_t* w, int N, int K, uint16_t* wt) {
     return guard([&] {
         REQ(e && w && wt && N > 0 && N % 16 == 0 && K > 0 && K % 256 == 0, Q35_ERR_ARG, "bad weight shape");

@@ -5,8 +5,8 @@ speccheck/mtp.py:36-179 `MTPDraft` / `greedy_mtp`) on top of the C ABI in
 include/q35.h. There is no CPU fallback: if the HIP library is missing or no GPU is
 visible, every entry point raises.
 """
-from .engine import (EOS_IDS, VOCAB, Engine, EngineError, Forward, State, greedy_mtp,
+from .engine import (EOS_IDS, VOCAB, Engine, EngineError, Forward, MtpPolicy, State, greedy_mtp,
                      lib_path, load_library, safetensors_scan)
 
-__all__ = ["Engine", "EngineError", "Forward", "State", "greedy_mtp", "load_library",
+__all__ = ["Engine", "EngineError", "Forward", "MtpPolicy", "State", "greedy_mtp", "load_library",
            "lib_path", "safetensors_scan", "VOCAB", "EOS_IDS"]

@@ -60,6 +60,12 @@ _SIGS = {
                        C.c_void_p, C.c_void_p], C.c_int),
     "q35_mtp_round_stop": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int32,
                             C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "q35_mtp_policy_create": ([C.c_int, C.c_double, C.c_double, C.POINTER(C.c_void_p)], C.c_int),
+    "q35_mtp_policy_free": ([C.c_void_p], C.c_int),
+    "q35_mtp_policy_k": ([C.c_void_p, C.POINTER(C.c_int32)], C.c_int),
+    "q35_mtp_policy_note": ([C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.POINTER(C.c_double)], C.c_int),
+    "q35_mtp_adaptive_step": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int32,
+                               C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "q35_op_tile_weight": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p], C.c_int),
     "q35_op_gemm": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p], C.c_int),
     "q35_op_gdn_step": ([C.c_void_p] * 8 + [C.c_int], C.c_int),
@@ -218,6 +224,41 @@ class Engine:
         return ms.value
 
 
+class MtpPolicy:
+    """Adaptive speculation depth of one request (mtpadapt::Tracker, engine/mtp_adaptive.h):
+    k = 2 -> 1 -> 0 (plain) from the request's own rounds; costs <= 0 take the reference's
+    round / step ratios (1.58 at k = 1, 1.90 at k = 2)."""
+
+    def __init__(self, start_k: int = 2, cost_k1: float = 0.0, cost_k2: float = 0.0):
+        h = C.c_void_p()
+        _ck(load_library().q35_mtp_policy_create(start_k, cost_k1, cost_k2, C.byref(h)))
+        self.h = h
+
+    @property
+    def k(self) -> int:
+        v = C.c_int32()
+        _ck(load_library().q35_mtp_policy_k(self.h, C.byref(v)))
+        return v.value
+
+    def note(self, k_round: int, emitted: int):
+        """Feed one round; returns (change or None, est) with change = (from, to, rounds seen)."""
+        ch = np.full(3, -1, np.int32)
+        est = C.c_double()
+        _ck(load_library().q35_mtp_policy_note(self.h, k_round, emitted, _p(ch), C.byref(est)))
+        return (tuple(int(x) for x in ch) if ch[0] >= 0 else None), est.value
+
+    def close(self):
+        if self.h:
+            load_library().q35_mtp_policy_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class State:
     """`lanes` independent requests (RequestState, engine/state.h:83-116)."""
 
@@ -343,6 +384,23 @@ class State:
         return [list(emit[i, :ne[i]]) for i in range(n)]
 
 
+    def mtp_adaptive_step(self, cur, policies, lanes=None, stop: int = -1, stats: np.ndarray | None = None):
+        """One turn of the lanes, each at its policy's depth (q35_mtp_adaptive_step): returns the
+        emitted tokens per lane and the depth each lane ran at (0 = a plain step)."""
+        c = _i32(cur)
+        n = c.size
+        assert len(policies) == n
+        ln = _i32(lanes) if lanes is not None else None
+        pol = (C.c_void_p * n)(*[p.h.value for p in policies])
+        emit = np.full((n, 3), -1, np.int32)
+        ne = np.zeros(n, np.int32)
+        dep = np.zeros(n, np.int32)
+        st = stats if stats is not None else np.zeros(4, np.int64)
+        _ck(load_library().q35_mtp_adaptive_step(self.eng.h, self.h, _p(ln) if ln is not None else None, n, _p(c),
+                                                 C.cast(pol, C.c_void_p), stop, _p(emit), _p(ne), _p(dep), _p(st)))
+        return [list(emit[i, :ne[i]]) for i in range(n)], dep
+
+
 class Forward:
     """One lane driven like specimpl.Forward (prefill / decode / greedy)."""
 
@@ -388,14 +446,19 @@ class Forward:
         return out
 
 
-def greedy_mtp(f: Forward, ids, steps: int, k: int = 2, stop_on_eos: bool = True):
-    """speccheck/mtp.py:97-179 with the batched verify and rollback done in the engine."""
+def greedy_mtp(f: Forward, ids, steps: int, k: int = 2, stop_on_eos: bool = True,
+               policy: "MtpPolicy | None" = None):
+    """speccheck/mtp.py:97-179 with the batched verify and rollback done in the engine; with a
+    policy, each round's depth is the policy's (engine/mtp_adaptive.h), 0 meaning a plain step."""
     assert f.state.mtp_k >= k
     stats = np.zeros(4, np.int64)
     t = f.prefill(ids)
     out = [t]
     while len(out) < steps + 1 and not (stop_on_eos and out[-1] in EOS_IDS):
-        em = f.state.mtp_round([out[-1]], k, [f.lane], stats)[0]
+        if policy is not None:
+            em = f.state.mtp_adaptive_step([out[-1]], [policy], [f.lane], stats=stats)[0][0]
+        else:
+            em = f.state.mtp_round([out[-1]], k, [f.lane], stats)[0]
         out.extend(int(x) for x in em)
     return out, dict(drafted=int(stats[0]), accepted=int(stats[1]), bonus=int(stats[2]),
                      verify_tokens=int(stats[3]), target_forwards=int(stats[2]) + 1)

@@ -32,6 +32,12 @@ round adds an "ACCEPT ..." line and a turn that ran rounds ends with "MTPSTAT ..
 logits dump is armed, steps are plain (one priced row per printed token). The drafter's own
 K/V cache is kept across feeds (the reference clears it at a feed); that changes which
 drafts are proposed, never the tokens printed.
+
+The depth of each round is adaptive by default, as the reference's session runs it
+(`--mtp-adaptive 1`, engine/decode_run.cpp:189-198, engine/mtp_adaptive.h): --mtp-k is the
+ceiling, the request's tracker demotes 2 -> 1 -> plain steps from what its rounds emitted
+("MTPADAPT round= k= est= prev_k= window_rounds= plain=" on each change), and a `feed` or
+`reset` starts a fresh tracker (engine/decode_run.cpp:2478-2483, 2510-2516).
 """
 from __future__ import annotations
 
@@ -41,7 +47,7 @@ from pathlib import Path
 
 import numpy as np
 
-from .engine import VOCAB, Engine, EngineError, State
+from .engine import VOCAB, Engine, EngineError, MtpPolicy, State
 
 STOP_TOKEN = 248046                  # engine/decode_step.h:492 (kStopToken)
 DEFAULT_CAP = 4096                   # engine/decode_run.cpp:72 (kSessionDefaultCap)
@@ -51,10 +57,13 @@ class Session:
     """One lane's session state machine; `handle` runs one command line and passes every
     output line to `emit` as soon as it exists (GEN lines stream)."""
 
-    def __init__(self, eng: Engine, cap: int = DEFAULT_CAP, out_dir: str | None = None, mtp_k: int = 0):
+    def __init__(self, eng: Engine, cap: int = DEFAULT_CAP, out_dir: str | None = None, mtp_k: int = 0,
+                 adaptive: bool = True):
         self.eng = eng
         self.cap = cap
         self.mtp_k = mtp_k
+        self.adaptive = adaptive and mtp_k > 0
+        self.policy = MtpPolicy(mtp_k) if self.adaptive else None
         self.state = State(eng, 1, cap, mtp_k=mtp_k, mtp_cap=cap if mtp_k else 0)
         self.rounds = 0
         self.turn = np.zeros(4, np.int64)     # drafted, accepted, bonus, verified rows this turn
@@ -64,11 +73,19 @@ class Session:
         self.out_dir = out_dir
         self.lo, self.hi, self.seq = 0, -1, 0
 
+    def _new_turn(self):
+        """A fresh adaptive tracker (mtpaccept::session_new_turn, engine/mtp_accept.cpp:501-504)."""
+        if self.adaptive:
+            self.policy.close()
+            self.policy = MtpPolicy(self.mtp_k)
+
     def ready_line(self) -> str:
         return f"READY cap={self.cap}"
 
     def close(self):
         self.state.close()
+        if self.policy is not None:
+            self.policy.close()
 
     # ---------------------------------------------------------------- logits dump
     def _armed(self) -> bool:
@@ -97,6 +114,7 @@ class Session:
             return False
         if cmd == "reset":
             self.state.reset([0])
+            self._new_turn()
             self.sampled, self.stopped, self.poisoned = -1, False, False
             emit("RESET prefix_len=0")
             return True
@@ -116,6 +134,7 @@ class Session:
                 return True
         try:
             if cmd == "feed":
+                self._new_turn()
                 toks = [self.sampled] if self.sampled >= 0 else []
                 for w in args:               # ids up to the first word that is not one
                     try:
@@ -139,8 +158,9 @@ class Session:
                         stop = True
                         break
                     want = self._armed()
-                    if self.mtp_k and not want:
-                        k, p = self.mtp_k, self.state.prefix_len(0)
+                    k = self.policy.k if self.adaptive else self.mtp_k
+                    if k and not want:
+                        p = self.state.prefix_len(0)
                         rows = k + 1
                         if p + rows > self.cap:
                             emit(f"ROUND-SKIP reason=context_limit anchor={p} cap={self.cap} rows={rows}")
@@ -152,6 +172,11 @@ class Session:
                             a = len(em) - 1
                             emit(f"ACCEPT round={self.rounds} anchor={p} fed={cur} k={k} n_accepted={a} "
                                  f"emitted={len(em)} pos={p}->{self.state.prefix_len(0)}")
+                            if self.adaptive:
+                                ch, est = self.policy.note(k, len(em))
+                                if ch:
+                                    emit(f"MTPADAPT round={self.rounds} k={ch[1]} est={est:.4f} prev_k={ch[0]} "
+                                         f"window_rounds={ch[2]} plain={int(ch[1] == 0)}")
                             for i, t in enumerate(em[:-1]):    # the accepted drafts (fed, so shown now)
                                 emit(f"GEN {t} {p + i}")
                                 emitted += 1
@@ -213,12 +238,14 @@ def main(argv=None) -> int:
     ap.add_argument("--out", help="directory for opt-in logits dumps")
     ap.add_argument("--graph", type=int, default=1, help="capture decode steps in hipGraphs")
     ap.add_argument("--mtp-k", type=int, default=2, help="drafts per speculative round; 0: plain steps")
+    ap.add_argument("--mtp-adaptive", type=int, default=1, choices=(0, 1),
+                    help="1: each round's depth from the request's own accept history (engine/mtp_adaptive.h)")
     a = ap.parse_args(argv)
     eng = Engine(max_rows=a.max_rows, max_ctx=a.cap, seed=None if a.checkpoint else a.seed, use_graph=bool(a.graph))
     if a.checkpoint:
         n, sk = eng.load_checkpoint(a.checkpoint)
         print(f"LOADED tensors={n} skipped={sk}", flush=True)
-    s = Session(eng, a.cap, a.out, mtp_k=a.mtp_k)
+    s = Session(eng, a.cap, a.out, mtp_k=a.mtp_k, adaptive=bool(a.mtp_adaptive))
 
     def emit(line: str):
         print(line, flush=True)

@@ -74,3 +74,48 @@ def test_mtp_rounds_with_accepts_match_plain_steps():
         assert hist.get(2, 0) > 0 and hist.get(0, 0) > 0
     finally:
         eng.close()
+
+
+def test_adaptive_step_mixed_depths_lossless():
+    """q35_mtp_adaptive_step over 24 lanes whose policies start at depths 2, 1 and 0 (all three
+    groups in one turn): every lane's emitted stream equals plain greedy steps of the same lane,
+    and with random-init weights (no draft accepted) the depths walk 2 -> 1 -> 0 at the policy's
+    thresholds (16 rounds at k = 2, 24 at k = 1)."""
+    from oracle.weights import lane_prompt_ids
+    from qwen35 import Engine, MtpPolicy, State
+    eng = Engine(max_rows=96, max_ctx=512, seed=0, use_graph=True)
+    try:
+        n = 24
+        spec = State(eng, n, 320, mtp_k=2, mtp_cap=256)
+        plain = State(eng, n, 320)
+        cur, pref = [], []
+        for i in range(n):
+            ids = lane_prompt_ids(60 + i, 0, 4 + i % 5)
+            y = spec.prefill(i, ids)
+            assert plain.prefill(i, ids) == y
+            cur.append(int(y))
+        pol = [MtpPolicy(2 if i % 3 == 0 else 1 if i % 3 == 1 else 0) for i in range(n)]
+        streams = [[c] for c in cur]
+        depth_hist = []
+        for turn in range(45):
+            em, dep = spec.mtp_adaptive_step(cur, pol)
+            depth_hist.append(dep.copy())
+            for i in range(n):
+                streams[i] += [int(t) for t in em[i]]
+                cur[i] = int(em[i][-1])
+        lens = min(len(s) for s in streams)
+        pc = [s[0] for s in streams]
+        for step in range(lens - 1):
+            pc = [int(t) for t in plain.decode_step(pc)]
+            for i in range(n):
+                assert pc[i] == streams[i][step + 1], (i, step)
+        d = np.array(depth_hist)                  # [turn][lane]
+        assert (d[:16, 0] == 2).all() and (d[16:40, 0] == 1).all() and (d[40:, 0] == 0).all()
+        assert (d[:24, 1] == 1).all() and (d[24:, 1] == 0).all()
+        assert (d[:, 2] == 0).all()
+        for p in pol:
+            p.close()
+        spec.close()
+        plain.close()
+    finally:
+        eng.close()

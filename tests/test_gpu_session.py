@@ -177,3 +177,36 @@ def test_session_mtp_rounds_match_plain(tmp_path, monkeypatch):
         assert cut_mattered and accepted > 0
     finally:
         eng.close()
+
+
+def test_session_adaptive_depth_abandons_and_matches_plain(tmp_path):
+    """Random-init weights: the drafter never agrees, so each round emits one token; the
+    session's adaptive tracker (engine/mtp_adaptive.h) demotes 2 -> 1 after 16 rounds (estimate
+    1 / 1.90) and abandons after 24 more (1 / 1.58), and the transcript is the plain session's.
+    A feed starts a fresh tracker: the next turn speculates at k = 2 again."""
+    from oracle.weights import lane_prompt_ids
+    from qwen35 import Engine
+    from qwen35.session import Session
+    keep = ("GEN ", "FED ", "END ")
+    eng = Engine(max_rows=64, max_ctx=512, seed=0, use_graph=True)
+    try:
+        logs = {}
+        for k in (0, 2):
+            out = []
+            s = Session(eng, 512, str(tmp_path), mtp_k=k)
+            for t in range(2):
+                s.handle("feed " + " ".join(str(x) for x in lane_prompt_ids(21, t, 6)), out.append)
+                s.handle("gen 100", out.append)
+            s.close()
+            logs[k] = out
+        assert [l for l in logs[0] if l.startswith(keep)] == [l for l in logs[2] if l.startswith(keep)]
+        ad = [l for l in logs[2] if l.startswith("MTPADAPT ")]
+        print("adaptive session:", ad, flush=True)
+        assert len(ad) == 4                                   # two changes in each of the two turns
+        assert "k=1 " in ad[0] and "window_rounds=16 " in ad[0] and "prev_k=2 " in ad[0]
+        assert "k=0 " in ad[1] and "window_rounds=24 " in ad[1] and ad[1].endswith("plain=1")
+        assert "k=1 " in ad[2] and "k=0 " in ad[3]
+        acc = [l for l in logs[2] if l.startswith("ACCEPT ")]
+        assert sum(" k=2 " in l for l in acc) == 32 and sum(" k=1 " in l for l in acc) == 48
+    finally:
+        eng.close()
