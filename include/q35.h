@@ -170,6 +170,13 @@ int q35_op_gemm(q35_engine* e, const uint16_t* w_tiled_dev, int N, int K, const 
  * receive the new state in slot 1; o [B][2048] f32 (before the gated norm). */
 int q35_op_gdn_step(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w, const uint16_t* A_log,
                     const uint16_t* dt_bias, float* S2, float* W2, float* o, int B);
+/* q35_op_gdn_step without any allocation, for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops); it has no counterpart in the reference. Same arguments and
+ * results; its scratch (the lane list, B ints) is a fixed per-GPU device array of 4,096 entries
+ * held until the process ends, so B <= 4096 (larger B: Q35_ERR_CAP). Enqueued on the engine
+ * stream without waiting (q35_sync waits); calls that overlap on one GPU race on the array. */
+int q35_op_gdn_step_noalloc(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w, const uint16_t* A_log,
+                            const uint16_t* dt_bias, float* S2, float* W2, float* o, int B);
 /* The same step with the layer's gated RMSNorm (engine/kernels_gdn.cpp:525, specimpl.py:142-147,
  * 304-305): y [B][2048] bf16 = bf16(w * (o * rsqrt(mean_head(o^2) + 1e-6)) * silu(z)) per
  * 128-wide head, with gnorm [128] bf16, made where the engine makes it for B lanes: in the

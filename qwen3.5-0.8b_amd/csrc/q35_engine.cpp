@@ -12,6 +12,7 @@
 #include <cstring>
 #include <functional>
 #include <map>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -190,6 +191,47 @@ T* halloc(size_t n) {
 void copy_sync(q35_engine* e, void* dst, const void* src, size_t n, hipMemcpyKind kind) {
     HCK(hipMemcpyAsync(dst, src, n, kind, e->st));
     HCK(hipStreamSynchronize(e->st));
+}
+
+// ------------------------------------------------------------------ allocation-free GDN step
+// q35_op_gdn_step_noalloc's only scratch (the row -> lane index list of its rows) lives in this
+// file-scope device array: one copy per GPU, held until the process ends, shared by every
+// call on that GPU. In host code `scratch` names a host-side stand-in, so its device address
+// is looked up once per device (at q35_create, with the device current) and only that
+// address is ever passed to kernels.
+constexpr int kNoAllocMaxLanes = 4096;
+static __device__ __align__(256) int scratch[kNoAllocMaxLanes];
+std::mutex g_scratch_mu;
+std::map<int, int*> g_scratch_ptr;   // device ordinal -> device address of `scratch`
+
+std::map<int, std::string> g_scratch_err;   // device ordinal -> why the lookup failed
+
+// Never fails the caller (q35_create): a failed lookup is recorded and reported by the
+// allocation-free entry point, the only user of the array.
+void init_noalloc_scratch(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr.count(device) || g_scratch_err.count(device)) return;
+    int* p = nullptr;
+    const hipError_t rc = hipGetSymbolAddress((void**)&p, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || p == nullptr) {
+        (void)hipGetLastError();
+        g_scratch_err[device] = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(rc);
+        return;
+    }
+    g_scratch_ptr[device] = p;
+}
+
+int* noalloc_scratch(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch_ptr.find(device);
+    if (it != g_scratch_ptr.end()) return it->second;
+    auto er = g_scratch_err.find(device);
+    throw Q35Error(Q35_ERR_HIP, er != g_scratch_err.end() ? er->second : "scratch of this device was not set up");
+}
+
+__global__ void iota_kernel(int* p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = i;
 }
 
 // ------------------------------------------------------------------ weight registry
@@ -671,6 +713,7 @@ int q35_create(const q35_config* cfg, q35_engine** out) {
         auto* e = new q35_engine();
         e->device = cfg->device; e->R = cfg->max_rows; e->max_ctx = cfg->max_ctx; e->use_graph = cfg->use_graph;
         HCK(hipSetDevice(e->device));
+        init_noalloc_scratch(e->device);
         HCK(gemm_init());
         HCK(attn_init());
         HCK(gdn_init());
@@ -1440,6 +1483,30 @@ int q35_op_gdn_step_norm(q35_engine* e, const uint16_t* proj, const uint16_t* co
                          const uint16_t* dt_bias, const uint16_t* gnorm, float* S2, float* W2, float* o,
                          uint16_t* y, int B, int form) {
     return guard([&] { op_gdn(e, proj, conv_w, A_log, dt_bias, gnorm, S2, W2, o, y, B, form); });
+}
+
+// The allocation-free form of q35_op_gdn_step: no hipMalloc / hipFree and no host copy (the
+// lane list is written on the device into the per-GPU `scratch` array); asynchronous on the
+// engine stream (q35_sync waits for it). Calls that overlap on one GPU share the array.
+int q35_op_gdn_step_noalloc(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w, const uint16_t* A_log,
+                            const uint16_t* dt_bias, float* S2, float* W2, float* o, int B) {
+    return guard([&] {
+        REQ(e && proj && conv_w && A_log && dt_bias && S2 && W2 && o && B > 0, Q35_ERR_ARG, "bad gdn call");
+        REQ(B <= kNoAllocMaxLanes, Q35_ERR_CAP,
+            "B exceeds the allocation-free GDN step's maximum of " + std::to_string(kNoAllocMaxLanes) + " lanes");
+        int* lanes = noalloc_scratch(e->device);
+        hipLaunchKernelGGL(iota_kernel, dim3((B + 255) / 256), dim3(256), 0, e->st, lanes, B);
+        HCK(hipGetLastError());
+        GdnArgs g{};
+        g.proj = proj; g.o = o; g.conv_w = conv_w; g.A_log = A_log; g.dt_bias = dt_bias;
+        g.S = S2; g.S_lane = 2 * kSLayer; g.S_slot = kSLayer; g.S_layer = 0;
+        g.win = W2; g.W_lane = 2 * kWLayer; g.W_slot = kWLayer; g.W_layer = 0;
+        g.cur = nullptr; g.nslots = 2; g.ckpt = 0;
+        g.lane = lanes; g.T = 1; g.nlanes = B;
+        const int cs = B <= 8 ? 8 : B <= 32 ? 4 : B <= 64 ? 2 : 1;
+        if (cs == 1) HCK(launch_gdn_persist(g, e->st));
+        else HCK(launch_gdn(g, cs, e->st));
+    });
 }
 
 int q35_op_gemm_a(q35_engine* e, const uint16_t* wt, int N, int K, int amode, const void* x, int ldx,

@@ -69,6 +69,7 @@ _SIGS = {
     "q35_op_tile_weight": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p], C.c_int),
     "q35_op_gemm": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p], C.c_int),
     "q35_op_gdn_step": ([C.c_void_p] * 8 + [C.c_int], C.c_int),
+    "q35_op_gdn_step_noalloc": ([C.c_void_p] * 8 + [C.c_int], C.c_int),
     "q35_op_gdn_step_norm": ([C.c_void_p] * 10 + [C.c_int, C.c_int], C.c_int),
     "q35_op_gemm_a": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
                        C.c_int, C.c_void_p, C.c_int, C.c_void_p], C.c_int),
@@ -199,6 +200,11 @@ class Engine:
 
     def op_gdn_step(self, proj: int, conv_w: int, A_log: int, dt_bias: int, S2: int, W2: int, o: int, B: int):
         _ck(load_library().q35_op_gdn_step(self.h, *[C.c_void_p(p) for p in (proj, conv_w, A_log, dt_bias, S2, W2, o)], B))
+
+    def op_gdn_step_noalloc(self, proj: int, conv_w: int, A_log: int, dt_bias: int, S2: int, W2: int, o: int, B: int):
+        """The allocation-free GDN step (asynchronous on the engine stream: sync() waits)."""
+        _ck(load_library().q35_op_gdn_step_noalloc(self.h, *[C.c_void_p(p) for p in (proj, conv_w, A_log, dt_bias,
+                                                                                       S2, W2, o)], B))
 
     def op_gdn_step_norm(self, proj: int, conv_w: int, A_log: int, dt_bias: int, gnorm: int, S2: int, W2: int,
                          o: int, y: int, B: int, form: int = 0):
