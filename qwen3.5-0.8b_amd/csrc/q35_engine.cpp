@@ -91,7 +91,6 @@ struct q35_state {
     uint16_t *kc = nullptr, *vc = nullptr;    // [lanes][6][2][cap][256]
     uint16_t *mkc = nullptr, *mvc = nullptr;  // [lanes][2][mtp_cap][256]
     uint16_t* hlast = nullptr;                // [lanes][1024] post-final-norm row of the last body
-    int* cur_dev = nullptr;                   // [lanes]
     std::vector<int> prefix, mtp_len, cur;
     long long S_lane() const { return (long long)nslots * kGdnLayers * kSLayer; }
     long long W_lane() const { return (long long)nslots * kGdnLayers * 18432; }
@@ -125,17 +124,15 @@ struct q35_engine {
     float *o, *q, *sc, *stats, *part, *pval, *inv_freq;
     float* kpart;
     uint16_t* prod;
-    int *pidx, *tok_dev, *rlane, *rpos, *rslot, *ridx_src, *ridx_dst, *din = nullptr;
+    int *pidx, *tok_dev, *rlane, *rpos, *rslot, *rcur, *ridx_src, *ridx_dst, *din = nullptr;
     int sc_ld = 0, max_chunks = 0;
     float* logits_dev = nullptr;
     int logits_rows = 0;
     float* topv_dev = nullptr;       // [R] the argmax's logit value per row (all-rows prefill)
     std::map<std::string, hipGraphExec_t> graphs;   // captured decode steps
     // pinned staging
-    int *h_tok, *h_lane, *h_pos, *h_slot, *h_out, *h_src, *h_dst, *hin = nullptr;
-    int* h_cur = nullptr;            // pinned staging of a state's `cur` for its upload
-    int h_cur_cap = 0;               // (one engine buffer, sized for the largest state)
-    // Row metadata on the device (token, lane, position, slot, row indices; a state's `cur`)
+    int *h_tok, *h_lane, *h_pos, *h_slot, *h_rcur, *h_out, *h_src, *h_dst, *hin = nullptr;
+    // Row metadata on the device (token, lane, position, slot, the state slot of the row's lane, row indices)
     // changes only by the uploads below, which bump meta_epoch, and by a decode step, which
     // advances positions, slots and `cur` on the device and leaves its sampled tokens in the
     // token row. The next decode step of the same state and lanes, fed exactly those tokens
@@ -382,15 +379,17 @@ void alloc_scratch(q35_engine* e) {
     e->gchunk = dalloc<float>(gdn_chunk_ws_floats(R));
     e->gcdec = dalloc<float>((size_t)((R + 63) / 64) * kHv);
     e->prod = dalloc<uint16_t>(R * kFF);
-    // row metadata: one device block and one pinned host block, [tok|lane|pos|slot|src|dst]
-    // with stride R, so a step's inputs go up in a single copy
-    e->din = dalloc<int>(6 * (size_t)R);
-    e->hin = halloc<int>(6 * (size_t)R);
-    int* d[6];
-    int* hh[6];
-    for (int i = 0; i < 6; ++i) { d[i] = e->din + (size_t)i * R; hh[i] = e->hin + (size_t)i * R; }
-    e->tok_dev = d[0]; e->rlane = d[1]; e->rpos = d[2]; e->rslot = d[3]; e->ridx_src = d[4]; e->ridx_dst = d[5];
-    e->h_tok = hh[0]; e->h_lane = hh[1]; e->h_pos = hh[2]; e->h_slot = hh[3]; e->h_src = hh[4]; e->h_dst = hh[5];
+    // row metadata: one device block and one pinned host block,
+    // [tok|lane|pos|slot|cur|src|dst] with stride R, so a step's inputs go up in a single copy;
+    // `cur` is the GDN state slot of the row's lane (read together with the lane, so the GDN
+    // kernels' state addresses wait for one load, not two dependent ones)
+    e->din = dalloc<int>(7 * (size_t)R);
+    e->hin = halloc<int>(7 * (size_t)R);
+    int* d[7];
+    int* hh[7];
+    for (int i = 0; i < 7; ++i) { d[i] = e->din + (size_t)i * R; hh[i] = e->hin + (size_t)i * R; }
+    e->tok_dev = d[0]; e->rlane = d[1]; e->rpos = d[2]; e->rslot = d[3]; e->rcur = d[4]; e->ridx_src = d[5]; e->ridx_dst = d[6];
+    e->h_tok = hh[0]; e->h_lane = hh[1]; e->h_pos = hh[2]; e->h_slot = hh[3]; e->h_rcur = hh[4]; e->h_src = hh[5]; e->h_dst = hh[6];
     e->h_out = halloc<int>(R);
     // rope inverse frequencies, f32 as the oracle forms them (specimpl.py:151-156):
     // inv_i = 1 / f32(theta ** f32(2i/64))
@@ -424,19 +423,16 @@ void upload_meta(q35_engine* e, int upto, int n) {
     ++e->meta_epoch;
     HCK(hipMemcpyAsync(e->din, e->hin, ((size_t)upto * e->R + n) * sizeof(int), hipMemcpyHostToDevice, e->st));
 }
-void upload_rows(q35_engine* e, int R) { upload_meta(e, 3, R); }   // tok, lane, pos, slot
+void upload_rows(q35_engine* e, int R) { upload_meta(e, 4, R); }   // tok, lane, pos, slot, cur
 // src / dst row indices only (tok_dev may hold device-written tokens): one copy
 void upload_idx(q35_engine* e, int n) {
     ++e->meta_epoch;
     HCK(hipMemcpyAsync(e->ridx_src, e->h_src, ((size_t)e->R + n) * sizeof(int), hipMemcpyHostToDevice, e->st));
 }
 
-// `cur` goes through pinned staging: the host advances s->cur right after enqueueing a
-// body, so the copy must not read the live vector. Callers drain the stream before a body.
-void upload_cur(q35_engine* e, q35_state* s) {
-    ++e->meta_epoch;
-    for (int i = 0; i < s->lanes; ++i) e->h_cur[i] = s->cur[i];
-    HCK(hipMemcpyAsync(s->cur_dev, e->h_cur, s->lanes * sizeof(int), hipMemcpyHostToDevice, e->st));
+// Per-row state slots from the lanes' host `cur` (rows staged in h_lane).
+void stage_rcur(q35_engine* e, q35_state* s, int R) {
+    for (int r = 0; r < R; ++r) e->h_rcur[r] = s->cur[e->h_lane[r]];
 }
 
 // Y != nullptr: bf16 store; Y == nullptr: k-block chains to e->kpart (summed by the next
@@ -552,8 +548,8 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt);
 void body(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
     REQ(e->weights_ready, Q35_ERR_STATE, "weights not initialised");
     REQ(R > 0 && R <= e->R, Q35_ERR_CAP, "rows exceed engine max_rows");
+    stage_rcur(e, s, R);
     upload_rows(e, R);
-    upload_cur(e, s);
     body_kernels(e, s, R, T, ckpt);
 }
 
@@ -579,7 +575,7 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
             g.S_layer = (long long)gdn_slot(l) * kSLayer;
             g.win = s->win; g.W_lane = s->W_lane(); g.W_slot = (long long)kGdnLayers * 18432;
             g.W_layer = (long long)gdn_slot(l) * 18432;
-            g.cur = s->cur_dev; g.nslots = s->nslots; g.ckpt = ckpt ? 1 : 0;
+            g.cur = e->rcur; g.nslots = s->nslots; g.ckpt = ckpt ? 1 : 0;
             g.lane = e->rlane; g.T = T; g.nlanes = nl;
             // a prompt wave of one lane: chunked (UT-transform) form
             const bool chunked = e->gdn_chunked && !small && nl == 1 && T >= 64 && !ckpt;
@@ -737,7 +733,7 @@ int q35_destroy(q35_engine* e) {
                       e->sc, e->stats, e->part, e->pval, e->pidx, e->prod, e->din, e->inv_freq,
                       e->logits_dev, e->kpart, e->gchunk, e->gcdec, e->topv_dev};
         for (void* p : ds) if (p) hipFree(p);
-        void* hs[] = {e->hin, e->h_out, e->h_cur};
+        void* hs[] = {e->hin, e->h_out};
         for (void* p : hs) if (p) hipHostFree(p);
         hipEventDestroy(e->ev0);
         hipEventDestroy(e->ev1);
@@ -868,13 +864,6 @@ int q35_state_alloc(q35_engine* e, int lanes, int cap, int mtp_k, int mtp_cap, q
             s->mvc = dalloc<uint16_t>((size_t)lanes * s->mkv_lane());
         }
         s->hlast = dalloc<uint16_t>((size_t)lanes * kHidden);
-        s->cur_dev = dalloc<int>(lanes);
-        if (lanes > e->h_cur_cap) {      // no body is in flight: callers drain the stream
-            HCK(hipStreamSynchronize(e->st));
-            if (e->h_cur) HCK(hipHostFree(e->h_cur));
-            e->h_cur = halloc<int>(lanes);
-            e->h_cur_cap = lanes;
-        }
         s->prefix.assign(lanes, 0);
         s->mtp_len.assign(lanes, 0);
         s->cur.assign(lanes, 0);
@@ -901,7 +890,7 @@ int q35_state_free(q35_engine* e, q35_state* s) {
                 else ++it;
             }
         }
-        void* ds[] = {s->S, s->win, s->kc, s->vc, s->mkc, s->mvc, s->hlast, s->cur_dev};
+        void* ds[] = {s->S, s->win, s->kc, s->vc, s->mkc, s->mvc, s->hlast};
         for (void* p : ds) if (p) hipFree(p);
         delete s;
     });
@@ -1229,15 +1218,15 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
                    e->fast_prefix[i] == s->prefix[ls[i]] && e->fast_cur[i] == s->cur[ls[i]];
         e->fast_s = nullptr;                 // re-armed only when this step completes
         if (!fast) {
-            upload_meta(e, 5, n);        // tok, lane, pos, slot, src, dst in one copy
-            upload_cur(e, s);
+            stage_rcur(e, s, n);
+            upload_meta(e, 6, n);        // tok, lane, pos, slot, cur, src, dst in one copy
         }
         auto step = [&] {
             body_kernels(e, s, n, 1, false);
             lm_head(e, 0, n, out_logits != nullptr,
                     small_rows(n) && !b1_partials(e, n, 1, false) ? e->final_norm : nullptr);
             HCK(launch_copy_rows_advance(e->nrm, e->ridx_src, s->hlast, e->ridx_dst, n, kHidden, e->rpos, e->rslot,
-                                         e->rlane, s->cur_dev, s->nslots, e->st));
+                                         e->rcur, s->nslots, e->st));
         };
         if (e->use_graph && e->kprof == 0) {
             if (out_logits) ensure_logits(e, n);

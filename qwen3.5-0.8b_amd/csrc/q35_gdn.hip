@@ -34,7 +34,7 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     const int tid = threadIdx.x;
     const int jc = (tid % CG) * CW, kg = tid / CG;
     const int lane = a.lane[gi * a.T];
-    const int cur = a.cur ? a.cur[lane] : 0;
+    const int cur = a.cur ? a.cur[gi * a.T] : 0;
 
     __shared__ float qs[128], ks[128], vs[VC];
     constexpr int NG = 16;            // fixed reduction groups of 8 k-rows, for every CS
@@ -220,7 +220,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     auto prefetch = [&](int item) {
         const int gi = item >> 4, h = item & 15;
         const int ln = a.lane[gi];
-        const int cu = a.cur ? a.cur[ln] : 0;
+        const int cu = a.cur ? a.cur[gi] : 0;
         const float* Sin = a.S + ln * a.S_lane + a.S_layer + (long long)h * 16384 + cu * a.S_slot;
 #pragma unroll
         for (int i = 0; i < KR; ++i)
@@ -232,7 +232,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     for (; item < nitems; item += gridDim.x) {
         const int gi = item >> 4, h = item & 15;
         const int lane = a.lane[gi];
-        const int cur = a.cur ? a.cur[lane] : 0;
+        const int cur = a.cur ? a.cur[gi] : 0;
         float* Sbase = a.S + lane * a.S_lane + a.S_layer + (long long)h * 16384;
         float* Wbase = a.win + lane * a.W_lane + a.W_layer;
         const float* Win = Wbase + cur * a.W_slot;

@@ -52,7 +52,7 @@ __global__ void __launch_bounds__(256) gdn_chunk_conv(GdnArgs a) {
     const int t0 = blockIdx.x * kConvRows;
     const int n = min(kConvRows, a.T - t0);
     const int lane = a.lane[0];
-    const int cur = a.cur ? a.cur[lane] : 0;
+    const int cur = a.cur ? a.cur[0] : 0;
     const float* Win = a.win + lane * a.W_lane + a.W_layer + cur * a.W_slot;
     const uint2 cpk = *(const uint2*)(a.conv_w + (size_t)ch * 4);
     const float cw0 = __uint_as_float(cpk.x << 16), cw1 = __uint_as_float(cpk.x & 0xffff0000u);
@@ -289,7 +289,7 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
     const int h = blockIdx.x, n0 = blockIdx.y * 16;
     const int tid = threadIdx.x, ln = tid & 63, wv = tid >> 6;
     const int lane = a.lane[0];
-    const int cur = a.cur ? a.cur[lane] : 0;
+    const int cur = a.cur ? a.cur[0] : 0;
     float* Sbase = a.S + lane * a.S_lane + a.S_layer + (long long)h * 16384;
     const float* Sin = Sbase + cur * a.S_slot;
     float* Sout = Sbase + ((cur + 1) % a.nslots) * a.S_slot;

@@ -87,7 +87,7 @@ struct GdnArgs {
     long long S_lane, S_slot, S_layer;
     float* win;
     long long W_lane, W_slot, W_layer;
-    const int* cur;            // [lanes] current slot of each state lane
+    const int* cur;            // [R] current state slot of each row's lane (null: slot 0)
     int nslots;
     int ckpt;                  // 0: state after the last row -> slot (cur + 1) % nslots;
                                // 1: state after row t -> slot (cur + 1 + t) % nslots
@@ -152,8 +152,9 @@ hipError_t launch_tile(const uint16_t* src, int N, int K, uint16_t* dst, int row
                        hipStream_t st);
 hipError_t launch_copy_rows(const uint16_t* src, const int* src_rows, uint16_t* dst, const int* dst_rows,
                             int n, int width, hipStream_t st);
+// The decode step's last kernel: copy rows src -> dst and advance each row's position, cache
+// slot and state slot (cur) for the next step of the same lanes.
 hipError_t launch_copy_rows_advance(const uint16_t* src, const int* src_rows, uint16_t* dst, const int* dst_rows,
-                                    int n, int width, int* pos, int* slot, const int* lane, int* cur, int nslots,
-                                    hipStream_t st);
+                                    int n, int width, int* pos, int* slot, int* cur, int nslots, hipStream_t st);
 
 }  // namespace q35
