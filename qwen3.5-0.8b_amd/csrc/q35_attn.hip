@@ -439,6 +439,218 @@ __global__ void __launch_bounds__(256) attn_combine(AttnArgs a) {
     a.out[(size_t)r * 2048 + qh * 256 + tid] = gated_out(a, r, qh, tid, acc);
 }
 
+// ---------------------------------------------------------------- split path, 4-wave blocks
+// The split path's kernels with more waves per block and the same arithmetic, so a row's
+// K/V streams over 4x the waves (batch 1 uses a quarter of the CUs otherwise):
+//   attn_scores4   (row, kv head, 64-slot slice): wave w scores 16-slot sub-tile w (8 KiB of
+//                  K) and, with PREP, makes q head 4j + w (wave 0 also the new K row); wave 0
+//                  then forms the slice stats from all four sub-tiles' values in score_slice's
+//                  order (max, then e summed sub-tile-major)
+//   attn_pv4       (row, kv head, 128-slot part, 64-dim quarter): one wave, thread (dim group
+//                  dl, slot group tg) accumulates 16 slots x 8 dims in pv_part's order; the
+//                  8 slot groups are summed as pv_part sums them ((g0 + g1) + (g2 + g3)) + ...
+template <bool PREP>
+__global__ void __launch_bounds__(256) attn_scores4(AttnArgs a) {
+    __shared__ uint16_t qb[16][256];
+    __shared__ uint16_t knew[256];
+    __shared__ float svl[4][4][64];          // [sub-tile][r][lane]
+    const int r = blockIdx.x, j = blockIdx.y, q = blockIdx.z;
+    const int slot = a.rm.slot[r];
+    if (q * 64 > slot) return;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, n = lane & 15, g = lane >> 4;
+    const int lrow = a.rm.lane[r];
+    q35_u32x4 qf[8], kf[8];
+    load_k_sub(a, lrow, j, q, wv, slot, kf);
+    const bool own = PREP && q == (slot >> 6);
+    if (PREP) {
+        const int pos = a.rm.pos[r];
+        const uint16_t* pr = a.proj + (size_t)r * kAttnInRows;
+        float o[4];
+        head_norm_rope_wave(a, pr + (4 * j + wv) * 512, a.q_norm, pos, o);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int d = lane + 64 * w;
+            const uint16_t hi = f2bf(o[w]);
+            qb[wv][d] = hi;
+            qb[4 + wv][d] = f2bf(o[w] - bf2f(hi));
+            qb[8 + wv][d] = 0;
+            qb[12 + wv][d] = 0;
+        }
+        if (own && wv == 0) {
+            head_norm_rope_wave(a, pr + kAttnKOff + j * 256, a.k_norm, pos, o);
+            const size_t base = lrow * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const int d = lane + 64 * w;
+                const uint16_t kb = f2bf(o[w]);
+                knew[d] = kb;
+                a.kc[base + kv_tiled_offset(slot, d)] = kb;
+                a.vc[base + (size_t)slot * 256 + d] = pr[kAttnVOff + j * 256 + d];
+            }
+        }
+    } else {
+        const float* qp = a.q + ((size_t)r * kNq + 4 * j + wv) * 256;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int d = lane + 64 * w;
+            const float qv = qp[d];
+            const uint16_t hi = f2bf(qv);
+            qb[wv][d] = hi;
+            qb[4 + wv][d] = f2bf(qv - bf2f(hi));
+            qb[8 + wv][d] = 0;
+            qb[12 + wv][d] = 0;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[s] = *(const q35_u32x4*)&qb[n][s * 32 + g * 8];
+    if (own && n == (slot & 15) && wv == (slot >> 4) - q * 4) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) kf[s] = *(const q35_u32x4*)&knew[s * 32 + g * 8];
+    }
+    float* dst = a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld;
+    const int t0 = q * 64;
+    {
+        q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&kf[s], *(const q35_bf16x8*)&qf[s], acc, 0, 0, 0);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const float lo = row_down4(acc[rr]);   // lanes n < 4 add the q_lo column n + 4
+            const float sc = (acc[rr] + lo) * 0.0625f;
+            const int t = t0 + wv * 16 + 4 * g + rr;
+            const bool ok = n < 4 && t <= slot;
+            svl[wv][rr][lane] = ok ? sc : -INFINITY;
+            if (ok) dst[n * a.sc_ld + t] = sc;
+        }
+    }
+    __syncthreads();
+    if (wv != 0) return;
+    float sv[4][4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) sv[st][rr] = svl[st][rr][lane];
+    float m = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) m = fmaxf(m, sv[st][rr]);
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, xor32(m));
+    float e = 0.f;
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) e += sv[st][rr] > -INFINITY ? expf(sv[st][rr] - m) : 0.f;
+    e += __shfl_xor(e, 16, 64);
+    e += xor32(e);
+    if (lane < 4) {
+        float* sp = a.stats + ((size_t)r * kNq + 4 * j + lane) * a.max_chunks * 8 + 2 * q;
+        sp[0] = m;
+        sp[1] = e;
+    }
+}
+
+__global__ void __launch_bounds__(64) attn_pv4(AttnArgs a) {
+    __shared__ float p[4][kPart];
+    __shared__ float red[8][4][64];          // [slot group][head][dim of the quarter]
+    const int r = blockIdx.x, j = blockIdx.y, pc = blockIdx.z >> 2, dq = blockIdx.z & 3;
+    const int slot = a.rm.slot[r];
+    if (pc >= slot / kPart + 1) return;
+    const int tid = threadIdx.x, dl = tid & 7, tg = tid >> 3;
+    const int lrow = a.rm.lane[r];
+    const int t0 = pc * kPart;
+    // V rows first (unconditional clamped loads), as load_v does
+    q35_u32x4 vv[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int t = t0 + tg * 16 + u;
+        const uint16_t* vp = a.vc + lrow * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + min(t, slot)) * 256 +
+                             dq * 64 + dl * 8;
+        const q35_u32x4 v = __builtin_nontemporal_load((const q35_u32x4*)vp);
+        const uint32_t keep = t <= slot ? 0xffffffffu : 0u;
+        vv[u] = (q35_u32x4){v[0] & keep, v[1] & keep, v[2] & keep, v[3] & keep};
+    }
+    // this part's raw scores (independent of the softmax statistics: loaded early)
+    const int n = min(kPart, slot + 1 - t0);
+    const float* scores = a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld;
+    float sraw[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int idx = tid + k * 64, i = idx >> 7, t = idx & 127;
+        sraw[k] = scores[i * a.sc_ld + t0 + min(t, n - 1)];
+    }
+    // the softmax (max, sum) of the 4 heads with softmax_ml's arithmetic per head, the heads
+    // interleaved so that their loads are in flight together
+    const float* stats = a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 8;
+    const size_t sst = (size_t)a.max_chunks * 8;
+    const int nsl = slot / 64 + 1;
+    float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    for (int i = tid; i < nsl; i += 64) {
+        float v[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) v[h] = stats[h * sst + 2 * i];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) m[h] = fmaxf(m[h], v[h]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) m[h] = fmaxf(m[h], __shfl_xor(m[h], o, 64));
+    float l[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int i = tid; i < nsl; i += 64) {
+        float sm[4], se[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) { sm[h] = stats[h * sst + 2 * i]; se[h] = stats[h * sst + 2 * i + 1]; }
+#pragma unroll
+        for (int h = 0; h < 4; ++h) l[h] += se[h] * expf(sm[h] - m[h]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) l[h] += __shfl_xor(l[h], o, 64);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int idx = tid + k * 64, i = idx >> 7, t = idx & 127;
+        const float mi = i == 0 ? m[0] : i == 1 ? m[1] : i == 2 ? m[2] : m[3];
+        const float li = i == 0 ? l[0] : i == 1 ? l[1] : i == 2 ? l[2] : l[3];
+        p[i][t] = t < n ? rbf(expf(sraw[k] - mi) / li) : 0.f;
+    }
+    __syncthreads();
+    float acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int t = tg * 16 + u;
+        float pp[4] = {p[0][t], p[1][t], p[2][t], p[3][t]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float v = (e & 1) ? __uint_as_float(vv[u][e >> 1] & 0xffff0000u) : __uint_as_float(vv[u][e >> 1] << 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i][e] = fmaf(pp[i], v, acc[i][e]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[tg][i][dl * 8 + e] = acc[i][e];
+    __syncthreads();
+    float* pp = a.part + (((size_t)r * a.max_chunks * 2 + pc) * kNq + 4 * j) * 256 + dq * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int d = tid;
+        float w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = red[2 * k][i][d] + red[2 * k + 1][i][d];
+        pp[i * 256 + d] = ((w[0] + w[1]) + w[2]) + w[3];
+    }
+}
+
 // Batched lanes: one block per (row, kv head) runs every chunk's scores into LDS, the
 // softmax, every part's P.V and the gated sum -- the same device functions and orders as the
 // split kernels, without the score / stats / partial round trips through HBM.
@@ -779,11 +991,19 @@ hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
         const int nseg = std::max(1, 8 / pairs), seg = (a.T + nseg - 1) / nseg;
         hipLaunchKernelGGL(attn_fused, dim3((pairs * nseg + 7) / 8 * seg * 8), dim3(256), lds, st, a, lds_slots);
     } else {
-        if (prep_in_scores(a))
-            hipLaunchKernelGGL(attn_scores_prep, dim3(a.R, kNkv, a.max_chunks * 4), dim3(64), 0, st, a);
-        else
-            hipLaunchKernelGGL(attn_scores, dim3(a.R, kNkv, a.max_chunks * 4), dim3(64), 0, st, a);
-        hipLaunchKernelGGL(attn_pv, dim3(a.R, kNkv, a.max_chunks * 2), dim3(256), 0, st, a);
+        if (a.split4) {
+            if (prep_in_scores(a))
+                hipLaunchKernelGGL(attn_scores4<true>, dim3(a.R, kNkv, a.max_chunks * 4), dim3(256), 0, st, a);
+            else
+                hipLaunchKernelGGL(attn_scores4<false>, dim3(a.R, kNkv, a.max_chunks * 4), dim3(256), 0, st, a);
+            hipLaunchKernelGGL(attn_pv4, dim3(a.R, kNkv, a.max_chunks * 8), dim3(64), 0, st, a);
+        } else {
+            if (prep_in_scores(a))
+                hipLaunchKernelGGL(attn_scores_prep, dim3(a.R, kNkv, a.max_chunks * 4), dim3(64), 0, st, a);
+            else
+                hipLaunchKernelGGL(attn_scores, dim3(a.R, kNkv, a.max_chunks * 4), dim3(64), 0, st, a);
+            hipLaunchKernelGGL(attn_pv, dim3(a.R, kNkv, a.max_chunks * 2), dim3(256), 0, st, a);
+        }
         hipLaunchKernelGGL(attn_combine, dim3(a.R, kNq), dim3(256), 0, st, a);
     }
     return hipGetLastError();

@@ -19,6 +19,7 @@ struct KernelForms {
     int gemm_pre = 1;          // batched K = 1024 GEMMs: all loads up front (1) or k-block pipelined (0)
     int lmhead_persist = 1;    // tied lm_head at batched lanes: persistent kernel (1) or 64 x 256 tiles (0)
     int partial_rows = 1024;   // batched kEPartial GEMMs with M >= this leave one (summed) chain
+    int attn_split4 = 1;       // split attention path: 4-wave score blocks, P.V split over dim quarters
     int attn_prompt = 1;       // prompt waves of >= 64 rows: flash-form MFMA kernel (1) or one-row kernels (0)
 };
 
@@ -134,6 +135,7 @@ struct AttnArgs {
     int T;                 // rows per lane (a lane's rows are consecutive; MTP verify: k + 1)
     const float* inv_freq; // [32] f32 rope inverse frequencies
     int prompt_flash;      // KernelForms::attn_prompt of the calling engine
+    int split4;            // KernelForms::attn_split4: split path in 4-wave score / dim-split P.V blocks
 };
 hipError_t launch_attn_prep(const AttnArgs& a, hipStream_t st);   // q/k norm + rope, cache append
 hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st);   // scores, softmax, P.V, gate

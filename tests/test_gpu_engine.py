@@ -367,3 +367,31 @@ def test_seeded_state_decode(oracle_weights, P):
             assert np.abs(S[gi] - f.rec[l].numpy()).max() <= 2e-2
     st.close()
     e.close()
+
+
+def test_split_attention_forms_identical(eng):
+    """The split attention path in 4-wave score blocks and dim-quarter P.V blocks gives the
+    bits of the one-wave score / 256-thread P.V kernels: a 40-token prompt wave (rows > 1:
+    attn_prep + scores), decode steps (prep folded into the scores) past a 128-slot part
+    boundary, and an MTP round (3-row verify) -- tokens, logits and state."""
+    from oracle.weights import lane_prompt_ids
+    from qwen35 import State
+    ids = lane_prompt_ids(91, 0, 40)
+    res = {}
+    for mode in (0, 1):
+        eng.set_option("attn_split4", mode)
+        st = State(eng, 1, 512, mtp_k=2, mtp_cap=64)
+        y, lg0 = st.prefill(0, ids, logits=True)
+        toks, lgs = [int(y)], [lg0]
+        for _ in range(100):
+            out, lg = st.decode_step([toks[-1]], logits=True)
+            toks.append(int(out[0]))
+            lgs.append(lg[0])
+        em = st.mtp_round([toks[-1]], 2)
+        res[mode] = (toks, lgs, em, st.read(0, "S"), st.read(0, "k", 140))
+        st.close()
+    eng.set_option("attn_split4", 1)
+    assert res[0][0] == res[1][0] and res[0][2] == res[1][2]
+    for a, b in zip(res[0][1], res[1][1]):
+        assert np.array_equal(a, b)
+    assert np.array_equal(res[0][3], res[1][3]) and np.array_equal(res[0][4], res[1][4])
