@@ -18,7 +18,10 @@ SRC = PKG / "csrc"
 OUT = PKG / "libqwen35.so"
 BUILD = PKG / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",
+# -ffp-contract=off: a * b + c stays two roundings unless a kernel asks for fmaf, so the
+# reduction trees and updates written with __fmul_rn / __fadd_rn (plain operators in HIP) round
+# the same way in every kernel that shares them
+FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I", str(SRC), "-I", str(PKG.parent / "include")]
 # MFMA accumulators in architectural VGPRs: without it the compiler keeps loop-carried

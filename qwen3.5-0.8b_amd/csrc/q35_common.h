@@ -106,6 +106,15 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// The delta rule's state update s + k * dv with the product rounded before the add, as the
+// reference's torch path forms S + k (x) dv (speccheck/specimpl.py:287-294). HIP's __fmul_rn /
+// __fadd_rn are plain operators that the compiler may fuse into one FMA; contraction is off
+// here, so every kernel that updates or replays a state row gets the same two roundings.
+__device__ __forceinline__ float delta_update(float s, float k, float dv) {
+#pragma clang fp contract(off)
+    return s + k * dv;
+}
+
 // ---------------------------------------------------------------- 1024-wide RMSNorm pieces
 // The zero-centred RMSNorm's reduction tree, written once so every kernel that normalises a
 // hidden row (the add+norm kernel, the GEMM A-producer) gives identical bits: element

@@ -91,7 +91,17 @@ struct q35_state {
     uint16_t *kc = nullptr, *vc = nullptr;    // [lanes][6][2][cap][256]
     uint16_t *mkc = nullptr, *mvc = nullptr;  // [lanes][2][mtp_cap][256]
     uint16_t* hlast = nullptr;                // [lanes][1024] post-final-norm row of the last body
-    std::vector<int> prefix, mtp_len, cur;
+    // MTP verify factors (GdnArgs): [lanes][2 sets][18][mtp_k + 1 rows][16 heads][kFacStride]
+    float* fac = nullptr;
+    // per lane: GDN state slot `cur`, conv window slot `wcur`, pending verify rows applied on
+    // top of slot cur (`pend`, from factor set `pset`)
+    std::vector<int> prefix, mtp_len, cur, wcur, pend, pset;
+    long long fac_row() const { return (long long)kHv * kFacStride; }
+    long long fac_layer() const { return (long long)(mtp_k + 1) * fac_row(); }
+    long long fac_set() const { return (long long)kGdnLayers * fac_layer(); }
+    long long fac_lane() const { return 2 * fac_set(); }
+    // the per-row encoding of a lane's pending rows (GdnArgs::pend)
+    int pend_code(int l) const { return pend[l] | (pset[l] << 4); }
     long long S_lane() const { return (long long)nslots * kGdnLayers * kSLayer; }
     long long W_lane() const { return (long long)nslots * kGdnLayers * 18432; }
     long long kv_lane() const { return (long long)kAttnLayers * 2 * capT * 256; }
@@ -124,14 +134,14 @@ struct q35_engine {
     float *o, *q, *sc, *stats, *part, *pval, *inv_freq;
     float* kpart;
     uint16_t* prod;
-    int *pidx, *tok_dev, *rlane, *rpos, *rslot, *rcur, *ridx_src, *ridx_dst, *din = nullptr;
+    int *pidx, *tok_dev, *rlane, *rpos, *rslot, *rcur, *rwcur, *rpend, *ridx_src, *ridx_dst, *din = nullptr;
     int sc_ld = 0, max_chunks = 0;
     float* logits_dev = nullptr;
     int logits_rows = 0;
     float* topv_dev = nullptr;       // [R] the argmax's logit value per row (all-rows prefill)
     std::map<std::string, hipGraphExec_t> graphs;   // captured decode steps
     // pinned staging
-    int *h_tok, *h_lane, *h_pos, *h_slot, *h_rcur, *h_out, *h_src, *h_dst, *hin = nullptr;
+    int *h_tok, *h_lane, *h_pos, *h_slot, *h_rcur, *h_rwcur, *h_rpend, *h_out, *h_src, *h_dst, *hin = nullptr;
     // Row metadata on the device (token, lane, position, slot, the state slot of the row's lane, row indices)
     // changes only by the uploads below, which bump meta_epoch, and by a decode step, which
     // advances positions, slots and `cur` on the device and leaves its sampled tokens in the
@@ -141,7 +151,7 @@ struct q35_engine {
     // seed, lane copy, restore, MTP rounds, allocation and release) bumps meta_epoch too.
     uint64_t meta_epoch = 0, fast_epoch = ~0ull;
     const void* fast_s = nullptr;
-    std::vector<int> fast_lanes, fast_prefix, fast_cur, fast_tok;
+    std::vector<int> fast_lanes, fast_prefix, fast_cur, fast_wcur, fast_tok;
 };
 
 namespace {
@@ -380,16 +390,19 @@ void alloc_scratch(q35_engine* e) {
     e->gcdec = dalloc<float>((size_t)((R + 63) / 64) * kHv);
     e->prod = dalloc<uint16_t>(R * kFF);
     // row metadata: one device block and one pinned host block,
-    // [tok|lane|pos|slot|cur|src|dst] with stride R, so a step's inputs go up in a single copy;
-    // `cur` is the GDN state slot of the row's lane (read together with the lane, so the GDN
-    // kernels' state addresses wait for one load, not two dependent ones)
-    e->din = dalloc<int>(7 * (size_t)R);
-    e->hin = halloc<int>(7 * (size_t)R);
-    int* d[7];
-    int* hh[7];
-    for (int i = 0; i < 7; ++i) { d[i] = e->din + (size_t)i * R; hh[i] = e->hin + (size_t)i * R; }
-    e->tok_dev = d[0]; e->rlane = d[1]; e->rpos = d[2]; e->rslot = d[3]; e->rcur = d[4]; e->ridx_src = d[5]; e->ridx_dst = d[6];
-    e->h_tok = hh[0]; e->h_lane = hh[1]; e->h_pos = hh[2]; e->h_slot = hh[3]; e->h_rcur = hh[4]; e->h_src = hh[5]; e->h_dst = hh[6];
+    // [tok|lane|pos|slot|cur|wcur|pend|src|dst] with stride R, so a step's inputs go up in a
+    // single copy; cur / wcur / pend are the GDN state slot, window slot and pending verify
+    // rows of the row's lane (read together with the lane, so the GDN kernels' addresses wait
+    // for one load, not two dependent ones)
+    e->din = dalloc<int>(9 * (size_t)R);
+    e->hin = halloc<int>(9 * (size_t)R);
+    int* d[9];
+    int* hh[9];
+    for (int i = 0; i < 9; ++i) { d[i] = e->din + (size_t)i * R; hh[i] = e->hin + (size_t)i * R; }
+    e->tok_dev = d[0]; e->rlane = d[1]; e->rpos = d[2]; e->rslot = d[3]; e->rcur = d[4]; e->rwcur = d[5];
+    e->rpend = d[6]; e->ridx_src = d[7]; e->ridx_dst = d[8];
+    e->h_tok = hh[0]; e->h_lane = hh[1]; e->h_pos = hh[2]; e->h_slot = hh[3]; e->h_rcur = hh[4]; e->h_rwcur = hh[5];
+    e->h_rpend = hh[6]; e->h_src = hh[7]; e->h_dst = hh[8];
     e->h_out = halloc<int>(R);
     // rope inverse frequencies, f32 as the oracle forms them (specimpl.py:151-156):
     // inv_i = 1 / f32(theta ** f32(2i/64))
@@ -423,16 +436,47 @@ void upload_meta(q35_engine* e, int upto, int n) {
     ++e->meta_epoch;
     HCK(hipMemcpyAsync(e->din, e->hin, ((size_t)upto * e->R + n) * sizeof(int), hipMemcpyHostToDevice, e->st));
 }
-void upload_rows(q35_engine* e, int R) { upload_meta(e, 4, R); }   // tok, lane, pos, slot, cur
+void upload_rows(q35_engine* e, int R) { upload_meta(e, 6, R); }   // tok, lane, pos, slot, cur, wcur, pend
 // src / dst row indices only (tok_dev may hold device-written tokens): one copy
 void upload_idx(q35_engine* e, int n) {
     ++e->meta_epoch;
     HCK(hipMemcpyAsync(e->ridx_src, e->h_src, ((size_t)e->R + n) * sizeof(int), hipMemcpyHostToDevice, e->st));
 }
 
-// Per-row state slots from the lanes' host `cur` (rows staged in h_lane).
+// Per-row state slots and pending rows from the lanes' host values (rows staged in h_lane).
 void stage_rcur(q35_engine* e, q35_state* s, int R) {
-    for (int r = 0; r < R; ++r) e->h_rcur[r] = s->cur[e->h_lane[r]];
+    for (int r = 0; r < R; ++r) {
+        const int l = e->h_lane[r];
+        e->h_rcur[r] = s->cur[l];
+        e->h_rwcur[r] = s->wcur[l];
+        e->h_rpend[r] = s->pend_code(l);
+    }
+}
+
+// After a body without checkpoints over these lanes: both slots advance, nothing pending.
+void advance_lane(q35_state* s, int l) {
+    s->cur[l] = (s->cur[l] + 1) % s->nslots;
+    s->wcur[l] = (s->wcur[l] + 1) % s->nslots;
+    s->pend[l] = 0;
+}
+
+// Applies pending verify rows to the states of these lanes (before host reads, copies and the
+// chunked prompt form, which take a state slot as it stands).
+void materialize(q35_engine* e, q35_state* s, const std::vector<int>& lanes) {
+    std::vector<int> ls;
+    for (int l : lanes)
+        if (s->pend[l] > 0) ls.push_back(l);
+    if (ls.empty()) return;
+    const int n = (int)ls.size();
+    REQ(n <= e->R, Q35_ERR_CAP, "too many lanes to materialize at once");
+    HCK(hipStreamSynchronize(e->st));
+    for (int i = 0; i < n; ++i) { e->h_lane[i] = ls[i]; }
+    stage_rcur(e, s, n);
+    upload_meta(e, 6, n);
+    HCK(launch_gdn_materialize(s->S, s->S_lane(), (long long)kGdnLayers * kSLayer, e->rlane, e->rcur, e->rpend, s->fac,
+                               s->fac_lane(), s->fac_set(), s->fac_layer(), s->fac_row(), s->nslots, n, e->st));
+    HCK(hipStreamSynchronize(e->st));
+    for (int l : ls) { s->cur[l] = (s->cur[l] + 1) % s->nslots; s->pend[l] = 0; }
 }
 
 // Y != nullptr: bf16 store; Y == nullptr: k-block chains to e->kpart (summed by the next
@@ -549,6 +593,16 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt);
 void body(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
     REQ(e->weights_ready, Q35_ERR_STATE, "weights not initialised");
     REQ(R > 0 && R <= e->R, Q35_ERR_CAP, "rows exceed engine max_rows");
+    if (R / T == 1 && e->gdn_chunked && !small_rows(R) && T >= 64 && !ckpt && s->pend[e->h_lane[0]] > 0) {
+        // the chunked prompt form reads a state slot as it stands: apply the pending rows first
+        std::vector<int> keep(e->h_lane, e->h_lane + R), pos(e->h_pos, e->h_pos + R), sl(e->h_slot, e->h_slot + R),
+            tk(e->h_tok, e->h_tok + R);
+        materialize(e, s, {keep[0]});
+        std::copy(keep.begin(), keep.end(), e->h_lane);
+        std::copy(pos.begin(), pos.end(), e->h_pos);
+        std::copy(sl.begin(), sl.end(), e->h_slot);
+        std::copy(tk.begin(), tk.end(), e->h_tok);
+    }
     stage_rcur(e, s, R);
     upload_rows(e, R);
     body_kernels(e, s, R, T, ckpt);
@@ -576,7 +630,12 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
             g.S_layer = (long long)gdn_slot(l) * kSLayer;
             g.win = s->win; g.W_lane = s->W_lane(); g.W_slot = (long long)kGdnLayers * 18432;
             g.W_layer = (long long)gdn_slot(l) * 18432;
-            g.cur = e->rcur; g.nslots = s->nslots; g.ckpt = ckpt ? 1 : 0;
+            g.cur = e->rcur; g.wcur = e->rwcur; g.pend = e->rpend; g.nslots = s->nslots; g.ckpt = ckpt ? 1 : 0;
+            if (s->fac) {
+                g.fac = s->fac + (long long)gdn_slot(l) * s->fac_layer();
+                g.fac_lane = s->fac_lane(); g.fac_set = s->fac_set(); g.fac_row = s->fac_row();
+                g.fac_write = ckpt ? 1 : 0;
+            }
             g.lane = e->rlane; g.T = T; g.nlanes = nl;
             // a prompt wave of one lane: chunked (UT-transform) form
             const bool chunked = e->gdn_chunked && !small && nl == 1 && T >= 64 && !ckpt;
@@ -865,9 +924,13 @@ int q35_state_alloc(q35_engine* e, int lanes, int cap, int mtp_k, int mtp_cap, q
             s->mvc = dalloc<uint16_t>((size_t)lanes * s->mkv_lane());
         }
         s->hlast = dalloc<uint16_t>((size_t)lanes * kHidden);
+        if (mtp_k > 0) s->fac = dalloc<float>((size_t)lanes * s->fac_lane());
         s->prefix.assign(lanes, 0);
         s->mtp_len.assign(lanes, 0);
         s->cur.assign(lanes, 0);
+        s->wcur.assign(lanes, 0);
+        s->pend.assign(lanes, 0);
+        s->pset.assign(lanes, 0);
         // zeroed on the engine stream (non-blocking: a null-stream memset could still be
         // running when the first body's kernels start)
         HCK(hipMemsetAsync(s->S, 0, (size_t)lanes * s->S_lane() * 4, e->st));
@@ -891,7 +954,7 @@ int q35_state_free(q35_engine* e, q35_state* s) {
                 else ++it;
             }
         }
-        void* ds[] = {s->S, s->win, s->kc, s->vc, s->mkc, s->mvc, s->hlast};
+        void* ds[] = {s->S, s->win, s->kc, s->vc, s->mkc, s->mvc, s->hlast, s->fac};
         for (void* p : ds) if (p) hipFree(p);
         delete s;
     });
@@ -907,7 +970,7 @@ int q35_state_reset(q35_engine* e, q35_state* s, const int32_t* lanes, int n) {
             check_lane(s, l);
             HCK(hipMemsetAsync(s->S + l * s->S_lane(), 0, s->S_lane() * 4, e->st));
             HCK(hipMemsetAsync(s->win + l * s->W_lane(), 0, s->W_lane() * 4, e->st));
-            s->prefix[l] = 0; s->mtp_len[l] = 0; s->cur[l] = 0;
+            s->prefix[l] = 0; s->mtp_len[l] = 0; s->cur[l] = 0; s->wcur[l] = 0; s->pend[l] = 0; s->pset[l] = 0;
         }
         HCK(hipStreamSynchronize(e->st));
     });
@@ -931,7 +994,7 @@ int q35_state_seed(q35_engine* e, q35_state* s, uint64_t seed, int prefix_len) {
                     HCK(launch_gen_normal_kv_tiled(stream_key(seed, "state.k." + tag), s1, prefix_len, s->kc + off, e->st));
                     HCK(launch_gen_normal_plain(stream_key(seed, "state.v." + tag), s1, (long long)prefix_len * 256, s->vc + off, e->st));
                 }
-            s->prefix[l] = prefix_len; s->mtp_len[l] = 0; s->cur[l] = 0;
+            s->prefix[l] = prefix_len; s->mtp_len[l] = 0; s->cur[l] = 0; s->wcur[l] = 0; s->pend[l] = 0; s->pset[l] = 0;
         }
         HCK(hipStreamSynchronize(e->st));
     });
@@ -955,11 +1018,12 @@ static void state_io(q35_engine* e, q35_state* s, int lane, int which, int n_slo
         if (write) copy_sync(e, dev, (char*)host + off_bytes, nb, hipMemcpyHostToDevice);
         else copy_sync(e, (char*)host + off_bytes, dev, nb, hipMemcpyDeviceToHost);
     };
-    const int cur = s->cur[lane];
     if (which == 0) {
-        cp(s->S + lane * s->S_lane() + (long long)cur * kGdnLayers * kSLayer, 0, (size_t)kGdnLayers * kSLayer * 4);
+        if (!write) materialize(e, s, {lane});   // the state with its pending verify rows applied
+        cp(s->S + lane * s->S_lane() + (long long)s->cur[lane] * kGdnLayers * kSLayer, 0, (size_t)kGdnLayers * kSLayer * 4);
+        if (write) s->pend[lane] = 0;            // the written state replaces them
     } else if (which == 1) {
-        cp(s->win + lane * s->W_lane() + (long long)cur * kGdnLayers * 18432, 0, (size_t)kGdnLayers * 18432 * 4);
+        cp(s->win + lane * s->W_lane() + (long long)s->wcur[lane] * kGdnLayers * 18432, 0, (size_t)kGdnLayers * 18432 * 4);
     } else if (which >= 2 && which <= 5) {
         // K / V caches: [heads][n_slots][256] bf16 row-major on the host. V is stored that way;
         // K is stored in 16-slot tiles (kv_tiled_offset) and converted here.
@@ -1007,12 +1071,13 @@ static void copy_lane(q35_engine* e, q35_state* src, int sl, q35_state* dst, int
     REQ(P <= dst->cap, Q35_ERR_CAP, "prefix exceeds the destination lane's cache capacity");
     REQ(dst->mtp_cap == 0 || M <= dst->mtp_cap, Q35_ERR_CAP, "MTP cache exceeds the destination's");
     if (src == dst && sl == dl) return;
+    materialize(e, src, {sl});
     auto d2d = [&](void* d, const void* s_, size_t nb) {
         if (nb) HCK(hipMemcpyAsync(d, s_, nb, hipMemcpyDeviceToDevice, e->st));
     };
     const long long sS = (long long)kGdnLayers * kSLayer, sW = (long long)kGdnLayers * 18432;
     d2d(dst->S + dl * dst->S_lane() + dst->cur[dl] * sS, src->S + sl * src->S_lane() + src->cur[sl] * sS, sS * 4);
-    d2d(dst->win + dl * dst->W_lane() + dst->cur[dl] * sW, src->win + sl * src->W_lane() + src->cur[sl] * sW, sW * 4);
+    d2d(dst->win + dl * dst->W_lane() + dst->wcur[dl] * sW, src->win + sl * src->W_lane() + src->wcur[sl] * sW, sW * 4);
     // K: whole 16-slot tiles (the slots past P of the last tile are never read before written)
     const size_t ktile = (size_t)(P + 15) / 16 * 4096 * 2, vrows = (size_t)P * 512;
     for (int a = 0; a < kAttnLayers * 2; ++a) {
@@ -1032,6 +1097,7 @@ static void copy_lane(q35_engine* e, q35_state* src, int sl, q35_state* dst, int
     HCK(hipStreamSynchronize(e->st));
     dst->prefix[dl] = P;
     dst->mtp_len[dl] = Mc;
+    dst->pend[dl] = 0;
 }
 
 // Snapshot blob: a header, then S f32 [18][16][128][128], window f32 [18][3][6144], K and V
@@ -1156,7 +1222,7 @@ void prefill_waves(q35_engine* e, q35_state* s, int lane, const int32_t* ids, in
         }
         body(e, s, T, T, false);
         s->prefix[lane] += T;
-        s->cur[lane] = (s->cur[lane] + 1) % s->nslots;
+        advance_lane(s, lane);
         const uint16_t* normw = small_rows(T) && !b1_partials(e, T, T, false) ? e->final_norm : nullptr;
         if (all_rows) {
             // the body's tokens are consumed: lm_head leaves row r0 + i's id in tok_dev[i]
@@ -1216,18 +1282,19 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
         bool fast = e->fast_s == (const void*)s && e->fast_epoch == e->meta_epoch && (int)e->fast_lanes.size() == n;
         for (int i = 0; fast && i < n; ++i)
             fast = e->fast_lanes[i] == ls[i] && e->fast_tok[i] == tokens[i] &&
-                   e->fast_prefix[i] == s->prefix[ls[i]] && e->fast_cur[i] == s->cur[ls[i]];
+                   e->fast_prefix[i] == s->prefix[ls[i]] && e->fast_cur[i] == s->cur[ls[i]] &&
+                   e->fast_wcur[i] == s->wcur[ls[i]] && s->pend[ls[i]] == 0;
         e->fast_s = nullptr;                 // re-armed only when this step completes
         if (!fast) {
             stage_rcur(e, s, n);
-            upload_meta(e, 6, n);        // tok, lane, pos, slot, cur, src, dst in one copy
+            upload_meta(e, 8, n);        // tok, lane, pos, slot, cur, wcur, pend, src, dst in one copy
         }
         auto step = [&] {
             body_kernels(e, s, n, 1, false);
             lm_head(e, 0, n, out_logits != nullptr,
                     small_rows(n) && !b1_partials(e, n, 1, false) ? e->final_norm : nullptr);
             HCK(launch_copy_rows_advance(e->nrm, e->ridx_src, s->hlast, e->ridx_dst, n, kHidden, e->rpos, e->rslot,
-                                         e->rcur, s->nslots, e->st));
+                                         e->rcur, e->rwcur, e->rpend, s->nslots, e->st));
         };
         if (e->use_graph && e->kprof == 0) {
             if (out_logits) ensure_logits(e, n);
@@ -1255,7 +1322,7 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
         }
         for (int i = 0; i < n; ++i) {
             s->prefix[ls[i]] += 1;
-            s->cur[ls[i]] = (s->cur[ls[i]] + 1) % s->nslots;
+            advance_lane(s, ls[i]);
         }
         HCK(hipMemcpyAsync(e->h_out, e->tok_dev, n * sizeof(int), hipMemcpyDeviceToHost, e->st));
         if (out_logits) HCK(hipMemcpyAsync(out_logits, e->logits_dev, (size_t)n * kVocab * 4, hipMemcpyDeviceToHost, e->st));
@@ -1265,7 +1332,10 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
         e->fast_tok.assign(out_tok, out_tok + n);
         e->fast_prefix.resize(n);
         e->fast_cur.resize(n);
-        for (int i = 0; i < n; ++i) { e->fast_prefix[i] = s->prefix[ls[i]]; e->fast_cur[i] = s->cur[ls[i]]; }
+        e->fast_wcur.resize(n);
+        for (int i = 0; i < n; ++i) {
+            e->fast_prefix[i] = s->prefix[ls[i]]; e->fast_cur[i] = s->cur[ls[i]]; e->fast_wcur[i] = s->wcur[ls[i]];
+        }
         e->fast_epoch = e->meta_epoch;
         e->fast_s = s;
     });
@@ -1359,7 +1429,12 @@ int q35_mtp_round_stop(q35_engine* e, q35_state* s, const int32_t* lanes, int n,
             n_emit[i] = m;
             const int l = ls[i];
             s->prefix[l] = P[i] + a + 1;
-            s->cur[l] = (s->cur[l] + 1 + a) % s->nslots;
+            // the verify body recorded every row as factors on top of slot cur (after moving
+            // the lane's earlier pending rows into slot cur + 1): rows 0..a are now pending
+            if (s->pend[l] > 0) s->cur[l] = (s->cur[l] + 1) % s->nslots;
+            s->pend[l] = a + 1;
+            s->pset[l] ^= 1;
+            s->wcur[l] = (s->wcur[l] + 1 + a) % s->nslots;
             if (a == k) s->mtp_len[l] += k;
             rows[i] = i * T + a;
             if (stats) { stats[0] += k; stats[1] += a; stats[2] += 1; stats[3] += T; }

@@ -10,10 +10,12 @@
 // o = S^T q~. Replaces engine/kernels_gdn.cpp:35-536 (conv, gates, rec) of the reference.
 //
 // The state is never updated in place (the conv window's q/k channels are read by every
-// column-slice block of a head): the state after row t goes to slot (cur + 1 + t) % nslots,
-// for every row when `ckpt` is set (MTP verify candidates), else only the last row's
-// state, to slot (cur + 1) % nslots;
-// the engine advances `cur` after the step.
+// column-slice block of a head): the state after the last row goes to slot (cur + 1) %
+// nslots and the window to slot (wcur + 1) % nslots; with `ckpt` (MTP verify candidates) the
+// window after every row t goes to slot (wcur + 1 + t) % nslots and each row's state update is
+// recorded as factors (gamma, k~, dv) instead of a 1 MiB state per row (GdnArgs: replaying
+// them gives the same bits), so a rollback to row a is "slot cur plus pending rows 0..a".
+// The engine advances the slots after the step.
 //
 // Grid: (lane group, head, column slice). A block owns VC = 128/CS value columns of one
 // head; thread (column group, kg) holds S[kg*KR .. kg*KR+KR) of CW adjacent columns in
@@ -35,6 +37,9 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     const int jc = (tid % CG) * CW, kg = tid / CG;
     const int lane = a.lane[gi * a.T];
     const int cur = a.cur ? a.cur[gi * a.T] : 0;
+    const int wcur = a.wcur ? a.wcur[gi * a.T] : cur;
+    const int pnd = a.pend ? a.pend[gi * a.T] : 0;
+    const int npend = pnd & 15, pset = (pnd >> 4) & 1;
 
     __shared__ float qs[128], ks[128], vs[VC];
     constexpr int NG = 16;            // fixed reduction groups of 8 k-rows, for every CS
@@ -48,7 +53,7 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     float* Sbase = a.S + lane * a.S_lane + a.S_layer + (long long)h * 16384;
     float* Wbase = a.win + lane * a.W_lane + a.W_layer;
     const float* Sin = Sbase + cur * a.S_slot;
-    const float* Win = Wbase + cur * a.W_slot;
+    const float* Win = Wbase + wcur * a.W_slot;
 
     // channels: tid < 128 -> q channel, else k channel; tid < VC also a v channel
     const int cqk = tid < 128 ? h * 128 + tid : 2048 + h * 128 + (tid - 128);
@@ -77,6 +82,39 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
             s[i][0] = v[0]; s[i][CW > 1 ? 1 : 0] = v[1]; s[i][CW > 2 ? 2 : 0] = v[2]; s[i][CW > 3 ? 3 : 0] = v[3];
         } else {
             s[i][0] = p[0];
+        }
+    }
+
+    if (npend) {
+        // the lane's pending rows, replayed with the recurrence's own rounded operations
+        const float* F0 = a.fac + lane * a.fac_lane + pset * a.fac_set + h * kFacStride;
+        for (int p = 0; p < npend; ++p) {
+            const float* F = F0 + p * a.fac_row;
+            const float gp = F[256];
+            float kk[KR], dd[CW];
+#pragma unroll
+            for (int i = 0; i < KR; ++i) kk[i] = F[kg * KR + i];
+#pragma unroll
+            for (int c = 0; c < CW; ++c) dd[c] = F[128 + cs * VC + jc + c];
+#pragma unroll
+            for (int i = 0; i < KR; ++i)
+#pragma unroll
+                for (int c = 0; c < CW; ++c) {
+                    s[i][c] = __fmul_rn(s[i][c], gp);
+                    s[i][c] = delta_update(s[i][c], kk[i], dd[c]);
+                }
+        }
+        if (a.ckpt && a.fac_write) {
+            // the base of this verify's factors: slot cur + 1 (the engine moves `cur` there)
+            float* So = Sbase + ((cur + 1) % a.nslots) * a.S_slot;
+#pragma unroll
+            for (int i = 0; i < KR; ++i) {
+                float* p = So + (kg * KR + i) * 128 + cs * VC + jc;
+                if (CW == 4)
+                    __builtin_nontemporal_store((q35_f32x4){s[i][0], s[i][CW > 1 ? 1 : 0], s[i][CW > 2 ? 2 : 0], s[i][CW > 3 ? 3 : 0]},
+                                                (q35_f32x4*)p);
+                else p[0] = s[i][0];
+            }
         }
     }
 
@@ -145,6 +183,15 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
             for (int i = 0; i < NG; ++i) rj += red_r[i][jc + c];
             dv[c] = __fmul_rn(beta, vs[jc + c] - rj);
         }
+        if (a.ckpt && a.fac_write) {      // row t's factors, into the set not being read
+            float* F = a.fac + lane * a.fac_lane + (1 - pset) * a.fac_set + t * a.fac_row + h * kFacStride;
+            if (kg == 0) {
+#pragma unroll
+                for (int c = 0; c < CW; ++c) F[128 + cs * VC + jc + c] = dv[c];
+            }
+            if (cs == 0 && tid >= 128) F[tid - 128] = ks[tid - 128];
+            if (cs == 0 && tid == 0) F[256] = gam;
+        }
 #pragma unroll
         for (int c = 0; c < CW; ++c)
 #pragma unroll
@@ -152,7 +199,7 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
                 float op = 0.f;
 #pragma unroll
                 for (int i = gq * 8; i < gq * 8 + 8; ++i) {
-                    s[i][c] = __fadd_rn(s[i][c], __fmul_rn(ks[kg * KR + i], dv[c]));
+                    s[i][c] = delta_update(s[i][c], ks[kg * KR + i], dv[c]);
                     op = fmaf(qs[kg * KR + i], s[i][c], op);
                 }
                 red_o[kg * GPT + gq][jc + c] = op;
@@ -180,7 +227,7 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
                 a.y[(size_t)r * 2048 + h * 128 + tid] = f2bf(__fmul_rn(__fmul_rn(w, __fmul_rn(ohead[tid], rs)), silu_f(z)));
             }
         }
-        if (a.ckpt || t == a.T - 1) {
+        if ((a.ckpt && !a.fac_write) || (!a.ckpt && t == a.T - 1)) {
             const int slot = (cur + 1 + (a.ckpt ? t : 0)) % a.nslots;
             float* So = Sbase + slot * a.S_slot;
 #pragma unroll
@@ -191,7 +238,9 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
                                                 (q35_f32x4*)p);
                 else p[0] = s[i][0];
             }
-            float* Wo = Wbase + slot * a.W_slot;
+        }
+        if (a.ckpt || t == a.T - 1) {
+            float* Wo = Wbase + ((wcur + 1 + (a.ckpt ? t : 0)) % a.nslots) * a.W_slot;
             if (cs == 0) { Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2; }
             if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
         }
@@ -233,9 +282,12 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         const int gi = item >> 4, h = item & 15;
         const int lane = a.lane[gi];
         const int cur = a.cur ? a.cur[gi] : 0;
+        const int wcur = a.wcur ? a.wcur[gi] : cur;
+        const int pnd = a.pend ? a.pend[gi] : 0;
+        const int npend = pnd & 15, pset = (pnd >> 4) & 1;
         float* Sbase = a.S + lane * a.S_lane + a.S_layer + (long long)h * 16384;
         float* Wbase = a.win + lane * a.W_lane + a.W_layer;
-        const float* Win = Wbase + cur * a.W_slot;
+        const float* Win = Wbase + wcur * a.W_slot;
         const uint16_t* pr = a.proj + (size_t)gi * kGdnInRows;
         const int cqk = tid < 128 ? h * 128 + tid : 2048 + h * 128 + (tid - 128);
         const int cv = 4096 + h * 128 + tid;
@@ -266,6 +318,26 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (item + gridDim.x < nitems) prefetch(item + gridDim.x);
+        if (npend) {
+            // the lane's pending rows (gdn_kernel's replay, this block's thread mapping)
+            const float* F0 = a.fac + lane * a.fac_lane + pset * a.fac_set + h * kFacStride;
+            for (int p = 0; p < npend; ++p) {
+                const float* F = F0 + p * a.fac_row;
+                const float gp = F[256];
+                float kk[KR], dd[CW];
+#pragma unroll
+                for (int i = 0; i < KR; ++i) kk[i] = F[kg * KR + i];
+#pragma unroll
+                for (int c = 0; c < CW; ++c) dd[c] = F[128 + jc + c];
+#pragma unroll
+                for (int i = 0; i < KR; ++i)
+#pragma unroll
+                    for (int c = 0; c < CW; ++c) {
+                        s[i][c] = __fmul_rn(s[i][c], gp);
+                        s[i][c] = delta_update(s[i][c], kk[i], dd[c]);
+                    }
+            }
+        }
         cw[0] = __uint_as_float(cpk.x << 16); cw[1] = __uint_as_float(cpk.x & 0xffff0000u);
         cw[2] = __uint_as_float(cpk.y << 16); cw[3] = __uint_as_float(cpk.y & 0xffff0000u);
         cvw[0] = __uint_as_float(dpk.x << 16); cvw[1] = __uint_as_float(dpk.x & 0xffff0000u);
@@ -331,7 +403,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                 float op = 0.f;
 #pragma unroll
                 for (int i = gq * 8; i < gq * 8 + 8; ++i) {
-                    s[i][c] = __fadd_rn(s[i][c], __fmul_rn(ks[kg * KR + i], dv[c]));
+                    s[i][c] = delta_update(s[i][c], ks[kg * KR + i], dv[c]);
                     op = fmaf(qs[kg * KR + i], s[i][c], op);
                 }
                 red[kg * GPT + gq][jc + c] = op;
@@ -362,11 +434,50 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         for (int i = 0; i < KR; ++i)
             __builtin_nontemporal_store((q35_f32x4){s[i][0], s[i][1], s[i][2], s[i][3]},
                                         (q35_f32x4*)(So + (kg * KR + i) * 128 + jc));
-        float* Wo = Wbase + slot * a.W_slot;
+        float* Wo = Wbase + ((wcur + 1) % a.nslots) * a.W_slot;
         Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2;
         if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
         __syncthreads();          // LDS scratch (qs, ks, red, ohead) is reused by the next item
     }
+}
+
+// Pending rows applied to a lane's state of every layer: block (row, layer, head), thread
+// (k row tid / 2, value columns 64 (tid % 2) .. +64), the replay of gdn_kernel.
+__global__ void __launch_bounds__(256) gdn_materialize(float* S, long long S_lane, long long S_slot, const int* lanes,
+                                                       const int* curs, const int* pends, const float* fac,
+                                                       long long fac_lane, long long fac_set, long long fac_layer,
+                                                       long long fac_row, int nslots) {
+    const int r = blockIdx.x, l = blockIdx.y, h = blockIdx.z, tid = threadIdx.x;
+    const int pnd = pends[r], npend = pnd & 15, pset = (pnd >> 4) & 1;
+    if (!npend) return;
+    const int lane = lanes[r], cur = curs[r];
+    const int i = tid >> 1, c0 = (tid & 1) * 64;
+    const float* Sin = S + lane * S_lane + cur * S_slot + (long long)l * kSLayer + (long long)h * 16384 + i * 128 + c0;
+    float* So = S + lane * S_lane + ((cur + 1) % nslots) * S_slot + (long long)l * kSLayer + (long long)h * 16384 + i * 128 + c0;
+    float v[64];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) *(q35_f32x4*)&v[4 * q] = *(const q35_f32x4*)(Sin + 4 * q);
+    const float* F0 = fac + lane * fac_lane + pset * fac_set + l * fac_layer + h * kFacStride;
+    for (int p = 0; p < npend; ++p) {
+        const float* F = F0 + p * fac_row;
+        const float gp = F[256], kk = F[i];
+#pragma unroll
+        for (int c = 0; c < 64; ++c) {
+            v[c] = __fmul_rn(v[c], gp);
+            v[c] = delta_update(v[c], kk, F[128 + c0 + c]);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) *(q35_f32x4*)(So + 4 * q) = *(const q35_f32x4*)&v[4 * q];
+}
+
+hipError_t launch_gdn_materialize(float* S, long long S_lane, long long S_slot, const int* lane, const int* cur,
+                                  const int* pend, const float* fac, long long fac_lane, long long fac_set,
+                                  long long fac_layer, long long fac_row, int nslots, int n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(gdn_materialize, dim3(n, kGdnLayers, kHv), dim3(256), 0, st, S, S_lane, S_slot, lane, cur,
+                       pend, fac, fac_lane, fac_set, fac_layer, fac_row, nslots);
+    return hipGetLastError();
 }
 
 hipError_t gdn_init() {

@@ -18,7 +18,8 @@
 //                   on v_mfma_f32_16x16x4_f32 (f32 products, f32 accumulate). The value columns
 //                   of the delta rule never mix, so 8 slices per head run independently.
 //
-// The state is read from slot cur and written to slot (cur + 1) % nslots, the conv window
+// The state is read from slot cur and written to slot (cur + 1) % nslots (no rows pending:
+// the engine applies them first), the conv window, from slot wcur to (wcur + 1) % nslots,
 // likewise, exactly as the recurrent kernel does for a wave without checkpoints.
 #include <type_traits>
 
@@ -53,7 +54,8 @@ __global__ void __launch_bounds__(256) gdn_chunk_conv(GdnArgs a) {
     const int n = min(kConvRows, a.T - t0);
     const int lane = a.lane[0];
     const int cur = a.cur ? a.cur[0] : 0;
-    const float* Win = a.win + lane * a.W_lane + a.W_layer + cur * a.W_slot;
+    const int wcur = a.wcur ? a.wcur[0] : cur;
+    const float* Win = a.win + lane * a.W_lane + a.W_layer + wcur * a.W_slot;
     const uint2 cpk = *(const uint2*)(a.conv_w + (size_t)ch * 4);
     const float cw0 = __uint_as_float(cpk.x << 16), cw1 = __uint_as_float(cpk.x & 0xffff0000u);
     const float cw2 = __uint_as_float(cpk.y << 16), cw3 = __uint_as_float(cpk.y & 0xffff0000u);
@@ -77,7 +79,7 @@ __global__ void __launch_bounds__(256) gdn_chunk_conv(GdnArgs a) {
         }
     }
     if (t0 + kConvRows >= a.T) {      // the run holding the wave's last row: window after the wave
-        float* Wo = a.win + lane * a.W_lane + a.W_layer + ((cur + 1) % a.nslots) * a.W_slot;
+        float* Wo = a.win + lane * a.W_lane + a.W_layer + ((wcur + 1) % a.nslots) * a.W_slot;
         Wo[ch] = w0; Wo[6144 + ch] = w1; Wo[12288 + ch] = w2;
     }
 }

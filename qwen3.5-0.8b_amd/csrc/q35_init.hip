@@ -118,7 +118,7 @@ __global__ void copy_rows_kernel(const uint16_t* src, const int* src_rows, uint1
 // sampled token is already in place: the argmax writes it to the token row)
 __global__ void copy_rows_advance_kernel(const uint16_t* src, const int* src_rows, uint16_t* dst,
                                          const int* dst_rows, int width, int* pos, int* slot,
-                                         int* cur, int nslots) {
+                                         int* cur, int* wcur, int* pend, int nslots) {
     const int i = blockIdx.x;
     const uint16_t* s = src + (size_t)src_rows[i] * width;
     uint16_t* d = dst + (size_t)dst_rows[i] * width;
@@ -127,14 +127,17 @@ __global__ void copy_rows_advance_kernel(const uint16_t* src, const int* src_row
         pos[i] += 1;
         slot[i] += 1;
         cur[i] = (cur[i] + 1) % nslots;
+        wcur[i] = (wcur[i] + 1) % nslots;
+        pend[i] = 0;
     }
 }
 
 hipError_t launch_copy_rows_advance(const uint16_t* src, const int* src_rows, uint16_t* dst, const int* dst_rows,
-                                    int n, int width, int* pos, int* slot, int* cur, int nslots, hipStream_t st) {
+                                    int n, int width, int* pos, int* slot, int* cur, int* wcur, int* pend, int nslots,
+                                    hipStream_t st) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(copy_rows_advance_kernel, dim3(n), dim3(256), 0, st, src, src_rows, dst, dst_rows, width,
-                       pos, slot, cur, nslots);
+                       pos, slot, cur, wcur, pend, nslots);
     return hipGetLastError();
 }
 

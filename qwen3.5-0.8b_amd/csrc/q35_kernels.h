@@ -88,10 +88,25 @@ struct GdnArgs {
     long long S_lane, S_slot, S_layer;
     float* win;
     long long W_lane, W_slot, W_layer;
-    const int* cur;            // [R] current state slot of each row's lane (null: slot 0)
+    const int* cur;            // [R] state slot of each row's lane (null: slot 0)
+    const int* wcur;           // [R] conv window slot of each row's lane (null: = cur)
     int nslots;
-    int ckpt;                  // 0: state after the last row -> slot (cur + 1) % nslots;
-                               // 1: state after row t -> slot (cur + 1 + t) % nslots
+    int ckpt;                  // 0: state after the last row -> slot (cur + 1) % nslots, window
+                               //    -> slot (wcur + 1) % nslots;
+                               // 1: window after row t -> slot (wcur + 1 + t) % nslots, and the
+                               //    state after every row as factors (below) if fac_write, else
+                               //    the state after row t -> slot (cur + 1 + t) % nslots
+    // Pending rank-1 updates (MTP verify rows): the state of a lane is the one in slot `cur`
+    // followed by its pending rows p = 0 .. n-1, each S = e^g S; S += k~ dv^T with the
+    // recorded f32 (gamma, k~, dv) -- the same two rounded operations as the recurrence, so
+    // replaying them gives the verify kernel's bits. pend[r] = n | (set << 4); fac points at
+    // this layer's factors of lane 0, set 0, row 0: [lane][set][layer][row][head][kFacStride].
+    const int* pend;           // [R] (null: none pending)
+    float* fac;
+    long long fac_lane, fac_set, fac_row;
+    int fac_write;             // ckpt: write row t's factors into set 1 - (pending set), keep no
+                               // per-row state; a lane with pending rows first has them
+                               // applied and the result stored to slot (cur + 1) % nslots
     const int* lane;           // [R] state lane of each row
     int T;                     // rows per lane (rows of one lane are consecutive)
     int nlanes;
@@ -114,6 +129,13 @@ size_t gdn_chunk_ws_floats(int max_rows);
 // as launch_gdn(a, 1, st), with the next item's state prefetched into LDS.
 hipError_t launch_gdn_persist(const GdnArgs& a, hipStream_t st);
 hipError_t gdn_init();     // one-time kernel attribute setup
+constexpr int kFacStride = 264;   // per (row, head): k~ [128] | dv [128] | gamma | pad
+// Applies the pending rows of n lanes to their states: for each row r < n (lanes lane[r],
+// slots cur[r], pend[r] as in GdnArgs), every GDN layer's state in slot cur -> slot (cur + 1)
+// % nslots. fac points at lane 0, set 0, layer 0, row 0; fac_layer is the layer stride.
+hipError_t launch_gdn_materialize(float* S, long long S_lane, long long S_slot, const int* lane, const int* cur,
+                                  const int* pend, const float* fac, long long fac_lane, long long fac_set,
+                                  long long fac_layer, long long fac_row, int nslots, int n, hipStream_t st);
 
 struct AttnArgs {
     const uint16_t* proj;  // [R][5120]: (q|gate) x 8 heads interleaved, k, v
@@ -155,8 +177,10 @@ hipError_t launch_tile(const uint16_t* src, int N, int K, uint16_t* dst, int row
 hipError_t launch_copy_rows(const uint16_t* src, const int* src_rows, uint16_t* dst, const int* dst_rows,
                             int n, int width, hipStream_t st);
 // The decode step's last kernel: copy rows src -> dst and advance each row's position, cache
-// slot and state slot (cur) for the next step of the same lanes.
+// slot, state and window slots (cur, wcur) for the next step of the same lanes; nothing is
+// pending after a step (pend = 0).
 hipError_t launch_copy_rows_advance(const uint16_t* src, const int* src_rows, uint16_t* dst, const int* dst_rows,
-                                    int n, int width, int* pos, int* slot, int* cur, int nslots, hipStream_t st);
+                                    int n, int width, int* pos, int* slot, int* cur, int* wcur, int* pend, int nslots,
+                                    hipStream_t st);
 
 }  // namespace q35

@@ -7,8 +7,9 @@ settings: norm factors +4 / +4 (picks repeat: whole rounds accepted) and -4 / -4
 target's picks alternate). Checked per lane against a plain State fed the same tokens one
 step at a time: every emitted token is the plain step's argmax, and after the rounds the
 GDN state S, the conv window and the K/V rows of both states are bit-identical (the verify
-rows and the kept state slot are those of plain steps: the rollback picked the right
-slot and prefix)."""
+rows and the kept state are those of plain steps: the rollback kept the right pending rows,
+window slot and prefix), also after a 70-token prompt wave (the chunked form, which first
+applies the lane's pending verify rows to its state)."""
 import numpy as np
 import pytest
 
@@ -62,6 +63,12 @@ def test_mtp_rounds_with_accepts_match_plain_steps():
                         assert got == e[j], (bits, r, i, j)
                     cur[i] = e[-1]
                     assert spec.prefix_len(i) == plain.prefix_len(i)
+            # a prompt wave of >= 64 rows takes the chunked form, which reads a state slot as
+            # it stands: lanes with verify rows still pending are brought up to date first
+            for i in (0, 3):
+                ids = lane_prompt_ids(70 + i, 1, 70)
+                assert spec.prefill(i, ids) == plain.prefill(i, ids), (bits, i)
+                cur[i] = None
             for i in range(lanes):
                 P = plain.prefix_len(i)
                 for which in ("S", "win"):
