@@ -427,16 +427,21 @@ __global__ void __launch_bounds__(256) attn_combine(AttnArgs a) {
     const int r = blockIdx.x, qh = blockIdx.y, tid = threadIdx.x;
     const int nparts = a.rm.slot[r] / kPart + 1;
     const float* pp = a.part + ((size_t)r * a.max_chunks * 2 * kNq + qh) * 256 + tid;
+    const uint16_t graw = a.proj[(size_t)r * kAttnInRows + qh * 512 + 256 + tid];
     float acc = 0.f;
-    for (int c0 = 0; c0 < nparts; c0 += 8) {
-        float v[8];
+    // 40 parts per round (a 5,120-slot context in one), all loads issued before the adds:
+    // unconditional from clamped part indices, so no branch makes the compiler wait per load
+    for (int c0 = 0; c0 < nparts; c0 += 40) {
+        float v[40];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = c0 + u < nparts ? pp[(size_t)(c0 + u) * kNq * 256] : 0.f;
+        for (int u = 0; u < 40; ++u) v[u] = pp[(size_t)min(c0 + u, nparts - 1) * kNq * 256];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < 40; ++u)
             if (c0 + u < nparts) acc += v[u];
     }
-    a.out[(size_t)r * 2048 + qh * 256 + tid] = gated_out(a, r, qh, tid, acc);
+    const float o = rbf(acc);
+    const float g = rbf(sigmoid_f(bf2f(graw)));
+    a.out[(size_t)r * 2048 + qh * 256 + tid] = f2bf(o * g);
 }
 
 // ---------------------------------------------------------------- split path, 4-wave blocks
@@ -587,20 +592,41 @@ __global__ void __launch_bounds__(64) attn_pv4(AttnArgs a) {
     const float* stats = a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 8;
     const size_t sst = (size_t)a.max_chunks * 8;
     const int nsl = slot / 64 + 1;
+    // slices tid and tid + 64 held in registers (up to 128 slices, an 8,192-slot context),
+    // the rest re-read in the second pass; unconditional clamped loads, masked values
     float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    for (int i = tid; i < nsl; i += 64) {
-        float v[4];
+    float sm0[4][2], se0[4][2];
 #pragma unroll
-        for (int h = 0; h < 4; ++h) v[h] = stats[h * sst + 2 * i];
+    for (int u = 0; u < 2; ++u) {
+        const int i = min(tid + 64 * u, nsl - 1);
+        const bool ok = tid + 64 * u < nsl;
 #pragma unroll
-        for (int h = 0; h < 4; ++h) m[h] = fmaxf(m[h], v[h]);
+        for (int h = 0; h < 4; ++h) {
+            const float2 v = *(const float2*)(stats + h * sst + 2 * i);
+            sm0[h][u] = ok ? v.x : -INFINITY;
+            se0[h][u] = v.y;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) m[h] = fmaxf(m[h], sm0[h][u]);
+    for (int i = tid + 128; i < nsl; i += 64) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h) m[h] = fmaxf(m[h], stats[h * sst + 2 * i]);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1)
 #pragma unroll
         for (int h = 0; h < 4; ++h) m[h] = fmaxf(m[h], __shfl_xor(m[h], o, 64));
     float l[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int i = tid; i < nsl; i += 64) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+        if (tid + 64 * u < nsl) {
+#pragma unroll
+            for (int h = 0; h < 4; ++h) l[h] += se0[h][u] * expf(sm0[h][u] - m[h]);
+        }
+    for (int i = tid + 128; i < nsl; i += 64) {
         float sm[4], se[4];
 #pragma unroll
         for (int h = 0; h < 4; ++h) { sm[h] = stats[h * sst + 2 * i]; se[h] = stats[h * sst + 2 * i + 1]; }
