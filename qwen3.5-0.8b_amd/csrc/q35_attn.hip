@@ -101,19 +101,24 @@ __device__ __forceinline__ void load_q_frags(const AttnArgs& a, int r, int j, ui
 // K fragments of sub-tile st of 64-slot slice q for this lane: K tile 4q + st of the tiled
 // cache, step s = one contiguous KiB (the tile index is clamped to `slot`'s tile; slots past
 // `slot` are masked later).
+// NT: nontemporal loads (streamed once: one row per lane); cached when the lane's several rows
+// (MTP verify rows) read the same K/V from L2 in consecutive blocks.
+template <bool NT = true>
 __device__ __forceinline__ void load_k_sub(const AttnArgs& a, int lrow, int j, int q, int st, int slot,
                                            q35_u32x4* kf) {
     const int lane = threadIdx.x & 63;
     const int tile = min(q * 4 + st, slot >> 4);
     const uint16_t* kp = a.kc + lrow * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256 + (size_t)tile * 4096 + lane * 8;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) kf[s] = __builtin_nontemporal_load((const q35_u32x4*)(kp + s * 512));
+    for (int s = 0; s < 8; ++s)
+        kf[s] = NT ? __builtin_nontemporal_load((const q35_u32x4*)(kp + s * 512)) : *(const q35_u32x4*)(kp + s * 512);
 }
 
+template <bool NT = true>
 __device__ __forceinline__ void load_k_slice(const AttnArgs& a, int lrow, int j, int q, int slot,
                                              q35_u32x4 (*kf)[8]) {
 #pragma unroll
-    for (int st = 0; st < 4; ++st) load_k_sub(a, lrow, j, q, st, slot, kf[st]);
+    for (int st = 0; st < 4; ++st) load_k_sub<NT>(a, lrow, j, q, st, slot, kf[st]);
 }
 
 // Scores of the 64-slot slice q (slots q*64 .. +64, masked beyond `slot`) by one wave.
@@ -123,7 +128,7 @@ __device__ __forceinline__ void load_k_slice(const AttnArgs& a, int lrow, int j,
 // refilled with slice qnext's as soon as its MFMA chain has consumed them (unconditionally:
 // past the end every lane reloads row `slot`, so the wait counts stay exact and the loads
 // stay in flight across iterations).
-template <bool REFILL>
+template <bool REFILL, bool NT = true>
 __device__ __forceinline__ void score_slice(const AttnArgs& a, int lrow, int j, int q, int slot,
                                             const q35_u32x4* qf, q35_u32x4 (*kf)[8], int qnext,
                                             float* dst, size_t dst_stride, float* stats, size_t stats_stride) {
@@ -137,7 +142,7 @@ __device__ __forceinline__ void score_slice(const AttnArgs& a, int lrow, int j, 
 #pragma unroll
         for (int s = 0; s < 8; ++s)
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&kf[st][s], *(const q35_bf16x8*)&qf[s], acc, 0, 0, 0);
-        if (REFILL) load_k_sub(a, lrow, j, qnext, st, slot, kf[st]);
+        if (REFILL) load_k_sub<NT>(a, lrow, j, qnext, st, slot, kf[st]);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const float lo = row_down4(acc[rr]);   // lanes n < 4 add the q_lo column n + 4
@@ -316,23 +321,25 @@ __device__ __forceinline__ void softmax_ml(const float* stats, size_t stats_stri
 // of the row's scores (head stride s_stride); ml must be ready. Contains barriers.
 // V row u of this thread's 16-slot group in part pc (zero beyond `slot`; the load itself is
 // unconditional, from row min(t, slot), so no branch splits the wait counts).
+template <bool NT = true>
 __device__ __forceinline__ q35_u32x4 load_v(const AttnArgs& a, int lrow, int j, int pc, int u, int slot) {
     const int tid = threadIdx.x, dg = tid & 31, tg = tid >> 5;
     const int t = pc * kPart + tg * 16 + u;
     const uint16_t* vp = a.vc + lrow * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + min(t, slot)) * 256 + dg * 8;
-    const q35_u32x4 v = __builtin_nontemporal_load((const q35_u32x4*)vp);
+    const q35_u32x4 v = NT ? __builtin_nontemporal_load((const q35_u32x4*)vp) : *(const q35_u32x4*)vp;
     const uint32_t keep = t <= slot ? 0xffffffffu : 0u;
     return (q35_u32x4){v[0] & keep, v[1] & keep, v[2] & keep, v[3] & keep};
 }
 
+template <bool NT = true>
 __device__ __forceinline__ void load_v_part(const AttnArgs& a, int lrow, int j, int pc, int slot, q35_u32x4* vv) {
 #pragma unroll
-    for (int u = 0; u < 16; ++u) vv[u] = load_v(a, lrow, j, pc, u, slot);
+    for (int u = 0; u < 16; ++u) vv[u] = load_v<NT>(a, lrow, j, pc, u, slot);
 }
 
 // vv holds part pc's V rows on entry; with REFILL each row register is refilled with part
 // pnext's as soon as it has been used (unconditionally, as for the K fragments).
-template <bool REFILL>
+template <bool REFILL, bool NT = true>
 __device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int pc, int slot,
                                         q35_u32x4* vv, int pnext,
                                         const float* scores, size_t s_stride, float (*ml)[2],
@@ -369,7 +376,7 @@ __device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int 
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i][e] = fmaf(pp[i], v, acc[i][e]);
         }
-        if (REFILL) vv[u] = load_v(a, lrow, j, pnext, u, slot);
+        if (REFILL) vv[u] = load_v<NT>(a, lrow, j, pnext, u, slot);
     }
     // slot groups 2w and 2w+1 live in wave w (lanes 0-31 and 32-63): add in group order
 #pragma unroll
@@ -680,6 +687,7 @@ __global__ void __launch_bounds__(64) attn_pv4(AttnArgs a) {
 // Batched lanes: one block per (row, kv head) runs every chunk's scores into LDS, the
 // softmax, every part's P.V and the gated sum -- the same device functions and orders as the
 // split kernels, without the score / stats / partial round trips through HBM.
+template <bool NT>
 __global__ void __launch_bounds__(256) attn_fused(AttnArgs a, int lds_slots) {
     extern __shared__ float fl[];
     float* scl = fl;                                    // [4][lds_slots]
@@ -711,19 +719,19 @@ __global__ void __launch_bounds__(256) attn_fused(AttnArgs a, int lds_slots) {
     {
         const int wv = tid >> 6;
         q35_u32x4 kf[4][8];
-        load_k_slice(a, lrow, j, wv, slot, kf);
+        load_k_slice<NT>(a, lrow, j, wv, slot, kf);
         load_q_frags(a, r, j, qb, qf);
         for (int c = 0; c < nch; ++c)    // wave wv takes slices 4c + wv
-            score_slice<true>(a, lrow, j, 4 * c + wv, slot, qf, kf, 4 * (c + 1) + wv, scl, lds_slots, stl, sst);
+            score_slice<true, NT>(a, lrow, j, 4 * c + wv, slot, qf, kf, 4 * (c + 1) + wv, scl, lds_slots, stl, sst);
     }
     __syncthreads();
     q35_u32x4 vv[16];
-    load_v_part(a, lrow, j, 0, slot, vv);
+    load_v_part<NT>(a, lrow, j, 0, slot, vv);
     softmax_ml(stl, sst, slot / 64 + 1, ml);
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     for (int pc = 0; pc < nparts; ++pc) {
         float out[4];
-        pv_part<true>(a, lrow, j, pc, slot, vv, pc + 1, scl, lds_slots, ml, p, red, out);
+        pv_part<true, NT>(a, lrow, j, pc, slot, vv, pc + 1, scl, lds_slots, ml, p, red, out);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] += out[i];
     }
@@ -984,7 +992,9 @@ __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
 }
 
 hipError_t attn_init() {
-    const hipError_t e = hipFuncSetAttribute((const void*)attn_fused, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+    hipError_t e = hipFuncSetAttribute((const void*)attn_fused<true>, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+    if (e != hipSuccess) return e;
+    e = hipFuncSetAttribute((const void*)attn_fused<false>, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
     if (e != hipSuccess) return e;
     return hipFuncSetAttribute((const void*)attn_prompt, hipFuncAttributeMaxDynamicSharedMemorySize, kPrLds);
 }
@@ -1015,7 +1025,9 @@ hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
         if (a.T < 1 || a.R % a.T) return hipErrorInvalidValue;
         const int pairs = a.R / a.T * kNkv;
         const int nseg = std::max(1, 8 / pairs), seg = (a.T + nseg - 1) / nseg;
-        hipLaunchKernelGGL(attn_fused, dim3((pairs * nseg + 7) / 8 * seg * 8), dim3(256), lds, st, a, lds_slots);
+        const dim3 grid((pairs * nseg + 7) / 8 * seg * 8);
+        if (a.T == 1) hipLaunchKernelGGL(attn_fused<true>, grid, dim3(256), lds, st, a, lds_slots);
+        else hipLaunchKernelGGL(attn_fused<false>, grid, dim3(256), lds, st, a, lds_slots);
     } else {
         if (a.split4) {
             if (prep_in_scores(a))
