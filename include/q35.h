@@ -208,7 +208,10 @@ int q35_kprof_read(q35_engine* e, float* total_ms, int* launches);
  * column tiles per block of the one-row norm GEMVs), "gemm_pre" (batched K = 1024 GEMMs issue
  * all loads up front), "lmhead_persist" (persistent lm_head at batched lanes), "partial_rows"
  * (>= 17: batched out/o/down GEMMs with at least this many rows sum their k-block chains in
- * the block, one chain for the add+norm; default 1,024). Not bit-identical, a different
+ * the block, one chain for the add+norm; default 1,024), "attn_split4" (split attention path
+ * in 4-wave score blocks and dim-quarter P.V blocks), "gdn_defer" (0 .. 4, default 3: a decode
+ * step keeps each lane's GDN state update as pending factors for up to this many steps and
+ * writes the state with the next one; 0 writes it every step). Not bit-identical, a different
  * rounding point within the stated tolerance: "attn_prompt" (1: prompt waves of one lane with
  * >= 64 rows use the flash-form MFMA attention kernel, 0: the one-row kernels). */
 int q35_set_option(q35_engine* e, const char* name, int value);

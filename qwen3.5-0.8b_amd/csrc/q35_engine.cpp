@@ -91,13 +91,14 @@ struct q35_state {
     uint16_t *kc = nullptr, *vc = nullptr;    // [lanes][6][2][cap][256]
     uint16_t *mkc = nullptr, *mvc = nullptr;  // [lanes][2][mtp_cap][256]
     uint16_t* hlast = nullptr;                // [lanes][1024] post-final-norm row of the last body
-    // MTP verify factors (GdnArgs): [lanes][2 sets][18][mtp_k + 1 rows][16 heads][kFacStride]
+    // GDN state updates kept as factors (GdnArgs), MTP verify rows and deferred decode rows:
+    // [lanes][2 sets][18][max(mtp_k + 1, kMaxDefer) rows][16 heads][kFacStride]
     float* fac = nullptr;
-    // per lane: GDN state slot `cur`, conv window slot `wcur`, pending verify rows applied on
-    // top of slot cur (`pend`, from factor set `pset`)
+    // per lane: GDN state slot `cur`, conv window slot `wcur`, pending rows applied on top of
+    // slot cur (`pend`, from factor set `pset`)
     std::vector<int> prefix, mtp_len, cur, wcur, pend, pset;
     long long fac_row() const { return (long long)kHv * kFacStride; }
-    long long fac_layer() const { return (long long)(mtp_k + 1) * fac_row(); }
+    long long fac_layer() const { return (long long)std::max(mtp_k + 1, kMaxDefer) * fac_row(); }
     long long fac_set() const { return (long long)kGdnLayers * fac_layer(); }
     long long fac_lane() const { return 2 * fac_set(); }
     // the per-row encoding of a lane's pending rows (GdnArgs::pend)
@@ -151,7 +152,7 @@ struct q35_engine {
     // seed, lane copy, restore, MTP rounds, allocation and release) bumps meta_epoch too.
     uint64_t meta_epoch = 0, fast_epoch = ~0ull;
     const void* fast_s = nullptr;
-    std::vector<int> fast_lanes, fast_prefix, fast_cur, fast_wcur, fast_tok;
+    std::vector<int> fast_lanes, fast_prefix, fast_cur, fast_wcur, fast_pend, fast_tok;
 };
 
 namespace {
@@ -459,6 +460,18 @@ void advance_lane(q35_state* s, int l) {
     s->wcur[l] = (s->wcur[l] + 1) % s->nslots;
     s->pend[l] = 0;
 }
+// After a decode step run with `defer` (the host side of copy_rows_advance_kernel): a lane
+// with fewer than `defer` pending rows gained one (its state slot stays), else its state moved.
+void advance_decode(q35_state* s, int l, int defer) {
+    if (s->pend[l] < defer) {
+        s->pend[l] += 1;
+        s->wcur[l] = (s->wcur[l] + 1) % s->nslots;
+    } else {
+        advance_lane(s, l);
+    }
+}
+// The deferral depth of a decode step (GdnArgs::defer), bounded by the factor rows per set.
+int step_defer(const q35_engine* e) { return std::min(std::max(e->forms.gdn_defer, 0), kMaxDefer); }
 
 // Applies pending verify rows to the states of these lanes (before host reads, copies and the
 // chunked prompt form, which take a state slot as it stands).
@@ -588,7 +601,7 @@ void finish_norm(q35_engine* e, int R, const uint16_t* nw, uint16_t* out) {
 
 // Runs the 24-layer body over R = nl * T rows (rows of one lane consecutive) and leaves the
 // final-normed rows in e->nrm. ckpt: write the GDN state after every row (MTP verify).
-void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt);
+void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt, int defer = 0);
 
 void body(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
     REQ(e->weights_ready, Q35_ERR_STATE, "weights not initialised");
@@ -608,8 +621,9 @@ void body(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
     body_kernels(e, s, R, T, ckpt);
 }
 
-// The launches of one body pass (no host transfers: capturable in a hipGraph).
-void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
+// The launches of one body pass (no host transfers: capturable in a hipGraph). defer: a
+// decode step's GDN deferral depth (T = 1, no checkpoints; GdnArgs::defer).
+void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt, int defer) {
     const int nl = R / T;
     const int cs = nl <= 8 ? 8 : nl <= 32 ? 4 : nl <= 64 ? 2 : 1;
     const bool small = small_rows(R);
@@ -631,11 +645,10 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt) {
             g.win = s->win; g.W_lane = s->W_lane(); g.W_slot = (long long)kGdnLayers * 18432;
             g.W_layer = (long long)gdn_slot(l) * 18432;
             g.cur = e->rcur; g.wcur = e->rwcur; g.pend = e->rpend; g.nslots = s->nslots; g.ckpt = ckpt ? 1 : 0;
-            if (s->fac) {
-                g.fac = s->fac + (long long)gdn_slot(l) * s->fac_layer();
-                g.fac_lane = s->fac_lane(); g.fac_set = s->fac_set(); g.fac_row = s->fac_row();
-                g.fac_write = ckpt ? 1 : 0;
-            }
+            g.fac = s->fac + (long long)gdn_slot(l) * s->fac_layer();
+            g.fac_lane = s->fac_lane(); g.fac_set = s->fac_set(); g.fac_row = s->fac_row();
+            g.fac_write = ckpt ? 1 : 0;
+            g.defer = T == 1 && !ckpt ? defer : 0;
             g.lane = e->rlane; g.T = T; g.nlanes = nl;
             // a prompt wave of one lane: chunked (UT-transform) form
             const bool chunked = e->gdn_chunked && !small && nl == 1 && T >= 64 && !ckpt;
@@ -909,7 +922,8 @@ int q35_state_alloc(q35_engine* e, int lanes, int cap, int mtp_k, int mtp_cap, q
     return guard([&] {
         if (e) ++e->meta_epoch;           // a state buffer may reuse a freed address
         REQ(e && out, Q35_ERR_ARG, "null argument");
-        REQ(lanes > 0 && cap > 0 && mtp_k >= 0 && mtp_k <= 4 && mtp_cap >= 0, Q35_ERR_ARG, "bad state shape");
+        REQ(lanes > 0 && lanes <= 65535 && cap > 0 && mtp_k >= 0 && mtp_k <= 4 && mtp_cap >= 0, Q35_ERR_ARG,
+            "bad state shape");
         REQ(cap <= e->max_ctx && mtp_cap <= e->max_ctx, Q35_ERR_CAP, "cap exceeds engine max_ctx");
         auto* s = new q35_state();
         s->lanes = lanes; s->cap = cap; s->mtp_cap = mtp_cap; s->mtp_k = mtp_k;
@@ -924,7 +938,7 @@ int q35_state_alloc(q35_engine* e, int lanes, int cap, int mtp_k, int mtp_cap, q
             s->mvc = dalloc<uint16_t>((size_t)lanes * s->mkv_lane());
         }
         s->hlast = dalloc<uint16_t>((size_t)lanes * kHidden);
-        if (mtp_k > 0) s->fac = dalloc<float>((size_t)lanes * s->fac_lane());
+        s->fac = dalloc<float>((size_t)lanes * s->fac_lane());
         s->prefix.assign(lanes, 0);
         s->mtp_len.assign(lanes, 0);
         s->cur.assign(lanes, 0);
@@ -1283,23 +1297,24 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
         for (int i = 0; fast && i < n; ++i)
             fast = e->fast_lanes[i] == ls[i] && e->fast_tok[i] == tokens[i] &&
                    e->fast_prefix[i] == s->prefix[ls[i]] && e->fast_cur[i] == s->cur[ls[i]] &&
-                   e->fast_wcur[i] == s->wcur[ls[i]] && s->pend[ls[i]] == 0;
+                   e->fast_wcur[i] == s->wcur[ls[i]] && e->fast_pend[i] == s->pend_code(ls[i]);
         e->fast_s = nullptr;                 // re-armed only when this step completes
         if (!fast) {
             stage_rcur(e, s, n);
             upload_meta(e, 8, n);        // tok, lane, pos, slot, cur, wcur, pend, src, dst in one copy
         }
+        const int defer = step_defer(e);
         auto step = [&] {
-            body_kernels(e, s, n, 1, false);
+            body_kernels(e, s, n, 1, false, defer);
             lm_head(e, 0, n, out_logits != nullptr,
                     small_rows(n) && !b1_partials(e, n, 1, false) ? e->final_norm : nullptr);
             HCK(launch_copy_rows_advance(e->nrm, e->ridx_src, s->hlast, e->ridx_dst, n, kHidden, e->rpos, e->rslot,
-                                         e->rcur, e->rwcur, e->rpend, s->nslots, e->st));
+                                         e->rcur, e->rwcur, e->rpend, s->nslots, defer, e->st));
         };
         if (e->use_graph && e->kprof == 0) {
             if (out_logits) ensure_logits(e, n);
             char key[128];
-            std::snprintf(key, sizeof key, "dec:%p:%d:%d:%d", (void*)s, n, out_logits ? 1 : 0, e->n_layers);
+            std::snprintf(key, sizeof key, "dec:%p:%d:%d:%d:%d", (void*)s, n, out_logits ? 1 : 0, e->n_layers, defer);
             auto it = e->graphs.find(key);
             if (it == e->graphs.end()) {
                 hipGraph_t g;
@@ -1322,7 +1337,7 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
         }
         for (int i = 0; i < n; ++i) {
             s->prefix[ls[i]] += 1;
-            advance_lane(s, ls[i]);
+            advance_decode(s, ls[i], defer);
         }
         HCK(hipMemcpyAsync(e->h_out, e->tok_dev, n * sizeof(int), hipMemcpyDeviceToHost, e->st));
         if (out_logits) HCK(hipMemcpyAsync(out_logits, e->logits_dev, (size_t)n * kVocab * 4, hipMemcpyDeviceToHost, e->st));
@@ -1333,8 +1348,10 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
         e->fast_prefix.resize(n);
         e->fast_cur.resize(n);
         e->fast_wcur.resize(n);
+        e->fast_pend.resize(n);
         for (int i = 0; i < n; ++i) {
             e->fast_prefix[i] = s->prefix[ls[i]]; e->fast_cur[i] = s->cur[ls[i]]; e->fast_wcur[i] = s->wcur[ls[i]];
+            e->fast_pend[i] = s->pend_code(ls[i]);
         }
         e->fast_epoch = e->meta_epoch;
         e->fast_s = s;
@@ -1617,10 +1634,11 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             HCK(hipStreamSynchronize(e->st));
             e->gdn_chunked = value ? 1 : 0;
         } else if (n == "b1_partials" || n == "attn_prompt" || n == "partial_rows" || n == "gemv_tpb" ||
-                   n == "gemm_pre" || n == "lmhead_persist" || n == "attn_split4") {
+                   n == "gemm_pre" || n == "lmhead_persist" || n == "attn_split4" || n == "gdn_defer") {
             // kernel-form switches of this engine: captured steps hold the old forms
             REQ(n != "partial_rows" || value >= 17, Q35_ERR_ARG, "partial_rows must exceed the 16-row batch-1 path");
             REQ(n != "gemv_tpb" || value == 1 || value == 2, Q35_ERR_ARG, "gemv_tpb is 1 or 2");
+            REQ(n != "gdn_defer" || (value >= 0 && value <= kMaxDefer), Q35_ERR_ARG, "gdn_defer is 0 .. 4");
             HCK(hipStreamSynchronize(e->st));
             if (n == "b1_partials") e->b1_partials = value ? 1 : 0;
             else if (n == "attn_prompt") e->forms.attn_prompt = value ? 1 : 0;
@@ -1628,6 +1646,7 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             else if (n == "gemv_tpb") e->forms.gemv_tpb = value;
             else if (n == "gemm_pre") e->forms.gemm_pre = value ? 1 : 0;
             else if (n == "attn_split4") e->forms.attn_split4 = value ? 1 : 0;
+            else if (n == "gdn_defer") e->forms.gdn_defer = value;
             else e->forms.lmhead_persist = value ? 1 : 0;
             for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
             e->graphs.clear();

@@ -15,6 +15,9 @@
 // window after every row t goes to slot (wcur + 1 + t) % nslots and each row's state update is
 // recorded as factors (gamma, k~, dv) instead of a 1 MiB state per row (GdnArgs: replaying
 // them gives the same bits), so a rollback to row a is "slot cur plus pending rows 0..a".
+// A decode step with `defer` records a lane's row the same way (row n of the set being read,
+// when fewer than `defer` rows are pending) and leaves slot cur as it is, so the 1 MiB state
+// of a lane is written once every defer + 1 steps and read every step.
 // The engine advances the slots after the step.
 //
 // Grid: (lane group, head, column slice). A block owns VC = 128/CS value columns of one
@@ -40,6 +43,7 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     const int wcur = a.wcur ? a.wcur[gi * a.T] : cur;
     const int pnd = a.pend ? a.pend[gi * a.T] : 0;
     const int npend = pnd & 15, pset = (pnd >> 4) & 1;
+    const bool rec = !a.ckpt && npend < a.defer;    // this decode row becomes pending row npend
 
     __shared__ float qs[128], ks[128], vs[VC];
     constexpr int NG = 16;            // fixed reduction groups of 8 k-rows, for every CS
@@ -183,8 +187,11 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
             for (int i = 0; i < NG; ++i) rj += red_r[i][jc + c];
             dv[c] = __fmul_rn(beta, vs[jc + c] - rj);
         }
-        if (a.ckpt && a.fac_write) {      // row t's factors, into the set not being read
-            float* F = a.fac + lane * a.fac_lane + (1 - pset) * a.fac_set + t * a.fac_row + h * kFacStride;
+        if ((a.ckpt && a.fac_write) || rec) {
+            // verify row t's factors, into the set not being read; a deferred decode row's as
+            // row npend of the set being read (rows 0 .. npend-1 are the ones replayed)
+            float* F = a.fac + lane * a.fac_lane + (rec ? pset : 1 - pset) * a.fac_set + (rec ? npend : t) * a.fac_row +
+                       h * kFacStride;
             if (kg == 0) {
 #pragma unroll
                 for (int c = 0; c < CW; ++c) F[128 + cs * VC + jc + c] = dv[c];
@@ -227,7 +234,7 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
                 a.y[(size_t)r * 2048 + h * 128 + tid] = f2bf(__fmul_rn(__fmul_rn(w, __fmul_rn(ohead[tid], rs)), silu_f(z)));
             }
         }
-        if ((a.ckpt && !a.fac_write) || (!a.ckpt && t == a.T - 1)) {
+        if ((a.ckpt && !a.fac_write) || (!a.ckpt && t == a.T - 1 && !rec)) {
             const int slot = (cur + 1 + (a.ckpt ? t : 0)) % a.nslots;
             float* So = Sbase + slot * a.S_slot;
 #pragma unroll
@@ -250,11 +257,21 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
 
 // Persistent form of gdn_kernel<1> for one decode row per lane (T = 1, no checkpoints):
 // each block walks (row, head) items gi*16 + h = blockIdx.x, + gridDim.x, ...; while item i
-// computes, item i+1's 64 KiB state streams into LDS with global_load_lds (no VGPRs), so
-// the CU's memory pipe stays busy through the compute phases. Per item the loads of its own
-// operands are issued before the next item's prefetch, so waiting for them never waits for
-// the prefetch (the vector memory counter completes in order). Same thread mapping and
-// arithmetic, statement for statement, as gdn_kernel<1> with T = 1.
+// computes, everything item i+1 reads is already in flight: its 64 KiB state and its pending
+// factor rows stream into LDS with global_load_lds (no VGPRs), its conv window, conv taps,
+// projection row and gates into registers. The items' row metadata (lane, slots, pending
+// rows) is read once, at the start, into LDS. So an item waits on memory once, at its top,
+// for loads issued a whole item earlier (and for the previous item's stores, which the same
+// counter tracks). All of those loads are unconditional (clamped indices): a load under a
+// branch would make the compiler wait for it where the branch joins. Same thread mapping
+// and arithmetic, statement for statement, as gdn_kernel<1> with T = 1.
+// A block barrier for LDS traffic only: __syncthreads() also orders global memory, for which
+// the compiler makes every wave wait for all of its outstanding loads first, including the
+// next item's prefetch, which would then never overlap an item's compute.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+constexpr int kPersistMaxItems = 128;      // items per block: rows <= 4,096 at 512 blocks
+
 __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     constexpr int VC = 128, CW = 4, CG = 32, KR = 16, NG = 16, GPT = 2;
     const int tid = threadIdx.x, lane64 = tid & 63, wv = tid >> 6;
@@ -266,50 +283,87 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     __shared__ float gate_s[2];
     __shared__ float ohead[128];
     __shared__ float hss2[2];
-    auto prefetch = [&](int item) {
-        const int gi = item >> 4, h = item & 15;
+    // the item's pending factor rows (row p at p * kFacStride); 5 KiB, so that two blocks
+    // (2 x 64 KiB of state) still fit a CU
+    __shared__ __attribute__((aligned(16))) float fbuf[kMaxPend * kFacStride];
+    // item k's row metadata: lane | cur << 16 | wcur << 20 | pend code << 24
+    __shared__ int meta[kPersistMaxItems];
+    const int nk = (nitems - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    for (int k = tid; k < nk; k += 256) {
+        const int gi = ((int)blockIdx.x + k * (int)gridDim.x) >> 4;
         const int ln = a.lane[gi];
         const int cu = a.cur ? a.cur[gi] : 0;
+        const int wc = a.wcur ? a.wcur[gi] : cu;
+        const int pn = a.pend ? a.pend[gi] : 0;
+        meta[k] = ln | (cu << 16) | (wc << 20) | (pn << 24);
+    }
+    __syncthreads();
+
+    // per-item operands in registers (loaded one item ahead; bf16 kept as raw bits until use,
+    // so no conversion makes the compiler wait for a load in the fetch)
+    const bool hasv = tid < VC;
+    struct Ops {
+        float w0, w1, w2, v0, v1, v2;
+        uint16_t x, xv, zz, gw, bb, aa, alog, dtb;
+        uint2 cpk, dpk;
+    };
+    const uint16_t* gnw = a.gnorm ? a.gnorm : a.dt_bias;   // any valid address when unused
+    auto fetch = [&](int k, Ops& o) {
+        const int item = (int)blockIdx.x + k * (int)gridDim.x;
+        const int gi = item >> 4, h = item & 15;
+        const int m = meta[k];
+        const int ln = m & 0xffff, cu = (m >> 16) & 15, wc = (m >> 20) & 15, pn = (m >> 24) & 31;
         const float* Sin = a.S + ln * a.S_lane + a.S_layer + (long long)h * 16384 + cu * a.S_slot;
 #pragma unroll
         for (int i = 0; i < KR; ++i)
             __builtin_amdgcn_global_load_lds((const void*)(Sin + (kg * KR + i) * 128 + jc),
                                              (__attribute__((address_space(3))) void*)(sbuf + (wv * KR + i) * 64), 16, 0, 0);
-    };
-    int item = blockIdx.x;
-    if (item < nitems) prefetch(item);
-    for (; item < nitems; item += gridDim.x) {
-        const int gi = item >> 4, h = item & 15;
-        const int lane = a.lane[gi];
-        const int cur = a.cur ? a.cur[gi] : 0;
-        const int wcur = a.wcur ? a.wcur[gi] : cur;
-        const int pnd = a.pend ? a.pend[gi] : 0;
-        const int npend = pnd & 15, pset = (pnd >> 4) & 1;
-        float* Sbase = a.S + lane * a.S_lane + a.S_layer + (long long)h * 16384;
-        float* Wbase = a.win + lane * a.W_lane + a.W_layer;
-        const float* Win = Wbase + wcur * a.W_slot;
+        // factor rows 0 .. npend-1: 16-byte chunk c = 66 p + q of row p, chunks tid, tid + 256
+        const int nc = (pn & 15) * (kFacStride / 4);
+        const float* F0 = a.fac + ln * a.fac_lane + ((pn >> 4) & 1) * a.fac_set + h * kFacStride;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int c = tid + 256 * u;
+            if (c < nc) {
+                const int p = c / (kFacStride / 4), q = c % (kFacStride / 4);
+                __builtin_amdgcn_global_load_lds((const void*)(F0 + p * a.fac_row + 4 * q),
+                                                 (__attribute__((address_space(3))) void*)(fbuf + 1024 * u + wv * 256),
+                                                 16, 0, 0);
+            }
+        }
+        const float* Win = a.win + ln * a.W_lane + a.W_layer + wc * a.W_slot;
         const uint16_t* pr = a.proj + (size_t)gi * kGdnInRows;
         const int cqk = tid < 128 ? h * 128 + tid : 2048 + h * 128 + (tid - 128);
+        const int cv = 4096 + h * 128 + (tid & 127);      // threads >= 128 load a valid channel, unused
+        o.w0 = Win[cqk]; o.w1 = Win[6144 + cqk]; o.w2 = Win[12288 + cqk];
+        o.v0 = Win[cv]; o.v1 = Win[6144 + cv]; o.v2 = Win[12288 + cv];
+        o.cpk = *(const uint2*)(a.conv_w + (size_t)cqk * 4);
+        o.dpk = *(const uint2*)(a.conv_w + (size_t)cv * 4);
+        o.x = pr[cqk];
+        o.xv = pr[cv];
+        o.zz = pr[kGdnZOff + h * 128 + (tid & 127)];
+        o.gw = gnw[a.gnorm ? (tid & 127) : 0];
+        o.bb = pr[kGdnBOff + h];
+        o.aa = pr[kGdnAOff + h];
+        o.alog = a.A_log[h];
+        o.dtb = a.dt_bias[h];
+    };
+    Ops nx;
+    if (nk > 0) fetch(0, nx);
+    for (int k = 0; k < nk; ++k) {
+        const int item = (int)blockIdx.x + k * (int)gridDim.x;
+        const int gi = item >> 4, h = item & 15;
+        const int m = meta[k];
+        const int lane = m & 0xffff, cur = (m >> 16) & 15, wcur = (m >> 20) & 15, pnd = (m >> 24) & 31;
+        const int npend = pnd & 15, pset = (pnd >> 4) & 1;
+        const bool rec = npend < a.defer;          // this row becomes pending row npend
+        float* Sbase = a.S + lane * a.S_lane + a.S_layer + (long long)h * 16384;
+        float* Wbase = a.win + lane * a.W_lane + a.W_layer;
+        const int cqk = tid < 128 ? h * 128 + tid : 2048 + h * 128 + (tid - 128);
         const int cv = 4096 + h * 128 + tid;
-        const bool hasv = tid < VC;
-        // this item's operands first
-        float w0 = Win[cqk], w1 = Win[6144 + cqk], w2 = Win[12288 + cqk];
-        float v0 = 0.f, v1 = 0.f, v2 = 0.f;
-        float cw[4], cvw[4] = {0.f, 0.f, 0.f, 0.f};
-        const uint2 cpk = *(const uint2*)(a.conv_w + (size_t)cqk * 4);
-        uint2 dpk = {0u, 0u};
-        float xv = 0.f, zz = 0.f, gw = 0.f;
-        if (hasv) {
-            v0 = Win[cv]; v1 = Win[6144 + cv]; v2 = Win[12288 + cv];
-            dpk = *(const uint2*)(a.conv_w + (size_t)cv * 4);
-            xv = bf2f(pr[cv]);
-            if (a.y) { zz = bf2f(pr[kGdnZOff + h * 128 + tid]); gw = bf2f(a.gnorm[tid]); }
-        }
-        const float x = bf2f(pr[cqk]);
-        float bb = 0.f, aa = 0.f, alog = 0.f;
-        if (tid == 0) { bb = bf2f(pr[kGdnBOff + h]); aa = bf2f(pr[kGdnAOff + h]); alog = bf2f(a.A_log[h]); aa += bf2f(a.dt_bias[h]); }
-        // this item's state: land its prefetch, move it to registers, then prefetch the next
+        // this item's state, factors and operands (issued one item ago)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const Ops op = nx;
         float s[KR][CW];
 #pragma unroll
         for (int i = 0; i < KR; ++i) {
@@ -317,12 +371,11 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
             s[i][0] = v[0]; s[i][1] = v[1]; s[i][2] = v[2]; s[i][3] = v[3];
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (item + gridDim.x < nitems) prefetch(item + gridDim.x);
         if (npend) {
+            lds_barrier();      // every wave's share of the factor rows has landed
             // the lane's pending rows (gdn_kernel's replay, this block's thread mapping)
-            const float* F0 = a.fac + lane * a.fac_lane + pset * a.fac_set + h * kFacStride;
             for (int p = 0; p < npend; ++p) {
-                const float* F = F0 + p * a.fac_row;
+                const float* F = fbuf + p * kFacStride;
                 const float gp = F[256];
                 float kk[KR], dd[CW];
 #pragma unroll
@@ -337,42 +390,52 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                         s[i][c] = delta_update(s[i][c], kk[i], dd[c]);
                     }
             }
+            lds_barrier();      // fbuf is refilled by the next item's fetch
         }
-        cw[0] = __uint_as_float(cpk.x << 16); cw[1] = __uint_as_float(cpk.x & 0xffff0000u);
-        cw[2] = __uint_as_float(cpk.y << 16); cw[3] = __uint_as_float(cpk.y & 0xffff0000u);
-        cvw[0] = __uint_as_float(dpk.x << 16); cvw[1] = __uint_as_float(dpk.x & 0xffff0000u);
-        cvw[2] = __uint_as_float(dpk.y << 16); cvw[3] = __uint_as_float(dpk.y & 0xffff0000u);
-        const float A = -expf(alog);
+        if (k + 1 < nk) fetch(k + 1, nx);
+        float w0 = op.w0, w1 = op.w1, w2 = op.w2, v0 = op.v0, v1 = op.v1, v2 = op.v2;
+        float cw[4], cvw[4];
+        cw[0] = __uint_as_float(op.cpk.x << 16); cw[1] = __uint_as_float(op.cpk.x & 0xffff0000u);
+        cw[2] = __uint_as_float(op.cpk.y << 16); cw[3] = __uint_as_float(op.cpk.y & 0xffff0000u);
+        cvw[0] = __uint_as_float(op.dpk.x << 16); cvw[1] = __uint_as_float(op.dpk.x & 0xffff0000u);
+        cvw[2] = __uint_as_float(op.dpk.y << 16); cvw[3] = __uint_as_float(op.dpk.y & 0xffff0000u);
+        const float A = -expf(bf2f(op.alog));
+        const float ox = bf2f(op.x), oxv = bf2f(op.xv);
         // causal conv: taps over [w0, w1, w2, raw] in order, f32, one rounding, bf16 SiLU
         {
             float u = 0.f;
-            u = u + w0 * cw[0]; u = u + w1 * cw[1]; u = u + w2 * cw[2]; u = u + x * cw[3];
+            u = u + w0 * cw[0]; u = u + w1 * cw[1]; u = u + w2 * cw[2]; u = u + ox * cw[3];
             float uq = rbf(silu_f(rbf(u)));
-            w0 = w1; w1 = w2; w2 = x;
+            w0 = w1; w1 = w2; w2 = ox;
             if (tid < 128) qs[tid] = uq; else ks[tid - 128] = uq;
             if (hasv) {
                 float uv = 0.f;
-                uv = uv + v0 * cvw[0]; uv = uv + v1 * cvw[1]; uv = uv + v2 * cvw[2]; uv = uv + xv * cvw[3];
+                uv = uv + v0 * cvw[0]; uv = uv + v1 * cvw[1]; uv = uv + v2 * cvw[2]; uv = uv + oxv * cvw[3];
                 vs[tid] = rbf(silu_f(rbf(uv)));
-                v0 = v1; v1 = v2; v2 = xv;
+                v0 = v1; v1 = v2; v2 = oxv;
             }
             float ss = wave_sum(uq * uq);
             if ((tid & 63) == 0) wred[tid >> 6] = ss;
             if (tid == 0) {
+                const float aa = bf2f(op.aa) + bf2f(op.dtb);
                 float sp = aa > 20.f ? aa : log1pf(expf(aa));
                 float g = A * sp;
                 gate_s[0] = expf(g);
-                gate_s[1] = sigmoid_f(bb);
+                gate_s[1] = sigmoid_f(bf2f(op.bb));
             }
         }
-        __syncthreads();
+        // the conv window after this row: its values are final now
+        float* Wo = Wbase + ((wcur + 1) % a.nslots) * a.W_slot;
+        Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2;
+        if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
+        lds_barrier();
         {
             const float rq = rsqrtf((wred[0] + wred[1]) + 1e-6f);
             const float rk = rsqrtf((wred[2] + wred[3]) + 1e-6f);
             if (tid < 128) qs[tid] = __fmul_rn(__fmul_rn(qs[tid], rq), 0.08838834764831845f);
             else ks[tid - 128] = __fmul_rn(ks[tid - 128], rk);
         }
-        __syncthreads();
+        lds_barrier();
         const float gam = gate_s[0], beta = gate_s[1];
 #pragma unroll
         for (int c = 0; c < CW; ++c)
@@ -386,7 +449,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                 }
                 red[kg * GPT + gq][jc + c] = rp;
             }
-        __syncthreads();
+        lds_barrier();
         float dv[CW];
 #pragma unroll
         for (int c = 0; c < CW; ++c) {
@@ -395,20 +458,34 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
             for (int i = 0; i < NG; ++i) rj += red[i][jc + c];
             dv[c] = __fmul_rn(beta, vs[jc + c] - rj);
         }
-        __syncthreads();          // red is reused for the o partials
+        if (rec) {                // gdn_kernel's factor record of a deferred row
+            float* F = a.fac + lane * a.fac_lane + pset * a.fac_set + npend * a.fac_row + h * kFacStride;
+            if (kg == 0) *(q35_f32x4*)(F + 128 + jc) = (q35_f32x4){dv[0], dv[1], dv[2], dv[3]};
+            if (tid >= 128) F[tid - 128] = ks[tid - 128];
+            if (tid == 0) F[256] = gam;
+        }
+        lds_barrier();          // red is reused for the o partials
 #pragma unroll
         for (int c = 0; c < CW; ++c)
 #pragma unroll
             for (int gq = 0; gq < GPT; ++gq) {
-                float op = 0.f;
+                float op2 = 0.f;
 #pragma unroll
                 for (int i = gq * 8; i < gq * 8 + 8; ++i) {
                     s[i][c] = delta_update(s[i][c], ks[kg * KR + i], dv[c]);
-                    op = fmaf(qs[kg * KR + i], s[i][c], op);
+                    op2 = fmaf(qs[kg * KR + i], s[i][c], op2);
                 }
-                red[kg * GPT + gq][jc + c] = op;
+                red[kg * GPT + gq][jc + c] = op2;
             }
-        __syncthreads();
+        if (!rec) {
+            const int slot = (cur + 1) % a.nslots;
+            float* So = Sbase + slot * a.S_slot;
+#pragma unroll
+            for (int i = 0; i < KR; ++i)
+                __builtin_nontemporal_store((q35_f32x4){s[i][0], s[i][1], s[i][2], s[i][3]},
+                                            (q35_f32x4*)(So + (kg * KR + i) * 128 + jc));
+        }
+        lds_barrier();
         if (kg == 0) {
 #pragma unroll
             for (int c = 0; c < CW; ++c) {
@@ -420,24 +497,15 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
             }
         }
         if (a.y) {
-            __syncthreads();
+            lds_barrier();
             if (tid < 2) hss2[tid] = half_head_ss_regs(ohead + 64 * tid);
-            __syncthreads();
+            lds_barrier();
             if (tid < 128) {
                 const float rs = head_rsqrt(hss2[0], hss2[1]);
-                a.y[(size_t)gi * 2048 + h * 128 + tid] = f2bf(__fmul_rn(__fmul_rn(gw, __fmul_rn(ohead[tid], rs)), silu_f(zz)));
+                a.y[(size_t)gi * 2048 + h * 128 + tid] = f2bf(__fmul_rn(__fmul_rn(bf2f(op.gw), __fmul_rn(ohead[tid], rs)), silu_f(bf2f(op.zz))));
             }
         }
-        const int slot = (cur + 1) % a.nslots;
-        float* So = Sbase + slot * a.S_slot;
-#pragma unroll
-        for (int i = 0; i < KR; ++i)
-            __builtin_nontemporal_store((q35_f32x4){s[i][0], s[i][1], s[i][2], s[i][3]},
-                                        (q35_f32x4*)(So + (kg * KR + i) * 128 + jc));
-        float* Wo = Wbase + ((wcur + 1) % a.nslots) * a.W_slot;
-        Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2;
-        if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
-        __syncthreads();          // LDS scratch (qs, ks, red, ohead) is reused by the next item
+        lds_barrier();          // LDS scratch (qs, ks, red, ohead) is reused by the next item
     }
 }
 
@@ -488,6 +556,7 @@ hipError_t launch_gdn_persist(const GdnArgs& a, hipStream_t st) {
     if (a.nlanes <= 0 || a.T != 1 || a.ckpt) return hipErrorInvalidValue;
     const int nitems = a.nlanes * kHv;
     const int grid = nitems < 512 ? nitems : 512;      // two blocks per CU
+    if ((nitems + grid - 1) / grid > kPersistMaxItems) return hipErrorInvalidValue;
     hipLaunchKernelGGL(gdn_persist, dim3(grid), dim3(256), 64 * 1024, st, a, nitems);
     return hipGetLastError();
 }

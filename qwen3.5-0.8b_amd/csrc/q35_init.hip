@@ -118,7 +118,7 @@ __global__ void copy_rows_kernel(const uint16_t* src, const int* src_rows, uint1
 // sampled token is already in place: the argmax writes it to the token row)
 __global__ void copy_rows_advance_kernel(const uint16_t* src, const int* src_rows, uint16_t* dst,
                                          const int* dst_rows, int width, int* pos, int* slot,
-                                         int* cur, int* wcur, int* pend, int nslots) {
+                                         int* cur, int* wcur, int* pend, int nslots, int defer) {
     const int i = blockIdx.x;
     const uint16_t* s = src + (size_t)src_rows[i] * width;
     uint16_t* d = dst + (size_t)dst_rows[i] * width;
@@ -126,18 +126,23 @@ __global__ void copy_rows_advance_kernel(const uint16_t* src, const int* src_row
     if (threadIdx.x == 0) {
         pos[i] += 1;
         slot[i] += 1;
-        cur[i] = (cur[i] + 1) % nslots;
+        const int p = pend[i];
+        if ((p & 15) < defer) {
+            pend[i] = p + 1;
+        } else {
+            cur[i] = (cur[i] + 1) % nslots;
+            pend[i] = p & 16;
+        }
         wcur[i] = (wcur[i] + 1) % nslots;
-        pend[i] = 0;
     }
 }
 
 hipError_t launch_copy_rows_advance(const uint16_t* src, const int* src_rows, uint16_t* dst, const int* dst_rows,
                                     int n, int width, int* pos, int* slot, int* cur, int* wcur, int* pend, int nslots,
-                                    hipStream_t st) {
+                                    int defer, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(copy_rows_advance_kernel, dim3(n), dim3(256), 0, st, src, src_rows, dst, dst_rows, width,
-                       pos, slot, cur, wcur, pend, nslots);
+                       pos, slot, cur, wcur, pend, nslots, defer);
     return hipGetLastError();
 }
 

@@ -21,6 +21,8 @@ struct KernelForms {
     int partial_rows = 1024;   // batched kEPartial GEMMs with M >= this leave one (summed) chain
     int attn_split4 = 1;       // split attention path: 4-wave score blocks, P.V split over dim quarters
     int attn_prompt = 1;       // prompt waves of >= 64 rows: flash-form MFMA kernel (1) or one-row kernels (0)
+    int gdn_defer = 3;         // decode steps: a lane's GDN state update is kept as pending factors for up
+                               // to this many steps, the state written on the next (0: every step)
 };
 
 struct GemmArgs {
@@ -107,6 +109,9 @@ struct GdnArgs {
     int fac_write;             // ckpt: write row t's factors into set 1 - (pending set), keep no
                                // per-row state; a lane with pending rows first has them
                                // applied and the result stored to slot (cur + 1) % nslots
+    int defer;                 // decode rows (T = 1, ckpt = 0): a lane with n < defer pending rows
+                               // records this row as pending row n of its own set (factors) and
+                               // keeps slot cur; otherwise its state goes to slot (cur + 1) % nslots
     const int* lane;           // [R] state lane of each row
     int T;                     // rows per lane (rows of one lane are consecutive)
     int nlanes;
@@ -130,6 +135,8 @@ size_t gdn_chunk_ws_floats(int max_rows);
 hipError_t launch_gdn_persist(const GdnArgs& a, hipStream_t st);
 hipError_t gdn_init();     // one-time kernel attribute setup
 constexpr int kFacStride = 264;   // per (row, head): k~ [128] | dv [128] | gamma | pad
+constexpr int kMaxDefer = 4;      // factor rows per set available to deferred decode rows
+constexpr int kMaxPend = 5;       // pending rows a lane can hold (MTP verify: k + 1 <= 5 rows)
 // Applies the pending rows of n lanes to their states: for each row r < n (lanes lane[r],
 // slots cur[r], pend[r] as in GdnArgs), every GDN layer's state in slot cur -> slot (cur + 1)
 // % nslots. fac points at lane 0, set 0, layer 0, row 0; fac_layer is the layer stride.
@@ -177,10 +184,12 @@ hipError_t launch_tile(const uint16_t* src, int N, int K, uint16_t* dst, int row
 hipError_t launch_copy_rows(const uint16_t* src, const int* src_rows, uint16_t* dst, const int* dst_rows,
                             int n, int width, hipStream_t st);
 // The decode step's last kernel: copy rows src -> dst and advance each row's position, cache
-// slot, state and window slots (cur, wcur) for the next step of the same lanes; nothing is
-// pending after a step (pend = 0).
+// slot, state and window slots (cur, wcur) for the next step of the same lanes. With the
+// step's `defer` (GdnArgs::defer) a row with n < defer pending rows keeps cur and has n + 1
+// pending rows after the step; any other row moves cur to the next slot with none pending
+// (the pending set bit is kept).
 hipError_t launch_copy_rows_advance(const uint16_t* src, const int* src_rows, uint16_t* dst, const int* dst_rows,
                                     int n, int width, int* pos, int* slot, int* cur, int* wcur, int* pend, int nslots,
-                                    hipStream_t st);
+                                    int defer, hipStream_t st);
 
 }  // namespace q35
