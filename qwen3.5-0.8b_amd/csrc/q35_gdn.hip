@@ -271,21 +271,24 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 constexpr int kPersistMaxItems = 128;      // items per block: rows <= 4,096 at 512 blocks
+constexpr int kPersistLds = 64 * 1024 + kMaxPend * kFacStride * 4;   // state + factor rows
 
 __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     constexpr int VC = 128, CW = 4, CG = 32, KR = 16, NG = 16, GPT = 2;
     const int tid = threadIdx.x, lane64 = tid & 63, wv = tid >> 6;
     const int jc = (tid % CG) * CW, kg = tid / CG;
-    extern __shared__ q35_f32x4 sbuf[];      // [4 waves][16 rows][64 lanes]: next item's state
+    // Dynamic LDS, the only target of the LDS-DMA prefetch (so the compiler need not make an
+    // access to the static arrays below wait for it): the next item's state [4 waves][16 rows]
+    // [64 lanes], then its pending factor rows (row p at p * kFacStride; 5 KiB, so that two
+    // blocks still fit a CU)
+    extern __shared__ q35_f32x4 sbuf[];
+    float* fbuf = (float*)(sbuf + 4096);
     __shared__ float qs[128], ks[128], vs[VC];
     __shared__ float red[NG][VC];            // r partials, then o partials
     __shared__ float wred[4];
     __shared__ float gate_s[2];
     __shared__ float ohead[128];
     __shared__ float hss2[2];
-    // the item's pending factor rows (row p at p * kFacStride); 5 KiB, so that two blocks
-    // (2 x 64 KiB of state) still fit a CU
-    __shared__ __attribute__((aligned(16))) float fbuf[kMaxPend * kFacStride];
     // item k's row metadata: lane | cur << 16 | wcur << 20 | pend code << 24
     __shared__ int meta[kPersistMaxItems];
     const int nk = (nitems - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
@@ -308,16 +311,23 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         uint2 cpk, dpk;
     };
     const uint16_t* gnw = a.gnorm ? a.gnorm : a.dt_bias;   // any valid address when unused
+    // the next item's state rows 4g .. 4g+3 of this thread (the four groups are issued at four
+    // points of an item's compute, so the memory pipe stays busy through it instead of the
+    // wave stalling on one burst of 16 DMA issues and then leaving the pipe idle)
+    const float* Snext = nullptr;
+    auto fetch_rows = [&](int g) {
+#pragma unroll
+        for (int i = 4 * g; i < 4 * g + 4; ++i)
+            __builtin_amdgcn_global_load_lds((const void*)(Snext + (kg * KR + i) * 128 + jc),
+                                             (__attribute__((address_space(3))) void*)(sbuf + (wv * KR + i) * 64), 16, 0, 0);
+    };
     auto fetch = [&](int k, Ops& o) {
         const int item = (int)blockIdx.x + k * (int)gridDim.x;
         const int gi = item >> 4, h = item & 15;
         const int m = meta[k];
         const int ln = m & 0xffff, cu = (m >> 16) & 15, wc = (m >> 20) & 15, pn = (m >> 24) & 31;
-        const float* Sin = a.S + ln * a.S_lane + a.S_layer + (long long)h * 16384 + cu * a.S_slot;
-#pragma unroll
-        for (int i = 0; i < KR; ++i)
-            __builtin_amdgcn_global_load_lds((const void*)(Sin + (kg * KR + i) * 128 + jc),
-                                             (__attribute__((address_space(3))) void*)(sbuf + (wv * KR + i) * 64), 16, 0, 0);
+        Snext = a.S + ln * a.S_lane + a.S_layer + (long long)h * 16384 + cu * a.S_slot;
+        fetch_rows(0);
         // factor rows 0 .. npend-1: 16-byte chunk c = 66 p + q of row p, chunks tid, tid + 256
         const int nc = (pn & 15) * (kFacStride / 4);
         const float* F0 = a.fac + ln * a.fac_lane + ((pn >> 4) & 1) * a.fac_set + h * kFacStride;
@@ -349,7 +359,10 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         o.dtb = a.dt_bias[h];
     };
     Ops nx;
-    if (nk > 0) fetch(0, nx);
+    if (nk > 0) {
+        fetch(0, nx);
+        fetch_rows(1); fetch_rows(2); fetch_rows(3);
+    }
     for (int k = 0; k < nk; ++k) {
         const int item = (int)blockIdx.x + k * (int)gridDim.x;
         const int gi = item >> 4, h = item & 15;
@@ -392,7 +405,8 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
             }
             lds_barrier();      // fbuf is refilled by the next item's fetch
         }
-        if (k + 1 < nk) fetch(k + 1, nx);
+        const bool more = k + 1 < nk;
+        if (more) fetch(k + 1, nx);
         float w0 = op.w0, w1 = op.w1, w2 = op.w2, v0 = op.v0, v1 = op.v1, v2 = op.v2;
         float cw[4], cvw[4];
         cw[0] = __uint_as_float(op.cpk.x << 16); cw[1] = __uint_as_float(op.cpk.x & 0xffff0000u);
@@ -429,6 +443,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2;
         if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
         lds_barrier();
+        if (more) fetch_rows(1);
         {
             const float rq = rsqrtf((wred[0] + wred[1]) + 1e-6f);
             const float rk = rsqrtf((wred[2] + wred[3]) + 1e-6f);
@@ -450,6 +465,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                 red[kg * GPT + gq][jc + c] = rp;
             }
         lds_barrier();
+        if (more) fetch_rows(2);
         float dv[CW];
 #pragma unroll
         for (int c = 0; c < CW; ++c) {
@@ -465,6 +481,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
             if (tid == 0) F[256] = gam;
         }
         lds_barrier();          // red is reused for the o partials
+        if (more) fetch_rows(3);
 #pragma unroll
         for (int c = 0; c < CW; ++c)
 #pragma unroll
@@ -549,7 +566,7 @@ hipError_t launch_gdn_materialize(float* S, long long S_lane, long long S_slot, 
 }
 
 hipError_t gdn_init() {
-    return hipFuncSetAttribute((const void*)gdn_persist, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+    return hipFuncSetAttribute((const void*)gdn_persist, hipFuncAttributeMaxDynamicSharedMemorySize, kPersistLds);
 }
 
 hipError_t launch_gdn_persist(const GdnArgs& a, hipStream_t st) {
@@ -557,7 +574,7 @@ hipError_t launch_gdn_persist(const GdnArgs& a, hipStream_t st) {
     const int nitems = a.nlanes * kHv;
     const int grid = nitems < 512 ? nitems : 512;      // two blocks per CU
     if ((nitems + grid - 1) / grid > kPersistMaxItems) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gdn_persist, dim3(grid), dim3(256), 64 * 1024, st, a, nitems);
+    hipLaunchKernelGGL(gdn_persist, dim3(grid), dim3(256), kPersistLds, st, a, nitems);
     return hipGetLastError();
 }
 
