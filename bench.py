@@ -28,6 +28,7 @@ WEIGHT_BYTES = 1_504_793_280  # bf16 weights streamed per pass (text tower + tie
 S_BYTES = 18 * 16 * 128 * 128 * 4
 WIN_BYTES = 18 * 3 * 6144 * 4
 KV_BYTES_PER_SLOT = 6 * 2 * 2 * 256 * 2   # K and V, 6 layers, 2 kv heads
+FAC_ROW_BYTES = 16 * 264 * 4              # one pending GDN row of one layer: k~ | dv | gamma per head
 FAM = {"gemm": 1, "lm_head": 2, "gdn": 3, "attn": 4}
 KERNEL_NAMES = {"attn": "attn_fused", "gdn": "gdn_persist", "lm_head": "gemm_lmhead<8, 2> (tied lm_head)",
                 "gemm": "projection / MLP GEMMs"}
@@ -36,21 +37,30 @@ KERNEL_NAMES = {"attn": "attn_fused", "gdn": "gdn_persist", "lm_head": "gemm_lmh
 # the calibration are in the file named by TRAFFIC_SOURCE.
 TRAFFIC_SOURCE = "profiles/hbm_traffic_decode_b256_ctx4096.md"
 MEASURED_TRAFFIC = {
-    ("attn", 256, 4096): (1058422.4 * 2.0 + 1024.0 * 1.0) * 1024,                        # attn_fused
-    ("gdn", 256, 4096): (143107.0 * 2.0 + 283680.9 * 1.0) * 1024,                         # gdn_persist
-    ("lm_head", 256, 4096): (255558.8 * 2.0 + 38848.7 * 1.0) * 1024,                      # gemm_lmhead<8, 2>
+    ("attn", 256, 4096): (1058631.5 * 2.0 + 1024.0 * 1.0) * 1024,                        # attn_fused
+    ("gdn", 256, 4096): (146575.5 * 2.0 + 90254.0 * 1.0) * 1024,    # gdn_persist, gdn_defer 3 (4-step average)
+    ("lm_head", 256, 4096): (256114.4 * 2.0 + 38080.5 * 1.0) * 1024,                      # gemm_lmhead<8, 2>
 }
 
 
-def step_bytes(B: int, L: int) -> int:
+def gdn_lane_layer_bytes(d: int) -> float:
+    """Algorithmic bytes of one lane's GDN layer per decode step, averaged over the deferral
+    cycle of d + 1 steps (engine option gdn_defer = d): the 1 MiB state is read every step and
+    written once per cycle; the steps in between write one pending factor row and read the rows
+    pending before them (d / 2 on average); plus window r+w, qkv/z/b/a in, o (f32) and y (bf16) out."""
+    s = (1 << 20) * (1 + 1 / (d + 1)) + FAC_ROW_BYTES / 16 * (d / 2 + d / (d + 1))
+    return s + 2 * 73728 + 8224 * 2 + 2048 * 4 + 2048 * 2
+
+
+def step_bytes(B: int, L: int, d: int) -> int:
     """Algorithmic HBM bytes of one decode step over B lanes at context L."""
-    return WEIGHT_BYTES + B * (2 * S_BYTES + 2 * WIN_BYTES + KV_BYTES_PER_SLOT * (L + 1))
+    return int(WEIGHT_BYTES + B * (18 * gdn_lane_layer_bytes(d) + KV_BYTES_PER_SLOT * (L + 1)))
 
 
-def family_bytes(fam: str, B: int, L: int) -> int:
+def family_bytes(fam: str, B: int, L: int, d: int = 0) -> int:
     """Algorithmic bytes of all launches of one kernel family in one decode step."""
-    if fam == "gdn":       # per layer: S read+write, window r+w, qkv/a/b in, o out
-        return 18 * B * (2 * (1 << 20) + 2 * 73728 + 6176 * 2 + 2048 * 4)
+    if fam == "gdn":
+        return int(18 * B * gdn_lane_layer_bytes(d))
     if fam == "attn":      # attention core per layer: K and V of L+1 slots, f32 q, bf16 gate in, output
         return 6 * B * (2048 * (L + 1) + 8 * 256 * 4 + 2048 * 2 + 2048 * 2)
     if fam == "lm_head":
@@ -251,6 +261,8 @@ def main():
     ap.add_argument("--prefill-len", type=int, default=4096, help="one-lane prompt prefill length; 0 skips it")
     ap.add_argument("--prefill-rows", type=int, default=2048, help="prompt wave rows (the engine's max_rows)")
     ap.add_argument("--eager", action="store_true", help="launch kernels eagerly (no hipGraph)")
+    ap.add_argument("--gdn-defer", type=int, default=3,
+                    help="engine option gdn_defer: decode steps a GDN state update stays pending (0: written every step)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run one 1 GiB device-to-device torch copy first (counter calibration: "
                          "FETCH_SIZE/WRITE_SIZE of a known-size copy)")
@@ -275,14 +287,15 @@ def main():
                  max_ctx=L + max(args.steps, args.b1_steps, 3 * args.adaptive_turns, 12 * args.mtp_rounds) + args.warmup + 64,
                  seed=0,
                  use_graph=not args.eager)
+    eng.set_option("gdn_defer", args.gdn_defer)
     # timed value: graph replay, no per-kernel events
     wall, ev_s, _ = run_decode(eng, B, L, args.steps, args.warmup, None)
     ms = wall / args.steps * 1e3
     value = B * args.steps / wall
     wall1, ev1, kt1 = run_decode(eng, 1, L, args.b1_steps, args.warmup, None)
     ms1 = wall1 / args.b1_steps * 1e3
-    gbs = step_bytes(B, L) / (ms / 1e3) / 1e9
-    gbs1 = step_bytes(1, L) / (ms1 / 1e3) / 1e9
+    gbs = step_bytes(B, L, args.gdn_defer) / (ms / 1e3) / 1e9
+    gbs1 = step_bytes(1, L, args.gdn_defer) / (ms1 / 1e3) / 1e9
     # kernel rooflines: short eager passes with HIP events around each launch of one family
     rooflines = {}
     fams = [] if args.kprof == "none" else ([args.kprof] if args.kprof != "all" else ["attn", "gdn", "lm_head", "gemm"])
@@ -292,7 +305,7 @@ def main():
             continue
         per_launch_ms = kt[0] / kt[1]
         launches_per_step = kt[1] / args.kprof_steps
-        byt = family_bytes(kp, B, L) / launches_per_step
+        byt = family_bytes(kp, B, L, args.gdn_defer) / launches_per_step
         ach = byt / (per_launch_ms / 1e3) / 1e9
         rooflines[kp] = {"kernel": KERNEL_NAMES[kp], "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK,
                          "unit": "GB/s", "frac": round(ach / HBM_PEAK, 4), "traffic": MEASURED_TRAFFIC.get((kp, B, L)),
@@ -330,12 +343,15 @@ def main():
            "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
            "dtype": "bf16", "data": "synthetic (seeded random-init weights and state)",
            "config": {"workload": f"decode_b{B}_ctx{L}", "model": "Qwen3.5-0.8B text tower", "global_batch": B,
-                      "seq_len": L, "parallelism": "none (1 GPU)"},
+                      "seq_len": L, "parallelism": "none (1 GPU)", "gdn_defer": args.gdn_defer},
            "hbm_gbs_step": round(gbs, 1), "hbm_frac_step": round(gbs / HBM_PEAK, 4),
+           # the same step priced with the state written back every step (gdn_defer 0), as the
+           # reference's decode does: the bytes a non-deferring engine must move for this output
+           "hbm_frac_step_writeback_every_step": round(step_bytes(B, L, 0) / (ms / 1e3) / 1e9 / HBM_PEAK, 4),
            "event_ms_per_step": round(ev_s / args.steps * 1e3, 4),
            "batch1": {"tok_s": round(args.b1_steps / wall1, 2), "ms_per_step": round(ms1, 4),
                       "hbm_gbs": round(gbs1, 1), "hbm_frac": round(gbs1 / HBM_PEAK, 4),
-                      "bytes_per_token": step_bytes(1, L)},
+                      "bytes_per_token": step_bytes(1, L, args.gdn_defer)},
            "mtp_k2": mtp, "prefill": pre, "roofline": roof,
            "kernel_rooflines": {k: v for k, v in rooflines.items() if k != dominant}, "cpu_baseline": cpu}
     print(json.dumps(out))
