@@ -1644,7 +1644,7 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             else if (n == "attn_prompt") e->forms.attn_prompt = value ? 1 : 0;
             else if (n == "partial_rows") e->forms.partial_rows = value;
             else if (n == "gemv_tpb") e->forms.gemv_tpb = value;
-            else if (n == "gemm_pre") e->forms.gemm_pre = value ? 1 : 0;
+            else if (n == "gemm_pre") e->forms.gemm_pre = value;
             else if (n == "attn_split4") e->forms.attn_split4 = value ? 1 : 0;
             else if (n == "gdn_defer") e->forms.gdn_defer = value;
             else e->forms.lmhead_persist = value ? 1 : 0;

@@ -539,13 +539,13 @@ constexpr int kPreKB = kHidden / 256;
 
 template <int MT> constexpr int pre_lds_bytes() { return kPreKB * MT * 8 * 64 * 16; }
 
-template <int EM, int MT>
-__global__ void __launch_bounds__(256) gemm_pre(GemmArgs a) {
+template <int EM, int MT, int NW = 4>
+__global__ void __launch_bounds__(64 * NW) gemm_pre(GemmArgs a) {
     extern __shared__ q35_u32x4 dyn_lds[];
     q35_u32x4(*As)[MT][512] = (q35_u32x4(*)[MT][512])dyn_lds;          // [kb][mt][group * 64 + slot]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    constexpr int NW = 4, HW = 2;
+    constexpr int HW = NW / 2;
     const int mb = (a.M + MT * 16 - 1) / (MT * 16);
     const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
     const int nblk = (idx / mb) * 8 + xcd;
@@ -876,6 +876,17 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
     if ((EM == kEStore || EM == kESiluMul) && a.K == kHidden && a.forms.gemm_pre) {
         // 32-row blocks (64 KiB of A fragments: two blocks per CU); 64-row blocks (128 KiB,
         // one per CU) measured 10-35 % slower
+        // 64 x 128 blocks of 8 waves (one per CU, half the L2 -> CU bytes per output of the
+        // 32 x 64 tiles) when they fill the CUs in one round: gate|up at 256 lanes, 224 blocks,
+        // 16.8 -> 14.8 us in the model (in_proj's 288 blocks take two rounds: 21.7 us against
+        // 17.0; the attention qkv's 160 blocks leave CUs idle: 12.8 against 12.0); form 2 forces
+        // them (tests)
+        const int nb8 = EM == kESiluMul ? (a.N / 32 + 3) / 4 : (a.N / 16 + 7) / 8, mb4 = (a.M + 63) / 64;
+        const int grid8 = (nb8 + 7) / 8 * 8 * mb4;
+        if (a.forms.gemm_pre == 2 || (grid8 <= 256 && 4 * grid8 > 3 * 256)) {
+            hipLaunchKernelGGL((gemm_pre<EM, 4, 8>), dim3(grid8), dim3(512), pre_lds_bytes<4>(), st, a);
+            return;
+        }
         const int mb2 = (a.M + 31) / 32;
         hipLaunchKernelGGL((gemm_pre<EM, 2>), dim3((nb + 7) / 8 * 8 * mb2), dim3(256), pre_lds_bytes<2>(), st, a);
         return;
@@ -930,7 +941,9 @@ hipError_t gemm_init() {
 #undef Q35_ATTR
     if (hipFuncSetAttribute((const void*)gemm_lmhead<8, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, kLmLds) != hipSuccess ||
         hipFuncSetAttribute((const void*)gemm_pre<kEStore, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<2>()) != hipSuccess ||
-        hipFuncSetAttribute((const void*)gemm_pre<kESiluMul, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<2>()) != hipSuccess)
+        hipFuncSetAttribute((const void*)gemm_pre<kESiluMul, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<2>()) != hipSuccess ||
+        hipFuncSetAttribute((const void*)gemm_pre<kEStore, 4, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<4>()) != hipSuccess ||
+        hipFuncSetAttribute((const void*)gemm_pre<kESiluMul, 4, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<4>()) != hipSuccess)
         return hipGetLastError();
     return hipSuccess;
 }

@@ -133,9 +133,9 @@ def test_lm_head_persistent_row_chunks():
 
 @pytest.mark.parametrize("N", [1024, 5120, 7168, 8704])
 def test_k1024_gemm_forms_identical(eng, N):
-    """Batched K = 1024 projections: the all-loads-up-front kernel (32-row blocks, A fragments
-    DMA'd into LDS) and the k-block pipelined kernel give identical bits, for ragged (M = 17,
-    200) and full (M = 256) row counts."""
+    """Batched K = 1024 projections: the all-loads-up-front kernels (32 x 64 blocks and 64 x 128
+    blocks of 8 waves, A fragments DMA'd into LDS) and the k-block pipelined kernel give
+    identical bits, for ragged (M = 17, 200) and full (M = 256) row counts."""
     import torch
     print(f"k1024 gemm forms N={N}", flush=True)
     g = torch.Generator().manual_seed(N)
@@ -146,7 +146,7 @@ def test_k1024_gemm_forms_identical(eng, N):
     for M in (17, 200, 256):
         X = torch.randn(M, 1024, generator=g).to(torch.bfloat16).cuda()
         out = {}
-        for p in (0, 1):
+        for p in (0, 1, 2):
             eng.set_option("gemm_pre", p)
             Y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
             torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
@@ -156,6 +156,7 @@ def test_k1024_gemm_forms_identical(eng, N):
         eng.set_option("gemm_pre", 1)
         assert not torch.isnan(out[0].float()).any()
         assert torch.equal(out[0], out[1]), M
+        assert torch.equal(out[0], out[2]), M
 
 @pytest.mark.parametrize("B", [1, 64, 1024])
 def test_config2_gdn_step(eng, oracle_weights, B):
