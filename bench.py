@@ -30,7 +30,7 @@ WIN_BYTES = 18 * 3 * 6144 * 4
 KV_BYTES_PER_SLOT = 6 * 2 * 2 * 256 * 2   # K and V, 6 layers, 2 kv heads
 FAC_ROW_BYTES = 16 * 264 * 4              # one pending GDN row of one layer: k~ | dv | gamma per head
 FAM = {"gemm": 1, "lm_head": 2, "gdn": 3, "attn": 4}
-KERNEL_NAMES = {"attn": "attn_fused", "gdn": "gdn_persist", "lm_head": "gemm_lmhead<8, 2> (tied lm_head)",
+KERNEL_NAMES = {"attn": "attn_fused", "gdn": "gdn_persist", "lm_head": "gemm_lmhead3 (tied lm_head)",
                 "gemm": "projection / MLP GEMMs"}
 # HBM bytes per launch from an earlier rocprofv3 FETCH_SIZE / WRITE_SIZE run (not this run), each
 # scaled by what the same counter reads for a 1 GiB copy (FETCH x2.0, WRITE x1.0); the runs and
@@ -39,7 +39,6 @@ TRAFFIC_SOURCE = "profiles/hbm_traffic_decode_b256_ctx4096.md"
 MEASURED_TRAFFIC = {
     ("attn", 256, 4096): (1058631.5 * 2.0 + 1024.0 * 1.0) * 1024,                        # attn_fused
     ("gdn", 256, 4096): (146575.5 * 2.0 + 90254.0 * 1.0) * 1024,    # gdn_persist, gdn_defer 3 (4-step average)
-    ("lm_head", 256, 4096): (256114.4 * 2.0 + 38080.5 * 1.0) * 1024,                      # gemm_lmhead<8, 2>
 }
 
 
@@ -63,8 +62,8 @@ def family_bytes(fam: str, B: int, L: int, d: int = 0) -> int:
         return int(18 * B * gdn_lane_layer_bytes(d))
     if fam == "attn":      # attention core per layer: K and V of L+1 slots, f32 q, bf16 gate in, output
         return 6 * B * (2048 * (L + 1) + 8 * 256 * 4 + 2048 * 2 + 2048 * 2)
-    if fam == "lm_head":
-        return 248320 * 1024 * 2 + B * (1024 * 2 + 248320 // 16 * 8)
+    if fam == "lm_head":   # E once, A rows, one (max, index) partial per row and column stream
+        return 248320 * 1024 * 2 + B * (1024 * 2 + 128 * 8)
     if fam == "gemm":      # all projection + MLP GEMMs: weights once + activations
         w = WEIGHT_BYTES - 248320 * 1024 * 2 - 24 * 2048 - 1024 * 2
         act = B * 24 * 2 * (1024 + 8224 + 2048 + 1024 + 1024 + 7168 + 7168 + 1024)

@@ -207,7 +207,8 @@ int q35_kprof_read(q35_engine* e, float* total_ms, int* launches);
  * "b1_partials" (one-row bodies leave k-block chains for the next norm GEMV), "gemv_tpb" (1/2
  * column tiles per block of the one-row norm GEMVs), "gemm_pre" (batched K = 1024 GEMMs; 0: k-block
  * pipelined, 1: all loads issued up front, in 64 x 128 blocks when those fit the CUs in one
- * round, else 32 x 64; 2: always 64 x 128), "lmhead_persist" (persistent lm_head at batched lanes), "partial_rows"
+ * round, else 32 x 64; 2: always 64 x 128), "lmhead_persist" (lm_head at batched lanes: 0 tiled, 1 persistent with A in LDS, 3 -- the
+ * default -- persistent with A in registers and a running argmax per column stream), "partial_rows"
  * (>= 17: batched out/o/down GEMMs with at least this many rows sum their k-block chains in
  * the block, one chain for the add+norm; default 1,024), "attn_split4" (split attention path
  * in 4-wave score blocks and dim-quarter P.V blocks), "gdn_defer" (0 .. 4, default 3: a decode

@@ -697,7 +697,7 @@ void lm_head(q35_engine* e, int row0, int M, bool want_logits, const uint16_t* n
         KTimer kt(e, kFamLmHead);
         HCK(launch_gemm(a, amode, kEArgmax, e->st));
     }
-    HCK(launch_argmax(e->pval, e->pidx, kVocab / 16, kVocab / 16, M, e->tok_dev, top_val, e->st));
+    HCK(launch_argmax(e->pval, e->pidx, kVocab / 16, gemm_argmax_partials(a), M, e->tok_dev, top_val, e->st));
 }
 
 void save_hlast(q35_engine* e, q35_state* s, const std::vector<int>& src_rows, const std::vector<int>& lanes) {
@@ -1612,7 +1612,7 @@ int q35_op_lm_head_argmax(q35_engine* e, const uint16_t* x, int M, int32_t* tok,
         a.logits = logits; a.ldl = kVocab;
         a.part_val = e->pval; a.part_idx = e->pidx; a.ldp = kVocab / 16;
         HCK(launch_gemm(a, kAPlain, kEArgmax, e->st));
-        HCK(launch_argmax(e->pval, e->pidx, kVocab / 16, kVocab / 16, M, tok, nullptr, e->st));
+        HCK(launch_argmax(e->pval, e->pidx, kVocab / 16, gemm_argmax_partials(a), M, tok, nullptr, e->st));
     });
 }
 
@@ -1647,7 +1647,10 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             else if (n == "gemm_pre") e->forms.gemm_pre = value;
             else if (n == "attn_split4") e->forms.attn_split4 = value ? 1 : 0;
             else if (n == "gdn_defer") e->forms.gdn_defer = value;
-            else e->forms.lmhead_persist = value ? 1 : 0;
+            else {
+                REQ(value == 0 || value == 1 || value == 3, Q35_ERR_ARG, "lmhead_persist is 0, 1 or 3");
+                e->forms.lmhead_persist = value;
+            }
             for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
             e->graphs.clear();
         } else {

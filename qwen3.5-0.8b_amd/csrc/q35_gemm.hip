@@ -798,6 +798,130 @@ __global__ void __launch_bounds__(64 * NW) gemm_lmhead(GemmArgs a, int mb) {
     }
 }
 
+// Tied lm_head at batched lanes, second form: A in registers, the weight stream through an LDS
+// ring. A block of 8 waves owns 128 rows; wave w holds all 32 A fragments of rows 16 w .. +16
+// (128 VGPRs) and computes their full k-block chains in order, so each weight fragment read
+// from LDS feeds the 8 row groups of the block and no chain crosses waves. Units are single
+// 16-column tiles (all four k-blocks: 32 KiB, contiguous in the tiled layout); the ring holds
+// four of them and the DMA runs three units ahead (global_load_lds by all 512 threads). The
+// LDS fragment reads are inline asm (the compiler would make them wait for the in-flight DMA).
+// Argmax epilogue: each lane keeps the running (max, index) of its column over the stream's
+// tiles (their columns increase, so a strict > keeps the lowest index among equal values) and
+// the 16 lanes of a row are reduced once at the end: one (max, index) partial per (row, stream)
+// instead of one per (row, tile) -- the per-tile partial stores took half the kernel's time.
+constexpr int kLm3Unit = kLmKB * 8 * 64 * 16;                     // 32 KiB
+constexpr int kLm3Ring = 4;
+constexpr int kLm3Lds = kLm3Ring * kLm3Unit;                       // 128 KiB
+
+__global__ void __launch_bounds__(512) gemm_lmhead3(GemmArgs a, int mb) {
+    extern __shared__ q35_u32x4 dyn_lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
+    const int rb = k % mb;
+    const int streams = gridDim.x / mb;
+    const int stream = (k / mb) * 8 + xcd;
+    const int row0 = rb * 128 + wv * 16;
+    const int nunits = a.N / 16;
+
+    q35_u32x4 af[kLmKB][8];
+    {
+        const int m = row0 + (lane & 15), g = lane >> 4;
+        const uint16_t* xr = (const uint16_t*)a.X + (size_t)min(m, a.M - 1) * a.ldx;
+#pragma unroll
+        for (int kb = 0; kb < kLmKB; ++kb)
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const q35_u32x4 v = *(const q35_u32x4*)(xr + kb * 256 + g * 64 + s * 8);
+                af[kb][s] = m < a.M ? v : (q35_u32x4){0u, 0u, 0u, 0u};
+            }
+    }
+    // unit u's 32 KiB into ring slot r: 4 DMA instructions per thread, 16 bytes each
+    auto fetch = [&](int u, int r) {
+        const char* src = (const char*)(a.W + (size_t)u * kLmKB * 4096);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)(i * 512 + tid) * 16),
+                                             (__attribute__((address_space(3))) void*)(dyn_lds + r * 2048 + i * 512 + wv * 64),
+                                             16, 0, 0);
+    };
+    // the units of this stream: stream, stream + streams, ...; n-th unit in ring slot n % 4.
+    // Issued: always 3 ahead (past the end, a clamped reload of the last unit, so the per-unit
+    // DMA count -- and thus the wait count -- is constant)
+    const int nmine = stream < nunits ? (nunits - 1 - stream) / streams + 1 : 0;
+    auto unit_of = [&](int i) { return stream + min(i, nmine - 1) * streams; };
+    if (nmine > 0) {
+#pragma unroll
+        for (int i = 0; i < kLm3Ring - 1; ++i) fetch(unit_of(i), i);
+    }
+    const unsigned lds_lane = (unsigned)(size_t)(__attribute__((address_space(3))) const void*)dyn_lds + lane * 16;
+    float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    int bidx[4] = {0x7fffffff, 0x7fffffff, 0x7fffffff, 0x7fffffff};
+    for (int i = 0; i < nmine; ++i) {
+        // unit i landed (the 2 later units' 8 DMAs may still be in flight), for every wave
+        asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+        fetch(unit_of(i + kLm3Ring - 1), (i + kLm3Ring - 1) % kLm3Ring);
+        const unsigned base = lds_lane + (unsigned)((i % kLm3Ring) * kLm3Unit);
+        // two k-blocks' chains at a time, interleaved step by step; their 16 fragment reads are
+        // issued in (step, k-block) order and waited for two at a time (lgkmcnt counts to 15)
+        q35_f32x4 c[kLmKB];
+#pragma unroll
+        for (int kp = 0; kp < kLmKB; kp += 2) {
+            q35_u32x4 wf[8][2];
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(wf[s][h]) : "v"(base), "n"(((kp + h) * 8 + s) * 1024) : "memory");
+            c[kp] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
+            c[kp + 1] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                switch (s) {      // the immediate must be a constant: reads 2s, 2s + 1 have landed
+                    case 0: asm volatile("s_waitcnt lgkmcnt(14)" : "+v"(wf[0][0]), "+v"(wf[0][1])); break;
+                    case 1: asm volatile("s_waitcnt lgkmcnt(12)" : "+v"(wf[1][0]), "+v"(wf[1][1])); break;
+                    case 2: asm volatile("s_waitcnt lgkmcnt(10)" : "+v"(wf[2][0]), "+v"(wf[2][1])); break;
+                    case 3: asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(wf[3][0]), "+v"(wf[3][1])); break;
+                    case 4: asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(wf[4][0]), "+v"(wf[4][1])); break;
+                    case 5: asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(wf[5][0]), "+v"(wf[5][1])); break;
+                    case 6: asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(wf[6][0]), "+v"(wf[6][1])); break;
+                    default: asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(wf[7][0]), "+v"(wf[7][1])); break;
+                }
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    c[kp + h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(af[kp + h][s]), as_bf(wf[s][h]), c[kp + h], 0, 0, 0);
+            }
+        }
+        q35_f32x4 sum;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sum[r] = ((c[0][r] + c[1][r]) + c[2][r]) + c[3][r];
+        const int col = unit_of(i) * 16 + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = row0 + 4 * (lane >> 4) + r;
+            const float v = rbf(sum[r]);
+            if (row < a.M && a.logits) a.logits[(unsigned)(row * a.ldl + col)] = v;
+            if (v > best[r]) { best[r] = v; bidx[r] = col; }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = row0 + 4 * (lane >> 4) + r;
+        argmax16(best[r], bidx[r]);
+        if ((lane & 15) == 0 && row < a.M && nmine > 0) {
+            a.part_val[(unsigned)(row * a.ldp + stream)] = best[r];
+            a.part_idx[(unsigned)(row * a.ldp + stream)] = bidx[r];
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the clamped reloads past the end
+}
+
+// column streams of the gemm_lmhead3 launch for M <= 512 rows (128 rows per block)
+static int lmhead3_streams(int M) {
+    const int mb3 = (M + 127) / 128;
+    return 256 / mb3 / 8 * 8;
+}
+
 // Final argmax over the per-tile partials of each row: lowest id among the maxima.
 __global__ void __launch_bounds__(1024) argmax_rows(const float* pv, const int* pi, int ldp, int n,
                                                     int* out_tok, float* out_val) {
@@ -862,7 +986,12 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
             c.part_idx = a.part_idx + (size_t)r0 * a.ldp;
             const int mbk = (c.M + 63) / 64;
             const int streams = max(8, 256 / mbk / 8 * 8);
-            hipLaunchKernelGGL((gemm_lmhead<8, 2>), dim3(mbk * streams), dim3(512), kLmLds, st, c, mbk);
+            if (a.forms.lmhead_persist == 3) {
+                const int mb3 = (c.M + 127) / 128;
+                hipLaunchKernelGGL(gemm_lmhead3, dim3(lmhead3_streams(c.M) * mb3), dim3(512), kLm3Lds, st, c, mb3);
+            }
+            else
+                hipLaunchKernelGGL((gemm_lmhead<8, 2>), dim3(mbk * streams), dim3(512), kLmLds, st, c, mbk);
         }
         return;
     }
@@ -940,6 +1069,7 @@ hipError_t gemm_init() {
     Q35_ATTR(kANormX, kEStore) Q35_ATTR(kANormX, kEArgmax) Q35_ATTR(kANormXP, kEStore)
 #undef Q35_ATTR
     if (hipFuncSetAttribute((const void*)gemm_lmhead<8, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, kLmLds) != hipSuccess ||
+        hipFuncSetAttribute((const void*)gemm_lmhead3, hipFuncAttributeMaxDynamicSharedMemorySize, kLm3Lds) != hipSuccess ||
         hipFuncSetAttribute((const void*)gemm_pre<kEStore, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<2>()) != hipSuccess ||
         hipFuncSetAttribute((const void*)gemm_pre<kESiluMul, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<2>()) != hipSuccess ||
         hipFuncSetAttribute((const void*)gemm_pre<kEStore, 4, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<4>()) != hipSuccess ||
@@ -988,6 +1118,12 @@ hipError_t launch_produce(const GemmArgs& a, int amode, hipStream_t st) {
     else if (amode == kAGatedNorm) hipLaunchKernelGGL((produce_kernel<kAGatedNorm>), dim3(a.M), dim3(256), 0, st, p);
     else return hipErrorInvalidValue;
     return hipGetLastError();
+}
+
+int gemm_argmax_partials(const GemmArgs& a) {
+    if (a.M > 16 && a.K == kHidden && a.N % 64 == 0 && a.forms.lmhead_persist == 3)
+        return std::min(lmhead3_streams(a.M > 512 ? 256 : a.M), a.N / 16);
+    return (a.N + 15) / 16;
 }
 
 hipError_t launch_argmax(const float* pv, const int* pi, int ldp, int n, int rows, int* tok,

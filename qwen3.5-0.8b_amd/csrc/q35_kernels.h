@@ -17,7 +17,9 @@ enum { kEStore = 0, kEArgmax = 1, kEPartial = 2, kEResidual = 3, kESiluMul = 4 }
 struct KernelForms {
     int gemv_tpb = 2;          // one-row norm GEMVs (N >= 4096): column tiles per block, 1 or 2
     int gemm_pre = 1;          // batched K = 1024 GEMMs: all loads up front (1) or k-block pipelined (0)
-    int lmhead_persist = 1;    // tied lm_head at batched lanes: persistent kernel (1) or 64 x 256 tiles (0)
+    int lmhead_persist = 3;    // tied lm_head at batched lanes: 64 x 256 tiles (0), persistent with A in LDS
+                               // (1), persistent with A in registers, the weights through an LDS ring
+                               // and one argmax partial per (row, column stream) (3)
     int partial_rows = 1024;   // batched kEPartial GEMMs with M >= this leave one (summed) chain
     int attn_split4 = 1;       // split attention path: 4-wave score blocks, P.V split over dim quarters
     int attn_prompt = 1;       // prompt waves of >= 64 rows: flash-form MFMA kernel (1) or one-row kernels (0)
@@ -52,6 +54,8 @@ hipError_t gemm_init();
 // k-block chains a batched kEPartial GEMM leaves in kpart
 int gemm_partial_chains(int M, int K, const KernelForms& f);
 hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st);
+// kEArgmax: how many (max, index) partials per row the launch for `a` writes (launch_argmax's n)
+int gemm_argmax_partials(const GemmArgs& a);
 // The batched A producer alone: a.prod [M][K] bf16 = the producer's A operand (kASiluMul or
 // kAGatedNorm), as launch_gemm stages it for M > 16.
 hipError_t launch_produce(const GemmArgs& a, int amode, hipStream_t st);

@@ -85,15 +85,16 @@ def test_config1_lm_head_argmax(eng, oracle_weights):
 
 @pytest.mark.parametrize("M", [17, 100, 250, 256])
 def test_lm_head_persistent_equals_tiled(eng, M):
-    """The persistent lm_head kernel (A resident in LDS, 64 x 32 wave tiles) and the 64 x 256
-    tiled kernel follow the same reduction order: identical logits and tokens, including a
-    ragged last row block (M = 17, 100, 250)."""
+    """The persistent lm_head kernels (A resident in LDS with 64 x 32 wave tiles; A in
+    registers with the weights streamed through an LDS ring and a running argmax per column
+    stream) and the 64 x 256 tiled kernel follow the same reduction order: identical logits and
+    tokens, including a ragged last row block (M = 17, 100, 250)."""
     import torch
     print(f"lm_head persistent vs tiled M={M}", flush=True)
     g = torch.Generator().manual_seed(M)
     X = torch.randn(M, 1024, generator=g).to(torch.bfloat16).cuda()
     out = {}
-    for p in (0, 1):
+    for p in (0, 1, 3):
         eng.set_option("lmhead_persist", p)
         tok = torch.full((M,), -1, dtype=torch.int32, device="cuda")
         lg = torch.full((M, 248320), float("nan"), dtype=torch.float32, device="cuda")
@@ -101,9 +102,10 @@ def test_lm_head_persistent_equals_tiled(eng, M):
         eng.op_lm_head_argmax(X.data_ptr(), M, tok.data_ptr(), lg.data_ptr())
         eng.sync()
         out[p] = (tok.cpu(), lg.cpu())
-    eng.set_option("lmhead_persist", 1)
-    assert torch.equal(out[0][0], out[1][0])
-    assert torch.equal(out[0][1], out[1][1])
+    eng.set_option("lmhead_persist", 3)
+    for p in (1, 3):
+        assert torch.equal(out[0][0], out[p][0]), p
+        assert torch.equal(out[0][1], out[p][1]), p
 
 
 
@@ -118,7 +120,7 @@ def test_lm_head_persistent_row_chunks():
         M = 700
         X = torch.randn(M, 1024, generator=torch.Generator().manual_seed(700)).to(torch.bfloat16).cuda()
         out = {}
-        for p in (0, 1):
+        for p in (0, 1, 3):
             e.set_option("lmhead_persist", p)
             tok = torch.full((M,), -1, dtype=torch.int32, device="cuda")
             lg = torch.full((M, 248320), float("nan"), dtype=torch.float32, device="cuda")
@@ -126,8 +128,9 @@ def test_lm_head_persistent_row_chunks():
             e.op_lm_head_argmax(X.data_ptr(), M, tok.data_ptr(), lg.data_ptr())
             e.sync()
             out[p] = (tok.cpu(), lg.cpu())
-        assert torch.equal(out[0][0], out[1][0])
-        assert torch.equal(out[0][1], out[1][1])
+        for p in (1, 3):
+            assert torch.equal(out[0][0], out[p][0]), p
+            assert torch.equal(out[0][1], out[p][1]), p
     finally:
         e.close()
 
