@@ -287,8 +287,6 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     __shared__ float red[NG][VC];            // r partials, then o partials
     __shared__ float wred[4];
     __shared__ float gate_s[2];
-    __shared__ float ohead[128];
-    __shared__ float hss2[2];
     // item k's row metadata: lane | cur << 16 | wcur << 20 | pend code << 24
     __shared__ int meta[kPersistMaxItems];
     const int nk = (nitems - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
@@ -307,8 +305,8 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     const bool hasv = tid < VC;
     struct Ops {
         float w0, w1, w2, v0, v1, v2;
-        uint16_t x, xv, zz, gw, bb, aa, alog, dtb;
-        uint2 cpk, dpk;
+        uint16_t x, xv, bb, aa, alog, dtb;
+        uint2 cpk, dpk, z4, g4;      // z4 / g4: z and gnorm of columns 4 (lane % 32) .. +3 (wave 0's y)
     };
     const uint16_t* gnw = a.gnorm ? a.gnorm : a.dt_bias;   // any valid address when unused
     // the next item's state rows 4g .. 4g+3 of this thread (the four groups are issued at four
@@ -351,8 +349,8 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         o.dpk = *(const uint2*)(a.conv_w + (size_t)cv * 4);
         o.x = pr[cqk];
         o.xv = pr[cv];
-        o.zz = pr[kGdnZOff + h * 128 + (tid & 127)];
-        o.gw = gnw[a.gnorm ? (tid & 127) : 0];
+        o.z4 = *(const uint2*)(pr + kGdnZOff + h * 128 + (lane64 & 31) * 4);
+        o.g4 = *(const uint2*)(gnw + (a.gnorm ? (lane64 & 31) * 4 : 0));
         o.bb = pr[kGdnBOff + h];
         o.aa = pr[kGdnAOff + h];
         o.alog = a.A_log[h];
@@ -444,14 +442,17 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
         lds_barrier();
         if (more) fetch_rows(1);
-        {
-            const float rq = rsqrtf((wred[0] + wred[1]) + 1e-6f);
-            const float rk = rsqrtf((wred[2] + wred[3]) + 1e-6f);
-            if (tid < 128) qs[tid] = __fmul_rn(__fmul_rn(qs[tid], rq), 0.08838834764831845f);
-            else ks[tid - 128] = __fmul_rn(ks[tid - 128], rk);
-        }
-        lds_barrier();
+        // q~ and k~ of this thread's 16 rows, normalised where they are read (the same two
+        // rounded products as a normalisation pass, without its barrier)
+        const float rq = rsqrtf((wred[0] + wred[1]) + 1e-6f);
+        const float rk = rsqrtf((wred[2] + wred[3]) + 1e-6f);
         const float gam = gate_s[0], beta = gate_s[1];
+        float kn[KR], qn[KR];
+#pragma unroll
+        for (int i = 0; i < KR; ++i) {
+            kn[i] = __fmul_rn(ks[kg * KR + i], rk);
+            qn[i] = __fmul_rn(__fmul_rn(qs[kg * KR + i], rq), 0.08838834764831845f);
+        }
 #pragma unroll
         for (int c = 0; c < CW; ++c)
 #pragma unroll
@@ -460,7 +461,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
 #pragma unroll
                 for (int i = gq * 8; i < gq * 8 + 8; ++i) {
                     s[i][c] = __fmul_rn(s[i][c], gam);
-                    rp = fmaf(s[i][c], ks[kg * KR + i], rp);
+                    rp = fmaf(s[i][c], kn[i], rp);
                 }
                 red[kg * GPT + gq][jc + c] = rp;
             }
@@ -477,7 +478,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         if (rec) {                // gdn_kernel's factor record of a deferred row
             float* F = a.fac + lane * a.fac_lane + pset * a.fac_set + npend * a.fac_row + h * kFacStride;
             if (kg == 0) *(q35_f32x4*)(F + 128 + jc) = (q35_f32x4){dv[0], dv[1], dv[2], dv[3]};
-            if (tid >= 128) F[tid - 128] = ks[tid - 128];
+            if (tid >= 128) F[tid - 128] = __fmul_rn(ks[tid - 128], rk);
             if (tid == 0) F[256] = gam;
         }
         lds_barrier();          // red is reused for the o partials
@@ -489,8 +490,8 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                 float op2 = 0.f;
 #pragma unroll
                 for (int i = gq * 8; i < gq * 8 + 8; ++i) {
-                    s[i][c] = delta_update(s[i][c], ks[kg * KR + i], dv[c]);
-                    op2 = fmaf(qs[kg * KR + i], s[i][c], op2);
+                    s[i][c] = delta_update(s[i][c], kn[i], dv[c]);
+                    op2 = fmaf(qn[i], s[i][c], op2);
                 }
                 red[kg * GPT + gq][jc + c] = op2;
             }
@@ -503,26 +504,42 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                                             (q35_f32x4*)(So + (kg * KR + i) * 128 + jc));
         }
         lds_barrier();
-        if (kg == 0) {
+        // wave 0 finishes the head: lane L < 32 sums the o partials of columns 4L .. 4L+3 and
+        // makes their gated-norm outputs; the head's two half sums of squares are formed as
+        // half_head_ss forms them (quads in column order, each ((o0^2 + o1^2) + (o2^2 + o3^2)))
+        // from the quads of lanes 0-15 and 16-31. No barrier ends the item: every LDS array the
+        // next item writes before its first barrier was last read before this item's last one,
+        // except red (read here), which the next item writes only after that first barrier.
+        if (wv == 0) {
+            float oj[CW];
 #pragma unroll
             for (int c = 0; c < CW; ++c) {
-                float oj = 0.f;
+                oj[c] = 0.f;
 #pragma unroll
-                for (int i = 0; i < NG; ++i) oj += red[i][jc + c];
-                a.o[(size_t)gi * 2048 + h * 128 + jc + c] = oj;
-                ohead[jc + c] = oj;
+                for (int i = 0; i < NG; ++i) oj[c] += red[i][jc + c];
+            }
+            if (lane64 < 32) *(q35_f32x4*)(a.o + (size_t)gi * 2048 + h * 128 + jc) = (q35_f32x4){oj[0], oj[1], oj[2], oj[3]};
+            if (a.y) {
+                const float q = __fadd_rn(__fadd_rn(__fmul_rn(oj[0], oj[0]), __fmul_rn(oj[1], oj[1])),
+                                          __fadd_rn(__fmul_rn(oj[2], oj[2]), __fmul_rn(oj[3], oj[3])));
+                float ss0 = 0.f, ss1 = 0.f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    ss0 = __fadd_rn(ss0, __shfl(q, j, 64));
+                    ss1 = __fadd_rn(ss1, __shfl(q, 16 + j, 64));
+                }
+                const float rs = head_rsqrt(ss0, ss1);
+                const float zc[4] = {__uint_as_float(op.z4.x << 16), __uint_as_float(op.z4.x & 0xffff0000u),
+                                     __uint_as_float(op.z4.y << 16), __uint_as_float(op.z4.y & 0xffff0000u)};
+                const float wc[4] = {__uint_as_float(op.g4.x << 16), __uint_as_float(op.g4.x & 0xffff0000u),
+                                     __uint_as_float(op.g4.y << 16), __uint_as_float(op.g4.y & 0xffff0000u)};
+                uint32_t yb[4];
+#pragma unroll
+                for (int c = 0; c < CW; ++c) yb[c] = f2bf(__fmul_rn(__fmul_rn(wc[c], __fmul_rn(oj[c], rs)), silu_f(zc[c])));
+                if (lane64 < 32)
+                    *(uint2*)(a.y + (size_t)gi * 2048 + h * 128 + jc) = (uint2){yb[0] | (yb[1] << 16), yb[2] | (yb[3] << 16)};
             }
         }
-        if (a.y) {
-            lds_barrier();
-            if (tid < 2) hss2[tid] = half_head_ss_regs(ohead + 64 * tid);
-            lds_barrier();
-            if (tid < 128) {
-                const float rs = head_rsqrt(hss2[0], hss2[1]);
-                a.y[(size_t)gi * 2048 + h * 128 + tid] = f2bf(__fmul_rn(__fmul_rn(bf2f(op.gw), __fmul_rn(ohead[tid], rs)), silu_f(bf2f(op.zz))));
-            }
-        }
-        lds_barrier();          // LDS scratch (qs, ks, red, ohead) is reused by the next item
     }
 }
 
