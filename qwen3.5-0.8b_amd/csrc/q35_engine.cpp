@@ -517,17 +517,33 @@ inline bool small_rows(int R) { return R <= 16; }
 inline bool b1_partials(const q35_engine* e, int R, int T, bool ckpt) {
     return e->b1_partials && R == 1 && T == 1 && !ckpt;
 }
+// Bodies of 2 .. 16 rows (MTP verify at batch 1, short prompt waves, a few lanes): the same
+// one-wave-per-(column tile, k-block) chains, folded by the add+norm kernel of the batched path
+// (one launch for all rows: a GEMM producer per row would repeat the fold in every block), the
+// norm GEMMs then taking the normed rows as plain A. 10.2 -> ~4.5 + 3 us for down at 3 rows.
+inline bool mid_partials(const q35_engine* e, int R) { return e->forms.mid_partials && R > 1 && small_rows(R); }
+// Whether the body leaves the final-normed rows in e->nrm (else the lm_head applies the norm).
+inline bool body_final_normed(const q35_engine* e, int R, int T, bool ckpt) {
+    return !small_rows(R) || b1_partials(e, R, T, ckpt) || mid_partials(e, R);
+}
 struct B1Res {
     uint16_t* cur;     // residual row as of the last fold
     uint16_t* alt;     // receives the next fold
     int pend = 0;      // k-block chains pending in e->kpart
+    bool mid = false;  // 2 .. 16 rows: chains folded by the add+norm kernel into e->x (in place)
 };
 
 // RMSNorm GEMM of the residual row: folds pending chains first (one-row bodies).
 void norm_gemm(q35_engine* e, B1Res* rr, const uint16_t* W, int N, int R, uint16_t* Y, int ldy,
                const uint16_t* normw) {
-    if (!rr) {
+    if (!rr || (rr->mid && !rr->pend)) {
         gemm(e, W, N, kHidden, R, e->x, kHidden, Y, ldy, kANormX, nullptr, 0, normw);
+        return;
+    }
+    if (rr->mid) {
+        HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, rr->pend, normw, e->h, R, e->st));
+        rr->pend = 0;
+        gemm(e, W, N, kHidden, R, e->h, kHidden, Y, ldy);
         return;
     }
     GemmArgs a{};
@@ -627,8 +643,9 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt, int defe
     const int nl = R / T;
     const int cs = nl <= 8 ? 8 : nl <= 32 ? 4 : nl <= 64 ? 2 : 1;
     const bool small = small_rows(R);
-    B1Res res{e->x, e->h};          // e->h is unused by small bodies
-    B1Res* rr = b1_partials(e, R, T, ckpt) ? &res : nullptr;
+    B1Res res{e->x, e->h};          // one-row bodies: e->h is the second residual buffer
+    res.mid = mid_partials(e, R);   // 2 .. 16 rows: e->x folded in place, e->h the normed rows
+    B1Res* rr = b1_partials(e, R, T, ckpt) || res.mid ? &res : nullptr;
     HCK(launch_addnorm(0, e->tok_dev, e->E, e->x, nullptr, nullptr, 0, e->L[0].norm_in, small ? nullptr : e->h,
                        R, e->st));
     for (int l = 0; l < e->n_layers; ++l) {
@@ -676,7 +693,8 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt, int defe
     }
     // one-row body: the last layer's chains and the final norm in one add+norm launch; the
     // normed row is in e->nrm, so the caller's lm_head takes no norm weight
-    if (rr) HCK(launch_addnorm(3, nullptr, nullptr, rr->cur, nullptr, e->kpart, rr->pend, e->final_norm, e->nrm, 1, e->st));
+    if (rr) HCK(launch_addnorm(3, nullptr, nullptr, rr->cur, nullptr, e->kpart, rr->pend, e->final_norm, e->nrm,
+                               rr->mid ? R : 1, e->st));
 }
 
 // lm_head + argmax over rows [row0, row0 + M); tokens into e->tok_dev[0..M). After a
@@ -1237,7 +1255,7 @@ void prefill_waves(q35_engine* e, q35_state* s, int lane, const int32_t* ids, in
         body(e, s, T, T, false);
         s->prefix[lane] += T;
         advance_lane(s, lane);
-        const uint16_t* normw = small_rows(T) && !b1_partials(e, T, T, false) ? e->final_norm : nullptr;
+        const uint16_t* normw = !body_final_normed(e, T, T, false) ? e->final_norm : nullptr;
         if (all_rows) {
             // the body's tokens are consumed: lm_head leaves row r0 + i's id in tok_dev[i]
             for (int r0 = 0; r0 < T; r0 += kAllChunk) {
@@ -1306,8 +1324,7 @@ int q35_decode_step(q35_engine* e, q35_state* s, const int32_t* lanes, int n, co
         const int defer = step_defer(e);
         auto step = [&] {
             body_kernels(e, s, n, 1, false, defer);
-            lm_head(e, 0, n, out_logits != nullptr,
-                    small_rows(n) && !b1_partials(e, n, 1, false) ? e->final_norm : nullptr);
+            lm_head(e, 0, n, out_logits != nullptr, !body_final_normed(e, n, 1, false) ? e->final_norm : nullptr);
             HCK(launch_copy_rows_advance(e->nrm, e->ridx_src, s->hlast, e->ridx_dst, n, kHidden, e->rpos, e->rslot,
                                          e->rcur, e->rwcur, e->rpend, s->nslots, defer, e->st));
         };
@@ -1432,7 +1449,7 @@ int q35_mtp_round_stop(q35_engine* e, q35_state* s, const int32_t* lanes, int n,
                 e->h_lane[r] = ls[i]; e->h_pos[r] = P[i] + t; e->h_slot[r] = P[i] + t;
             }
         body(e, s, R, T, true);
-        lm_head(e, 0, R, false, small_rows(R) ? e->final_norm : nullptr);
+        lm_head(e, 0, R, false, !body_final_normed(e, R, T, true) ? e->final_norm : nullptr);
         HCK(hipMemcpyAsync(e->h_out, e->tok_dev, R * sizeof(int), hipMemcpyDeviceToHost, e->st));
         HCK(hipStreamSynchronize(e->st));
         std::vector<int> rows(n);
@@ -1634,7 +1651,7 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             HCK(hipStreamSynchronize(e->st));
             e->gdn_chunked = value ? 1 : 0;
         } else if (n == "b1_partials" || n == "attn_prompt" || n == "partial_rows" || n == "gemv_tpb" ||
-                   n == "gemm_pre" || n == "lmhead_persist" || n == "attn_split4" || n == "gdn_defer") {
+                   n == "gemm_pre" || n == "lmhead_persist" || n == "attn_split4" || n == "gdn_defer" || n == "mid_partials") {
             // kernel-form switches of this engine: captured steps hold the old forms
             REQ(n != "partial_rows" || value >= 17, Q35_ERR_ARG, "partial_rows must exceed the 16-row batch-1 path");
             REQ(n != "gemv_tpb" || value == 1 || value == 2, Q35_ERR_ARG, "gemv_tpb is 1 or 2");
@@ -1647,6 +1664,7 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             else if (n == "gemm_pre") e->forms.gemm_pre = value;
             else if (n == "attn_split4") e->forms.attn_split4 = value ? 1 : 0;
             else if (n == "gdn_defer") e->forms.gdn_defer = value;
+            else if (n == "mid_partials") e->forms.mid_partials = value ? 1 : 0;
             else {
                 REQ(value == 0 || value == 1 || value == 3, Q35_ERR_ARG, "lmhead_persist is 0, 1 or 3");
                 e->forms.lmhead_persist = value;

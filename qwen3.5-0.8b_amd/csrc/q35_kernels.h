@@ -23,6 +23,7 @@ struct KernelForms {
     int partial_rows = 1024;   // batched kEPartial GEMMs with M >= this leave one (summed) chain
     int attn_split4 = 1;       // split attention path: 4-wave score blocks, P.V split over dim quarters
     int attn_prompt = 1;       // prompt waves of >= 64 rows: flash-form MFMA kernel (1) or one-row kernels (0)
+    int mid_partials = 1;      // bodies of 2 .. 16 rows: k-block chains + add+norm (0: residual-epilogue GEMMs)
     int gdn_defer = 3;         // decode steps: a lane's GDN state update is kept as pending factors for up
                                // to this many steps, the state written on the next (0: every step)
 };
