@@ -16,8 +16,10 @@
 // Kernels (all follow the order above):
 //   gemm_small_m   one 16-row tile; wave w of a block owns k-block w (M <= 16, batch 1);
 //                  with a producer the wave builds its A tile cooperatively in LDS
-//   gemm_pre       K = 1024 at M > 16: 32-row blocks, every load issued up front (A by LDS-DMA)
-//   gemm_lmhead    tied lm_head at M > 16: persistent, A resident in LDS
+//   gemm_pre       K = 1024 at M > 16: 32 x 64 (or 64 x 128) blocks, every load issued up front
+//                  (A by LDS-DMA)
+//   gemm_lmhead3   tied lm_head at M > 16: persistent, A in registers, the weights through an
+//                  LDS ring, a running argmax per column stream (gemm_lmhead: A resident in LDS)
 //   gemm_large_m   4 waves x 16 columns, 64 rows per block; the A tile of each k-block is
 //                  staged once in LDS in MFMA fragment order, the next k-block's loads in
 //                  flight meanwhile (batched lanes);
@@ -972,11 +974,11 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
     // 64-row tiles: more blocks in flight (W tiles are re-read from L2 by the M tiles)
     const int nb = EM == kESiluMul ? (a.N / 32 + 1) / 2 : (a.N / 16 + 3) / 4, mb = (a.M + 63) / 64;
     if (EM == kEArgmax && a.K == kHidden && a.N % 64 == 0 && a.forms.lmhead_persist) {
-        // persistent blocks with A resident in LDS: mbk row blocks x (256 / mbk) column
-        // streams, one block per CU (the 128 KiB of A fragments allow no second). Above 512
-        // rows (MTP verify: 3 rows per lane) in launches of at most 256 rows: rows are
-        // independent, and one pass with more row blocks than CUs would run a second partial
-        // wave of blocks.
+        // persistent blocks, one per CU: gemm_lmhead3 (form 3: 128 rows per block, A in
+        // registers) or gemm_lmhead (form 1: 64 rows per block, A resident in LDS), row blocks x
+        // column streams = 256 blocks. Above 512 rows (MTP verify: 3 rows per lane) in launches
+        // of at most 256 rows: rows are independent, and one pass with more row blocks than CUs
+        // would run a second partial wave of blocks.
         for (int r0 = 0; r0 < a.M; r0 += a.M > 512 ? 256 : a.M) {
             GemmArgs c = a;
             c.M = min(a.M - r0, a.M > 512 ? 256 : a.M);
@@ -989,8 +991,7 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
             if (a.forms.lmhead_persist == 3) {
                 const int mb3 = (c.M + 127) / 128;
                 hipLaunchKernelGGL(gemm_lmhead3, dim3(lmhead3_streams(c.M) * mb3), dim3(512), kLm3Lds, st, c, mb3);
-            }
-            else
+            } else
                 hipLaunchKernelGGL((gemm_lmhead<8, 2>), dim3(mbk * streams), dim3(512), kLmLds, st, c, mbk);
         }
         return;
