@@ -590,7 +590,9 @@ hipError_t launch_gdn_persist(const GdnArgs& a, hipStream_t st) {
     if (a.nlanes <= 0 || a.T != 1 || a.ckpt) return hipErrorInvalidValue;
     const int nitems = a.nlanes * kHv;
     const int grid = nitems < 512 ? nitems : 512;      // two blocks per CU
-    if ((nitems + grid - 1) / grid > kPersistMaxItems) return hipErrorInvalidValue;
+    // more than 128 items per block (above 4,096 lanes): the one-block-per-(row, head) kernel,
+    // same bits
+    if ((nitems + grid - 1) / grid > kPersistMaxItems) return launch_gdn(a, 1, st);
     hipLaunchKernelGGL(gdn_persist, dim3(grid), dim3(256), kPersistLds, st, a, nitems);
     return hipGetLastError();
 }
