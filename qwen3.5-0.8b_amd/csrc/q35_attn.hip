@@ -25,6 +25,9 @@
 namespace q35 {
 
 constexpr int kChunk = 256;
+// attn_fused<*, 2>: dynamic LDS of its two items, the CU's 160 KiB less both halves' static
+// arrays (ubuf, p, ml, nparts)
+constexpr int kFused2MaxLds = 160 * 1024 - 20560;
 
 __device__ __forceinline__ float block_sum256a(float v, float* red) {
     v = wave_sum(v);
@@ -80,7 +83,7 @@ __global__ void __launch_bounds__(256) attn_prep(AttnArgs a) {
 // q fragments of kv group j for row r (all 256 threads; contains a barrier).
 __device__ __forceinline__ void load_q_frags(const AttnArgs& a, int r, int j, uint16_t (*qb)[256],
                                              q35_u32x4* qf) {
-    const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
+    const int tid = threadIdx.x & 255, lane = tid & 63, n = lane & 15, g = lane >> 4;
     const float* q = a.q + ((size_t)r * kNq + 4 * j) * 256;
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
@@ -301,7 +304,7 @@ constexpr int kPart = 128;
 // takes head h, lane i folds slices i, i + 64, ... in order, then a fixed xor butterfly.
 // Needs 4 waves.
 __device__ __forceinline__ void softmax_ml(const float* stats, size_t stats_stride, int nsl, float (*ml)[2]) {
-    const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, h = (threadIdx.x >> 6) & 3;
     const float* st = stats + h * stats_stride;
     float m = -INFINITY;
     for (int i = lane; i < nsl; i += 64) m = fmaxf(m, st[2 * i]);
@@ -323,7 +326,7 @@ __device__ __forceinline__ void softmax_ml(const float* stats, size_t stats_stri
 // unconditional, from row min(t, slot), so no branch splits the wait counts).
 template <bool NT = true>
 __device__ __forceinline__ q35_u32x4 load_v(const AttnArgs& a, int lrow, int j, int pc, int u, int slot) {
-    const int tid = threadIdx.x, dg = tid & 31, tg = tid >> 5;
+    const int tid = threadIdx.x & 255, dg = tid & 31, tg = tid >> 5;
     const int t = pc * kPart + tg * 16 + u;
     const uint16_t* vp = a.vc + lrow * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + min(t, slot)) * 256 + dg * 8;
     const q35_u32x4 v = NT ? __builtin_nontemporal_load((const q35_u32x4*)vp) : *(const q35_u32x4*)vp;
@@ -344,7 +347,7 @@ __device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int 
                                         q35_u32x4* vv, int pnext,
                                         const float* scores, size_t s_stride, float (*ml)[2],
                                         float (*p)[kPart], float (*red)[2][256], float* out) {
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x & 255;
     const int t0 = pc * kPart;
     const int n = min(kPart, slot + 1 - t0);
     const int dg = tid & 31, tg = tid >> 5;
@@ -687,33 +690,47 @@ __global__ void __launch_bounds__(64) attn_pv4(AttnArgs a) {
 // Batched lanes: one block per (row, kv head) runs every chunk's scores into LDS, the
 // softmax, every part's P.V and the gated sum -- the same device functions and orders as the
 // split kernels, without the score / stats / partial round trips through HBM.
-template <bool NT>
-__global__ void __launch_bounds__(256) attn_fused(AttnArgs a, int lds_slots) {
+// NI = 2 (one row per lane): a block of 512 threads runs two (row, kv head) items, one per
+// 256-thread half, with their own LDS. Two one-item blocks sharing a CU do not progress
+// evenly (the older block's waves win the issue arbitration: at 256 lanes and ctx 4096 the
+// first-dispatched half of the grid finished at ~260 us and the other at ~330 us, the CUs
+// half idle in between); the halves of one block meet at every barrier, so both items end
+// together. A half with fewer parts runs idle parts (its loads clamped, its sums not added)
+// to keep the barrier count equal.
+template <bool NT, int NI>
+__global__ void __launch_bounds__(256 * NI) attn_fused(AttnArgs a, int lds_slots) {
     extern __shared__ float fl[];
-    float* scl = fl;                                    // [4][lds_slots]
-    float* stl = fl + 4 * lds_slots;                    // [4][8 * max_chunks]
-    __shared__ float ubuf[2048];                        // q staging, then the P.V reduction
-    uint16_t(*qb)[256] = (uint16_t(*)[256])ubuf;
-    float(*red)[2][256] = (float(*)[2][256])ubuf;
-    __shared__ float p[4][kPart];
-    __shared__ float ml[4][2];
+    const int half = NI == 1 ? 0 : (int)(threadIdx.x >> 8);
+    const size_t item_lds = (size_t)4 * lds_slots + (size_t)4 * 8 * a.max_chunks;
+    float* scl = fl + half * item_lds;                  // [4][lds_slots]
+    float* stl = scl + 4 * lds_slots;                   // [4][8 * max_chunks]
+    __shared__ float ubuf_all[NI][2048];                // q staging, then the P.V reduction
+    __shared__ float p_all[NI][4][kPart];
+    __shared__ float ml_all[NI][4][2];
+    __shared__ int nparts_all[NI];
+    uint16_t(*qb)[256] = (uint16_t(*)[256])ubuf_all[half];
+    float(*red)[2][256] = (float(*)[2][256])ubuf_all[half];
+    float(*p)[kPart] = p_all[half];
+    float(*ml)[2] = ml_all[half];
     // Block order: the T rows of one lane read the same K/V, so they run as consecutive
     // blocks of one XCD (blocks go round-robin to the 8 XCDs) and share its L2 stream. With
     // fewer (lane, kv head) pairs than XCDs (a prompt wave of one lane) each pair's rows are
     // cut into `nseg` contiguous segments of `seg` rows so that every XCD gets a segment:
-    // virtual pair v -> XCD v % 8, blocks 8 ((v / 8) seg + i) + v % 8.
-    const int T = a.T, tid = threadIdx.x;
+    // virtual pair v -> XCD v % 8, blocks 8 ((v / 8) seg + i) + v % 8. With NI = 2 the
+    // virtual blocks 16 (b / 8) + b % 8 and that + 8 run in block b (same XCD).
+    const int T = a.T, tid = threadIdx.x & 255;
     const int npairs = (a.R / T) * kNkv;
     const int nseg = max(1, 8 / npairs), seg = (T + nseg - 1) / nseg;
-    const int xcd = blockIdx.x & 7, kk = blockIdx.x >> 3;
+    const int vb = NI == 1 ? (int)blockIdx.x : (int)(blockIdx.x >> 3) * 16 + half * 8 + (int)(blockIdx.x & 7);
+    const int xcd = vb & 7, kk = vb >> 3;
     const int v = (kk / seg) * 8 + xcd;
-    if (v >= npairs * nseg) return;
     const int pr = v / nseg, t = (v % nseg) * seg + kk % seg;
-    if (t >= T) return;
-    const int j = pr % kNkv, r = (pr / kNkv) * T + t;
-    const int slot = a.rm.slot[r];
+    const bool active = v < npairs * nseg && t < T;
+    if (NI == 1 && !active) return;
+    const int j = pr % kNkv, r = active ? (pr / kNkv) * T + t : 0;
+    const int slot = active ? a.rm.slot[r] : 0;
     const int lrow = a.rm.lane[r];
-    const int nch = slot / kChunk + 1, nparts = slot / kPart + 1;
+    const int nch = active ? slot / kChunk + 1 : 0, nparts = active ? slot / kPart + 1 : 0;
     const size_t sst = (size_t)a.max_chunks * 8;
     q35_u32x4 qf[8];
     {
@@ -724,17 +741,23 @@ __global__ void __launch_bounds__(256) attn_fused(AttnArgs a, int lds_slots) {
         for (int c = 0; c < nch; ++c)    // wave wv takes slices 4c + wv
             score_slice<true, NT>(a, lrow, j, 4 * c + wv, slot, qf, kf, 4 * (c + 1) + wv, scl, lds_slots, stl, sst);
     }
+    if (NI > 1 && tid == 0) nparts_all[half] = nparts;
     __syncthreads();
+    int np = nparts;
+    if (NI > 1) np = max(nparts_all[0], nparts_all[NI - 1]);
     q35_u32x4 vv[16];
     load_v_part<NT>(a, lrow, j, 0, slot, vv);
     softmax_ml(stl, sst, slot / 64 + 1, ml);
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int pc = 0; pc < nparts; ++pc) {
+    for (int pc = 0; pc < np; ++pc) {
         float out[4];
         pv_part<true, NT>(a, lrow, j, pc, slot, vv, pc + 1, scl, lds_slots, ml, p, red, out);
+        if (NI == 1 || pc < nparts) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] += out[i];
+            for (int i = 0; i < 4; ++i) acc[i] += out[i];
+        }
     }
+    if (!active) return;
 #pragma unroll
     for (int i = 0; i < 4; ++i) a.out[(size_t)r * 2048 + (4 * j + i) * 256 + tid] = gated_out(a, r, 4 * j + i, tid, acc[i]);
 }
@@ -992,9 +1015,11 @@ __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
 }
 
 hipError_t attn_init() {
-    hipError_t e = hipFuncSetAttribute((const void*)attn_fused<true>, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+    hipError_t e = hipFuncSetAttribute((const void*)attn_fused<true, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
     if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute((const void*)attn_fused<false>, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+    e = hipFuncSetAttribute((const void*)attn_fused<false, 1>, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+    if (e != hipSuccess) return e;
+    e = hipFuncSetAttribute((const void*)attn_fused<true, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, kFused2MaxLds);
     if (e != hipSuccess) return e;
     return hipFuncSetAttribute((const void*)attn_prompt, hipFuncAttributeMaxDynamicSharedMemorySize, kPrLds);
 }
@@ -1003,6 +1028,8 @@ static size_t fused_lds(const AttnArgs& a) {
     return (size_t)(4 * ((a.cap + 63) / 64 * 64) + 4 * 8 * a.max_chunks) * 4;
 }
 static bool use_fused(const AttnArgs& a) { return a.R >= 64 && fused_lds(a) <= 96 * 1024; }
+// two items per block (one row per lane) when both items' LDS fits the CU
+static bool use_fused2(const AttnArgs& a) { return a.T == 1 && a.fused_pair && 2 * fused_lds(a) <= (size_t)kFused2MaxLds; }
 // one row per lane on the split path: the prep runs inside the slice score kernel
 static bool prep_in_scores(const AttnArgs& a) { return !use_fused(a) && a.T == 1; }
 
@@ -1026,8 +1053,12 @@ hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
         const int pairs = a.R / a.T * kNkv;
         const int nseg = std::max(1, 8 / pairs), seg = (a.T + nseg - 1) / nseg;
         const dim3 grid((pairs * nseg + 7) / 8 * seg * 8);
-        if (a.T == 1) hipLaunchKernelGGL(attn_fused<true>, grid, dim3(256), lds, st, a, lds_slots);
-        else hipLaunchKernelGGL(attn_fused<false>, grid, dim3(256), lds, st, a, lds_slots);
+        if (use_fused2(a))
+            hipLaunchKernelGGL((attn_fused<true, 2>), dim3((grid.x + 15) / 16 * 8), dim3(512), 2 * lds, st, a, lds_slots);
+        else if (a.T == 1)
+            hipLaunchKernelGGL((attn_fused<true, 1>), grid, dim3(256), lds, st, a, lds_slots);
+        else
+            hipLaunchKernelGGL((attn_fused<false, 1>), grid, dim3(256), lds, st, a, lds_slots);
     } else {
         if (a.split4) {
             if (prep_in_scores(a))

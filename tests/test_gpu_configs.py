@@ -228,3 +228,36 @@ def test_config3_attention_batched(oracle_weights, B, L):
         assert d.max() <= LOGIT_MAX and d.mean() <= LOGIT_MEAN
     s1.close()
     e.close()
+
+
+def test_attention_two_items_per_block_bit_identical():
+    """One row per lane at batched lanes runs two (row, kv head) items per attention block
+    (engine option attn_pair). With ragged contexts (lanes l and l + 4, which share a block,
+    alternate between 300 and 900 cached slots, so the halves run different part counts) and
+    100 lanes (the last block has idle halves), logits and tokens equal the one-item blocks'
+    bit for bit."""
+    from qwen35 import Engine, State
+    print("attention two items per block", flush=True)
+    B = 100
+    e = Engine(max_rows=128, max_ctx=1024, seed=0, use_graph=False)
+    try:
+        toks = [int(t) for t in np.random.default_rng(5).integers(0, 248320, B)]
+        outs = []
+        for pair in (1, 0):
+            e.set_option("attn_pair", pair)
+            short, long_ = State(e, B, 1000), State(e, B, 1000)
+            short.seed(3, 300)
+            long_.seed(4, 900)
+            for ln in range(B):
+                if (ln // 4) % 2:
+                    long_.copy_lane(ln, short, ln)
+            outs.append(short.decode_step(toks, logits=True))
+            outs.append(short.decode_step(outs[-1][0], logits=True))
+            short.close()
+            long_.close()
+        for k in range(2):
+            assert np.array_equal(outs[k][0], outs[2 + k][0]), k
+            assert np.array_equal(outs[k][1].view(np.uint32), outs[2 + k][1].view(np.uint32)), k
+    finally:
+        e.set_option("attn_pair", 1)
+        e.close()
