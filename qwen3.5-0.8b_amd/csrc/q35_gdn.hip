@@ -286,7 +286,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     __shared__ float qs[128], ks[128], vs[VC];
     __shared__ float red[NG][VC];            // r partials, then o partials
     __shared__ float wred[4];
-    __shared__ float gate_s[2];
+    __shared__ float gate_s[2][2];           // (decay, beta) of items with even / odd k
     // item k's row metadata: lane | cur << 16 | wcur << 20 | pend code << 24
     __shared__ int meta[kPersistMaxItems];
     const int nk = (nitems - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
@@ -309,6 +309,17 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         uint2 cpk, dpk, z4, g4;      // z4 / g4: z and gnorm of columns 4 (lane % 32) .. +3 (wave 0's y)
     };
     const uint16_t* gnw = a.gnorm ? a.gnorm : a.dt_bias;   // any valid address when unused
+    // an item's gates (decay e^g, g = -e^A_log softplus(a + dt_bias); beta = sigmoid(b)), made by
+    // one thread: for item k + 1 by thread 64 while wave 0 finishes item k (waves 1-3 would
+    // otherwise wait for it at the next item's first barrier), for the first item in its conv phase
+    auto gates = [&](const Ops& o, float* dst) {
+        const float A = -expf(bf2f(o.alog));
+        const float aa = bf2f(o.aa) + bf2f(o.dtb);
+        float sp = aa > 20.f ? aa : log1pf(expf(aa));
+        float g = A * sp;
+        dst[0] = expf(g);
+        dst[1] = sigmoid_f(bf2f(o.bb));
+    };
     // the next item's state rows 4g .. 4g+3 of this thread (the four groups are issued at four
     // points of an item's compute, so the memory pipe stays busy through it instead of the
     // wave stalling on one burst of 16 DMA issues and then leaving the pipe idle)
@@ -411,7 +422,6 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         cw[2] = __uint_as_float(op.cpk.y << 16); cw[3] = __uint_as_float(op.cpk.y & 0xffff0000u);
         cvw[0] = __uint_as_float(op.dpk.x << 16); cvw[1] = __uint_as_float(op.dpk.x & 0xffff0000u);
         cvw[2] = __uint_as_float(op.dpk.y << 16); cvw[3] = __uint_as_float(op.dpk.y & 0xffff0000u);
-        const float A = -expf(bf2f(op.alog));
         const float ox = bf2f(op.x), oxv = bf2f(op.xv);
         // causal conv: taps over [w0, w1, w2, raw] in order, f32, one rounding, bf16 SiLU
         {
@@ -428,13 +438,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
             }
             float ss = wave_sum(uq * uq);
             if ((tid & 63) == 0) wred[tid >> 6] = ss;
-            if (tid == 0) {
-                const float aa = bf2f(op.aa) + bf2f(op.dtb);
-                float sp = aa > 20.f ? aa : log1pf(expf(aa));
-                float g = A * sp;
-                gate_s[0] = expf(g);
-                gate_s[1] = sigmoid_f(bf2f(op.bb));
-            }
+            if (tid == 0 && k == 0) gates(op, gate_s[0]);
         }
         // the conv window after this row: its values are final now
         float* Wo = Wbase + ((wcur + 1) % a.nslots) * a.W_slot;
@@ -446,7 +450,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         // rounded products as a normalisation pass, without its barrier)
         const float rq = rsqrtf((wred[0] + wred[1]) + 1e-6f);
         const float rk = rsqrtf((wred[2] + wred[3]) + 1e-6f);
-        const float gam = gate_s[0], beta = gate_s[1];
+        const float gam = gate_s[k & 1][0], beta = gate_s[k & 1][1];
         float kn[KR], qn[KR];
 #pragma unroll
         for (int i = 0; i < KR; ++i) {
@@ -510,6 +514,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         // from the quads of lanes 0-15 and 16-31. No barrier ends the item: every LDS array the
         // next item writes before its first barrier was last read before this item's last one,
         // except red (read here), which the next item writes only after that first barrier.
+        if (more && tid == 64) gates(nx, gate_s[(k + 1) & 1]);
         if (wv == 0) {
             float oj[CW];
 #pragma unroll
