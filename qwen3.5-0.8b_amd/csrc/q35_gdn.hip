@@ -38,6 +38,19 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     const int gi = blockIdx.x, h = blockIdx.y, cs = blockIdx.z;
     const int tid = threadIdx.x;
     const int jc = (tid % CG) * CW, kg = tid / CG;
+    // channels: tid < 128 -> q channel, else k channel; tid < VC also a v channel
+    const int cqk = tid < 128 ? h * 128 + tid : 2048 + h * 128 + (tid - 128);
+    const int cv = 4096 + h * 128 + cs * VC + tid;
+    const bool hasv = tid < VC;
+    const int cvc = hasv ? cv : cqk;                 // a valid channel for every thread
+    // first, every load that does not depend on the row's lane and slots (one memory round
+    // trip with the row metadata, instead of one more after the state): the first row's
+    // projection inputs, the conv taps and the gate parameters, as raw bits
+    const uint16_t* pr0 = a.proj + (size_t)(gi * a.T) * kGdnInRows;
+    uint16_t xr = pr0[cqk], xvr = pr0[cvc], bbr = pr0[kGdnBOff + h], aar = pr0[kGdnAOff + h];
+    const uint2 cpk = *(const uint2*)(a.conv_w + (size_t)cqk * 4);
+    const uint2 dpk = *(const uint2*)(a.conv_w + (size_t)cvc * 4);
+    const uint16_t alogr = a.A_log[h], dtbr = a.dt_bias[h];
     const int lane = a.lane[gi * a.T];
     const int cur = a.cur ? a.cur[gi * a.T] : 0;
     const int wcur = a.wcur ? a.wcur[gi * a.T] : cur;
@@ -59,24 +72,8 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     const float* Sin = Sbase + cur * a.S_slot;
     const float* Win = Wbase + wcur * a.W_slot;
 
-    // channels: tid < 128 -> q channel, else k channel; tid < VC also a v channel
-    const int cqk = tid < 128 ? h * 128 + tid : 2048 + h * 128 + (tid - 128);
-    const int cv = 4096 + h * 128 + cs * VC + tid;
-    const bool hasv = tid < VC;
     float w0 = Win[cqk], w1 = Win[6144 + cqk], w2 = Win[12288 + cqk];
-    float v0 = 0.f, v1 = 0.f, v2 = 0.f;
-    if (hasv) { v0 = Win[cv]; v1 = Win[6144 + cv]; v2 = Win[12288 + cv]; }
-    float cw[4], cvw[4] = {0.f, 0.f, 0.f, 0.f};
-    {
-        uint2 c = *(const uint2*)(a.conv_w + (size_t)cqk * 4);
-        cw[0] = __uint_as_float(c.x << 16); cw[1] = __uint_as_float(c.x & 0xffff0000u);
-        cw[2] = __uint_as_float(c.y << 16); cw[3] = __uint_as_float(c.y & 0xffff0000u);
-        if (hasv) {
-            uint2 d = *(const uint2*)(a.conv_w + (size_t)cv * 4);
-            cvw[0] = __uint_as_float(d.x << 16); cvw[1] = __uint_as_float(d.x & 0xffff0000u);
-            cvw[2] = __uint_as_float(d.y << 16); cvw[3] = __uint_as_float(d.y & 0xffff0000u);
-        }
-    }
+    float v0 = Win[cvc], v1 = Win[6144 + cvc], v2 = Win[12288 + cvc];   // used by v channels only
     float s[KR][CW];
 #pragma unroll
     for (int i = 0; i < KR; ++i) {
@@ -122,22 +119,32 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
         }
     }
 
-    const float A = -expf(bf2f(a.A_log[h]));
-    const float dtb = bf2f(a.dt_bias[h]);
+    float cw[4], cvw[4];
+    cw[0] = __uint_as_float(cpk.x << 16); cw[1] = __uint_as_float(cpk.x & 0xffff0000u);
+    cw[2] = __uint_as_float(cpk.y << 16); cw[3] = __uint_as_float(cpk.y & 0xffff0000u);
+    cvw[0] = __uint_as_float(dpk.x << 16); cvw[1] = __uint_as_float(dpk.x & 0xffff0000u);
+    cvw[2] = __uint_as_float(dpk.y << 16); cvw[3] = __uint_as_float(dpk.y & 0xffff0000u);
+    const float A = -expf(bf2f(alogr));
+    const float dtb = bf2f(dtbr);
 
     for (int t = 0; t < a.T; ++t) {
         const int r = gi * a.T + t;
         const uint16_t* pr = a.proj + (size_t)r * kGdnInRows;
+        const uint16_t xcur = xr, xvcur = xvr, bbcur = bbr, aacur = aar;
+        if (t + 1 < a.T) {      // the next row's inputs load while this row computes
+            const uint16_t* pn = pr + kGdnInRows;
+            xr = pn[cqk]; xvr = pn[cvc]; bbr = pn[kGdnBOff + h]; aar = pn[kGdnAOff + h];
+        }
         // causal conv: taps over [w0, w1, w2, raw] in order, f32, one rounding, bf16 SiLU
         {
-            float x = bf2f(pr[cqk]);
+            float x = bf2f(xcur);
             float u = 0.f;
             u = u + w0 * cw[0]; u = u + w1 * cw[1]; u = u + w2 * cw[2]; u = u + x * cw[3];
             float uq = rbf(silu_f(rbf(u)));
             w0 = w1; w1 = w2; w2 = x;
             if (tid < 128) qs[tid] = uq; else ks[tid - 128] = uq;
             if (hasv) {
-                float xv = bf2f(pr[cv]);
+                float xv = bf2f(xvcur);
                 float uv = 0.f;
                 uv = uv + v0 * cvw[0]; uv = uv + v1 * cvw[1]; uv = uv + v2 * cvw[2]; uv = uv + xv * cvw[3];
                 vs[tid] = rbf(silu_f(rbf(uv)));
@@ -147,8 +154,8 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
             float ss = wave_sum(uq * uq);
             if ((tid & 63) == 0) wred[tid >> 6] = ss;
             if (tid == 0) {
-                float bb = bf2f(pr[kGdnBOff + h]);
-                float aa = bf2f(pr[kGdnAOff + h]) + dtb;
+                float bb = bf2f(bbcur);
+                float aa = bf2f(aacur) + dtb;
                 float sp = aa > 20.f ? aa : log1pf(expf(aa));
                 float g = A * sp;
                 gate_s[0] = expf(g);
