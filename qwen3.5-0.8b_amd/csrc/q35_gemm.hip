@@ -160,7 +160,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, q35_f32x4 sum, int n
 // 57 KiB of chain reads per block, more than its weight tile) is shared by TPB tiles; every
 // wave runs TPB MFMA chains on the same A fragments. Used with TPB = 2 for N >= 4096
 // (batch 1: 1,171 -> 1,209 tok/s; TPB = 4, a quarter of the blocks: 1,168).
-template <int AM, int EM, int TPB = 1>
+// KP: chain loads of the kANormXP fold (16, or 8 when the producing GEMM left at most 8)
+template <int AM, int EM, int TPB = 1, int KP = 16>
 __global__ void __launch_bounds__(TPB > 1 ? 256 : 1024) gemm_small_m(GemmArgs a) {   // TPB > 1: K = 1024, 4 waves
     const int nt = blockIdx.x * TPB;
     const int mt = blockIdx.y;
@@ -242,9 +243,9 @@ __global__ void __launch_bounds__(TPB > 1 ? 256 : 1024) gemm_small_m(GemmArgs a)
             const uint16_t* xr0 = (const uint16_t*)a.X;
             const int q0 = 256 * kb + 4 * lane;
             const uint2 xq = *(const uint2*)(xr0 + q0);
-            float4 d[16];
+            float4 d[KP];
 #pragma unroll
-            for (int j = 0; j < 16; ++j)     // unconditional clamped loads: no wait at a join
+            for (int j = 0; j < KP; ++j)     // unconditional clamped loads: no wait at a join
                 d[j] = *(const float4*)(a.kpart + (size_t)min(j, a.kpb - 1) * kHidden + q0);
             const q35_u32x4 wc = *(const q35_u32x4*)(a.aux_w + k0);
             asm volatile("" ::: "memory");     // keep the producer's loads ahead of W
@@ -252,7 +253,7 @@ __global__ void __launch_bounds__(TPB > 1 ? 256 : 1024) gemm_small_m(GemmArgs a)
             __builtin_amdgcn_sched_barrier(0);   // ... and its arithmetic behind W's issue
             float4 dsum = d[0];
 #pragma unroll
-            for (int j = 1; j < 16; ++j)
+            for (int j = 1; j < KP; ++j)
                 if (j < a.kpb) { dsum.x = dsum.x + d[j].x; dsum.y = dsum.y + d[j].y; dsum.z = dsum.z + d[j].z; dsum.w = dsum.w + d[j].w; }
             const float xv0[4] = {__uint_as_float(xq.x << 16), __uint_as_float(xq.x & 0xffff0000u),
                                   __uint_as_float(xq.y << 16), __uint_as_float(xq.y & 0xffff0000u)};
@@ -1055,9 +1056,12 @@ static hipError_t launch_am_em(const GemmArgs& a, hipStream_t st) {
         if (EM == kEPartial)
             hipLaunchKernelGGL((gemm_small_m<AM, EM>), dim3(a.N / 16, 1, KB), dim3(64), lds, st, a);
         else if ((AM == kANormX || AM == kANormXP) && EM == kEStore && a.M == 1 && a.forms.gemv_tpb == 2 &&
-                 a.N % 32 == 0 && a.N >= 4096 && KB == 4)
-            hipLaunchKernelGGL((gemm_small_m<AM, EM, 2>), dim3(a.N / 32, 1, 1), dim3(64 * KB), 0, st, a);
-        else
+                 a.N % 32 == 0 && a.N >= 4096 && KB == 4) {
+            if (AM == kANormXP && a.kpb <= 8)      // after out_proj / o_proj (8 chains)
+                hipLaunchKernelGGL((gemm_small_m<AM, EM, 2, 8>), dim3(a.N / 32, 1, 1), dim3(64 * KB), 0, st, a);
+            else
+                hipLaunchKernelGGL((gemm_small_m<AM, EM, 2>), dim3(a.N / 32, 1, 1), dim3(64 * KB), 0, st, a);
+        } else
             hipLaunchKernelGGL((gemm_small_m<AM, EM>), dim3(a.N / 16, 1, 1), dim3(64 * KB), lds, st, a);
         return hipGetLastError();
     }
