@@ -81,6 +81,16 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
+// A wave-uniform pointer as scalar registers the compiler cannot fold with a lane's offset, so
+// that p + (32-bit lane offset) takes the scalar-base global address form (no vector address
+// arithmetic per load).
+__device__ __forceinline__ const char* uniform_ptr(const char* p) {
+    const unsigned long long u = (unsigned long long)p;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)u);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(u >> 32));
+    return (const char*)(((unsigned long long)hi << 32) | lo);
+}
+
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 

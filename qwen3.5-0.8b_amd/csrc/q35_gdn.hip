@@ -283,7 +283,11 @@ constexpr int kPersistLds = 64 * 1024 + kMaxPend * kFacStride * 4;   // state + 
 __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     constexpr int VC = 128, CW = 4, CG = 32, KR = 16, NG = 16, GPT = 2;
     const int tid = threadIdx.x, lane64 = tid & 63, wv = tid >> 6;
-    const int jc = (tid % CG) * CW, kg = tid / CG;
+    // wave w owns value columns 32w .. 32w+31 over all 128 k rows: lane (kg, quad) holds k rows
+    // 16 kg .. +15 of columns jc .. jc+3. The delta rule's columns are independent, so the r and
+    // o reductions over k stay inside the wave (through its own columns of red, no barrier).
+    const int jc = wv * 32 + (lane64 & 7) * CW, kg = lane64 >> 3;
+    const int cc = wv * 32 + (lane64 & 31);      // the column a lane < 32 reduces
     // Dynamic LDS, the only target of the LDS-DMA prefetch (so the compiler need not make an
     // access to the static arrays below wait for it): the next item's state [4 waves][16 rows]
     // [64 lanes], then its pending factor rows (row p at p * kFacStride; 5 KiB, so that two
@@ -294,6 +298,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     __shared__ float red[NG][VC];            // r partials, then o partials
     __shared__ float wred[4];
     __shared__ float gate_s[2][2];           // (decay, beta) of items with even / odd k
+    __shared__ float qq[32];                 // the item's 32 quads of o^2, in column order
     // item k's row metadata: lane | cur << 16 | wcur << 20 | pend code << 24
     __shared__ int meta[kPersistMaxItems];
     const int nk = (nitems - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
@@ -313,7 +318,8 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     struct Ops {
         float w0, w1, w2, v0, v1, v2;
         uint16_t x, xv, bb, aa, alog, dtb;
-        uint2 cpk, dpk, z4, g4;      // z4 / g4: z and gnorm of columns 4 (lane % 32) .. +3 (wave 0's y)
+        uint16_t z1, g1;             // z and gnorm weight of column cc (y of lanes < 32)
+        uint2 cpk, dpk;
     };
     const uint16_t* gnw = a.gnorm ? a.gnorm : a.dt_bias;   // any valid address when unused
     // an item's gates (decay e^g, g = -e^A_log softplus(a + dt_bias); beta = sigmoid(b)), made by
@@ -330,21 +336,48 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     // the next item's state rows 4g .. 4g+3 of this thread (the four groups are issued at four
     // points of an item's compute, so the memory pipe stays busy through it instead of the
     // wave stalling on one burst of 16 DMA issues and then leaving the pipe idle)
-    const float* Snext = nullptr;
+    // (wave-uniform head base in scalar registers plus the lane's fixed 32-bit byte offset: the
+    // loads take the scalar-base address form and cost no vector address arithmetic)
+    const char* Snext = nullptr;
+    const unsigned voff = (unsigned)(kg * KR * 128 + jc) * 4u;
+    const int wvu = __builtin_amdgcn_readfirstlane(wv);
     auto fetch_rows = [&](int g) {
 #pragma unroll
         for (int i = 4 * g; i < 4 * g + 4; ++i)
-            __builtin_amdgcn_global_load_lds((const void*)(Snext + (kg * KR + i) * 128 + jc),
-                                             (__attribute__((address_space(3))) void*)(sbuf + (wv * KR + i) * 64), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(uniform_ptr(Snext + i * 512) + voff),
+                                             (__attribute__((address_space(3))) void*)(sbuf + (wvu * KR + i) * 64), 16, 0, 0);
     };
     auto fetch = [&](int k, Ops& o) {
         const int item = (int)blockIdx.x + k * (int)gridDim.x;
         const int gi = item >> 4, h = item & 15;
-        const int m = meta[k];
+        const int m = __builtin_amdgcn_readfirstlane(meta[k]);
         const int ln = m & 0xffff, cu = (m >> 16) & 15, wc = (m >> 20) & 15, pn = (m >> 24) & 31;
-        Snext = a.S + ln * a.S_lane + a.S_layer + (long long)h * 16384 + cu * a.S_slot;
+        Snext = (const char*)(a.S + ln * a.S_lane + a.S_layer + (long long)h * 16384 + cu * a.S_slot);
         fetch_rows(0);
-        // factor rows 0 .. npend-1: 16-byte chunk c = 66 p + q of row p, chunks tid, tid + 256
+        const float* Win = a.win + ln * a.W_lane + a.W_layer + wc * a.W_slot;
+        const uint16_t* pr = a.proj + (size_t)gi * kGdnInRows;
+        const int cqk = tid < 128 ? h * 128 + tid : 2048 + h * 128 + (tid - 128);
+        const int cv = 4096 + h * 128 + (tid & 127);      // threads >= 128 load a valid channel, unused
+        o.w0 = Win[cqk]; o.w1 = Win[6144 + cqk]; o.w2 = Win[12288 + cqk];
+        o.v0 = Win[cv]; o.v1 = Win[6144 + cv]; o.v2 = Win[12288 + cv];
+        o.cpk = *(const uint2*)(a.conv_w + (size_t)cqk * 4);
+        o.dpk = *(const uint2*)(a.conv_w + (size_t)cv * 4);
+        o.x = pr[cqk];
+        o.xv = pr[cv];
+        o.z1 = pr[kGdnZOff + h * 128 + cc];
+        o.g1 = gnw[a.gnorm ? cc : 0];
+        o.bb = pr[kGdnBOff + h];
+        o.aa = pr[kGdnAOff + h];
+        o.alog = a.A_log[h];
+        o.dtb = a.dt_bias[h];
+    };
+    // item k's pending factor rows 0 .. npend-1 into fbuf: 16-byte chunk c = 66 p + q of row p,
+    // chunks tid, tid + 256 (issued once every wave is done with the previous rows)
+    auto fetch_fac = [&](int k) {
+        const int item = (int)blockIdx.x + k * (int)gridDim.x;
+        const int h = item & 15;
+        const int m = meta[k];
+        const int ln = m & 0xffff, pn = (m >> 24) & 31;
         const int nc = (pn & 15) * (kFacStride / 4);
         const float* F0 = a.fac + ln * a.fac_lane + ((pn >> 4) & 1) * a.fac_set + h * kFacStride;
 #pragma unroll
@@ -357,26 +390,14 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                                                  16, 0, 0);
             }
         }
-        const float* Win = a.win + ln * a.W_lane + a.W_layer + wc * a.W_slot;
-        const uint16_t* pr = a.proj + (size_t)gi * kGdnInRows;
-        const int cqk = tid < 128 ? h * 128 + tid : 2048 + h * 128 + (tid - 128);
-        const int cv = 4096 + h * 128 + (tid & 127);      // threads >= 128 load a valid channel, unused
-        o.w0 = Win[cqk]; o.w1 = Win[6144 + cqk]; o.w2 = Win[12288 + cqk];
-        o.v0 = Win[cv]; o.v1 = Win[6144 + cv]; o.v2 = Win[12288 + cv];
-        o.cpk = *(const uint2*)(a.conv_w + (size_t)cqk * 4);
-        o.dpk = *(const uint2*)(a.conv_w + (size_t)cv * 4);
-        o.x = pr[cqk];
-        o.xv = pr[cv];
-        o.z4 = *(const uint2*)(pr + kGdnZOff + h * 128 + (lane64 & 31) * 4);
-        o.g4 = *(const uint2*)(gnw + (a.gnorm ? (lane64 & 31) * 4 : 0));
-        o.bb = pr[kGdnBOff + h];
-        o.aa = pr[kGdnAOff + h];
-        o.alog = a.A_log[h];
-        o.dtb = a.dt_bias[h];
     };
+    // orders a wave's own LDS traffic for the compiler: one wave's LDS accesses execute in
+    // program order, so lanes of the wave see each other's earlier writes without a barrier
+    auto wave_sync = [] { asm volatile("" ::: "memory"); };
     Ops nx;
     if (nk > 0) {
         fetch(0, nx);
+        fetch_fac(0);
         fetch_rows(1); fetch_rows(2); fetch_rows(3);
     }
     for (int k = 0; k < nk; ++k) {
@@ -419,7 +440,6 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                         s[i][c] = delta_update(s[i][c], kk[i], dd[c]);
                     }
             }
-            lds_barrier();      // fbuf is refilled by the next item's fetch
         }
         const bool more = k + 1 < nk;
         if (more) fetch(k + 1, nx);
@@ -452,7 +472,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2;
         if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
         lds_barrier();
-        if (more) fetch_rows(1);
+        if (more) { fetch_fac(k + 1); fetch_rows(1); }   // fbuf's rows were read before this barrier
         // q~ and k~ of this thread's 16 rows, normalised where they are read (the same two
         // rounded products as a normalisation pass, without its barrier)
         const float rq = rsqrtf((wred[0] + wred[1]) + 1e-6f);
@@ -476,15 +496,21 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                 }
                 red[kg * GPT + gq][jc + c] = rp;
             }
-        lds_barrier();
+        wave_sync();
         if (more) fetch_rows(2);
-        float dv[CW];
-#pragma unroll
-        for (int c = 0; c < CW; ++c) {
+        // lane L < 32 sums column cc's 16 partials in order and leaves its dv in vs[cc] (read
+        // only here); the wave's lanes then take the dv of their four columns
+        if (lane64 < 32) {
             float rj = 0.f;
 #pragma unroll
-            for (int i = 0; i < NG; ++i) rj += red[i][jc + c];
-            dv[c] = __fmul_rn(beta, vs[jc + c] - rj);
+            for (int i = 0; i < NG; ++i) rj += red[i][cc];
+            vs[cc] = __fmul_rn(beta, vs[cc] - rj);
+        }
+        wave_sync();
+        float dv[CW];
+        {
+            const q35_f32x4 d4 = *(const q35_f32x4*)(vs + jc);
+            dv[0] = d4[0]; dv[1] = d4[1]; dv[2] = d4[2]; dv[3] = d4[3];
         }
         if (rec) {                // gdn_kernel's factor record of a deferred row
             float* F = a.fac + lane * a.fac_lane + pset * a.fac_set + npend * a.fac_row + h * kFacStride;
@@ -492,7 +518,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
             if (tid >= 128) F[tid - 128] = __fmul_rn(ks[tid - 128], rk);
             if (tid == 0) F[256] = gam;
         }
-        lds_barrier();          // red is reused for the o partials
+        wave_sync();            // red's columns of this wave are reused for the o partials
         if (more) fetch_rows(3);
 #pragma unroll
         for (int c = 0; c < CW; ++c)
@@ -514,43 +540,37 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                 __builtin_nontemporal_store((q35_f32x4){s[i][0], s[i][1], s[i][2], s[i][3]},
                                             (q35_f32x4*)(So + (kg * KR + i) * 128 + jc));
         }
-        lds_barrier();
-        // wave 0 finishes the head: lane L < 32 sums the o partials of columns 4L .. 4L+3 and
-        // makes their gated-norm outputs; the head's two half sums of squares are formed as
-        // half_head_ss forms them (quads in column order, each ((o0^2 + o1^2) + (o2^2 + o3^2)))
-        // from the quads of lanes 0-15 and 16-31. No barrier ends the item: every LDS array the
-        // next item writes before its first barrier was last read before this item's last one,
-        // except red (read here), which the next item writes only after that first barrier.
+        wave_sync();
+        // the head's outputs: lane L < 32 sums column cc's 16 o partials in order and stores o;
+        // the gated norm needs the head's two half sums of squares, formed as half_head_ss forms
+        // them (quads in column order, each ((o0^2 + o1^2) + (o2^2 + o3^2))): a quad's four
+        // lanes pair up by shuffles and its first lane leaves the quad in qq. The barrier ending
+        // the item also keeps the next item's conv phase (qs, ks, vs, wred) from running ahead
+        // of a wave still reading them.
+        float oc = 0.f;
+#pragma unroll
+        for (int i = 0; i < NG; ++i) oc += red[i][cc];
+        {
+            const float t = __fmul_rn(oc, oc);
+            const float t2 = __fadd_rn(t, __shfl_xor(t, 1, 64));            // lanes 4j, 4j + 2
+            const float q = __fadd_rn(t2, __shfl_down(t2, 2, 64));          // lane 4j
+            if (lane64 < 32) {
+                a.o[(size_t)gi * 2048 + h * 128 + cc] = oc;
+                if ((lane64 & 3) == 0) qq[cc >> 2] = q;
+            }
+        }
         if (more && tid == 64) gates(nx, gate_s[(k + 1) & 1]);
-        if (wv == 0) {
-            float oj[CW];
+        lds_barrier();
+        if (a.y && lane64 < 32) {
+            float ss0 = 0.f, ss1 = 0.f;
 #pragma unroll
-            for (int c = 0; c < CW; ++c) {
-                oj[c] = 0.f;
-#pragma unroll
-                for (int i = 0; i < NG; ++i) oj[c] += red[i][jc + c];
+            for (int j = 0; j < 16; ++j) {
+                ss0 = __fadd_rn(ss0, qq[j]);
+                ss1 = __fadd_rn(ss1, qq[16 + j]);
             }
-            if (lane64 < 32) *(q35_f32x4*)(a.o + (size_t)gi * 2048 + h * 128 + jc) = (q35_f32x4){oj[0], oj[1], oj[2], oj[3]};
-            if (a.y) {
-                const float q = __fadd_rn(__fadd_rn(__fmul_rn(oj[0], oj[0]), __fmul_rn(oj[1], oj[1])),
-                                          __fadd_rn(__fmul_rn(oj[2], oj[2]), __fmul_rn(oj[3], oj[3])));
-                float ss0 = 0.f, ss1 = 0.f;
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    ss0 = __fadd_rn(ss0, __shfl(q, j, 64));
-                    ss1 = __fadd_rn(ss1, __shfl(q, 16 + j, 64));
-                }
-                const float rs = head_rsqrt(ss0, ss1);
-                const float zc[4] = {__uint_as_float(op.z4.x << 16), __uint_as_float(op.z4.x & 0xffff0000u),
-                                     __uint_as_float(op.z4.y << 16), __uint_as_float(op.z4.y & 0xffff0000u)};
-                const float wc[4] = {__uint_as_float(op.g4.x << 16), __uint_as_float(op.g4.x & 0xffff0000u),
-                                     __uint_as_float(op.g4.y << 16), __uint_as_float(op.g4.y & 0xffff0000u)};
-                uint32_t yb[4];
-#pragma unroll
-                for (int c = 0; c < CW; ++c) yb[c] = f2bf(__fmul_rn(__fmul_rn(wc[c], __fmul_rn(oj[c], rs)), silu_f(zc[c])));
-                if (lane64 < 32)
-                    *(uint2*)(a.y + (size_t)gi * 2048 + h * 128 + jc) = (uint2){yb[0] | (yb[1] << 16), yb[2] | (yb[3] << 16)};
-            }
+            const float rs = head_rsqrt(ss0, ss1);
+            const float yv = __fmul_rn(__fmul_rn(bf2f(op.g1), __fmul_rn(oc, rs)), silu_f(bf2f(op.z1)));
+            a.y[(size_t)gi * 2048 + h * 128 + cc] = f2bf(yv);
         }
     }
 }
