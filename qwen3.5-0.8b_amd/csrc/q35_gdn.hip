@@ -21,23 +21,39 @@
 // The engine advances the slots after the step.
 //
 // Grid: (lane group, head, column slice). A block owns VC = 128/CS value columns of one
-// head; thread (column group, kg) holds S[kg*KR .. kg*KR+KR) of CW adjacent columns in
-// registers (CW = 4 when a block owns the whole head: 16-byte state loads and stores).
+// head and wave w owns VC/4 of them over all 128 k rows: lane (kg, column group) holds
+// S[kg*KR .. kg*KR+KR) of CW adjacent columns in registers (CW = 4 when a block owns the
+// whole head: 16-byte state loads and stores). The delta rule's value columns are
+// independent, so the reductions over k stay inside a wave (its own columns of red_r /
+// red_o, no barrier); a row needs one block barrier (after the conv phase: q~, k~, v and the
+// gates are read by every wave), plus one for the fused gated norm. The conv outputs, norms
+// and gates are double-buffered by row parity, so row t + 1's conv phase cannot overwrite
+// what a slower wave still reads of row t.
 #include "q35_common.h"
 #include "q35_kernels.h"
 
 namespace q35 {
 
+// A block barrier for LDS traffic only: __syncthreads() also orders global memory, for which
+// the compiler makes every wave wait for all of its outstanding loads first, including loads
+// issued ahead for later work, which would then never overlap the current work.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// orders a wave's own LDS traffic for the compiler: one wave's LDS accesses execute in
+// program order, so lanes of the wave see each other's earlier writes without a barrier
+__device__ __forceinline__ void wave_sync() { asm volatile("" ::: "memory"); }
+
 template <int CS>
 __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     constexpr int VC = 128 / CS;                 // value columns of this block
-    constexpr int CW = CS == 1 ? 4 : 1;          // adjacent columns per thread (16-byte I/O)
-    constexpr int CG = VC / CW;                  // column groups
-    constexpr int NKG = 256 / CG;                // k-row groups
-    constexpr int KR = 128 / NKG;                // k rows per thread (a multiple of 8)
+    constexpr int CW = CS == 1 ? 4 : 1;          // adjacent columns per lane (16-byte I/O)
+    constexpr int WC = VC / 4;                   // value columns of a wave
+    constexpr int CGW = WC / CW;                 // column groups of a wave
+    constexpr int NKW = 64 / CGW;                // k-row groups of a wave
+    constexpr int KR = 128 / NKW;                // k rows per lane (a multiple of 8)
     const int gi = blockIdx.x, h = blockIdx.y, cs = blockIdx.z;
-    const int tid = threadIdx.x;
-    const int jc = (tid % CG) * CW, kg = tid / CG;
+    const int tid = threadIdx.x, lane64 = tid & 63, wv = tid >> 6;
+    const int jc = wv * WC + (lane64 % CGW) * CW, kg = lane64 / CGW;
+    const int cc = wv * WC + (lane64 % WC);      // CS = 1: the column a lane < 32 reduces
     // channels: tid < 128 -> q channel, else k channel; tid < VC also a v channel
     const int cqk = tid < 128 ? h * 128 + tid : 2048 + h * 128 + (tid - 128);
     const int cv = 4096 + h * 128 + cs * VC + tid;
@@ -58,14 +74,13 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     const int npend = pnd & 15, pset = (pnd >> 4) & 1;
     const bool rec = !a.ckpt && npend < a.defer;    // this decode row becomes pending row npend
 
-    __shared__ float qs[128], ks[128], vs[VC];
+    __shared__ float qs[2][128], ks[2][128], vs[2][VC];   // by row parity
+    __shared__ float wred[2][4];
+    __shared__ float gate_s[2][2];
     constexpr int NG = 16;            // fixed reduction groups of 8 k-rows, for every CS
-    constexpr int GPT = KR / 8;       // groups per thread
+    constexpr int GPT = KR / 8;       // groups per lane
     __shared__ float red_r[NG][VC], red_o[NG][VC];
-    __shared__ float wred[4];
-    __shared__ float gate_s[2];
-    __shared__ float ohead[CS == 1 ? 128 : 1];
-    __shared__ float hss2[2];
+    __shared__ float qq[CS == 1 ? 32 : 1];           // CS = 1: the head's quads of o^2
 
     float* Sbase = a.S + lane * a.S_lane + a.S_layer + (long long)h * 16384;
     float* Wbase = a.win + lane * a.W_lane + a.W_layer;
@@ -129,6 +144,7 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
 
     for (int t = 0; t < a.T; ++t) {
         const int r = gi * a.T + t;
+        const int pb = t & 1;
         const uint16_t* pr = a.proj + (size_t)r * kGdnInRows;
         const uint16_t xcur = xr, xvcur = xvr, bbcur = bbr, aacur = aar;
         if (t + 1 < a.T) {      // the next row's inputs load while this row computes
@@ -142,35 +158,38 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
             u = u + w0 * cw[0]; u = u + w1 * cw[1]; u = u + w2 * cw[2]; u = u + x * cw[3];
             float uq = rbf(silu_f(rbf(u)));
             w0 = w1; w1 = w2; w2 = x;
-            if (tid < 128) qs[tid] = uq; else ks[tid - 128] = uq;
+            if (tid < 128) qs[pb][tid] = uq; else ks[pb][tid - 128] = uq;
             if (hasv) {
                 float xv = bf2f(xvcur);
                 float uv = 0.f;
                 uv = uv + v0 * cvw[0]; uv = uv + v1 * cvw[1]; uv = uv + v2 * cvw[2]; uv = uv + xv * cvw[3];
-                vs[tid] = rbf(silu_f(rbf(uv)));
+                vs[pb][tid] = rbf(silu_f(rbf(uv)));
                 v0 = v1; v1 = v2; v2 = xv;
             }
             // squared norms: waves 0-1 hold q, waves 2-3 hold k
             float ss = wave_sum(uq * uq);
-            if ((tid & 63) == 0) wred[tid >> 6] = ss;
+            if ((tid & 63) == 0) wred[pb][tid >> 6] = ss;
             if (tid == 0) {
                 float bb = bf2f(bbcur);
                 float aa = bf2f(aacur) + dtb;
                 float sp = aa > 20.f ? aa : log1pf(expf(aa));
                 float g = A * sp;
-                gate_s[0] = expf(g);
-                gate_s[1] = sigmoid_f(bb);
+                gate_s[pb][0] = expf(g);
+                gate_s[pb][1] = sigmoid_f(bb);
             }
         }
-        __syncthreads();
-        {
-            const float rq = rsqrtf((wred[0] + wred[1]) + 1e-6f);
-            const float rk = rsqrtf((wred[2] + wred[3]) + 1e-6f);
-            if (tid < 128) qs[tid] = __fmul_rn(__fmul_rn(qs[tid], rq), 0.08838834764831845f);
-            else ks[tid - 128] = __fmul_rn(ks[tid - 128], rk);
+        lds_barrier();
+        // q~ and k~ of this lane's rows, normalised where they are read (the same two rounded
+        // products as a normalisation pass)
+        const float rq = rsqrtf((wred[pb][0] + wred[pb][1]) + 1e-6f);
+        const float rk = rsqrtf((wred[pb][2] + wred[pb][3]) + 1e-6f);
+        const float gam = gate_s[pb][0], beta = gate_s[pb][1];
+        float kn[KR], qn[KR];
+#pragma unroll
+        for (int i = 0; i < KR; ++i) {
+            kn[i] = __fmul_rn(ks[pb][kg * KR + i], rk);
+            qn[i] = __fmul_rn(__fmul_rn(qs[pb][kg * KR + i], rq), 0.08838834764831845f);
         }
-        __syncthreads();
-        const float gam = gate_s[0], beta = gate_s[1];
         // reductions over k: 8-row partial sums, then the 16 partials in order -- the same
         // arithmetic for every column-slice count, so batched lanes match batch 1 exactly
 #pragma unroll
@@ -181,18 +200,29 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
 #pragma unroll
                 for (int i = gq * 8; i < gq * 8 + 8; ++i) {
                     s[i][c] = __fmul_rn(s[i][c], gam);
-                    rp = fmaf(s[i][c], ks[kg * KR + i], rp);
+                    rp = fmaf(s[i][c], kn[i], rp);
                 }
                 red_r[kg * GPT + gq][jc + c] = rp;
             }
-        __syncthreads();
+        wave_sync();
         float dv[CW];
+        if constexpr (CW == 4) {
+            // lane L < 32 sums column cc's 16 partials and leaves its dv in vs (read only
+            // here); the wave's lanes then take the dv of their four columns
+            if (lane64 < 32) {
+                float rj = 0.f;
 #pragma unroll
-        for (int c = 0; c < CW; ++c) {
+                for (int i = 0; i < NG; ++i) rj += red_r[i][cc];
+                vs[pb][cc] = __fmul_rn(beta, vs[pb][cc] - rj);
+            }
+            wave_sync();
+            const q35_f32x4 d4 = *(const q35_f32x4*)(vs[pb] + jc);
+            dv[0] = d4[0]; dv[CW > 1 ? 1 : 0] = d4[1]; dv[CW > 2 ? 2 : 0] = d4[2]; dv[CW > 3 ? 3 : 0] = d4[3];
+        } else {
             float rj = 0.f;
 #pragma unroll
-            for (int i = 0; i < NG; ++i) rj += red_r[i][jc + c];
-            dv[c] = __fmul_rn(beta, vs[jc + c] - rj);
+            for (int i = 0; i < NG; ++i) rj += red_r[i][jc];
+            dv[0] = __fmul_rn(beta, vs[pb][jc] - rj);
         }
         if ((a.ckpt && a.fac_write) || rec) {
             // verify row t's factors, into the set not being read; a deferred decode row's as
@@ -203,7 +233,7 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
 #pragma unroll
                 for (int c = 0; c < CW; ++c) F[128 + cs * VC + jc + c] = dv[c];
             }
-            if (cs == 0 && tid >= 128) F[tid - 128] = ks[tid - 128];
+            if (cs == 0 && tid >= 128) F[tid - 128] = __fmul_rn(ks[pb][tid - 128], rk);
             if (cs == 0 && tid == 0) F[256] = gam;
         }
 #pragma unroll
@@ -213,32 +243,46 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
                 float op = 0.f;
 #pragma unroll
                 for (int i = gq * 8; i < gq * 8 + 8; ++i) {
-                    s[i][c] = delta_update(s[i][c], ks[kg * KR + i], dv[c]);
-                    op = fmaf(qs[kg * KR + i], s[i][c], op);
+                    s[i][c] = delta_update(s[i][c], kn[i], dv[c]);
+                    op = fmaf(qn[i], s[i][c], op);
                 }
                 red_o[kg * GPT + gq][jc + c] = op;
             }
-        __syncthreads();
-        if (kg == 0) {
+        wave_sync();
+        if constexpr (CW == 4) {
+            // lane L < 32 sums column cc's o partials and stores o; with the fused gated norm
+            // the head's two half sums of squares are formed as half_head_ss forms them
+            // (quads in column order, each ((o0^2 + o1^2) + (o2^2 + o3^2))): a quad's four
+            // lanes pair up by shuffles and its first lane leaves the quad in qq
+            float oc = 0.f;
 #pragma unroll
-            for (int c = 0; c < CW; ++c) {
+            for (int i = 0; i < NG; ++i) oc += red_o[i][cc];
+            if (lane64 < 32) a.o[(size_t)r * 2048 + h * 128 + cc] = oc;
+            if (a.y) {
+                const float sq = __fmul_rn(oc, oc);
+                const float s2 = __fadd_rn(sq, __shfl_xor(sq, 1, 64));          // lanes 4j, 4j + 2
+                const float q4 = __fadd_rn(s2, __shfl_down(s2, 2, 64));         // lane 4j
+                if (lane64 < 32 && (lane64 & 3) == 0) qq[cc >> 2] = q4;
+                lds_barrier();
+                if (lane64 < 32) {
+                    float ss0 = 0.f, ss1 = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        ss0 = __fadd_rn(ss0, qq[j]);
+                        ss1 = __fadd_rn(ss1, qq[16 + j]);
+                    }
+                    const float rs = head_rsqrt(ss0, ss1);
+                    const float z = bf2f(pr[kGdnZOff + h * 128 + cc]);
+                    const float w = bf2f(a.gnorm[cc]);
+                    a.y[(size_t)r * 2048 + h * 128 + cc] = f2bf(__fmul_rn(__fmul_rn(w, __fmul_rn(oc, rs)), silu_f(z)));
+                }
+            }
+        } else {
+            if (kg == 0) {
                 float oj = 0.f;
 #pragma unroll
-                for (int i = 0; i < NG; ++i) oj += red_o[i][jc + c];
-                a.o[(size_t)r * 2048 + h * 128 + cs * VC + jc + c] = oj;
-                if (CS == 1) ohead[jc + c] = oj;
-            }
-        }
-        if (CS == 1 && a.y) {
-            // fused gated RMSNorm over the head: the GEMM producer's arithmetic, in LDS
-            __syncthreads();
-            if (tid < 2) hss2[tid] = half_head_ss_regs(ohead + 64 * tid);
-            __syncthreads();
-            if (tid < 128) {
-                const float rs = head_rsqrt(hss2[0], hss2[1]);
-                const float z = bf2f(pr[kGdnZOff + h * 128 + tid]);
-                const float w = bf2f(a.gnorm[tid]);
-                a.y[(size_t)r * 2048 + h * 128 + tid] = f2bf(__fmul_rn(__fmul_rn(w, __fmul_rn(ohead[tid], rs)), silu_f(z)));
+                for (int i = 0; i < NG; ++i) oj += red_o[i][jc];
+                a.o[(size_t)r * 2048 + h * 128 + cs * VC + jc] = oj;
             }
         }
         if ((a.ckpt && !a.fac_write) || (!a.ckpt && t == a.T - 1 && !rec)) {
@@ -258,7 +302,6 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
             if (cs == 0) { Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2; }
             if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
         }
-        __syncthreads();
     }
 }
 
@@ -272,10 +315,8 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
 // counter tracks). All of those loads are unconditional (clamped indices): a load under a
 // branch would make the compiler wait for it where the branch joins. Same thread mapping
 // and arithmetic, statement for statement, as gdn_kernel<1> with T = 1.
-// A block barrier for LDS traffic only: __syncthreads() also orders global memory, for which
-// the compiler makes every wave wait for all of its outstanding loads first, including the
-// next item's prefetch, which would then never overlap an item's compute.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// Barriers are lds_barrier(): __syncthreads() would make every wave wait for the next item's
+// prefetch, which would then never overlap an item's compute.
 
 constexpr int kPersistMaxItems = 128;      // items per block: rows <= 4,096 at 512 blocks
 constexpr int kPersistLds = 64 * 1024 + kMaxPend * kFacStride * 4;   // state + factor rows
@@ -391,9 +432,6 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
             }
         }
     };
-    // orders a wave's own LDS traffic for the compiler: one wave's LDS accesses execute in
-    // program order, so lanes of the wave see each other's earlier writes without a barrier
-    auto wave_sync = [] { asm volatile("" ::: "memory"); };
     Ops nx;
     if (nk > 0) {
         fetch(0, nx);
