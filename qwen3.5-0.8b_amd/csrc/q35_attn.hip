@@ -341,7 +341,8 @@ __device__ __forceinline__ void load_v_part(const AttnArgs& a, int lrow, int j, 
 }
 
 // vv holds part pc's V rows on entry; with REFILL each row register is refilled with part
-// pnext's as soon as it has been used (unconditionally, as for the K fragments).
+// pnext's as soon as it has been used (unconditionally, as for the K fragments). The barriers
+// are LDS-only, so the refills stay in flight until the next part's FMAs use them.
 template <bool REFILL, bool NT = true>
 __device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int pc, int slot,
                                         q35_u32x4* vv, int pnext,
@@ -357,13 +358,13 @@ __device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int 
         const int idx = tid + q * 256, i = idx >> 7, t = idx & 127;
         if (t < n) sraw[q] = scores[i * s_stride + t0 + t];
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const int idx = tid + q * 256, i = idx >> 7, t = idx & 127;
         p[i][t] = t < n ? rbf(expf(sraw[q] - ml[i][0]) / ml[i][1]) : 0.f;
     }
-    __syncthreads();
+    lds_barrier();
     float acc[4][8];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -398,11 +399,11 @@ __device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int 
 #pragma unroll
                 for (int e = 0; e < 8; ++e) red[tg >> 1][k][dg * 8 + e] = acc[2 * hp + k][e];
         }
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int k = 0; k < 2; ++k)
             out[2 * hp + k] = ((red[0][k][tid] + red[1][k][tid]) + red[2][k][tid]) + red[3][k][tid];
-        __syncthreads();
+        lds_barrier();
     }
 }
 
@@ -762,6 +763,208 @@ __global__ void __launch_bounds__(256 * NI) attn_fused(AttnArgs a, int lds_slots
     for (int i = 0; i < 4; ++i) a.out[(size_t)r * 2048 + (4 * j + i) * 256 + tid] = gated_out(a, r, 4 * j + i, tid, acc[i]);
 }
 
+// MTP verify rows at many lanes (T = 2 or 3 rows per lane at consecutive slots): one block
+// per (lane, kv head) for all T rows, so the lane's K/V stream from HBM once and through the
+// block once (one block per row re-read each line from L2 three times: ~45 GB/s per CU of
+// L2 -> CU traffic for the same HBM rate). Every K fragment feeds the score MFMAs of all T
+// rows: B tile u holds rows 2u and 2u + 1 as columns 8 (t % 2) + h (q hi) and + 4 (q lo), and
+// an MFMA output column depends only on its own B column, so a row's scores and slice stats
+// are the one-row kernel's bits. Each V part, loaded once into registers, feeds every row's
+// P.V in turn with pv_part's arithmetic and reductions. The scores go to the global scratch
+// (T rows x 4 heads x cap f32 do not fit LDS beside two blocks per CU); the block reads back
+// only what it wrote, after a block barrier.
+template <int T>
+__global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
+    extern __shared__ float stl_all[];                  // [T][4][8 * max_chunks] slice stats
+    __shared__ uint16_t qbuf[2][16][256];               // q staging (tiles), then the P.V reduction
+    __shared__ float p[4][kPart];
+    __shared__ float ml_all[T][4][2];
+    constexpr int NU = (T + 1) / 2;                     // q tiles
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, n = lane & 15, g = lane >> 4;
+    const int pr = blockIdx.x, j = pr % kNkv, r0 = (pr / kNkv) * T;
+    int slot_t[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) slot_t[t] = a.rm.slot[r0 + t];
+    int slot = slot_t[0];
+#pragma unroll
+    for (int t = 1; t < T; ++t) slot = max(slot, slot_t[t]);
+    const int lrow = a.rm.lane[r0];
+    const size_t sst = (size_t)a.max_chunks * 8;
+    // q fragments: tile u, column 8 (t % 2) + h = bf16(q) of row t = 2u + t % 2, head h, and
+    // + 4 its low part (zero columns for a missing row), as load_q_frags makes them
+    {
+#pragma unroll
+        for (int t = 0; t < 2 * NU; ++t)
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const int c = 8 * (t & 1) + h;
+                if (t < T) {
+                    const float qv = a.q[((size_t)(r0 + t) * kNq + 4 * j + h) * 256 + tid];
+                    const uint16_t hi = f2bf(qv);
+                    qbuf[t >> 1][c][tid] = hi;
+                    qbuf[t >> 1][c + 4][tid] = f2bf(qv - bf2f(hi));
+                } else {
+                    qbuf[t >> 1][c][tid] = 0;
+                    qbuf[t >> 1][c + 4][tid] = 0;
+                }
+            }
+        __syncthreads();
+    }
+    // (the q fragments are read from LDS at each use: T rows' fragments in registers beside
+    // a slice of K fragments would leave one wave per SIMD)
+    // scores: wave wv takes slices 4c + wv (score_slice's arithmetic, one MFMA chain per tile)
+    {
+        q35_u32x4 kf[4][8];
+        load_k_slice<true>(a, lrow, j, wv, slot, kf);
+        const int nch = slot / kChunk + 1;
+        const int tr = n >> 3;                           // this lane's row within a tile: 2u + tr
+        int lslot[NU];                                   // that row's slot (-1: no such row)
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            const int ta = 2 * u, tb = 2 * u + 1 < T ? 2 * u + 1 : 2 * u;
+            lslot[u] = tr == 0 ? slot_t[ta] : 2 * u + 1 < T ? slot_t[tb] : -1;
+        }
+        for (int c = 0; c < nch; ++c) {
+            const int q = 4 * c + wv, qnext = 4 * (c + 1) + wv, t0 = q * 64;
+            float sv[NU][4][4];
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                asm volatile("" ::: "memory");      // keeps the fragment reads here (not hoisted into registers)
+                q35_f32x4 acc[NU];
+#pragma unroll
+                for (int u = 0; u < NU; ++u) {
+                    acc[u] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int s = 0; s < 8; ++s) {
+                        const q35_u32x4 qv = *(const q35_u32x4*)&qbuf[u][n][s * 32 + g * 8];
+                        acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&kf[st][s], *(const q35_bf16x8*)&qv, acc[u], 0, 0, 0);
+                    }
+                }
+                load_k_sub<true>(a, lrow, j, qnext, st, slot, kf[st]);
+#pragma unroll
+                for (int u = 0; u < NU; ++u)
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const float lo = row_down4(acc[u][rr]);   // lanes with n % 8 < 4 add the q_lo column
+                        const float sc = (acc[u][rr] + lo) * 0.0625f;
+                        const int t = 2 * u + tr, tt = t0 + st * 16 + 4 * g + rr;
+                        const bool ok = (n & 7) < 4 && tt <= lslot[u];
+                        sv[u][st][rr] = ok ? sc : -INFINITY;
+                        if (ok) a.sc[((size_t)(r0 + t) * kNq + 4 * j + (n & 3)) * a.sc_ld + tt] = sc;
+                    }
+            }
+#pragma unroll
+            for (int u = 0; u < NU; ++u) {
+                float m = -INFINITY;
+#pragma unroll
+                for (int st = 0; st < 4; ++st)
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) m = fmaxf(m, sv[u][st][rr]);
+                m = fmaxf(m, __shfl_xor(m, 16, 64));
+                m = fmaxf(m, xor32(m));
+                float e = 0.f;
+#pragma unroll
+                for (int st = 0; st < 4; ++st)
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) e += sv[u][st][rr] > -INFINITY ? expf(sv[u][st][rr] - m) : 0.f;
+                e += __shfl_xor(e, 16, 64);
+                e += xor32(e);
+                const int t = 2 * u + tr;
+                if (g == 0 && (n & 7) < 4 && t0 <= lslot[u]) {
+                    float* sp = stl_all + ((size_t)t * 4 + (n & 3)) * sst + 2 * q;
+                    sp[0] = m;
+                    sp[1] = e;
+                }
+            }
+        }
+    }
+    __syncthreads();          // scores (global scratch) and stats (LDS) of every wave are in
+#pragma unroll
+    for (int t = 0; t < T; ++t) softmax_ml(stl_all + (size_t)t * 4 * sst, sst, slot_t[t] / 64 + 1, ml_all[t]);
+    // P.V: part pc's V rows in registers feed row 0, 1, .. T-1 in turn (pv_part for each),
+    // refilled with part pc + 1 after the last row's use; the q staging becomes the reduction
+    // buffer (every wave's last fragment read was before the barrier above)
+    float(*red)[2][256] = (float(*)[2][256])&qbuf[0][0][0];
+    const int dg = tid & 31, tg = tid >> 5;
+    q35_u32x4 vv[16];
+    load_v_part<true>(a, lrow, j, 0, slot, vv);
+    float acc_t[T][4];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc_t[t][i] = 0.f;
+    const int np = slot / kPart + 1;
+    for (int pc = 0; pc < np; ++pc) {
+        const int t0 = pc * kPart;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int nn = min(kPart, slot_t[t] + 1 - t0);
+            const float* scores = a.sc + ((size_t)(r0 + t) * kNq + 4 * j) * a.sc_ld;
+            float sraw[2] = {0.f, 0.f};
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int idx = tid + q * 256, i = idx >> 7, tt = idx & 127;
+                if (tt < nn) sraw[q] = scores[i * a.sc_ld + t0 + tt];
+            }
+            lds_barrier();
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int idx = tid + q * 256, i = idx >> 7, tt = idx & 127;
+                p[i][tt] = tt < nn ? rbf(expf(sraw[q] - ml_all[t][i][0]) / ml_all[t][i][1]) : 0.f;
+            }
+            lds_barrier();
+            float acc[4][8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int tt = tg * 16 + u;
+                float pp[4] = {p[0][tt], p[1][tt], p[2][tt], p[3][tt]};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float v = (e & 1) ? __uint_as_float(vv[u][e >> 1] & 0xffff0000u) : __uint_as_float(vv[u][e >> 1] << 16);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[i][e] = fmaf(pp[i], v, acc[i][e]);
+                }
+                if (t == T - 1) vv[u] = load_v<true>(a, lrow, j, pc + 1, u, slot);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float other = xor32(acc[i][e]);
+                    acc[i][e] = (tg & 1) ? other + acc[i][e] : acc[i][e] + other;
+                }
+            float out[4];
+#pragma unroll
+            for (int hp = 0; hp < 2; ++hp) {
+                if ((tg & 1) == 0) {
+#pragma unroll
+                    for (int k = 0; k < 2; ++k)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) red[tg >> 1][k][dg * 8 + e] = acc[2 * hp + k][e];
+                }
+                lds_barrier();
+#pragma unroll
+                for (int k = 0; k < 2; ++k)
+                    out[2 * hp + k] = ((red[0][k][tid] + red[1][k][tid]) + red[2][k][tid]) + red[3][k][tid];
+                lds_barrier();
+            }
+            if (pc < slot_t[t] / kPart + 1) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc_t[t][i] += out[i];
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            a.out[(size_t)(r0 + t) * 2048 + (4 * j + i) * 256 + tid] = gated_out(a, r0 + t, 4 * j + i, tid, acc_t[t][i]);
+}
+
 // ---------------------------------------------------------------- prompt waves (flash form)
 // A prompt wave of one lane (T >= 64 rows at consecutive slots): all of its rows read the
 // same K/V, so a block takes 16 rows x the 4 q heads of one kv head (64 query columns) and
@@ -1032,6 +1235,10 @@ static bool use_fused(const AttnArgs& a) { return a.R >= 64 && fused_lds(a) <= 9
 static bool use_fused2(const AttnArgs& a) { return a.T == 1 && a.fused_pair && 2 * fused_lds(a) <= (size_t)kFused2MaxLds; }
 // one row per lane on the split path: the prep runs inside the slice score kernel
 static bool prep_in_scores(const AttnArgs& a) { return !use_fused(a) && a.T == 1; }
+// a lane's 2-3 verify rows in one block when the (lane, kv head) blocks fill the CUs
+static bool use_rows(const AttnArgs& a) {
+    return a.rows_form && (a.T == 2 || a.T == 3) && a.R % a.T == 0 && a.R / a.T * kNkv >= 256;
+}
 
 hipError_t launch_attn_prep(const AttnArgs& a, hipStream_t st) {
     if (a.R <= 0 || a.max_chunks <= 0) return hipErrorInvalidValue;
@@ -1048,6 +1255,10 @@ hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
         // one lane's prompt wave: 16 rows per block, kv head by XCD half
         const int ngrp = (a.T + kPrRows - 1) / kPrRows;
         hipLaunchKernelGGL(attn_prompt, dim3((ngrp + 3) / 4 * 8), dim3(256), kPrLds, st, a);
+    } else if (use_rows(a)) {
+        const size_t lds = (size_t)a.T * 4 * 8 * a.max_chunks * 4;
+        if (a.T == 2) hipLaunchKernelGGL(attn_rows<2>, dim3(a.R / 2 * kNkv), dim3(256), lds, st, a);
+        else hipLaunchKernelGGL(attn_rows<3>, dim3(a.R / 3 * kNkv), dim3(256), lds, st, a);
     } else if (use_fused(a)) {
         if (a.T < 1 || a.R % a.T) return hipErrorInvalidValue;
         const int pairs = a.R / a.T * kNkv;

@@ -81,6 +81,14 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
+// A block barrier for LDS traffic only: __syncthreads() also orders global memory, for which
+// the compiler makes every wave wait for all of its outstanding loads first, including loads
+// issued ahead for later work, which would then never overlap the current work.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// orders a wave's own LDS traffic for the compiler: one wave's LDS accesses execute in
+// program order, so lanes of the wave see each other's earlier writes without a barrier
+__device__ __forceinline__ void wave_sync() { asm volatile("" ::: "memory"); }
+
 // A wave-uniform pointer as scalar registers the compiler cannot fold with a lane's offset, so
 // that p + (32-bit lane offset) takes the scalar-base global address form (no vector address
 // arithmetic per load).

@@ -589,6 +589,7 @@ void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16
     a.out = e->aout; a.R = R; a.T = T; a.inv_freq = e->inv_freq; a.prompt_flash = e->forms.attn_prompt;
     a.split4 = e->forms.attn_split4;
     a.fused_pair = e->forms.attn_pair;
+    a.rows_form = e->forms.attn_rows;
     HCK(launch_attn_prep(a, e->st));
     {
         KTimer kt(e, kFamAttn);      // the attention core alone (scores, softmax, P.V, gate)
@@ -1652,7 +1653,7 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             HCK(hipStreamSynchronize(e->st));
             e->gdn_chunked = value ? 1 : 0;
         } else if (n == "b1_partials" || n == "attn_prompt" || n == "partial_rows" || n == "gemv_tpb" ||
-                   n == "gemm_pre" || n == "lmhead_persist" || n == "attn_split4" || n == "attn_pair" ||
+                   n == "gemm_pre" || n == "lmhead_persist" || n == "attn_split4" || n == "attn_pair" || n == "attn_rows" ||
                    n == "gdn_defer" || n == "mid_partials") {
             // kernel-form switches of this engine: captured steps hold the old forms
             REQ(n != "partial_rows" || value >= 17, Q35_ERR_ARG, "partial_rows must exceed the 16-row batch-1 path");
@@ -1666,6 +1667,7 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             else if (n == "gemm_pre") e->forms.gemm_pre = value;
             else if (n == "attn_split4") e->forms.attn_split4 = value ? 1 : 0;
             else if (n == "attn_pair") e->forms.attn_pair = value ? 1 : 0;
+            else if (n == "attn_rows") e->forms.attn_rows = value ? 1 : 0;
             else if (n == "gdn_defer") e->forms.gdn_defer = value;
             else if (n == "mid_partials") e->forms.mid_partials = value ? 1 : 0;
             else {

@@ -34,14 +34,6 @@
 
 namespace q35 {
 
-// A block barrier for LDS traffic only: __syncthreads() also orders global memory, for which
-// the compiler makes every wave wait for all of its outstanding loads first, including loads
-// issued ahead for later work, which would then never overlap the current work.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-// orders a wave's own LDS traffic for the compiler: one wave's LDS accesses execute in
-// program order, so lanes of the wave see each other's earlier writes without a barrier
-__device__ __forceinline__ void wave_sync() { asm volatile("" ::: "memory"); }
-
 template <int CS>
 __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     constexpr int VC = 128 / CS;                 // value columns of this block

@@ -23,6 +23,7 @@ struct KernelForms {
     int partial_rows = 1024;   // batched kEPartial GEMMs with M >= this leave one (summed) chain
     int attn_split4 = 1;       // split attention path: 4-wave score blocks, P.V split over dim quarters
     int attn_pair = 1;         // fused attention, one row per lane: two (row, kv head) items per block
+    int attn_rows = 1;         // MTP verify (2-3 rows per lane) at >= 128 lanes: one block per (lane, kv head)
     int attn_prompt = 1;       // prompt waves of >= 64 rows: flash-form MFMA kernel (1) or one-row kernels (0)
     int mid_partials = 1;      // bodies of 2 .. 16 rows: k-block chains + add+norm (0: residual-epilogue GEMMs)
     int gdn_defer = 3;         // decode steps: a lane's GDN state update is kept as pending factors for up
@@ -172,6 +173,7 @@ struct AttnArgs {
     int prompt_flash;      // KernelForms::attn_prompt of the calling engine
     int split4;            // KernelForms::attn_split4: split path in 4-wave score / dim-split P.V blocks
     int fused_pair;        // KernelForms::attn_pair
+    int rows_form;         // KernelForms::attn_rows
 };
 hipError_t launch_attn_prep(const AttnArgs& a, hipStream_t st);   // q/k norm + rope, cache append
 hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st);   // scores, softmax, P.V, gate
