@@ -261,3 +261,45 @@ def test_attention_two_items_per_block_bit_identical():
     finally:
         e.set_option("attn_pair", 1)
         e.close()
+
+
+def test_verify_rows_attention_bit_identical():
+    """MTP verify bodies at >= 128 lanes run one attention block per (lane, kv head) for the
+    lane's 2-3 rows (engine option attn_rows). With ragged contexts (lanes alternate between
+    300 and 900 cached slots) and 128 lanes, a k = 2 round, a k = 1 round and a plain step
+    give the same emits, the same final-normed verify rows and the same step logits bit for
+    bit as the one-block-per-row kernel."""
+    from qwen35 import Engine, State
+    print("verify rows attention", flush=True)
+    B = 128
+    e = Engine(max_rows=3 * B, max_ctx=1024, seed=0, use_graph=False)
+    try:
+        toks = [int(t) for t in np.random.default_rng(6).integers(0, 248320, B)]
+        outs = []
+        for rows in (1, 0):
+            e.set_option("attn_rows", rows)
+            short, long_ = State(e, B, 1000, mtp_k=2, mtp_cap=64), State(e, B, 1000, mtp_k=2, mtp_cap=64)
+            short.seed(3, 300)
+            long_.seed(4, 900)
+            for ln in range(B):
+                if ln % 2:
+                    long_.copy_lane(ln, short, ln)
+            long_.close()
+            res = []
+            em = short.mtp_round(toks, 2)
+            res.append(em)
+            res.append(e.read_scratch("nrm", (3 * B, 1024), np.uint16))
+            em1 = short.mtp_round([x[-1] for x in em], 1)
+            res.append(em1)
+            res.append(e.read_scratch("nrm", (2 * B, 1024), np.uint16))
+            res.append(short.decode_step([x[-1] for x in em1], logits=True))
+            short.close()
+            outs.append(res)
+        a, b = outs
+        assert a[0] == b[0] and a[2] == b[2]
+        assert np.array_equal(a[1], b[1]) and np.array_equal(a[3], b[3])
+        assert np.array_equal(a[4][0], b[4][0])
+        assert np.array_equal(a[4][1].view(np.uint32), b[4][1].view(np.uint32))
+    finally:
+        e.set_option("attn_rows", 1)
+        e.close()
