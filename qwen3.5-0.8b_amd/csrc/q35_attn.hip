@@ -26,8 +26,8 @@ namespace q35 {
 
 constexpr int kChunk = 256;
 // attn_fused<*, 2>: dynamic LDS of its two items, the CU's 160 KiB less both halves' static
-// arrays (ubuf, p, ml, nparts)
-constexpr int kFused2MaxLds = 160 * 1024 - 20560;
+// arrays (ubuf, ml, nparts)
+constexpr int kFused2MaxLds = 160 * 1024 - 16464;
 
 __device__ __forceinline__ float block_sum256a(float v, float* red) {
     v = wave_sum(v);
@@ -65,7 +65,7 @@ __global__ void __launch_bounds__(256) attn_prep(AttnArgs a) {
     } else {
         const size_t base = lane * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256;
         a.kc[base + kv_tiled_offset(slot, d)] = f2bf(out);
-        a.vc[base + (size_t)slot * 256 + d] = pr[kAttnVOff + j * 256 + d];
+        a.vc[base + kv_v8_offset(slot, d)] = pr[kAttnVOff + j * 256 + d];
     }
 }
 
@@ -276,7 +276,7 @@ __global__ void __launch_bounds__(64) attn_scores_prep(AttnArgs a) {
             const uint16_t kb = f2bf(o[w]);
             knew[d] = kb;
             a.kc[base + kv_tiled_offset(slot, d)] = kb;
-            a.vc[base + (size_t)slot * 256 + d] = pr[kAttnVOff + j * 256 + d];
+            a.vc[base + kv_v8_offset(slot, d)] = pr[kAttnVOff + j * 256 + d];
         }
     }
     __syncthreads();
@@ -295,10 +295,15 @@ __global__ void __launch_bounds__(64) attn_scores_prep(AttnArgs a) {
                        a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 8, (size_t)a.max_chunks * 8);
 }
 
-// P.V over one 128-slot part: thread (dg, tg) owns dims dg*8..+8 for slots tg*16..+16 of
-// the part (16-byte V loads, issued before the softmax bookkeeping); the 8 slot groups are
-// summed in order (pairs in a wave by a lane swap, then the 4 waves through LDS).
+// P.V over one 128-slot part on MFMA (v_mfma_f32_16x16x32_bf16, k = slots): D = P V with
+// A = P (16 query columns x 32 slots: the normalised weights rounded to bf16, from LDS) and
+// B = V (32 slots x 16 dims: one 16-byte load of the 8-slot V layout per lane), one chain of
+// the part's four 32-slot steps from zero per 16-dim tile; the parts are summed in order.
+// Lane (n, g) of D holds query column 4g + r, dim n. A query column's result depends only on
+// its own row of P, so one row, a lane's several rows and the split path give the same bits.
+// A wave takes 4 dim tiles (64 dims): 16 V fragments per part.
 constexpr int kPart = 128;
+constexpr int kPlStride = kPart + 8;          // bf16 row stride of P in LDS (conflict-free reads)
 
 // Softmax (max, sum) of the row's 4 heads from the nsl slice stats -> ml[h][0..1]: wave h
 // takes head h, lane i folds slices i, i + 64, ... in order, then a fixed xor butterfly.
@@ -320,90 +325,75 @@ __device__ __forceinline__ void softmax_ml(const float* stats, size_t stats_stri
     }
 }
 
-// Partial P.V of part pc for dims d = tid of the 4 heads -> out[4]. `scores` points at head 0
-// of the row's scores (head stride s_stride); ml must be ready. Contains barriers.
-// V row u of this thread's 16-slot group in part pc (zero beyond `slot`; the load itself is
-// unconditional, from row min(t, slot), so no branch splits the wait counts).
+// V fragments of part pc for dim tiles dt0 .. dt0 + 3: vf[ks][i] = slots pc*128 + 32 ks + 8 g
+// .. +8 of dim 16 (dt0 + i) + n. Unconditional loads with the 8-slot group clamped to slot's
+// (past the end every lane re-reads that group, so the wait counts stay exact); slots past
+// `slot` are zeroed by mask_vf before use.
 template <bool NT = true>
-__device__ __forceinline__ q35_u32x4 load_v(const AttnArgs& a, int lrow, int j, int pc, int u, int slot) {
-    const int tid = threadIdx.x & 255, dg = tid & 31, tg = tid >> 5;
-    const int t = pc * kPart + tg * 16 + u;
-    const uint16_t* vp = a.vc + lrow * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + min(t, slot)) * 256 + dg * 8;
-    const q35_u32x4 v = NT ? __builtin_nontemporal_load((const q35_u32x4*)vp) : *(const q35_u32x4*)vp;
-    const uint32_t keep = t <= slot ? 0xffffffffu : 0u;
-    return (q35_u32x4){v[0] & keep, v[1] & keep, v[2] & keep, v[3] & keep};
-}
-
-template <bool NT = true>
-__device__ __forceinline__ void load_v_part(const AttnArgs& a, int lrow, int j, int pc, int slot, q35_u32x4* vv) {
+__device__ __forceinline__ void load_vf(const AttnArgs& a, int lrow, int j, int pc, int slot, int dt0,
+                                        q35_u32x4 (*vf)[4]) {
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const uint16_t* vb = a.vc + lrow * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256;
 #pragma unroll
-    for (int u = 0; u < 16; ++u) vv[u] = load_v<NT>(a, lrow, j, pc, u, slot);
+    for (int ks = 0; ks < 4; ++ks) {
+        const int sg = min(pc * 16 + 4 * ks + g, slot >> 3);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const q35_u32x4* p = (const q35_u32x4*)(vb + (size_t)sg * 2048 + (16 * (dt0 + i) + n) * 8);
+            vf[ks][i] = NT ? __builtin_nontemporal_load(p) : *p;
+        }
+    }
 }
 
-// vv holds part pc's V rows on entry; with REFILL each row register is refilled with part
-// pnext's as soon as it has been used (unconditionally, as for the K fragments). The barriers
-// are LDS-only, so the refills stay in flight until the next part's FMAs use them.
-template <bool REFILL, bool NT = true>
-__device__ __forceinline__ void pv_part(const AttnArgs& a, int lrow, int j, int pc, int slot,
-                                        q35_u32x4* vv, int pnext,
-                                        const float* scores, size_t s_stride, float (*ml)[2],
-                                        float (*p)[kPart], float (*red)[2][256], float* out) {
-    const int tid = threadIdx.x & 255;
-    const int t0 = pc * kPart;
-    const int n = min(kPart, slot + 1 - t0);
-    const int dg = tid & 31, tg = tid >> 5;
-    float sraw[2] = {0.f, 0.f};
+// Zero the V values of slots past `slot` in part pc's fragments (its last part only: V memory
+// past the written slots is not initialised, and a zero weight times a NaN would be NaN).
+__device__ __forceinline__ void mask_vf(int pc, int slot, q35_u32x4 (*vf)[4]) {
+    const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const int cnt = slot + 1 - (pc * 128 + 32 * ks + 8 * g);   // valid slots of the group
+        uint32_t mk[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            mk[w] = (cnt > 2 * w ? 0xffffu : 0u) | (cnt > 2 * w + 1 ? 0xffff0000u : 0u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            vf[ks][i] = (q35_u32x4){vf[ks][i][0] & mk[0], vf[ks][i][1] & mk[1], vf[ks][i][2] & mk[2], vf[ks][i][3] & mk[3]};
+    }
+}
+
+// The part's four 32-slot steps for the wave's 4 dim tiles: out[i] = D of tile dt0 + i.
+// pl: P in LDS, [16][kPlStride] bf16 (query column rows); rows >= nq are taken as zero.
+__device__ __forceinline__ void pv_mfma(const uint16_t* pl, int nq, q35_u32x4 (*vf)[4], q35_f32x4* out) {
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    q35_u32x4 af[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const q35_u32x4 v = *(const q35_u32x4*)(pl + n * kPlStride + 32 * ks + 8 * g);
+        af[ks] = n < nq ? v : (q35_u32x4){0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        q35_f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&af[ks], *(q35_bf16x8*)&vf[ks][i], d, 0, 0, 0);
+        out[i] = d;
+    }
+}
+
+// The weights of part pc for query columns c0 .. c0 + 3 (the 4 heads of one row) into P rows
+// c0 .. c0 + 3: p = bf16(e^(s - m) / l), zero past `slot`; `scores` -> head 0's scores of the
+// row (head stride s_stride), 256 threads, two weights each.
+__device__ __forceinline__ void part_weights(const float* scores, size_t s_stride, const float (*ml)[2], int pc,
+                                             int slot, uint16_t* pl, int c0) {
+    const int tid = threadIdx.x & 255, t0 = pc * kPart;
+    const int nn = min(kPart, slot + 1 - t0);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const int idx = tid + q * 256, i = idx >> 7, t = idx & 127;
-        if (t < n) sraw[q] = scores[i * s_stride + t0 + t];
-    }
-    lds_barrier();
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        const int idx = tid + q * 256, i = idx >> 7, t = idx & 127;
-        p[i][t] = t < n ? rbf(expf(sraw[q] - ml[i][0]) / ml[i][1]) : 0.f;
-    }
-    lds_barrier();
-    float acc[4][8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-        const int t = tg * 16 + u;
-        float pp[4] = {p[0][t], p[1][t], p[2][t], p[3][t]};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = (e & 1) ? __uint_as_float(vv[u][e >> 1] & 0xffff0000u) : __uint_as_float(vv[u][e >> 1] << 16);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i][e] = fmaf(pp[i], v, acc[i][e]);
-        }
-        if (REFILL) vv[u] = load_v<NT>(a, lrow, j, pnext, u, slot);
-    }
-    // slot groups 2w and 2w+1 live in wave w (lanes 0-31 and 32-63): add in group order
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float other = xor32(acc[i][e]);
-            acc[i][e] = (tg & 1) ? other + acc[i][e] : acc[i][e] + other;
-        }
-    // then the 4 waves in order, two heads per pass through an 8 KiB LDS buffer
-#pragma unroll
-    for (int hp = 0; hp < 2; ++hp) {
-        if ((tg & 1) == 0) {
-#pragma unroll
-            for (int k = 0; k < 2; ++k)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) red[tg >> 1][k][dg * 8 + e] = acc[2 * hp + k][e];
-        }
-        lds_barrier();
-#pragma unroll
-        for (int k = 0; k < 2; ++k)
-            out[2 * hp + k] = ((red[0][k][tid] + red[1][k][tid]) + red[2][k][tid]) + red[3][k][tid];
-        lds_barrier();
+        const float s = t < nn ? scores[i * s_stride + t0 + t] : 0.f;
+        pl[(c0 + i) * kPlStride + t] = t < nn ? f2bf(expf(s - ml[i][0]) / ml[i][1]) : (uint16_t)0;
     }
 }
 
@@ -415,22 +405,30 @@ __device__ __forceinline__ uint16_t gated_out(const AttnArgs& a, int r, int qh, 
     return f2bf(o * g);
 }
 
+// Split path, one block per (row, kv head, part): wave w takes dims 64w .. +64.
 __global__ void __launch_bounds__(256) attn_pv(AttnArgs a) {
-    __shared__ float p[4][kPart];
+    __shared__ uint16_t pl[16 * kPlStride];
     __shared__ float ml[4][2];
-    __shared__ float red[4][2][256];
     const int r = blockIdx.x, j = blockIdx.y, pc = blockIdx.z;
     const int slot = a.rm.slot[r];
     if (pc >= slot / kPart + 1) return;
-    q35_u32x4 vv[16];
-    load_v_part(a, a.rm.lane[r], j, pc, slot, vv);
-    softmax_ml(a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 8, (size_t)a.max_chunks * 8,
-               slot / 64 + 1, ml);
-    float out[4];
-    pv_part<false>(a, a.rm.lane[r], j, pc, slot, vv, 0, a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld, a.sc_ld, ml, p, red, out);
-    float* pp = a.part + (((size_t)r * a.max_chunks * 2 + pc) * kNq + 4 * j) * 256 + threadIdx.x;
+    const int lrow = a.rm.lane[r], wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    q35_u32x4 vf[4][4];
+    load_vf(a, lrow, j, pc, slot, 4 * wv, vf);
+    softmax_ml(a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 8, (size_t)a.max_chunks * 8, slot / 64 + 1, ml);
+    __syncthreads();
+    part_weights(a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld, a.sc_ld, ml, pc, slot, pl, 0);
+    __syncthreads();
+    if (pc == slot / kPart) mask_vf(pc, slot, vf);
+    q35_f32x4 out[4];
+    pv_mfma(pl, 4, vf, out);
+    if (lane < 16) {
+        float* pp = a.part + (((size_t)r * a.max_chunks * 2 + pc) * kNq + 4 * j) * 256 + 64 * wv + lane;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pp[i * 256] = out[i];
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int h = 0; h < 4; ++h) pp[h * 256 + 16 * i] = out[i][h];
+    }
 }
 
 // Sum of the 128-slot partials in part order, bf16, times bf16(sigmoid(gate)).
@@ -462,9 +460,8 @@ __global__ void __launch_bounds__(256) attn_combine(AttnArgs a) {
 //                  K) and, with PREP, makes q head 4j + w (wave 0 also the new K row); wave 0
 //                  then forms the slice stats from all four sub-tiles' values in score_slice's
 //                  order (max, then e summed sub-tile-major)
-//   attn_pv4       (row, kv head, 128-slot part, 64-dim quarter): one wave, thread (dim group
-//                  dl, slot group tg) accumulates 16 slots x 8 dims in pv_part's order; the
-//                  8 slot groups are summed as pv_part sums them ((g0 + g1) + (g2 + g3)) + ...
+//   attn_pv4       (row, kv head, 128-slot part, 64-dim quarter): one wave, the part's P.V
+//                  for its 4 dim tiles on MFMA (pv_mfma), the weights made in the wave
 template <bool PREP>
 __global__ void __launch_bounds__(256) attn_scores4(AttnArgs a) {
     __shared__ uint16_t qb[16][256];
@@ -501,7 +498,7 @@ __global__ void __launch_bounds__(256) attn_scores4(AttnArgs a) {
                 const uint16_t kb = f2bf(o[w]);
                 knew[d] = kb;
                 a.kc[base + kv_tiled_offset(slot, d)] = kb;
-                a.vc[base + (size_t)slot * 256 + d] = pr[kAttnVOff + j * 256 + d];
+                a.vc[base + kv_v8_offset(slot, d)] = pr[kAttnVOff + j * 256 + d];
             }
         }
     } else {
@@ -570,25 +567,16 @@ __global__ void __launch_bounds__(256) attn_scores4(AttnArgs a) {
 }
 
 __global__ void __launch_bounds__(64) attn_pv4(AttnArgs a) {
-    __shared__ float p[4][kPart];
-    __shared__ float red[8][4][64];          // [slot group][head][dim of the quarter]
+    __shared__ uint16_t pl[16 * kPlStride];
     const int r = blockIdx.x, j = blockIdx.y, pc = blockIdx.z >> 2, dq = blockIdx.z & 3;
     const int slot = a.rm.slot[r];
     if (pc >= slot / kPart + 1) return;
-    const int tid = threadIdx.x, dl = tid & 7, tg = tid >> 3;
+    const int tid = threadIdx.x;
     const int lrow = a.rm.lane[r];
     const int t0 = pc * kPart;
-    // V rows first (unconditional clamped loads), as load_v does
-    q35_u32x4 vv[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-        const int t = t0 + tg * 16 + u;
-        const uint16_t* vp = a.vc + lrow * a.kv_lane + a.kv_layer_off + ((size_t)j * a.cap + min(t, slot)) * 256 +
-                             dq * 64 + dl * 8;
-        const q35_u32x4 v = __builtin_nontemporal_load((const q35_u32x4*)vp);
-        const uint32_t keep = t <= slot ? 0xffffffffu : 0u;
-        vv[u] = (q35_u32x4){v[0] & keep, v[1] & keep, v[2] & keep, v[3] & keep};
-    }
+    // V fragments first (unconditional clamped loads), as load_vf does
+    q35_u32x4 vf[4][4];
+    load_vf(a, lrow, j, pc, slot, 4 * dq, vf);
     // this part's raw scores (independent of the softmax statistics: loaded early)
     const int n = min(kPart, slot + 1 - t0);
     const float* scores = a.sc + ((size_t)r * kNq + 4 * j) * a.sc_ld;
@@ -653,38 +641,18 @@ __global__ void __launch_bounds__(64) attn_pv4(AttnArgs a) {
         const int idx = tid + k * 64, i = idx >> 7, t = idx & 127;
         const float mi = i == 0 ? m[0] : i == 1 ? m[1] : i == 2 ? m[2] : m[3];
         const float li = i == 0 ? l[0] : i == 1 ? l[1] : i == 2 ? l[2] : l[3];
-        p[i][t] = t < n ? rbf(expf(sraw[k] - mi) / li) : 0.f;
+        pl[i * kPlStride + t] = t < n ? f2bf(expf(sraw[k] - mi) / li) : (uint16_t)0;
     }
     __syncthreads();
-    float acc[4][8];
+    if (pc == slot / kPart) mask_vf(pc, slot, vf);
+    q35_f32x4 out[4];
+    pv_mfma(pl, 4, vf, out);
+    if (tid < 16) {
+        float* pp = a.part + (((size_t)r * a.max_chunks * 2 + pc) * kNq + 4 * j) * 256 + dq * 64 + tid;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-        const int t = tg * 16 + u;
-        float pp[4] = {p[0][t], p[1][t], p[2][t], p[3][t]};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = (e & 1) ? __uint_as_float(vv[u][e >> 1] & 0xffff0000u) : __uint_as_float(vv[u][e >> 1] << 16);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i][e] = fmaf(pp[i], v, acc[i][e]);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) red[tg][i][dl * 8 + e] = acc[i][e];
-    __syncthreads();
-    float* pp = a.part + (((size_t)r * a.max_chunks * 2 + pc) * kNq + 4 * j) * 256 + dq * 64;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int d = tid;
-        float w[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) w[k] = red[2 * k][i][d] + red[2 * k + 1][i][d];
-        pp[i * 256 + d] = ((w[0] + w[1]) + w[2]) + w[3];
+            for (int h = 0; h < 4; ++h) pp[h * 256 + 16 * i] = out[i][h];
     }
 }
 
@@ -705,13 +673,10 @@ __global__ void __launch_bounds__(256 * NI) attn_fused(AttnArgs a, int lds_slots
     const size_t item_lds = (size_t)4 * lds_slots + (size_t)4 * 8 * a.max_chunks;
     float* scl = fl + half * item_lds;                  // [4][lds_slots]
     float* stl = scl + 4 * lds_slots;                   // [4][8 * max_chunks]
-    __shared__ float ubuf_all[NI][2048];                // q staging, then the P.V reduction
-    __shared__ float p_all[NI][4][kPart];
+    __shared__ float ubuf_all[NI][2048];                // q staging, then the part's weights
     __shared__ float ml_all[NI][4][2];
     __shared__ int nparts_all[NI];
     uint16_t(*qb)[256] = (uint16_t(*)[256])ubuf_all[half];
-    float(*red)[2][256] = (float(*)[2][256])ubuf_all[half];
-    float(*p)[kPart] = p_all[half];
     float(*ml)[2] = ml_all[half];
     // Block order: the T rows of one lane read the same K/V, so they run as consecutive
     // blocks of one XCD (blocks go round-robin to the 8 XCDs) and share its L2 stream. With
@@ -746,21 +711,38 @@ __global__ void __launch_bounds__(256 * NI) attn_fused(AttnArgs a, int lds_slots
     __syncthreads();
     int np = nparts;
     if (NI > 1) np = max(nparts_all[0], nparts_all[NI - 1]);
-    q35_u32x4 vv[16];
-    load_v_part<NT>(a, lrow, j, 0, slot, vv);
+    // P.V: wave wv takes dims 64 wv .. +64 (pv_mfma); each part's V fragments are refilled
+    // with the next part's right after their MFMAs and stay in flight across the LDS-only
+    // barriers. The q staging holds the part's weights.
+    const int wv = tid >> 6, lane = tid & 63;
+    uint16_t* pl = (uint16_t*)ubuf_all[half];
+    q35_u32x4 vf[4][4];
+    load_vf<NT>(a, lrow, j, 0, slot, 4 * wv, vf);
     softmax_ml(stl, sst, slot / 64 + 1, ml);
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    q35_f32x4 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
     for (int pc = 0; pc < np; ++pc) {
-        float out[4];
-        pv_part<true, NT>(a, lrow, j, pc, slot, vv, pc + 1, scl, lds_slots, ml, p, red, out);
+        lds_barrier();          // ml is in; every wave is done with the previous part's weights
+        part_weights(scl, lds_slots, ml, pc, slot, pl, 0);
+        lds_barrier();
+        if (pc == nparts - 1) mask_vf(pc, slot, vf);
+        q35_f32x4 out[4];
+        pv_mfma(pl, 4, vf, out);
+        load_vf<NT>(a, lrow, j, pc + 1, slot, 4 * wv, vf);
         if (NI == 1 || pc < nparts) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] += out[i];
         }
     }
-    if (!active) return;
+    if (!active || lane >= 16) return;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a.out[(size_t)r * 2048 + (4 * j + i) * 256 + tid] = gated_out(a, r, 4 * j + i, tid, acc[i]);
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const int d = 64 * wv + 16 * i + lane;
+            a.out[(size_t)r * 2048 + (4 * j + h) * 256 + d] = gated_out(a, r, 4 * j + h, d, acc[i][h]);
+        }
 }
 
 // MTP verify rows at many lanes (T = 2 or 3 rows per lane at consecutive slots): one block
@@ -769,15 +751,14 @@ __global__ void __launch_bounds__(256 * NI) attn_fused(AttnArgs a, int lds_slots
 // L2 -> CU traffic for the same HBM rate). Every K fragment feeds the score MFMAs of all T
 // rows: B tile u holds rows 2u and 2u + 1 as columns 8 (t % 2) + h (q hi) and + 4 (q lo), and
 // an MFMA output column depends only on its own B column, so a row's scores and slice stats
-// are the one-row kernel's bits. Each V part, loaded once into registers, feeds every row's
-// P.V in turn with pv_part's arithmetic and reductions. The scores go to the global scratch
+// are the one-row kernel's bits. Each V part, loaded once into registers, feeds the P.V of
+// every row at once (the rows' weights are rows of P). The scores go to the global scratch
 // (T rows x 4 heads x cap f32 do not fit LDS beside two blocks per CU); the block reads back
 // only what it wrote, after a block barrier.
 template <int T>
 __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
     extern __shared__ float stl_all[];                  // [T][4][8 * max_chunks] slice stats
-    __shared__ uint16_t qbuf[2][16][256];               // q staging (tiles), then the P.V reduction
-    __shared__ float p[4][kPart];
+    __shared__ uint16_t qbuf[2][16][256];               // q staging (tiles), then the part's weights
     __shared__ float ml_all[T][4][2];
     constexpr int NU = (T + 1) / 2;                     // q tiles
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, n = lane & 15, g = lane >> 4;
@@ -881,88 +862,65 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
     __syncthreads();          // scores (global scratch) and stats (LDS) of every wave are in
 #pragma unroll
     for (int t = 0; t < T; ++t) softmax_ml(stl_all + (size_t)t * 4 * sst, sst, slot_t[t] / 64 + 1, ml_all[t]);
-    // P.V: part pc's V rows in registers feed row 0, 1, .. T-1 in turn (pv_part for each),
-    // refilled with part pc + 1 after the last row's use; the q staging becomes the reduction
-    // buffer (every wave's last fragment read was before the barrier above)
-    float(*red)[2][256] = (float(*)[2][256])&qbuf[0][0][0];
-    const int dg = tid & 31, tg = tid >> 5;
-    q35_u32x4 vv[16];
-    load_v_part<true>(a, lrow, j, 0, slot, vv);
-    float acc_t[T][4];
+    // P.V: P rows 4t + h hold row t's weights, so one pv_mfma per part serves every row (a
+    // query column's result depends only on its own weights: the one-row kernel's bits);
+    // the q staging holds the weights
+    uint16_t* pl = &qbuf[0][0][0];
+    q35_u32x4 vf[4][4];
+    load_vf<true>(a, lrow, j, 0, slot, 4 * wv, vf);
+    q35_f32x4 acc[4];
 #pragma unroll
-    for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc_t[t][i] = 0.f;
+    for (int i = 0; i < 4; ++i) acc[i] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
     const int np = slot / kPart + 1;
+    // the thread's two scores (head i = idx / 128, slot idx % 128 of the part, idx = tid,
+    // tid + 256) of every row, loaded one part ahead (clamped to the last slot: unconditional)
+    float sr[T][2];
+    auto load_scores = [&](int pc) {
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int idx = tid + q * 256, i = idx >> 7, tt = idx & 127;
+                sr[t][q] = a.sc[((size_t)(r0 + t) * kNq + 4 * j + i) * a.sc_ld + min(pc * kPart + tt, slot)];
+            }
+    };
+    load_scores(0);
     for (int pc = 0; pc < np; ++pc) {
-        const int t0 = pc * kPart;
+        lds_barrier();          // ml is in; every wave is done with the previous part's weights
+        // part_weights' arithmetic, from the scores in registers
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const int nn = min(kPart, slot_t[t] + 1 - t0);
-            const float* scores = a.sc + ((size_t)(r0 + t) * kNq + 4 * j) * a.sc_ld;
-            float sraw[2] = {0.f, 0.f};
+            const int nn = min(kPart, slot_t[t] + 1 - pc * kPart);
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 const int idx = tid + q * 256, i = idx >> 7, tt = idx & 127;
-                if (tt < nn) sraw[q] = scores[i * a.sc_ld + t0 + tt];
-            }
-            lds_barrier();
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const int idx = tid + q * 256, i = idx >> 7, tt = idx & 127;
-                p[i][tt] = tt < nn ? rbf(expf(sraw[q] - ml_all[t][i][0]) / ml_all[t][i][1]) : 0.f;
-            }
-            lds_barrier();
-            float acc[4][8];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const int tt = tg * 16 + u;
-                float pp[4] = {p[0][tt], p[1][tt], p[2][tt], p[3][tt]};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    float v = (e & 1) ? __uint_as_float(vv[u][e >> 1] & 0xffff0000u) : __uint_as_float(vv[u][e >> 1] << 16);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[i][e] = fmaf(pp[i], v, acc[i][e]);
-                }
-                if (t == T - 1) vv[u] = load_v<true>(a, lrow, j, pc + 1, u, slot);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float other = xor32(acc[i][e]);
-                    acc[i][e] = (tg & 1) ? other + acc[i][e] : acc[i][e] + other;
-                }
-            float out[4];
-#pragma unroll
-            for (int hp = 0; hp < 2; ++hp) {
-                if ((tg & 1) == 0) {
-#pragma unroll
-                    for (int k = 0; k < 2; ++k)
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) red[tg >> 1][k][dg * 8 + e] = acc[2 * hp + k][e];
-                }
-                lds_barrier();
-#pragma unroll
-                for (int k = 0; k < 2; ++k)
-                    out[2 * hp + k] = ((red[0][k][tid] + red[1][k][tid]) + red[2][k][tid]) + red[3][k][tid];
-                lds_barrier();
-            }
-            if (pc < slot_t[t] / kPart + 1) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc_t[t][i] += out[i];
+                pl[(4 * t + i) * kPlStride + tt] = tt < nn ? f2bf(expf(sr[t][q] - ml_all[t][i][0]) / ml_all[t][i][1]) : (uint16_t)0;
             }
         }
-    }
+        load_scores(pc + 1);
+        lds_barrier();
+        if (pc == np - 1) mask_vf(pc, slot, vf);
+        q35_f32x4 out[4];
+        pv_mfma(pl, 4 * T, vf, out);
+        load_vf<true>(a, lrow, j, pc + 1, slot, 4 * wv, vf);
+        // lane (n, g) holds row g's heads: add this part where it is one of that row's parts
+        const int tg = lane >> 4;
+        const int myslot = tg == 0 ? slot_t[0] : tg == 1 ? slot_t[T > 1 ? 1 : 0] : slot_t[T > 2 ? 2 : 0];
+        if (tg < T && pc < myslot / kPart + 1) {
 #pragma unroll
-    for (int t = 0; t < T; ++t)
+            for (int i = 0; i < 4; ++i) acc[i] += out[i];
+        }
+    }
+    const int tg = lane >> 4;
+    if (tg < T) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            a.out[(size_t)(r0 + t) * 2048 + (4 * j + i) * 256 + tid] = gated_out(a, r0 + t, 4 * j + i, tid, acc_t[t][i]);
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const int d = 64 * wv + 16 * i + (lane & 15);
+                a.out[(size_t)(r0 + tg) * 2048 + (4 * j + h) * 256 + d] = gated_out(a, r0 + tg, 4 * j + h, d, acc[i][h]);
+            }
+    }
 }
 
 // ---------------------------------------------------------------- prompt waves (flash form)
@@ -977,9 +935,8 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
 //                 rounded to bf16 as the P.V operand)
 //   O = P V       A = P straight from the S^T accumulators (lane (column, g) holds slots
 //                 4g + r of each 16-slot sub-tile: the MFMA's k index is taken in that order),
-//                 B = V columns read from LDS with ds_read_b64_tr_b16 (a 16-lane group reads
-//                 4 slots x 16 dims and receives them transposed), V tiles staged in LDS by
-//                 all 4 waves as padded 544-byte rows
+//                 B = V from LDS, staged by all 4 waves in the cache's 8-slot layout, where a
+//                 lane's 4 slots of one dim are one 8-byte read
 // The softmax normalisation comes last (O / l), so the bf16 rounding of the weights happens
 // before it rather than after as on the decode path (speccheck/specimpl.py:385-392 rounds
 // the normalised weights): same math, different rounding point -- prompt logits stay within
@@ -987,13 +944,13 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
 constexpr int kPrRows = 16;
 typedef short q35_s16x4 __attribute__((ext_vector_type(4)));
 
-// V tile rows in LDS: 32 16-byte chunks + 2 pad chunks (544 B): transposed reads of 4 rows x
-// 32 B per 16-lane group land on distinct banks, and every read address is one lane base plus
-// an immediate offset
-constexpr int kPrVRow = 34, kPrVBuf = 64 * kPrVRow * 16;    // 16-byte slots per row; bytes per V tile
+// V tile in LDS: the cache's 8-slot layout (kv_v8_offset) as it stands, 8 groups x 256 dims x
+// 8 slots (32 KiB); a lane's 4 slots of one dim are one 8-byte read, every read address one
+// lane base plus an immediate offset
+constexpr int kPrVBuf = 64 * 256 * 2;                       // bytes per V tile
 
 
-constexpr int kPrLds = 2 * 64 * 256 * 2 + 2 * kPrVBuf;   // K and V tiles, double-buffered: 132 KiB
+constexpr int kPrLds = 2 * 64 * 256 * 2 + 2 * kPrVBuf;   // K and V tiles, double-buffered: 128 KiB
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 q35_bf16x2;
 // two f32 -> packed bf16 (round to nearest even, v_cvt_pk_bf16_f32)
@@ -1005,7 +962,7 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
 __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t pr_lds[];
     uint16_t(*kt)[64 * 256] = (uint16_t(*)[64 * 256])pr_lds;
-    uint16_t* vt = pr_lds + 2 * 64 * 256;                          // [2][64 rows][kPrVRow slots]
+    uint16_t* vt = pr_lds + 2 * 64 * 256;                          // [2][8 groups][256 dims][8 slots]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int T = a.T, ngrp = (T + kPrRows - 1) / kPrRows;
@@ -1046,10 +1003,11 @@ __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
     const int ntiles = smax / 64 + 1;
     // K and V tiles (64 slots) reach LDS by direct-to-LDS loads (global_load_lds: lane i of
     // an instruction fills the 16-byte slot i of a 1 KiB run), issued one tile ahead: K in its
-    // cache layout (four 16-slot MFMA tiles, 32 KiB contiguous), V as padded rows of kPrVRow
-    // slots (34 runs; a pad slot takes a copy of the row's chunk 0). Cached loads: the 12 blocks of a kv head on one XCD read
-    // the same tiles and all but the first hit that XCD's L2. Slots past the group's last are
-    // clamped to it (K: scores masked; V: weights zero, values finite). The wave's 8 K and 8 V
+    // cache layout (four 16-slot MFMA tiles, 32 KiB contiguous), V in its 8-slot layout (eight
+    // 4 KiB groups, contiguous). Cached loads: the 12 blocks of a kv head on one XCD read
+    // the same tiles and all but the first hit that XCD's L2. Tiles and groups past the group's
+    // last slot are clamped to it (K: scores masked; V: weights zero, and the values of slots
+    // past the last are zeroed where they are read, in the last tile). The wave's 8 K and 8 V
     // runs per tile are its only vector-memory loads in the loop, so "s_waitcnt vmcnt(0)"
     // at the top of a tile waits for exactly that tile's data; every LDS read below is
     // inline asm, which keeps the compiler from waiting on the prefetch in flight.
@@ -1064,15 +1022,12 @@ __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
                 (__attribute__((address_space(3))) void*)&kt[buf][run * 512], 16, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < 9; ++i) {
-            const int run = 4 * i + wv;                   // 64-slot run of the padded V tile
-            if (run < 64 * kPrVRow / 64) {
-                const int sl = run * 64 + lane, row = sl / kPrVRow, pos = sl % kPrVRow;
-                const int slot = min(t0 + row, smax);
-                __builtin_amdgcn_global_load_lds(
-                    (const void*)(a.vc + kvbase + (size_t)slot * 256 + (pos < 32 ? pos : 0) * 8),
-                    (__attribute__((address_space(3))) void*)(vt + buf * (kPrVBuf / 2) + run * 512), 16, 0, 0);
-            }
+        for (int i = 0; i < 8; ++i) {
+            const int run = wv * 8 + i;                   // 1 KiB run: group run / 4, dims 64 (run % 4) ..
+            const int grp = min(t0 / 8 + (run >> 2), smax >> 3);
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(a.vc + kvbase + (size_t)grp * 2048 + (run & 3) * 512 + lane * 8),
+                (__attribute__((address_space(3))) void*)(vt + buf * (kPrVBuf / 2) + run * 512), 16, 0, 0);
         }
     };
     issue_tiles(0, 0);
@@ -1081,13 +1036,12 @@ __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
     q35_f32x4 o[16];
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt) o[dt] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
-    // LDS byte offsets: K fragment (sub-tile st, step s) at st*8192 + s*1024 + lane*16; V
-    // transposed reads: source lane n of group g points at row (4g + n/4) + 16c + 32ks of the
-    // tile, dims 16 dt + 4 (n % 4) .. +4: the lane's base (row 4g + n/4, its 8 bytes of the
-    // d-tile's 32) plus the immediate (16c + 32ks) * 544 + 32 dt
+    // LDS byte offsets: K fragment (sub-tile st, step s) at st*8192 + s*1024 + lane*16; V:
+    // lane (n, g) reads slots 32ks + 16c + 4g .. +4 of dim 16 dt + n, i.e. group 4ks + 2c + g/2,
+    // slots 4 (g % 2) .. +4: the lane's base plus the immediate (4ks + 2c) * 4096 + 256 dt
     const unsigned kb0 = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&kt[0][0] + lane * 16;
     const unsigned vlane = (unsigned)(size_t)(__attribute__((address_space(3))) void*)vt +
-                           (unsigned)((4 * g + (n >> 2)) * kPrVRow * 16 + (n & 3) * 8);
+                           (unsigned)(((g >> 1) * 2048 + n * 8 + 4 * (g & 1)) * 2);
 
     for (int it = 0; it < ntiles; ++it) {
         const int t0 = it * 64, buf = it & 1;
@@ -1164,26 +1118,35 @@ __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) o[dt][r] *= ar[r];
         }
-        // P.V: V fragments 8 d-tiles at a time (16 transposed reads, one wait, 8 MFMAs)
+        // P.V: V fragments 8 d-tiles at a time (16 reads, one wait, 8 MFMAs); in the last tile
+        // the values of slots past the group's last are zeroed (their memory is not initialised)
         const unsigned vb = vlane + (unsigned)(buf * kPrVBuf);
+        const bool last = it == ntiles - 1;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
+            uint2 mk[2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int cnt = last ? smax + 1 - (t0 + 32 * ks + 16 * c + 4 * g) : 4;   // valid slots of the 4
+                mk[c] = (uint2){(cnt > 0 ? 0xffffu : 0u) | (cnt > 1 ? 0xffff0000u : 0u),
+                                (cnt > 2 ? 0xffffu : 0u) | (cnt > 3 ? 0xffff0000u : 0u)};
+            }
 #pragma unroll
             for (int dh = 0; dh < 2; ++dh) {
                 uint2 v0[8], v1[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v0[u])
-                                 : "v"(vb), "n"((32 * ks) * kPrVRow * 16 + 32 * (8 * dh + u)) : "memory");
-                    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v1[u])
-                                 : "v"(vb), "n"((32 * ks + 16) * kPrVRow * 16 + 32 * (8 * dh + u)) : "memory");
+                    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v0[u])
+                                 : "v"(vb), "n"((4 * ks) * 4096 + 256 * (8 * dh + u)) : "memory");
+                    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v1[u])
+                                 : "v"(vb), "n"((4 * ks + 2) * 4096 + 256 * (8 * dh + u)) : "memory");
                 }
                 asm volatile("s_waitcnt lgkmcnt(0)"
                              : "+v"(v0[0]), "+v"(v0[1]), "+v"(v0[2]), "+v"(v0[3]), "+v"(v0[4]), "+v"(v0[5]), "+v"(v0[6]), "+v"(v0[7]),
                                "+v"(v1[0]), "+v"(v1[1]), "+v"(v1[2]), "+v"(v1[3]), "+v"(v1[4]), "+v"(v1[5]), "+v"(v1[6]), "+v"(v1[7]));
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    q35_u32x4 b = {v0[u].x, v0[u].y, v1[u].x, v1[u].y};
+                    q35_u32x4 b = {v0[u].x & mk[0].x, v0[u].y & mk[0].y, v1[u].x & mk[1].x, v1[u].y & mk[1].y};
                     o[8 * dh + u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&pa[ks], *(q35_bf16x8*)&b,
                                                                            o[8 * dh + u], 0, 0, 0);
                 }

@@ -54,6 +54,12 @@ __host__ __device__ inline size_t kv_tiled_offset(int slot, int d) {
     return (size_t)(slot >> 4) * 4096 + (d >> 5) * 512 + ((((d >> 3) & 3) << 4) | (slot & 15)) * 8 + (d & 7);
 }
 __host__ __device__ inline int kv_cap_padded(int cap) { return (cap + 15) & ~15; }
+// V cache of one (lane, layer, kv head): 8-slot groups, dim-major inside a group, so one
+// 16-byte load holds 8 consecutive slots of one dim -- a P.V fragment on MFMA (k = slots):
+// element (slot, d) at (slot/8) * 2048 + d * 8 + slot % 8.
+__host__ __device__ inline size_t kv_v8_offset(int slot, int d) {
+    return (size_t)(slot >> 3) * 2048 + d * 8 + (slot & 7);
+}
 
 __host__ __device__ inline size_t tiled_offset(int n, int k, int K) {
     int nt = n >> 4, kb = k >> 8, kk = k & 255;

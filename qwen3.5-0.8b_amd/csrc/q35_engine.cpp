@@ -1026,7 +1026,7 @@ int q35_state_seed(q35_engine* e, q35_state* s, uint64_t seed, int prefix_len) {
                     size_t off = l * s->kv_lane() + ((size_t)(a * 2 + j) * s->capT) * 256;
                     std::string tag = std::to_string(l) + "." + std::to_string(a) + "." + std::to_string(j);
                     HCK(launch_gen_normal_kv_tiled(stream_key(seed, "state.k." + tag), s1, prefix_len, s->kc + off, e->st));
-                    HCK(launch_gen_normal_plain(stream_key(seed, "state.v." + tag), s1, (long long)prefix_len * 256, s->vc + off, e->st));
+                    HCK(launch_gen_normal_kv_v8(stream_key(seed, "state.v." + tag), s1, prefix_len, s->vc + off, e->st));
                 }
             s->prefix[l] = prefix_len; s->mtp_len[l] = 0; s->cur[l] = 0; s->wcur[l] = 0; s->pend[l] = 0; s->pset[l] = 0;
         }
@@ -1059,8 +1059,9 @@ static void state_io(q35_engine* e, q35_state* s, int lane, int which, int n_slo
     } else if (which == 1) {
         cp(s->win + lane * s->W_lane() + (long long)s->wcur[lane] * kGdnLayers * 18432, 0, (size_t)kGdnLayers * 18432 * 4);
     } else if (which >= 2 && which <= 5) {
-        // K / V caches: [heads][n_slots][256] bf16 row-major on the host. V is stored that way;
-        // K is stored in 16-slot tiles (kv_tiled_offset) and converted here.
+        // K / V caches: [heads][n_slots][256] bf16 row-major on the host; on the device K is
+        // stored in 16-slot tiles (kv_tiled_offset) and V in 8-slot groups (kv_v8_offset),
+        // converted here.
         const bool mtp = which >= 4, isk = which == 2 || which == 4;
         const int cap = mtp ? s->mtp_cap : s->cap, capT = mtp ? s->mtp_capT : s->capT;
         const int heads = mtp ? 2 : kAttnLayers * 2;
@@ -1069,24 +1070,22 @@ static void state_io(q35_engine* e, q35_state* s, int lane, int which, int n_slo
         REQ((size_t)heads * n_slots * 512 <= bytes, Q35_ERR_ARG, "host buffer too small");
         uint16_t* base = (mtp ? (isk ? s->mkc : s->mvc) : (isk ? s->kc : s->vc)) +
                          lane * (mtp ? s->mkv_lane() : s->kv_lane());
-        if (!isk) {
-            for (int a = 0; a < heads; ++a)
-                cp(base + (size_t)a * capT * 256, (size_t)a * n_slots * 512, (size_t)n_slots * 512);
-        } else if (n_slots > 0) {
-            const int nt = (n_slots + 15) / 16;
+        if (n_slots > 0) {
+            const int nt = (n_slots + 15) / 16;      // whole 16-slot tiles (K) / pairs of 8-slot groups (V)
             std::vector<uint16_t> tiles((size_t)nt * 4096);
             uint16_t* h = (uint16_t*)host;
+            auto off = [&](int t, int d) { return isk ? kv_tiled_offset(t, d) : kv_v8_offset(t, d); };
             for (int a = 0; a < heads; ++a) {
                 uint16_t* dev = base + (size_t)a * capT * 256;
                 if (write) {   // keep the padding slots of the last tile as they are on the device
                     copy_sync(e, tiles.data(), dev, tiles.size() * 2, hipMemcpyDeviceToHost);
                     for (int t = 0; t < n_slots; ++t)
-                        for (int d = 0; d < 256; ++d) tiles[kv_tiled_offset(t, d)] = h[((size_t)a * n_slots + t) * 256 + d];
+                        for (int d = 0; d < 256; ++d) tiles[off(t, d)] = h[((size_t)a * n_slots + t) * 256 + d];
                     copy_sync(e, dev, tiles.data(), tiles.size() * 2, hipMemcpyHostToDevice);
                 } else {
                     copy_sync(e, tiles.data(), dev, tiles.size() * 2, hipMemcpyDeviceToHost);
                     for (int t = 0; t < n_slots; ++t)
-                        for (int d = 0; d < 256; ++d) h[((size_t)a * n_slots + t) * 256 + d] = tiles[kv_tiled_offset(t, d)];
+                        for (int d = 0; d < 256; ++d) h[((size_t)a * n_slots + t) * 256 + d] = tiles[off(t, d)];
                 }
             }
         }
@@ -1112,8 +1111,9 @@ static void copy_lane(q35_engine* e, q35_state* src, int sl, q35_state* dst, int
     const long long sS = (long long)kGdnLayers * kSLayer, sW = (long long)kGdnLayers * 18432;
     d2d(dst->S + dl * dst->S_lane() + dst->cur[dl] * sS, src->S + sl * src->S_lane() + src->cur[sl] * sS, sS * 4);
     d2d(dst->win + dl * dst->W_lane() + dst->wcur[dl] * sW, src->win + sl * src->W_lane() + src->wcur[sl] * sW, sW * 4);
-    // K: whole 16-slot tiles (the slots past P of the last tile are never read before written)
-    const size_t ktile = (size_t)(P + 15) / 16 * 4096 * 2, vrows = (size_t)P * 512;
+    // K: whole 16-slot tiles, V: whole 8-slot groups (the slots past P of the last tile or
+    // group are never read before written)
+    const size_t ktile = (size_t)(P + 15) / 16 * 4096 * 2, vrows = (size_t)(P + 7) / 8 * 4096;
     for (int a = 0; a < kAttnLayers * 2; ++a) {
         d2d(dst->kc + dl * dst->kv_lane() + (size_t)a * dst->capT * 256,
             src->kc + sl * src->kv_lane() + (size_t)a * src->capT * 256, ktile);
@@ -1125,7 +1125,7 @@ static void copy_lane(q35_engine* e, q35_state* src, int sl, q35_state* dst, int
         d2d(dst->mkc + dl * dst->mkv_lane() + (size_t)a * dst->mtp_capT * 256,
             src->mkc + sl * src->mkv_lane() + (size_t)a * src->mtp_capT * 256, (size_t)(Mc + 15) / 16 * 4096 * 2);
         d2d(dst->mvc + dl * dst->mkv_lane() + (size_t)a * dst->mtp_capT * 256,
-            src->mvc + sl * src->mkv_lane() + (size_t)a * src->mtp_capT * 256, (size_t)Mc * 512);
+            src->mvc + sl * src->mkv_lane() + (size_t)a * src->mtp_capT * 256, (size_t)(Mc + 7) / 8 * 4096);
     }
     d2d(dst->hlast + (size_t)dl * kHidden, src->hlast + (size_t)sl * kHidden, kHidden * 2);
     HCK(hipStreamSynchronize(e->st));

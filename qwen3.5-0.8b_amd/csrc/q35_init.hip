@@ -65,6 +65,19 @@ __global__ void gen_normal_kv_tiled(uint64_t key, float scale, long long n, uint
         dst[kv_tiled_offset((int)(i >> 8), (int)(i & 255))] = f2bf(normal_at(key, (uint64_t)i, scale));
 }
 
+// V cache rows of the plain stream's values (element i = slot * 256 + d) in the 8-slot layout
+__global__ void gen_normal_kv_v8(uint64_t key, float scale, long long n, uint16_t* dst) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i < n; i += (long long)gridDim.x * blockDim.x)
+        dst[kv_v8_offset((int)(i >> 8), (int)(i & 255))] = f2bf(normal_at(key, (uint64_t)i, scale));
+}
+
+hipError_t launch_gen_normal_kv_v8(uint64_t key, float scale, int n_slots, uint16_t* dst, hipStream_t st) {
+    if (n_slots <= 0) return hipSuccess;
+    hipLaunchKernelGGL(gen_normal_kv_v8, dim3(4096), dim3(256), 0, st, key, scale, (long long)n_slots * 256, dst);
+    return hipGetLastError();
+}
+
 hipError_t launch_gen_normal_kv_tiled(uint64_t key, float scale, int n_slots, uint16_t* dst, hipStream_t st) {
     if (n_slots <= 0) return hipSuccess;
     hipLaunchKernelGGL(gen_normal_kv_tiled, dim3(4096), dim3(256), 0, st, key, scale, (long long)n_slots * 256, dst);

@@ -183,6 +183,7 @@ hipError_t attn_init();   // one-time kernel attribute setup
 hipError_t launch_gen_normal_tiled(uint64_t key, float scale, int N, int K, int row_off_dst,
                                    uint16_t* dst, int Kdst, hipStream_t st);
 hipError_t launch_gen_normal_kv_tiled(uint64_t key, float scale, int n_slots, uint16_t* dst, hipStream_t st);
+hipError_t launch_gen_normal_kv_v8(uint64_t key, float scale, int n_slots, uint16_t* dst, hipStream_t st);
 hipError_t launch_gen_normal_plain(uint64_t key, float scale, long long n, uint16_t* dst,
                                    hipStream_t st);
 hipError_t launch_gen_normal_f32(uint64_t key, float scale, long long n, float* dst,
