@@ -791,12 +791,18 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
             }
         __syncthreads();
     }
-    // (the q fragments are read from LDS at each use: T rows' fragments in registers beside
-    // a slice of K fragments would leave one wave per SIMD)
     // scores: wave wv takes slices 4c + wv (score_slice's arithmetic, one MFMA chain per tile)
     {
-        q35_u32x4 kf[4][8];
-        load_k_slice<true>(a, lrow, j, wv, slot, kf);
+        // q fragments in registers, K two sub-tiles ahead (kf[st % 2] holds sub-tile st; the
+        // registers of sub-tile st are refilled with sub-tile st + 2, then the next slice's)
+        q35_u32x4 qf[NU][8];
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int s = 0; s < 8; ++s) qf[u][s] = *(const q35_u32x4*)&qbuf[u][n][s * 32 + g * 8];
+        q35_u32x4 kf[2][8];
+        load_k_sub<true>(a, lrow, j, wv, 0, slot, kf[0]);
+        load_k_sub<true>(a, lrow, j, wv, 1, slot, kf[1]);
         const int nch = slot / kChunk + 1;
         const int tr = n >> 3;                           // this lane's row within a tile: 2u + tr
         int lslot[NU];                                   // that row's slot (-1: no such row)
@@ -810,18 +816,16 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
             float sv[NU][4][4];
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
-                asm volatile("" ::: "memory");      // keeps the fragment reads here (not hoisted into registers)
                 q35_f32x4 acc[NU];
 #pragma unroll
                 for (int u = 0; u < NU; ++u) {
                     acc[u] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int s = 0; s < 8; ++s) {
-                        const q35_u32x4 qv = *(const q35_u32x4*)&qbuf[u][n][s * 32 + g * 8];
-                        acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&kf[st][s], *(const q35_bf16x8*)&qv, acc[u], 0, 0, 0);
-                    }
+                    for (int s = 0; s < 8; ++s)
+                        acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&kf[st & 1][s], *(const q35_bf16x8*)&qf[u][s], acc[u], 0, 0, 0);
                 }
-                load_k_sub<true>(a, lrow, j, qnext, st, slot, kf[st]);
+                if (st < 2) load_k_sub<true>(a, lrow, j, q, st + 2, slot, kf[st & 1]);
+                else load_k_sub<true>(a, lrow, j, qnext, st - 2, slot, kf[st & 1]);
 #pragma unroll
                 for (int u = 0; u < NU; ++u)
 #pragma unroll
