@@ -870,8 +870,11 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
     // query column's result depends only on its own weights: the one-row kernel's bits);
     // the q staging holds the weights
     uint16_t* pl = &qbuf[0][0][0];
-    q35_u32x4 vf[4][4];
-    load_vf<true>(a, lrow, j, 0, slot, 4 * wv, vf);
+    // V two parts ahead (the K and q registers of the score pass are free here): parts
+    // alternate between vfa and vfb, each refilled with the part after next once used
+    q35_u32x4 vfa[4][4], vfb[4][4];
+    load_vf<true>(a, lrow, j, 0, slot, 4 * wv, vfa);
+    load_vf<true>(a, lrow, j, 1, slot, 4 * wv, vfb);
     q35_f32x4 acc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
@@ -888,8 +891,10 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
                 sr[t][q] = a.sc[((size_t)(r0 + t) * kNq + 4 * j + i) * a.sc_ld + min(pc * kPart + tt, slot)];
             }
     };
-    load_scores(0);
-    for (int pc = 0; pc < np; ++pc) {
+    const int tg = lane >> 4;
+    const int myslot = tg == 0 ? slot_t[0] : tg == 1 ? slot_t[T > 1 ? 1 : 0] : slot_t[T > 2 ? 2 : 0];
+    // one part (a part at np, when np is odd, is idle: zero weights, its sum not added)
+    auto part = [&](int pc, q35_u32x4 (&vf)[4][4]) {
         lds_barrier();          // ml is in; every wave is done with the previous part's weights
         // part_weights' arithmetic, from the scores in registers
 #pragma unroll
@@ -906,16 +911,18 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
         if (pc == np - 1) mask_vf(pc, slot, vf);
         q35_f32x4 out[4];
         pv_mfma(pl, 4 * T, vf, out);
-        load_vf<true>(a, lrow, j, pc + 1, slot, 4 * wv, vf);
+        load_vf<true>(a, lrow, j, pc + 2, slot, 4 * wv, vf);
         // lane (n, g) holds row g's heads: add this part where it is one of that row's parts
-        const int tg = lane >> 4;
-        const int myslot = tg == 0 ? slot_t[0] : tg == 1 ? slot_t[T > 1 ? 1 : 0] : slot_t[T > 2 ? 2 : 0];
         if (tg < T && pc < myslot / kPart + 1) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] += out[i];
         }
+    };
+    load_scores(0);
+    for (int pc = 0; pc < np; pc += 2) {
+        part(pc, vfa);
+        part(pc + 1, vfb);
     }
-    const int tg = lane >> 4;
     if (tg < T) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
