@@ -716,24 +716,32 @@ __global__ void __launch_bounds__(256 * NI) attn_fused(AttnArgs a, int lds_slots
     // barriers. The q staging holds the part's weights.
     const int wv = tid >> 6, lane = tid & 63;
     uint16_t* pl = (uint16_t*)ubuf_all[half];
-    q35_u32x4 vf[4][4];
-    load_vf<NT>(a, lrow, j, 0, slot, 4 * wv, vf);
+    // V two parts ahead (the K registers of the score pass are free here): parts alternate
+    // between vfa and vfb, each refilled with the part after next once used; a part at np
+    // (np odd) is idle like a short half's parts: zero weights, its sum not added
+    q35_u32x4 vfa[4][4], vfb[4][4];
+    load_vf<NT>(a, lrow, j, 0, slot, 4 * wv, vfa);
+    load_vf<NT>(a, lrow, j, 1, slot, 4 * wv, vfb);
     softmax_ml(stl, sst, slot / 64 + 1, ml);
     q35_f32x4 acc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
-    for (int pc = 0; pc < np; ++pc) {
+    auto part = [&](int pc, q35_u32x4 (&vf)[4][4]) {
         lds_barrier();          // ml is in; every wave is done with the previous part's weights
         part_weights(scl, lds_slots, ml, pc, slot, pl, 0);
         lds_barrier();
         if (pc == nparts - 1) mask_vf(pc, slot, vf);
         q35_f32x4 out[4];
         pv_mfma(pl, 4, vf, out);
-        load_vf<NT>(a, lrow, j, pc + 1, slot, 4 * wv, vf);
-        if (NI == 1 || pc < nparts) {
+        load_vf<NT>(a, lrow, j, pc + 2, slot, 4 * wv, vf);
+        if (pc < nparts) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] += out[i];
         }
+    };
+    for (int pc = 0; pc < np; pc += 2) {
+        part(pc, vfa);
+        part(pc + 1, vfb);
     }
     if (!active || lane >= 16) return;
 #pragma unroll
