@@ -37,9 +37,9 @@ KERNEL_NAMES = {"attn": "attn_fused", "gdn": "gdn_persist", "lm_head": "gemm_lmh
 # the calibration are in the file named by TRAFFIC_SOURCE.
 TRAFFIC_SOURCE = "profiles/hbm_traffic_decode_b256_ctx4096.md"
 MEASURED_TRAFFIC = {
-    ("attn", 256, 4096): (1056334.5 * 2.0 + 1024.0 * 1.0) * 1024,                        # attn_fused
-    ("gdn", 256, 4096): (146574.3 * 2.0 + 90247.9 * 1.0) * 1024,    # gdn_persist, gdn_defer 3 (4-step average)
-    ("lm_head", 256, 4096): (250422.6 * 2.0 + 2048.0 * 1.0) * 1024,                       # gemm_lmhead3
+    ("attn", 256, 4096): (1058666.2 * 2.0 + 1024.0 * 1.0) * 1024,                        # attn_fused
+    ("gdn", 256, 4096): (146571.6 * 2.0 + 90239.4 * 1.0) * 1024,    # gdn_persist, gdn_defer 3 (4-step average)
+    ("lm_head", 256, 4096): (250422.2 * 2.0 + 2048.0 * 1.0) * 1024,                       # gemm_lmhead3
 }
 
 
