@@ -12,8 +12,9 @@
 //   attn_prep   (row, head)         q norm+rope -> f32 scratch; k norm+rope, v -> cache
 //   attn_scores (row, kv head, chunk) scores on MFMA -> scratch, per-chunk (max, sum e^(s-max))
 //   attn_pv     (row, kv head, 128-slot part) global (max, sum) from the chunk stats,
-//               p = bf16(e/l), partial P.V per part
+//               p = bf16(e/l), partial P.V per part on MFMA (V cache in 8-slot groups)
 //   attn_combine (row, q head)      sum of the parts in order, bf16, times bf16(sigmoid(gate))
+// plus attn_rows (MTP verify: a lane's rows in one block) and attn_prompt (prompt waves).
 // The k cache holds bf16(k post-rope); the reference's torch path keeps it in f32, so
 // k's rotated dims carry one extra bf16 rounding here (the cache layout is bf16 by design).
 #include <algorithm>
