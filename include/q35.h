@@ -215,7 +215,9 @@ int q35_kprof_read(q35_engine* e, float* total_ms, int* launches);
  * attention of one row per lane at batched lanes runs two (row, kv head) items per block when
  * their LDS fits the CU, so the two items on a CU finish together), "attn_rows" (default 1: MTP
  * verify bodies of 2-3 rows per lane at >= 128 lanes run one attention block per (lane, kv
- * head) for all of the lane's rows, streaming its K/V once), "gdn_defer" (0 .. 4, default 3: a decode
+ * head) for all of the lane's rows, streaming its K/V once), "gdn_rows" (default 1: those verify
+ * bodies' GDN layers in the persistent kernel, the next (lane, head) item prefetched),
+ * "gdn_defer" (0 .. 4, default 3: a decode
  * step keeps each lane's GDN state update as pending factors for up to this many steps and
  * writes the state with the next one; 0 writes it every step). Not bit-identical, a different
  * rounding point within the stated tolerance: "attn_prompt" (1: prompt waves of one lane with

@@ -678,6 +678,8 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt, int defe
                 KTimer kt(e, kFamGdn);
                 if (chunked) HCK(launch_gdn_chunked(g, e->st));
                 else if (cs == 1 && T == 1 && !ckpt) HCK(launch_gdn_persist(g, e->st));
+                else if (cs == 1 && ckpt && (T == 2 || T == 3) && e->forms.gdn_rows)
+                    HCK(launch_gdn_persist(g, e->st));         // MTP verify rows, persistent
                 else HCK(launch_gdn(g, cs, e->st));
             }
             if (fused_norm)
@@ -1653,7 +1655,7 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             HCK(hipStreamSynchronize(e->st));
             e->gdn_chunked = value ? 1 : 0;
         } else if (n == "b1_partials" || n == "attn_prompt" || n == "partial_rows" || n == "gemv_tpb" ||
-                   n == "gemm_pre" || n == "lmhead_persist" || n == "attn_split4" || n == "attn_pair" || n == "attn_rows" ||
+                   n == "gemm_pre" || n == "lmhead_persist" || n == "attn_split4" || n == "attn_pair" || n == "attn_rows" || n == "gdn_rows" ||
                    n == "gdn_defer" || n == "mid_partials") {
             // kernel-form switches of this engine: captured steps hold the old forms
             REQ(n != "partial_rows" || value >= 17, Q35_ERR_ARG, "partial_rows must exceed the 16-row batch-1 path");
@@ -1668,6 +1670,7 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             else if (n == "attn_split4") e->forms.attn_split4 = value ? 1 : 0;
             else if (n == "attn_pair") e->forms.attn_pair = value ? 1 : 0;
             else if (n == "attn_rows") e->forms.attn_rows = value ? 1 : 0;
+            else if (n == "gdn_rows") e->forms.gdn_rows = value ? 1 : 0;
             else if (n == "gdn_defer") e->forms.gdn_defer = value;
             else if (n == "mid_partials") e->forms.mid_partials = value ? 1 : 0;
             else {

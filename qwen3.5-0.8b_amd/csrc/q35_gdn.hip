@@ -313,7 +313,8 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
 constexpr int kPersistMaxItems = 128;      // items per block: rows <= 4,096 at 512 blocks
 constexpr int kPersistLds = 64 * 1024 + kMaxPend * kFacStride * 4;   // state + factor rows
 
-__global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
+template <int TR>
+__global__ void __launch_bounds__(256, 2) gdn_persist(GdnArgs a, int nitems) {
     constexpr int VC = 128, CW = 4, CG = 32, KR = 16, NG = 16, GPT = 2;
     const int tid = threadIdx.x, lane64 = tid & 63, wv = tid >> 6;
     // wave w owns value columns 32w .. 32w+31 over all 128 k rows: lane (kg, quad) holds k rows
@@ -336,7 +337,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     __shared__ int meta[kPersistMaxItems];
     const int nk = (nitems - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
     for (int k = tid; k < nk; k += 256) {
-        const int gi = ((int)blockIdx.x + k * (int)gridDim.x) >> 4;
+        const int gi = (((int)blockIdx.x + k * (int)gridDim.x) >> 4) * TR;   // the lane's first row
         const int ln = a.lane[gi];
         const int cu = a.cur ? a.cur[gi] : 0;
         const int wc = a.wcur ? a.wcur[gi] : cu;
@@ -350,21 +351,21 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
     const bool hasv = tid < VC;
     struct Ops {
         float w0, w1, w2, v0, v1, v2;
-        uint16_t x, xv, bb, aa, alog, dtb;
-        uint16_t z1, g1;             // z and gnorm weight of column cc (y of lanes < 32)
+        uint16_t x[TR], xv[TR], bb[TR], aa[TR], alog, dtb;
+        uint16_t z1[TR], g1;         // z and gnorm weight of column cc (y of lanes < 32)
         uint2 cpk, dpk;
     };
     const uint16_t* gnw = a.gnorm ? a.gnorm : a.dt_bias;   // any valid address when unused
     // an item's gates (decay e^g, g = -e^A_log softplus(a + dt_bias); beta = sigmoid(b)), made by
     // one thread: for item k + 1 by thread 64 while wave 0 finishes item k (waves 1-3 would
     // otherwise wait for it at the next item's first barrier), for the first item in its conv phase
-    auto gates = [&](const Ops& o, float* dst) {
+    auto gates = [&](const Ops& o, int t, float* dst) {
         const float A = -expf(bf2f(o.alog));
-        const float aa = bf2f(o.aa) + bf2f(o.dtb);
+        const float aa = bf2f(o.aa[t]) + bf2f(o.dtb);
         float sp = aa > 20.f ? aa : log1pf(expf(aa));
         float g = A * sp;
         dst[0] = expf(g);
-        dst[1] = sigmoid_f(bf2f(o.bb));
+        dst[1] = sigmoid_f(bf2f(o.bb[t]));
     };
     // the next item's state rows 4g .. 4g+3 of this thread (the four groups are issued at four
     // points of an item's compute, so the memory pipe stays busy through it instead of the
@@ -388,19 +389,23 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         Snext = (const char*)(a.S + ln * a.S_lane + a.S_layer + (long long)h * 16384 + cu * a.S_slot);
         fetch_rows(0);
         const float* Win = a.win + ln * a.W_lane + a.W_layer + wc * a.W_slot;
-        const uint16_t* pr = a.proj + (size_t)gi * kGdnInRows;
+        const uint16_t* pr0 = a.proj + (size_t)gi * TR * kGdnInRows;
         const int cqk = tid < 128 ? h * 128 + tid : 2048 + h * 128 + (tid - 128);
         const int cv = 4096 + h * 128 + (tid & 127);      // threads >= 128 load a valid channel, unused
         o.w0 = Win[cqk]; o.w1 = Win[6144 + cqk]; o.w2 = Win[12288 + cqk];
         o.v0 = Win[cv]; o.v1 = Win[6144 + cv]; o.v2 = Win[12288 + cv];
         o.cpk = *(const uint2*)(a.conv_w + (size_t)cqk * 4);
         o.dpk = *(const uint2*)(a.conv_w + (size_t)cv * 4);
-        o.x = pr[cqk];
-        o.xv = pr[cv];
-        o.z1 = pr[kGdnZOff + h * 128 + cc];
+#pragma unroll
+        for (int t = 0; t < TR; ++t) {
+            const uint16_t* pr = pr0 + (size_t)t * kGdnInRows;
+            o.x[t] = pr[cqk];
+            o.xv[t] = pr[cv];
+            o.z1[t] = pr[kGdnZOff + h * 128 + cc];
+            o.bb[t] = pr[kGdnBOff + h];
+            o.aa[t] = pr[kGdnAOff + h];
+        }
         o.g1 = gnw[a.gnorm ? cc : 0];
-        o.bb = pr[kGdnBOff + h];
-        o.aa = pr[kGdnAOff + h];
         o.alog = a.A_log[h];
         o.dtb = a.dt_bias[h];
     };
@@ -471,6 +476,17 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                     }
             }
         }
+        if constexpr (TR > 1) {
+            // MTP verify rows: a lane with pending rows has them applied and the result stored to
+            // slot cur + 1, the base of this verify's factors (gdn_kernel's ckpt path)
+            if (npend) {
+                float* So = Sbase + ((cur + 1) % a.nslots) * a.S_slot;
+#pragma unroll
+                for (int i = 0; i < KR; ++i)
+                    __builtin_nontemporal_store((q35_f32x4){s[i][0], s[i][1], s[i][2], s[i][3]},
+                                                (q35_f32x4*)(So + (kg * KR + i) * 128 + jc));
+            }
+        }
         const bool more = k + 1 < nk;
         if (more) fetch(k + 1, nx);
         float w0 = op.w0, w1 = op.w1, w2 = op.w2, v0 = op.v0, v1 = op.v1, v2 = op.v2;
@@ -479,7 +495,10 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         cw[2] = __uint_as_float(op.cpk.y << 16); cw[3] = __uint_as_float(op.cpk.y & 0xffff0000u);
         cvw[0] = __uint_as_float(op.dpk.x << 16); cvw[1] = __uint_as_float(op.dpk.x & 0xffff0000u);
         cvw[2] = __uint_as_float(op.dpk.y << 16); cvw[3] = __uint_as_float(op.dpk.y & 0xffff0000u);
-        const float ox = bf2f(op.x), oxv = bf2f(op.xv);
+#pragma unroll
+        for (int t = 0; t < TR; ++t) {
+        const int r = gi * TR + t;              // this row
+        const float ox = bf2f(op.x[t]), oxv = bf2f(op.xv[t]);
         // causal conv: taps over [w0, w1, w2, raw] in order, f32, one rounding, bf16 SiLU
         {
             float u = 0.f;
@@ -495,19 +514,21 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
             }
             float ss = wave_sum(uq * uq);
             if ((tid & 63) == 0) wred[tid >> 6] = ss;
-            if (tid == 0 && k == 0) gates(op, gate_s[0]);
+            if (TR == 1 && tid == 0 && k == 0) gates(op, 0, gate_s[0]);
+            if (TR > 1 && tid == 0) gates(op, t, gate_s[0]);       // read after this row's first barrier
         }
-        // the conv window after this row: its values are final now
-        float* Wo = Wbase + ((wcur + 1) % a.nslots) * a.W_slot;
+        // the conv window after this row: its values are final now (verify rows: slot wcur + 1 + t)
+        float* Wo = Wbase + ((wcur + 1 + t) % a.nslots) * a.W_slot;
         Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2;
         if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
         lds_barrier();
-        if (more) { fetch_fac(k + 1); fetch_rows(1); }   // fbuf's rows were read before this barrier
+        if (more && t == 0) { fetch_fac(k + 1); fetch_rows(1); }   // fbuf's rows were read before this barrier
+        if (TR > 1 && more && t == 1) fetch_rows(3);
         // q~ and k~ of this thread's 16 rows, normalised where they are read (the same two
         // rounded products as a normalisation pass, without its barrier)
         const float rq = rsqrtf((wred[0] + wred[1]) + 1e-6f);
         const float rk = rsqrtf((wred[2] + wred[3]) + 1e-6f);
-        const float gam = gate_s[k & 1][0], beta = gate_s[k & 1][1];
+        const float gam = gate_s[TR == 1 ? (k & 1) : 0][0], beta = gate_s[TR == 1 ? (k & 1) : 0][1];
         float kn[KR], qn[KR];
 #pragma unroll
         for (int i = 0; i < KR; ++i) {
@@ -527,7 +548,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                 red[kg * GPT + gq][jc + c] = rp;
             }
         wave_sync();
-        if (more) fetch_rows(2);
+        if (more && t == 0) fetch_rows(2);
         // lane L < 32 sums column cc's 16 partials in order and leaves its dv in vs[cc] (read
         // only here); the wave's lanes then take the dv of their four columns
         if (lane64 < 32) {
@@ -542,14 +563,17 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
             const q35_f32x4 d4 = *(const q35_f32x4*)(vs + jc);
             dv[0] = d4[0]; dv[1] = d4[1]; dv[2] = d4[2]; dv[3] = d4[3];
         }
-        if (rec) {                // gdn_kernel's factor record of a deferred row
-            float* F = a.fac + lane * a.fac_lane + pset * a.fac_set + npend * a.fac_row + h * kFacStride;
+        if (TR > 1 || rec) {
+            // gdn_kernel's factor records: a deferred decode row as row npend of the set being
+            // read; a verify row t into the set not being read
+            float* F = a.fac + lane * a.fac_lane + (TR > 1 ? 1 - pset : pset) * a.fac_set +
+                       (TR > 1 ? t : npend) * a.fac_row + h * kFacStride;
             if (kg == 0) *(q35_f32x4*)(F + 128 + jc) = (q35_f32x4){dv[0], dv[1], dv[2], dv[3]};
             if (tid >= 128) F[tid - 128] = __fmul_rn(ks[tid - 128], rk);
             if (tid == 0) F[256] = gam;
         }
         wave_sync();            // red's columns of this wave are reused for the o partials
-        if (more) fetch_rows(3);
+        if (TR == 1 && more) fetch_rows(3);
 #pragma unroll
         for (int c = 0; c < CW; ++c)
 #pragma unroll
@@ -562,7 +586,7 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                 }
                 red[kg * GPT + gq][jc + c] = op2;
             }
-        if (!rec) {
+        if (TR == 1 && !rec) {
             const int slot = (cur + 1) % a.nslots;
             float* So = Sbase + slot * a.S_slot;
 #pragma unroll
@@ -575,21 +599,21 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
         // the gated norm needs the head's two half sums of squares, formed as half_head_ss forms
         // them (quads in column order, each ((o0^2 + o1^2) + (o2^2 + o3^2))): a quad's four
         // lanes pair up by shuffles and its first lane leaves the quad in qq. The barrier ending
-        // the item also keeps the next item's conv phase (qs, ks, vs, wred) from running ahead
+        // the row also keeps the next row's conv phase (qs, ks, vs, wred) from running ahead
         // of a wave still reading them.
         float oc = 0.f;
 #pragma unroll
         for (int i = 0; i < NG; ++i) oc += red[i][cc];
         {
-            const float t = __fmul_rn(oc, oc);
-            const float t2 = __fadd_rn(t, __shfl_xor(t, 1, 64));            // lanes 4j, 4j + 2
+            const float tq = __fmul_rn(oc, oc);
+            const float t2 = __fadd_rn(tq, __shfl_xor(tq, 1, 64));          // lanes 4j, 4j + 2
             const float q = __fadd_rn(t2, __shfl_down(t2, 2, 64));          // lane 4j
             if (lane64 < 32) {
-                a.o[(size_t)gi * 2048 + h * 128 + cc] = oc;
+                a.o[(size_t)r * 2048 + h * 128 + cc] = oc;
                 if ((lane64 & 3) == 0) qq[cc >> 2] = q;
             }
         }
-        if (more && tid == 64) gates(nx, gate_s[(k + 1) & 1]);
+        if (TR == 1 && more && tid == 64) gates(nx, 0, gate_s[(k + 1) & 1]);
         lds_barrier();
         if (a.y && lane64 < 32) {
             float ss0 = 0.f, ss1 = 0.f;
@@ -599,8 +623,9 @@ __global__ void __launch_bounds__(256) gdn_persist(GdnArgs a, int nitems) {
                 ss1 = __fadd_rn(ss1, qq[16 + j]);
             }
             const float rs = head_rsqrt(ss0, ss1);
-            const float yv = __fmul_rn(__fmul_rn(bf2f(op.g1), __fmul_rn(oc, rs)), silu_f(bf2f(op.z1)));
-            a.y[(size_t)gi * 2048 + h * 128 + cc] = f2bf(yv);
+            const float yv = __fmul_rn(__fmul_rn(bf2f(op.g1), __fmul_rn(oc, rs)), silu_f(bf2f(op.z1[t])));
+            a.y[(size_t)r * 2048 + h * 128 + cc] = f2bf(yv);
+        }
         }
     }
 }
@@ -645,17 +670,26 @@ hipError_t launch_gdn_materialize(float* S, long long S_lane, long long S_slot, 
 }
 
 hipError_t gdn_init() {
-    return hipFuncSetAttribute((const void*)gdn_persist, hipFuncAttributeMaxDynamicSharedMemorySize, kPersistLds);
+    hipError_t e = hipFuncSetAttribute((const void*)gdn_persist<1>, hipFuncAttributeMaxDynamicSharedMemorySize, kPersistLds);
+    if (e != hipSuccess) return e;
+    e = hipFuncSetAttribute((const void*)gdn_persist<2>, hipFuncAttributeMaxDynamicSharedMemorySize, kPersistLds);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute((const void*)gdn_persist<3>, hipFuncAttributeMaxDynamicSharedMemorySize, kPersistLds);
 }
 
 hipError_t launch_gdn_persist(const GdnArgs& a, hipStream_t st) {
-    if (a.nlanes <= 0 || a.T != 1 || a.ckpt) return hipErrorInvalidValue;
+    // one decode row per lane, or MTP verify rows (T = 2, 3: checkpoints as factor records)
+    const bool verify = a.T > 1;
+    if (a.nlanes <= 0 || a.T < 1 || a.T > 3 || (verify && !(a.ckpt && a.fac_write)) || (!verify && a.ckpt))
+        return hipErrorInvalidValue;
     const int nitems = a.nlanes * kHv;
     const int grid = nitems < 512 ? nitems : 512;      // two blocks per CU
-    // more than 128 items per block (above 4,096 lanes): the one-block-per-(row, head) kernel,
+    // more than 128 items per block (above 4,096 lanes): the one-block-per-(lane, head) kernel,
     // same bits
     if ((nitems + grid - 1) / grid > kPersistMaxItems) return launch_gdn(a, 1, st);
-    hipLaunchKernelGGL(gdn_persist, dim3(grid), dim3(256), kPersistLds, st, a, nitems);
+    if (a.T == 1) hipLaunchKernelGGL(gdn_persist<1>, dim3(grid), dim3(256), kPersistLds, st, a, nitems);
+    else if (a.T == 2) hipLaunchKernelGGL(gdn_persist<2>, dim3(grid), dim3(256), kPersistLds, st, a, nitems);
+    else hipLaunchKernelGGL(gdn_persist<3>, dim3(grid), dim3(256), kPersistLds, st, a, nitems);
     return hipGetLastError();
 }
 

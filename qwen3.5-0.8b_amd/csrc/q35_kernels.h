@@ -26,6 +26,7 @@ struct KernelForms {
     int attn_rows = 1;         // MTP verify (2-3 rows per lane) at >= 128 lanes: one block per (lane, kv head)
     int attn_prompt = 1;       // prompt waves of >= 64 rows: flash-form MFMA kernel (1) or one-row kernels (0)
     int mid_partials = 1;      // bodies of 2 .. 16 rows: k-block chains + add+norm (0: residual-epilogue GEMMs)
+    int gdn_rows = 1;          // MTP verify (2-3 rows per lane, whole-head blocks): the persistent GDN kernel
     int gdn_defer = 3;         // decode steps: a lane's GDN state update is kept as pending factors for up
                                // to this many steps, the state written on the next (0: every step)
 };
