@@ -265,10 +265,11 @@ def test_attention_two_items_per_block_bit_identical():
 
 def test_verify_rows_attention_bit_identical():
     """MTP verify bodies at >= 128 lanes run one attention block per (lane, kv head) for the
-    lane's 2-3 rows (engine option attn_rows). With ragged contexts (lanes alternate between
-    300 and 900 cached slots) and 128 lanes, a k = 2 round, a k = 1 round and a plain step
-    give the same emits, the same final-normed verify rows and the same step logits bit for
-    bit as the one-block-per-row kernel."""
+    lane's 2-3 rows (engine option attn_rows) and their GDN layers in the persistent kernel
+    (gdn_rows). With ragged contexts (lanes alternate between 300 and 900 cached slots) and
+    128 lanes, a k = 2 round, a k = 1 round and a plain step give the same emits, the same
+    final-normed verify rows and the same step logits bit for bit as the one-block-per-row
+    attention kernel and the one-block-per-(lane, head) GDN kernel."""
     from qwen35 import Engine, State
     print("verify rows attention", flush=True)
     B = 128
@@ -278,6 +279,7 @@ def test_verify_rows_attention_bit_identical():
         outs = []
         for rows in (1, 0):
             e.set_option("attn_rows", rows)
+            e.set_option("gdn_rows", rows)
             short, long_ = State(e, B, 1000, mtp_k=2, mtp_cap=64), State(e, B, 1000, mtp_k=2, mtp_cap=64)
             short.seed(3, 300)
             long_.seed(4, 900)
@@ -302,4 +304,5 @@ def test_verify_rows_attention_bit_identical():
         assert np.array_equal(a[4][1].view(np.uint32), b[4][1].view(np.uint32))
     finally:
         e.set_option("attn_rows", 1)
+        e.set_option("gdn_rows", 1)
         e.close()
