@@ -705,8 +705,11 @@ __global__ void __launch_bounds__(256 * NI) attn_fused(AttnArgs a, int lds_slots
         q35_u32x4 kf[4][8];
         load_k_slice<NT>(a, lrow, j, wv, slot, kf);
         load_q_frags(a, r, j, qb, qf);
-        for (int c = 0; c < nch; ++c)    // wave wv takes slices 4c + wv
+        // wave wv takes slices 4c + wv; the last one refills nothing (no loads past the end
+        // ahead of the V stream's first loads)
+        for (int c = 0; c + 1 < nch; ++c)
             score_slice<true, NT>(a, lrow, j, 4 * c + wv, slot, qf, kf, 4 * (c + 1) + wv, scl, lds_slots, stl, sst);
+        if (nch > 0) score_slice<false, NT>(a, lrow, j, 4 * (nch - 1) + wv, slot, qf, kf, 0, scl, lds_slots, stl, sst);
     }
     if (NI > 1 && tid == 0) nparts_all[half] = nparts;
     __syncthreads();
