@@ -210,3 +210,33 @@ def test_session_adaptive_depth_abandons_and_matches_plain(tmp_path):
         assert sum(" k=2 " in l for l in acc) == 32 and sum(" k=1 " in l for l in acc) == 48
     finally:
         eng.close()
+
+
+def test_chat_driver_turns_match_forward(eng, tmp_path):
+    """Two text turns through the chat driver (render -> tokenize -> feed -> gen): the reply ids
+    equal a plain Forward over the rendered-and-tokenized transcript; the second turn extends
+    the first (the im_end close of a budget-ended reply, then the next user turn)."""
+    from test_textio import _write_tokenizer
+    from qwen35 import Forward, State
+    from qwen35.chat import ChatDriver
+    from qwen35.session import Session
+    from qwen35.textio import Tokenizer
+    _write_tokenizer(tmp_path / "tokenizer.json")
+    tok = Tokenizer(tmp_path)
+    s = Session(eng, 512)
+    d = ChatDriver(s, tok)
+    p1 = d.prompt_ids("PING hello")
+    g1 = d.turn("PING hello", max_new=4)
+    assert p1[:4] == [248045, 1, 4, 3] and len(g1) == 4 and not d.closed
+    p2 = d.prompt_ids("hello")
+    assert p2[:2] == [248046, 4]               # the truncated reply is closed first
+    g2 = d.turn("hello", max_new=3)
+    # the same transcript as one Forward: prompt, the 4 shown replies (each fed; the unshown 5th
+    # sample was dropped), then p2
+    f = Forward(eng, State(eng, 1, 512))
+    ref1 = f.greedy(p1, 3, stop_on_eos=False)
+    assert g1 == ref1[:4]
+    f2 = Forward(eng, State(eng, 1, 512))
+    ref2 = f2.greedy(p1 + g1 + p2, 2, stop_on_eos=False)
+    assert g2 == ref2[:3]
+    s.close()
