@@ -192,6 +192,22 @@ int q35_op_gdn_step_norm(q35_engine* e, const uint16_t* proj, const uint16_t* co
  * aux_w [128]). M <= 16 uses the one-row GEMM's in-register producer, M > 16 the batched one. */
 int q35_op_gemm_a(q35_engine* e, const uint16_t* w_tiled_dev, int N, int K, int amode, const void* x_dev, int ldx,
                   const void* x2_dev, int ldx2, const uint16_t* aux_dev, int M, uint16_t* y_dev);
+/* One gated GQA attention layer of the decode path on a state's K/V cache (attn_decode_layer,
+ * engine/kernels_attn.cpp:415; speccheck/specimpl.py:320-397): for lane i = lanes[i] (i when
+ * NULL), T rows at positions p_i .. p_i + T - 1 (p_i = pos[i], or the lane's prefix_len when pos
+ * is NULL; the lane's prefix_len is not changed). proj_dev [n*T][5120] bf16 holds the attention
+ * input projection rows in the engine's order ((q | gate) per q head x 8, k x 2, v x 2, 256
+ * each); q_norm_dev / k_norm_dev [256] bf16. Each row's q and k get the zero-centred RMSNorm and
+ * partial rope (64 dims, theta 1e7, position p_i + t); bf16(k) and v are written into attention
+ * layer `layer`'s cache slots p_i + t; each row attends causally over slots 0 .. p_i + t with
+ * scale 1/16, and out_dev [n*T][2048] bf16 = bf16(bf16(softmax . V) * sigmoid(gate)), the input
+ * of o_proj. form: 0 the engine's choice for the shape, 1 split (one-wave score, P.V and combine
+ * kernels), 2 split in 4-wave score / dim-quarter P.V blocks, 3 fused, 4 fused with two items per
+ * block (T = 1), 5 one block per (lane, kv head) for all T = 2 or 3 rows, 6 flash prompt form
+ * (one lane, T >= 64); a form the shape cannot take is Q35_ERR_ARG. Synchronous. */
+int q35_op_attn_decode(q35_engine* e, q35_state* s, int layer, const int32_t* lanes, const int32_t* pos, int n,
+                       int T, const uint16_t* proj_dev, const uint16_t* q_norm_dev, const uint16_t* k_norm_dev,
+                       uint16_t* out_dev, int form);
 int q35_op_lm_head_argmax(q35_engine* e, const uint16_t* x_dev, int M, int32_t* tok_dev, float* logits_dev);
 int q35_sync(q35_engine* e);
 /* Live per-kernel timing: with option "kprof" = family (1 projection/MLP GEMMs, 2 lm_head

@@ -1216,14 +1216,43 @@ hipError_t attn_init() {
 static size_t fused_lds(const AttnArgs& a) {
     return (size_t)(4 * ((a.cap + 63) / 64 * 64) + 4 * 8 * a.max_chunks) * 4;
 }
-static bool use_fused(const AttnArgs& a) { return a.R >= 64 && fused_lds(a) <= 96 * 1024; }
+static bool fused_fits(const AttnArgs& a) { return fused_lds(a) <= 96 * 1024; }
+static bool use_fused(const AttnArgs& a) {
+    if (a.force == kAttnFused || a.force == kAttnFusedPair) return fused_fits(a);
+    if (a.force != kAttnAuto) return false;
+    return a.R >= 64 && fused_fits(a);
+}
 // two items per block (one row per lane) when both items' LDS fits the CU
-static bool use_fused2(const AttnArgs& a) { return a.T == 1 && a.fused_pair && 2 * fused_lds(a) <= (size_t)kFused2MaxLds; }
+static bool use_fused2(const AttnArgs& a) {
+    if (a.force == kAttnFused) return false;
+    return a.T == 1 && (a.fused_pair || a.force == kAttnFusedPair) && 2 * fused_lds(a) <= (size_t)kFused2MaxLds;
+}
 // one row per lane on the split path: the prep runs inside the slice score kernel
 static bool prep_in_scores(const AttnArgs& a) { return !use_fused(a) && a.T == 1; }
 // a lane's 2-3 verify rows in one block when the (lane, kv head) blocks fill the CUs
 static bool use_rows(const AttnArgs& a) {
-    return a.rows_form && (a.T == 2 || a.T == 3) && a.R % a.T == 0 && a.R / a.T * kNkv >= 256;
+    const bool shape = (a.T == 2 || a.T == 3) && a.R % a.T == 0;
+    if (a.force == kAttnRows) return shape;
+    if (a.force != kAttnAuto) return false;
+    return a.rows_form && shape && a.R / a.T * kNkv >= 256;
+}
+static bool use_prompt(const AttnArgs& a) {
+    const bool shape = a.T >= 64 && a.R == a.T;
+    if (a.force == kAttnPrompt) return shape;
+    if (a.force != kAttnAuto) return false;
+    return a.prompt_flash && shape;
+}
+
+// Whether the forced form can run this shape (kAttnAuto always can).
+bool attn_form_ok(const AttnArgs& a) {
+    switch (a.force) {
+    case kAttnAuto: case kAttnSplit: case kAttnSplit4: return true;
+    case kAttnFused: return use_fused(a) && a.R % a.T == 0;
+    case kAttnFusedPair: return use_fused(a) && use_fused2(a);
+    case kAttnRows: return use_rows(a);
+    case kAttnPrompt: return use_prompt(a);
+    default: return false;
+    }
 }
 
 hipError_t launch_attn_prep(const AttnArgs& a, hipStream_t st) {
@@ -1237,7 +1266,8 @@ hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
     if (a.R <= 0 || a.max_chunks <= 0) return hipErrorInvalidValue;
     const int lds_slots = (a.cap + 63) / 64 * 64;
     const size_t lds = fused_lds(a);
-    if (a.prompt_flash && a.T >= 64 && a.R == a.T) {
+    if (!attn_form_ok(a)) return hipErrorInvalidValue;
+    if (use_prompt(a)) {
         // one lane's prompt wave: 16 rows per block, kv head by XCD half
         const int ngrp = (a.T + kPrRows - 1) / kPrRows;
         hipLaunchKernelGGL(attn_prompt, dim3((ngrp + 3) / 4 * 8), dim3(256), kPrLds, st, a);
@@ -1257,7 +1287,7 @@ hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
         else
             hipLaunchKernelGGL((attn_fused<false, 1>), grid, dim3(256), lds, st, a, lds_slots);
     } else {
-        if (a.split4) {
+        if (a.force == kAttnSplit4 || (a.force != kAttnSplit && a.split4)) {
             if (prep_in_scores(a))
                 hipLaunchKernelGGL(attn_scores4<true>, dim3(a.R, kNkv, a.max_chunks * 4), dim3(256), 0, st, a);
             else

@@ -1637,6 +1637,44 @@ int q35_op_lm_head_argmax(q35_engine* e, const uint16_t* x, int M, int32_t* tok,
     });
 }
 
+int q35_op_attn_decode(q35_engine* e, q35_state* s, int layer, const int32_t* lanes, const int32_t* pos, int n, int T,
+                       const uint16_t* proj, const uint16_t* q_norm, const uint16_t* k_norm, uint16_t* out, int form) {
+    return guard([&] {
+        REQ(e && s && proj && q_norm && k_norm && out && n > 0 && T > 0, Q35_ERR_ARG, "bad attention call");
+        REQ(layer >= 0 && layer < kAttnLayers, Q35_ERR_ARG, "attention layer is 0 .. 5");
+        REQ(form >= kAttnAuto && form <= kAttnPrompt, Q35_ERR_ARG, "form is 0 .. 6");
+        const int R = n * T;
+        REQ(R <= e->R, Q35_ERR_CAP, "rows exceed engine max_rows");
+        for (int i = 0; i < n; ++i) {
+            const int l = lanes ? lanes[i] : i;
+            REQ(l >= 0 && l < s->lanes, Q35_ERR_ARG, "lane out of range");
+            const int p = pos ? pos[i] : s->prefix[l];
+            REQ(p >= 0 && p + T <= s->cap, Q35_ERR_CAP, "rows past the lane's cache capacity");
+            for (int t = 0; t < T; ++t) {
+                const int r = i * T + t;
+                e->h_tok[r] = 0; e->h_lane[r] = l; e->h_pos[r] = p + t; e->h_slot[r] = p + t;
+            }
+        }
+        stage_rcur(e, s, R);
+        upload_rows(e, R);
+        AttnArgs a{};
+        a.proj = proj; a.q_norm = q_norm; a.k_norm = k_norm;
+        a.kc = s->kc; a.vc = s->vc; a.kv_lane = s->kv_lane(); a.kv_layer_off = (long long)layer * 2 * s->capT * 256;
+        a.cap = s->capT;
+        a.rm.lane = e->rlane; a.rm.pos = e->rpos; a.rm.slot = e->rslot;
+        a.q = e->q; a.sc = e->sc; a.sc_ld = e->sc_ld; a.stats = e->stats; a.part = e->part;
+        a.max_chunks = (a.cap + 255) / 256;
+        REQ(a.max_chunks <= e->max_chunks, Q35_ERR_CAP, "cache capacity exceeds engine max_ctx");
+        a.out = out; a.R = R; a.T = T; a.inv_freq = e->inv_freq; a.prompt_flash = e->forms.attn_prompt;
+        a.split4 = e->forms.attn_split4; a.fused_pair = e->forms.attn_pair; a.rows_form = e->forms.attn_rows;
+        a.force = form;
+        REQ(attn_form_ok(a), Q35_ERR_ARG, "this attention form cannot run this shape (rows, rows per lane, capacity)");
+        HCK(launch_attn_prep(a, e->st));
+        HCK(launch_attn_core(a, e->st));
+        HCK(hipStreamSynchronize(e->st));
+    });
+}
+
 int q35_set_option(q35_engine* e, const char* name, int value) {
     return guard([&] {
         REQ(e && name, Q35_ERR_ARG, "null argument");

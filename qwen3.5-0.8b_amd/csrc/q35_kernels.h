@@ -175,9 +175,14 @@ struct AttnArgs {
     int split4;            // KernelForms::attn_split4: split path in 4-wave score / dim-split P.V blocks
     int fused_pair;        // KernelForms::attn_pair
     int rows_form;         // KernelForms::attn_rows
+    int force;             // 0: the form chosen from the shape; else one form (AttnForce), for
+                           // the op-level parity harness; a form the shape cannot take is an error
 };
+enum AttnForce { kAttnAuto = 0, kAttnSplit = 1, kAttnSplit4 = 2, kAttnFused = 3, kAttnFusedPair = 4,
+                 kAttnRows = 5, kAttnPrompt = 6 };
 hipError_t launch_attn_prep(const AttnArgs& a, hipStream_t st);   // q/k norm + rope, cache append
 hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st);   // scores, softmax, P.V, gate
+bool attn_form_ok(const AttnArgs& a);     // the forced form (AttnArgs::force) can run this shape
 hipError_t attn_init();   // one-time kernel attribute setup
 
 // Synthetic init (portable stream, see q35_init.hip).

@@ -73,6 +73,8 @@ _SIGS = {
     "q35_op_gdn_step_norm": ([C.c_void_p] * 10 + [C.c_int, C.c_int], C.c_int),
     "q35_op_gemm_a": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
                        C.c_int, C.c_void_p, C.c_int, C.c_void_p], C.c_int),
+    "q35_op_attn_decode": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
+                           + [C.c_void_p] * 4 + [C.c_int], C.c_int),
     "q35_op_lm_head_argmax": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p], C.c_int),
     "q35_sync": ([C.c_void_p], C.c_int),
     "q35_kprof_read": ([C.c_void_p, C.POINTER(C.c_float), C.POINTER(C.c_int)], C.c_int),
@@ -216,6 +218,15 @@ class Engine:
         _ck(load_library().q35_op_gemm_a(self.h, C.c_void_p(wt_ptr), N, K, amode, C.c_void_p(x_ptr), ldx,
                                          C.c_void_p(x2_ptr) if x2_ptr else None, ldx2,
                                          C.c_void_p(aux_ptr) if aux_ptr else None, M, C.c_void_p(y_ptr)))
+
+    def op_attn_decode(self, state: "State", layer: int, lanes, pos, T: int, proj: int, q_norm: int, k_norm: int,
+                       out: int, form: int = 0):
+        """One attention layer on `state`'s cache (q35_op_attn_decode): rows of lane lanes[i] at
+        positions pos[i] .. pos[i] + T - 1 (None: the lanes' prefix lengths)."""
+        la = _i32(lanes)
+        pa = None if pos is None else _i32(pos)
+        _ck(load_library().q35_op_attn_decode(self.h, state.h, layer, _p(la), None if pa is None else _p(pa), la.size,
+                                              T, *[C.c_void_p(p) for p in (proj, q_norm, k_norm, out)], form))
 
     def op_lm_head_argmax(self, x_ptr: int, M: int, tok_ptr: int, logits_ptr: int = 0):
         _ck(load_library().q35_op_lm_head_argmax(self.h, C.c_void_p(x_ptr), M, C.c_void_p(tok_ptr),

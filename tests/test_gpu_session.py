@@ -225,8 +225,8 @@ def test_chat_driver_turns_match_forward(eng, tmp_path):
     tok = Tokenizer(tmp_path)
     s = Session(eng, 512)
     d = ChatDriver(s, tok)
-    p1 = d.prompt_ids("PING hello")
-    g1 = d.turn("PING hello", max_new=4)
+    p1 = d.prompt_ids("PING")
+    g1 = d.turn("PING", max_new=4)
     assert p1[:4] == [248045, 1, 4, 3] and len(g1) == 4 and not d.closed
     p2 = d.prompt_ids("hello")
     assert p2[:2] == [248046, 4]               # the truncated reply is closed first
