@@ -48,7 +48,7 @@ def gdn_lane_layer_bytes(d: int) -> float:
     cycle of d + 1 steps (engine option gdn_defer = d): the 1 MiB state is read every step and
     written once per cycle; the steps in between write one pending factor row and read the rows
     pending before them (d / 2 on average); plus window r+w, qkv/z/b/a in, o (f32) and y (bf16) out."""
-    s = (1 << 20) * (1 + 1 / (d + 1)) + FAC_ROW_BYTES / 16 * (d / 2 + d / (d + 1))
+    s = (1 << 20) * (1 + 1 / (d + 1)) + FAC_ROW_BYTES * (d / 2 + d / (d + 1))
     return s + 2 * 73728 + 8224 * 2 + 2048 * 4 + 2048 * 2
 
 
@@ -131,9 +131,9 @@ def run_prefill(eng, n: int, reps: int = 2):
     return {"tokens": n, "ms": round(best * 1e3, 2), "tok_s": round(n / best, 1), "wave_rows": eng.max_rows}
 
 
-def run_mtp(eng, B: int, ctx: int, rounds: int, warmup: int, seed: int = 1):
-    """Config 4: B seeded lanes at context ctx, each round = 2 MTP drafts + a 3-row verify with
-    greedy accept and rollback (q35_mtp_round). Returns emitted tokens/s and accept stats."""
+def run_mtp(eng, B: int, ctx: int, rounds: int, warmup: int, seed: int = 1, k: int = 2):
+    """Config 4: B seeded lanes at context ctx, each round = k MTP drafts + a (k+1)-row verify
+    with greedy accept and rollback (q35_mtp_round). Returns emitted tokens/s and accept stats."""
     import numpy as np
     import torch
     from qwen35 import State
@@ -143,7 +143,7 @@ def run_mtp(eng, B: int, ctx: int, rounds: int, warmup: int, seed: int = 1):
     tok = st.decode_step(tok)             # one plain step: sets each lane's last hidden row
     stats = np.zeros(4, np.int64)
     for _ in range(warmup):
-        em = st.mtp_round(tok, 2, stats=stats)
+        em = st.mtp_round(tok, k, stats=stats)
         tok = np.array([e[-1] for e in em], np.int32)
     stats[:] = 0
     eng.sync()
@@ -151,7 +151,7 @@ def run_mtp(eng, B: int, ctx: int, rounds: int, warmup: int, seed: int = 1):
     t0 = time.perf_counter()
     emitted = 0
     for _ in range(rounds):
-        em = st.mtp_round(tok, 2, stats=stats)
+        em = st.mtp_round(tok, k, stats=stats)
         emitted += sum(len(e) for e in em)
         tok = np.array([e[-1] for e in em], np.int32)
     torch.cuda.synchronize()
@@ -159,30 +159,40 @@ def run_mtp(eng, B: int, ctx: int, rounds: int, warmup: int, seed: int = 1):
     st.close()
     return {"tok_s": round(emitted / wall, 2), "ms_per_round": round(wall / rounds * 1e3, 3),
             "accept_rate": round(float(stats[1]) / max(int(stats[0]), 1), 4),
-            "tokens_per_round_per_lane": round(emitted / rounds / B, 3), "lanes": B, "k": 2, "seed": seed}
+            "tokens_per_round_per_lane": round(emitted / rounds / B, 3), "lanes": B, "k": k, "seed": seed}
 
 
-def run_mtp_adaptive(eng, B: int, ctx: int, turns: int):
+def run_mtp_adaptive(eng, B: int, ctx: int, turns: int, cost_k1: float = 0.0, cost_k2: float = 0.0):
     """Config 4 with the adaptive depth policy (engine/mtp_adaptive.h) per lane: every turn runs
-    each lane at its policy's depth (q35_mtp_adaptive_step). With random-init weights no draft
-    is accepted, so every lane demotes after 16 rounds and abandons after 24 more; reported are
-    the whole run's emitted tok/s and the steady state after abandonment."""
+    each lane at its policy's depth (q35_mtp_adaptive_step), each round billed at the round costs
+    measured on this GPU (cost_k1 / cost_k2 plain steps). With random-init weights no draft is
+    accepted, so every lane demotes after 16 rounds and abandons after 24 more; reported are the
+    whole run's emitted tok/s, the steady state after abandonment and the turn of each depth
+    change (the first and last lane to change)."""
     import numpy as np
     import torch
     from qwen35 import MtpPolicy, State
     st = State(eng, B, ctx + 3 * turns + 16, mtp_k=2, mtp_cap=2 * turns + 16)
     st.seed(1, ctx)
     tok = st.decode_step(np.random.default_rng(1).integers(0, 248320, size=B).astype(np.int32))
-    pol = [MtpPolicy(2) for _ in range(B)]
+    pol = [MtpPolicy(2, cost_k1, cost_k2) for _ in range(B)]
     eng.sync()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     emitted, t_abandon, e_abandon, depth_turns = 0, None, 0, {0: 0, 1: 0, 2: 0}
+    prev = np.full(B, 2)
+    changes = {}                    # "2->1" / "1->0": [first turn, last turn, lanes]
     for t in range(turns):
         em, dep = st.mtp_adaptive_step(tok, pol)
         emitted += sum(len(e) for e in em)
         for d in dep:
             depth_turns[int(d)] += 1
+        for a, b in ((2, 1), (1, 0)):
+            hit = int(((prev == a) & (dep == b)).sum())
+            if hit:
+                c = changes.setdefault(f"{a}->{b}", [t, t, 0])
+                c[1], c[2] = t, c[2] + hit
+        prev = np.asarray(dep).copy()
         tok = np.array([e[-1] for e in em], np.int32)
         if t_abandon is None and (dep == 0).all():
             t_abandon, e_abandon, n_abandon = time.perf_counter(), emitted, t
@@ -193,7 +203,9 @@ def run_mtp_adaptive(eng, B: int, ctx: int, turns: int):
     if t_abandon is not None and t_abandon < t0 + wall and turns - n_abandon > 1:
         steady = round((emitted - e_abandon) / (t0 + wall - t_abandon), 2)
     return {"tok_s_whole_run": round(emitted / wall, 2), "tok_s_after_abandon": steady, "turns": turns,
-            "lane_turns_at_depth": {str(k): v for k, v in depth_turns.items()}, "lanes": B}
+            "lane_turns_at_depth": {str(k): v for k, v in depth_turns.items()}, "lanes": B,
+            "depth_changes": {k: {"first_turn": v[0], "last_turn": v[1], "lanes": v[2]} for k, v in changes.items()},
+            "round_costs": {"k1": cost_k1, "k2": cost_k2}}
 
 
 def run_mtp_accepting(eng, B: int, ctx: int, rounds: int, d: int = 7):
@@ -234,22 +246,28 @@ def run_mtp_accepting(eng, B: int, ctx: int, rounds: int, d: int = 7):
             eng.load_tensor(n, saved[n])
 
 
-def cpu_baseline(ctx: int, budget_s: float = 15.0):
+def cpu_baseline(ctx: int, budget_s: float = 6.0, runs: int = 3):
     """The torch-CPU oracle (restatement of the reference's specimpl.py path) decoding lane 0
-    of the same seeded workload on the host cores: tok/s."""
+    of the same seeded workload on the host cores: the median tok/s of `runs` timed runs of
+    about budget_s each (median of 3), continuing one greedy sequence."""
+    import statistics
     import torch
     from oracle.seeded import seeded_forward
     from oracle.weights import WeightDict
     torch.set_grad_enabled(False)
     f = seeded_forward(WeightDict(0), 1, 0, ctx)
-    tok, n = 1234, 0
+    tok, total = 1234, 0
     f.decode(tok)                      # warm
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s or n < 2:
-        tok = int(f.logits(f.decode(tok))[-1].argmax())
-        n += 1
-    dt = time.perf_counter() - t0
-    return n / dt, torch.get_num_threads(), n
+    rates = []
+    for _ in range(runs):
+        n = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < budget_s or n < 2:
+            tok = int(f.logits(f.decode(tok))[-1].argmax())
+            n += 1
+        rates.append(n / (time.perf_counter() - t0))
+        total += n
+    return statistics.median(rates), torch.get_num_threads(), total, rates
 
 
 def main():
@@ -332,20 +350,27 @@ def main():
     if args.mtp_rounds > 0:
         mtp = run_mtp(eng, B, L, args.mtp_rounds, 1)
         mtp["round_cost_steps"] = round(mtp["ms_per_round"] / ms, 4)
+        mk1 = run_mtp(eng, B, L, args.mtp_rounds, 1, k=1)
+        mk1["round_cost_steps"] = round(mk1["ms_per_round"] / ms, 4)
         m1 = run_mtp(eng, 1, L, 4 * args.mtp_rounds, 2)
         m1["round_cost_steps"] = round(m1["ms_per_round"] / ms1, 4)
-        mtp = {"b%d" % B: mtp, "b1": m1,
-               "adaptive_b%d" % B: run_mtp_adaptive(eng, B, L, args.adaptive_turns),
+        m1k1 = run_mtp(eng, 1, L, 4 * args.mtp_rounds, 2, k=1)
+        m1k1["round_cost_steps"] = round(m1k1["ms_per_round"] / ms1, 4)
+        mtp = {"b%d" % B: mtp, "b%d_k1" % B: mk1, "b1": m1, "b1_k1": m1k1,
+               "adaptive_b%d" % B: run_mtp_adaptive(eng, B, L, args.adaptive_turns, mk1["round_cost_steps"],
+                                                    mtp["round_cost_steps"]),
                "note": "random-init weights: the drafter almost never agrees with the target"}
         mtp["accepting_b%d" % B] = run_mtp_accepting(eng, B, L, args.mtp_rounds)
         mtp["accepting_b1"] = run_mtp_accepting(eng, 1, L, 4 * args.mtp_rounds)
     pre = run_prefill(eng, args.prefill_len) if 0 < args.prefill_len <= eng.max_ctx - 64 else None
     cpu = None
     if not args.no_cpu:
-        tps, thr, n = cpu_baseline(L)
+        tps, thr, n, rates = cpu_baseline(L)
         cpu = {"value": round(tps, 3), "unit": "tok/s", "cores": thr, "nproc": len(os.sched_getaffinity(0)), "kind": "port",
+               "runs": [round(r, 3) for r in rates],
                "sample": f"oracle (torch CPU restatement of speccheck/specimpl.py) greedy decode of lane 0 "
-                         f"of this workload (seeded state, ctx {L}), batch 1, {n} tokens"}
+                         f"of this workload (seeded state, ctx {L}), batch 1: median of {len(rates)} timed runs "
+                         f"of ~6 s, {n} tokens in all"}
     out = {"metric": "decode tok/s at batch 1 and 256 (ctx 4k); achieved HBM GB/s vs 8 TB/s peak",
            "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,

@@ -791,6 +791,10 @@ int guard(const std::function<void()>& f) {
 }
 }  // namespace
 
+// The calling thread's error text, for the other translation units of the library (the MTP
+// policy entry points) that return a status without going through guard().
+void q35_set_error(const char* msg) { g_err = msg; }
+
 // ====================================================================== C ABI
 extern "C" {
 
@@ -1500,6 +1504,23 @@ int q35_mtp_adaptive_step(q35_engine* e, q35_state* s, const int32_t* lanes, int
             REQ(k <= s->mtp_k, Q35_ERR_STATE, "policy depth exceeds the state's MTP slots");
             grp[k].push_back(i);
             if (depth) depth[i] = k;
+        }
+        // every group's preconditions before any group runs: a later group's refusal must not
+        // leave earlier groups advanced with their emits unreported
+        for (int i = 0; i < n; ++i) {
+            const int l = lanes ? lanes[i] : i;
+            check_lane(s, l);
+            check_tok(cur[i]);
+            for (int j = 0; j < i; ++j) REQ((lanes ? lanes[j] : j) != l, Q35_ERR_ARG, "duplicate lane in one step");
+        }
+        for (int k = 2; k >= 0; --k) {
+            const int m = (int)grp[k].size();
+            REQ(m * (k + 1) <= e->R, Q35_ERR_CAP, "rows exceed max_rows");
+            for (int i : grp[k]) {
+                const int l = lanes ? lanes[i] : i;
+                REQ(s->prefix[l] + k + 1 <= s->cap, Q35_ERR_CAP, "lane cache is full");
+                REQ(k == 0 || s->mtp_len[l] + k <= s->mtp_cap, Q35_ERR_CAP, "MTP cache is full");
+            }
         }
         for (int k = 2; k >= 0; --k) {
             const int m = (int)grp[k].size();

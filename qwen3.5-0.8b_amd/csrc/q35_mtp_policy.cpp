@@ -14,12 +14,18 @@
 
 #include "../../include/q35.h"
 
+void q35_set_error(const char* msg);   // q35_engine.cpp: the text q35_last_error() reports
+
 namespace {
 constexpr int kWindow = 32;              // engine/mtp_adaptive.h kWindowRounds
 constexpr int kMinObserve = 16;          // kMinObserveRounds (k = 2 -> 1)
 constexpr int kMinObserveAbandon = 24;   // kMinObserveBeforeAbandon (k = 1 -> plain)
 constexpr double kDemote = 0.95, kAbandon = 0.90;
 constexpr double kCostK1 = 1.58, kCostK2 = 1.90;   // the reference's round / step midpoints
+int fail(int code, const char* msg) {
+    q35_set_error(msg);
+    return code;
+}
 }  // namespace
 
 struct q35_mtp_policy {
@@ -40,9 +46,10 @@ struct q35_mtp_policy {
 extern "C" {
 
 int q35_mtp_policy_create(int start_k, double cost_k1, double cost_k2, q35_mtp_policy** out) {
-    if (!out || start_k < 0 || start_k > 2) return Q35_ERR_ARG;
+    if (!out) return fail(Q35_ERR_ARG, "q35_mtp_policy_create: null output");
+    if (start_k < 0 || start_k > 2) return fail(Q35_ERR_ARG, "q35_mtp_policy_create: start_k is 0, 1 or 2");
     auto* p = new (std::nothrow) q35_mtp_policy();
-    if (!p) return Q35_ERR_STATE;
+    if (!p) return fail(Q35_ERR_STATE, "q35_mtp_policy_create: out of host memory");
     p->k = p->ceiling = start_k;
     if (cost_k1 > 0.0) p->cost1 = cost_k1;
     if (cost_k2 > 0.0) p->cost2 = cost_k2;
@@ -56,13 +63,15 @@ int q35_mtp_policy_free(q35_mtp_policy* p) {
 }
 
 int q35_mtp_policy_k(const q35_mtp_policy* p, int32_t* k) {
-    if (!p || !k) return Q35_ERR_ARG;
+    if (!p || !k) return fail(Q35_ERR_ARG, "q35_mtp_policy_k: null argument");
     *k = p->k;
     return Q35_OK;
 }
 
 int q35_mtp_policy_note(q35_mtp_policy* p, int k_round, int emitted, int32_t* change, double* est) {
-    if (!p || k_round < 0 || k_round > 2 || emitted < 0) return Q35_ERR_ARG;
+    if (!p) return fail(Q35_ERR_ARG, "q35_mtp_policy_note: null policy");
+    if (k_round < 0 || k_round > 2 || emitted < 0)
+        return fail(Q35_ERR_ARG, "q35_mtp_policy_note: k_round is 0 .. 2 and emitted >= 0");
     if (change) change[0] = change[1] = change[2] = -1;
     p->rounds[k_round]++;
     if (p->k == 0) {                                   // abandoned: sticky

@@ -47,7 +47,7 @@ from pathlib import Path
 
 import numpy as np
 
-from .engine import VOCAB, Engine, EngineError, MtpPolicy, State
+from .engine import MI355X_ROUND_COST, VOCAB, Engine, EngineError, MtpPolicy, State
 
 STOP_TOKEN = 248046                  # engine/decode_step.h:492 (kStopToken)
 DEFAULT_CAP = 4096                   # engine/decode_run.cpp:72 (kSessionDefaultCap)
@@ -63,7 +63,7 @@ class Session:
         self.cap = cap
         self.mtp_k = mtp_k
         self.adaptive = adaptive and mtp_k > 0
-        self.policy = MtpPolicy(mtp_k) if self.adaptive else None
+        self.policy = self._policy() if self.adaptive else None
         self.state = State(eng, 1, cap, mtp_k=mtp_k, mtp_cap=cap if mtp_k else 0)
         self.rounds = 0
         self.turn = np.zeros(4, np.int64)     # drafted, accepted, bonus, verified rows this turn
@@ -77,7 +77,11 @@ class Session:
         """A fresh adaptive tracker (mtpaccept::session_new_turn, engine/mtp_accept.cpp:501-504)."""
         if self.adaptive:
             self.policy.close()
-            self.policy = MtpPolicy(self.mtp_k)
+            self.policy = self._policy()
+
+    def _policy(self) -> MtpPolicy:
+        """A fresh tracker billing rounds at this engine's measured round costs."""
+        return MtpPolicy(self.mtp_k, MI355X_ROUND_COST[1], MI355X_ROUND_COST[2])
 
     def ready_line(self) -> str:
         return f"READY cap={self.cap}"

@@ -68,10 +68,10 @@ def test_start_at_k1_and_costs():
 
 
 def test_bad_arguments():
-    with pytest.raises(EngineError):
+    with pytest.raises(EngineError, match="start_k is 0, 1 or 2"):
         MtpPolicy(3)
     p = MtpPolicy(2)
-    with pytest.raises(EngineError):
+    with pytest.raises(EngineError, match="k_round is 0 .. 2"):
         p.note(3, 1)
-    with pytest.raises(EngineError):
+    with pytest.raises(EngineError, match="emitted >= 0"):
         p.note(2, -1)
