@@ -363,6 +363,11 @@ def main():
         mtp["accepting_b%d" % B] = run_mtp_accepting(eng, B, L, args.mtp_rounds)
         mtp["accepting_b1"] = run_mtp_accepting(eng, 1, L, 4 * args.mtp_rounds)
     pre = run_prefill(eng, args.prefill_len) if 0 < args.prefill_len <= eng.max_ctx - 64 else None
+    if pre is not None:
+        # the same prompt byte-identical to token-by-token feeding (prompt_exact): its price
+        eng.set_option("prompt_exact", 1)
+        pre["exact"] = run_prefill(eng, args.prefill_len, reps=1)
+        eng.set_option("prompt_exact", 0)
     cpu = None
     if not args.no_cpu:
         tps, thr, n, rates = cpu_baseline(L)

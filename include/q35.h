@@ -237,7 +237,11 @@ int q35_kprof_read(q35_engine* e, float* total_ms, int* launches);
  * step keeps each lane's GDN state update as pending factors for up to this many steps and
  * writes the state with the next one; 0 writes it every step). Not bit-identical, a different
  * rounding point within the stated tolerance: "attn_prompt" (1: prompt waves of one lane with
- * >= 64 rows use the flash-form MFMA attention kernel, 0: the one-row kernels). */
+ * >= 64 rows use the flash-form MFMA attention kernel, 0: the one-row kernels); "prompt_exact" (1:
+ * prompt waves run the decode step's arithmetic -- the one-row attention kernels and the recurrent
+ * GDN kernel -- so a prompt is byte-identical to feeding its tokens one decode step at a time,
+ * the reference's own equivalence for its prefill wave, engine/prefill.h:5-9; 0: the flash
+ * attention and chunked GDN forms, the default, equal to it within the stated tolerance). */
 int q35_set_option(q35_engine* e, const char* name, int value);
 /* Copy the current content of a named scratch buffer ("x", "h", "nrm", "delta", "proj",
  * "o", "gu", "aout", "q") to host, after the stream drains (diagnostics and tests). */

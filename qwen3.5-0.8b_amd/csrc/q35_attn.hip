@@ -398,6 +398,61 @@ __device__ __forceinline__ void part_weights(const float* scores, size_t s_strid
     }
 }
 
+// The softmax (max, sum) of a row's 4 heads from its nsl slice stats, in one wave, with
+// softmax_ml's arithmetic per head (lane i folds slices i, i + 64, ... in order, then the xor
+// butterfly), the heads interleaved so that their loads are in flight together. Every lane
+// ends with all four (m, l).
+__device__ __forceinline__ void wave_ml(const float* stats, size_t sst, int nsl, float* m, float* l) {
+    const int tid = threadIdx.x & 63;
+    // slices tid and tid + 64 held in registers (up to 128 slices, an 8,192-slot context),
+    // the rest re-read in the second pass; unconditional clamped loads, masked values
+#pragma unroll
+    for (int h = 0; h < 4; ++h) m[h] = -INFINITY;
+    float sm0[4][2], se0[4][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = min(tid + 64 * u, nsl - 1);
+        const bool ok = tid + 64 * u < nsl;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const float2 v = *(const float2*)(stats + h * sst + 2 * i);
+            sm0[h][u] = ok ? v.x : -INFINITY;
+            se0[h][u] = v.y;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) m[h] = fmaxf(m[h], sm0[h][u]);
+    for (int i = tid + 128; i < nsl; i += 64) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h) m[h] = fmaxf(m[h], stats[h * sst + 2 * i]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) m[h] = fmaxf(m[h], __shfl_xor(m[h], o, 64));
+#pragma unroll
+    for (int h = 0; h < 4; ++h) l[h] = 0.f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+        if (tid + 64 * u < nsl) {
+#pragma unroll
+            for (int h = 0; h < 4; ++h) l[h] += se0[h][u] * expf(sm0[h][u] - m[h]);
+        }
+    for (int i = tid + 128; i < nsl; i += 64) {
+        float sm[4], se[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) { sm[h] = stats[h * sst + 2 * i]; se[h] = stats[h * sst + 2 * i + 1]; }
+#pragma unroll
+        for (int h = 0; h < 4; ++h) l[h] += se[h] * expf(sm[h] - m[h]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) l[h] += __shfl_xor(l[h], o, 64);
+}
+
 // attention output element: bf16(bf16(sum of parts) * bf16(sigmoid(gate)))
 __device__ __forceinline__ uint16_t gated_out(const AttnArgs& a, int r, int qh, int d, float acc) {
     const uint16_t* pr = a.proj + (size_t)r * kAttnInRows;
@@ -587,56 +642,8 @@ __global__ void __launch_bounds__(64) attn_pv4(AttnArgs a) {
         const int idx = tid + k * 64, i = idx >> 7, t = idx & 127;
         sraw[k] = scores[i * a.sc_ld + t0 + min(t, n - 1)];
     }
-    // the softmax (max, sum) of the 4 heads with softmax_ml's arithmetic per head, the heads
-    // interleaved so that their loads are in flight together
-    const float* stats = a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 8;
-    const size_t sst = (size_t)a.max_chunks * 8;
-    const int nsl = slot / 64 + 1;
-    // slices tid and tid + 64 held in registers (up to 128 slices, an 8,192-slot context),
-    // the rest re-read in the second pass; unconditional clamped loads, masked values
-    float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    float sm0[4][2], se0[4][2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int i = min(tid + 64 * u, nsl - 1);
-        const bool ok = tid + 64 * u < nsl;
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            const float2 v = *(const float2*)(stats + h * sst + 2 * i);
-            sm0[h][u] = ok ? v.x : -INFINITY;
-            se0[h][u] = v.y;
-        }
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int h = 0; h < 4; ++h) m[h] = fmaxf(m[h], sm0[h][u]);
-    for (int i = tid + 128; i < nsl; i += 64) {
-#pragma unroll
-        for (int h = 0; h < 4; ++h) m[h] = fmaxf(m[h], stats[h * sst + 2 * i]);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
-#pragma unroll
-        for (int h = 0; h < 4; ++h) m[h] = fmaxf(m[h], __shfl_xor(m[h], o, 64));
-    float l[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-        if (tid + 64 * u < nsl) {
-#pragma unroll
-            for (int h = 0; h < 4; ++h) l[h] += se0[h][u] * expf(sm0[h][u] - m[h]);
-        }
-    for (int i = tid + 128; i < nsl; i += 64) {
-        float sm[4], se[4];
-#pragma unroll
-        for (int h = 0; h < 4; ++h) { sm[h] = stats[h * sst + 2 * i]; se[h] = stats[h * sst + 2 * i + 1]; }
-#pragma unroll
-        for (int h = 0; h < 4; ++h) l[h] += se[h] * expf(sm[h] - m[h]);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
-#pragma unroll
-        for (int h = 0; h < 4; ++h) l[h] += __shfl_xor(l[h], o, 64);
+    float m[4], l[4];
+    wave_ml(a.stats + ((size_t)r * kNq + 4 * j) * a.max_chunks * 8, (size_t)a.max_chunks * 8, slot / 64 + 1, m, l);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const int idx = tid + k * 64, i = idx >> 7, t = idx & 127;

@@ -1713,6 +1713,12 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
         } else if (n == "gdn_chunked") {
             HCK(hipStreamSynchronize(e->st));
             e->gdn_chunked = value ? 1 : 0;
+        } else if (n == "prompt_exact") {
+            // prompt waves in the decode step's arithmetic: the one-row attention kernels and the
+            // recurrent GDN kernel, so a prompt is byte-identical to feeding it token by token
+            HCK(hipStreamSynchronize(e->st));
+            e->gdn_chunked = value ? 0 : 1;
+            e->forms.attn_prompt = value ? 0 : 1;
         } else if (n == "b1_partials" || n == "attn_prompt" || n == "partial_rows" || n == "gemv_tpb" ||
                    n == "gemm_pre" || n == "lmhead_persist" || n == "attn_split4" || n == "attn_pair" || n == "attn_rows" || n == "gdn_rows" ||
                    n == "gdn_defer" || n == "mid_partials") {

@@ -80,8 +80,9 @@ def test_prefill_all_rows_equal_token_by_token(max_rows, n):
     from qwen35 import Engine, State
     ids = lane_prompt_ids(77, 0, n)
     e = Engine(max_rows=max_rows, max_ctx=512, seed=0)
-    e.set_option("attn_prompt", 0)    # the flash-form kernel rounds attention weights differently
-    e.set_option("gdn_chunked", 0)    # and the chunk form sums the delta rule in another order
+    # the flash-form kernel rounds attention weights before normalising and the chunk form sums
+    # the delta rule in another order: prompt_exact runs the decode step's kernels instead
+    e.set_option("prompt_exact", 1)
     try:
         sa = State(e, 1, 256)
         samp, top, lg = sa.prefill_all(0, ids, logits=True)
