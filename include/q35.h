@@ -174,7 +174,9 @@ int q35_op_gdn_step(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w,
  * capture, tight serving loops); it has no counterpart in the reference. Same arguments and
  * results; its scratch (the lane list, B ints) is a fixed per-GPU device array of 4,096 entries
  * held until the process ends, so B <= 4096 (larger B: Q35_ERR_CAP). Enqueued on the engine
- * stream without waiting (q35_sync waits); calls that overlap on one GPU race on the array. */
+ * stream without waiting (q35_sync waits). Calls of one engine are ordered on its stream; a call
+ * by another engine on the same GPU while the last call there is unfinished would race on the
+ * array and is refused (Q35_ERR_STATE): synchronise that engine first. */
 int q35_op_gdn_step_noalloc(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w, const uint16_t* A_log,
                             const uint16_t* dt_bias, float* S2, float* W2, float* o, int B);
 /* The same step with the layer's gated RMSNorm (engine/kernels_gdn.cpp:525, specimpl.py:142-147,

@@ -121,6 +121,7 @@ struct q35_engine {
     size_t kev_used = 0;
     hipStream_t st = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    hipEvent_t noalloc_ev = nullptr;   // recorded after each allocation-free call of this engine
     uint16_t* blob = nullptr;
     size_t blob_bytes = 0;
     bool weights_ready = false;
@@ -213,6 +214,10 @@ std::mutex g_scratch_mu;
 std::map<int, int*> g_scratch_ptr;   // device ordinal -> device address of `scratch`
 
 std::map<int, std::string> g_scratch_err;   // device ordinal -> why the lookup failed
+// device ordinal -> the engine whose allocation-free call used the array last, and the event
+// that engine records after each such call: another engine (another stream) is refused while
+// that event is pending, instead of racing on the array
+std::map<int, std::pair<const void*, hipEvent_t>> g_scratch_owner;
 
 // Never fails the caller (q35_create): a failed lookup is recorded and reported by the
 // allocation-free entry point, the only user of the array.
@@ -229,12 +234,32 @@ void init_noalloc_scratch(int device) {
     g_scratch_ptr[device] = p;
 }
 
-int* noalloc_scratch(int device) {
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
+// The array of `device` for a call by `owner`, whose work will be followed on its stream by
+// `ev`: refused while another owner's last call may still be running. The caller holds
+// g_scratch_mu until it has enqueued its work and recorded `ev`.
+int* noalloc_scratch(int device, const void* owner, hipEvent_t ev) {
     auto it = g_scratch_ptr.find(device);
-    if (it != g_scratch_ptr.end()) return it->second;
-    auto er = g_scratch_err.find(device);
-    throw Q35Error(Q35_ERR_HIP, er != g_scratch_err.end() ? er->second : "scratch of this device was not set up");
+    if (it == g_scratch_ptr.end()) {
+        auto er = g_scratch_err.find(device);
+        throw Q35Error(Q35_ERR_HIP, er != g_scratch_err.end() ? er->second : "scratch of this device was not set up");
+    }
+    auto ow = g_scratch_owner.find(device);
+    if (ow != g_scratch_owner.end() && ow->second.first != owner) {
+        const hipError_t q = hipEventQuery(ow->second.second);
+        if (q == hipErrorNotReady)
+            throw Q35Error(Q35_ERR_STATE, "the allocation-free scratch of this GPU is in use by another engine's "
+                                          "unfinished call (calls on one GPU share it): wait for that engine first");
+        (void)hipGetLastError();
+    }
+    g_scratch_owner[device] = {owner, ev};
+    return it->second;
+}
+
+// An engine going away gives up its claim on the array.
+void noalloc_release(int device, const void* owner) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto ow = g_scratch_owner.find(device);
+    if (ow != g_scratch_owner.end() && ow->second.first == owner) g_scratch_owner.erase(ow);
 }
 
 __global__ void iota_kernel(int* p, int n) {
@@ -815,6 +840,7 @@ int q35_create(const q35_config* cfg, q35_engine** out) {
         HCK(hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking));
         HCK(hipEventCreate(&e->ev0));
         HCK(hipEventCreate(&e->ev1));
+        HCK(hipEventCreateWithFlags(&e->noalloc_ev, hipEventDisableTiming));
         plan_weights(e);
         resolve_plain(e);
         alloc_scratch(e);
@@ -834,8 +860,10 @@ int q35_destroy(q35_engine* e) {
         for (void* p : ds) if (p) hipFree(p);
         void* hs[] = {e->hin, e->h_out};
         for (void* p : hs) if (p) hipHostFree(p);
+        noalloc_release(e->device, e);
         hipEventDestroy(e->ev0);
         hipEventDestroy(e->ev1);
+        if (e->noalloc_ev) hipEventDestroy(e->noalloc_ev);
         hipStreamDestroy(e->st);
         delete e;
     });
@@ -1611,14 +1639,16 @@ int q35_op_gdn_step_norm(q35_engine* e, const uint16_t* proj, const uint16_t* co
 
 // The allocation-free form of q35_op_gdn_step: no hipMalloc / hipFree and no host copy (the
 // lane list is written on the device into the per-GPU `scratch` array); asynchronous on the
-// engine stream (q35_sync waits for it). Calls that overlap on one GPU share the array.
+// engine stream (q35_sync waits for it). Calls that would overlap on one GPU -- another
+// engine's call while this GPU's last one is still running -- are refused (Q35_ERR_STATE).
 int q35_op_gdn_step_noalloc(q35_engine* e, const uint16_t* proj, const uint16_t* conv_w, const uint16_t* A_log,
                             const uint16_t* dt_bias, float* S2, float* W2, float* o, int B) {
     return guard([&] {
         REQ(e && proj && conv_w && A_log && dt_bias && S2 && W2 && o && B > 0, Q35_ERR_ARG, "bad gdn call");
         REQ(B <= kNoAllocMaxLanes, Q35_ERR_CAP,
             "B exceeds the allocation-free GDN step's maximum of " + std::to_string(kNoAllocMaxLanes) + " lanes");
-        int* lanes = noalloc_scratch(e->device);
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        int* lanes = noalloc_scratch(e->device, e, e->noalloc_ev);
         hipLaunchKernelGGL(iota_kernel, dim3((B + 255) / 256), dim3(256), 0, e->st, lanes, B);
         HCK(hipGetLastError());
         GdnArgs g{};
@@ -1630,6 +1660,7 @@ int q35_op_gdn_step_noalloc(q35_engine* e, const uint16_t* proj, const uint16_t*
         const int cs = B <= 8 ? 8 : B <= 32 ? 4 : B <= 64 ? 2 : 1;
         if (cs == 1) HCK(launch_gdn_persist(g, e->st));
         else HCK(launch_gdn(g, cs, e->st));
+        HCK(hipEventRecord(e->noalloc_ev, e->st));
     });
 }
 

@@ -26,3 +26,17 @@ def golden():
     import numpy as np
     d = REPO / "tests" / "golden"
     return {n: np.load(d / f"{n}.npz") for n in ("config0_greedy", "config0_chunk_prefill", "config0_online", "mtp_k2")}
+
+
+@pytest.fixture(scope="session", autouse=True)
+def _torch_hip_first():
+    """Initialise torch's HIP runtime before any test loads libqwen35.so: the tests use torch
+    for device buffers, and a process whose first HIP user was the library can leave torch
+    without a device."""
+    try:
+        import torch
+        if torch.cuda.is_available():
+            torch.zeros(1, device="cuda")
+    except ImportError:
+        pass
+    yield

@@ -19,6 +19,37 @@ def _inputs(B, seed):
     return proj, S2, W2
 
 
+def test_noalloc_refuses_another_engine_while_busy(oracle_weights):
+    """Two engines on one GPU share the array: while one engine's call is unfinished, the other
+    engine's call is refused (it would race); after a sync it runs, and matches."""
+    import torch
+    from qwen35 import Engine, EngineError
+    ea = Engine(max_rows=64, max_ctx=256, seed=None)
+    eb = Engine(max_rows=64, max_ctx=256, seed=None)
+    try:
+        p = "model.language_model.layers.0.linear_attn."
+        cw, al, db = (oracle_weights.p[p + n].contiguous().cuda() for n in ("conv1d.weight", "A_log", "dt_bias"))
+        B = 4096                     # ~8 GiB of state: a call that runs for milliseconds
+        print(f"noalloc two engines B={B}", flush=True)
+        proj = torch.randn(B, 8224, device="cuda").to(torch.bfloat16)
+        S2 = torch.zeros(B, 2, 16, 128, 128, dtype=torch.float32, device="cuda")
+        W2 = torch.zeros(B, 2, 3, 6144, dtype=torch.float32, device="cuda")
+        o = torch.empty(B, 2048, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        args = (proj.data_ptr(), cw.data_ptr(), al.data_ptr(), db.data_ptr(), S2.data_ptr(), W2.data_ptr(),
+                o.data_ptr())
+        ea.op_gdn_step_noalloc(*args, B)
+        with pytest.raises(EngineError, match="in use by another engine"):
+            eb.op_gdn_step_noalloc(*args, 8)
+        ea.op_gdn_step_noalloc(*args, B)          # the same engine: ordered on its stream
+        ea.sync()
+        eb.op_gdn_step_noalloc(*args, 8)          # the GPU's last call is done: runs
+        eb.sync()
+    finally:
+        ea.close()
+        eb.close()
+
+
 def test_noalloc_gdn_step_equals_allocating_step(oracle_weights):
     import torch
     from qwen35 import Engine, EngineError
