@@ -111,14 +111,16 @@ __device__ __forceinline__ void argmax16(float& v, int& idx) {
 
 // Epilogue of one 16x16 tile: lane holds D[row0 + 4*(lane/16) + r][col0 + lane%16].
 template <int EM>
-__device__ __forceinline__ void epilogue(const GemmArgs& a, q35_f32x4 sum, int nt, int row0, int lane) {
+__device__ __forceinline__ void epilogue(const GemmArgs& a, q35_f32x4 sum, int nt, int row0, int lane,
+                                         int kchain = -1) {
     const int col = nt * 16 + (lane & 15);
     const int g = lane >> 4;
-    if (EM == kEPartial) {      // sum is one k-block chain: blockIdx.z is its k-block
+    if (EM == kEPartial) {      // sum is the chain of k-block kchain (default: blockIdx.z)
+        const int kc = kchain >= 0 ? kchain : (int)blockIdx.z;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             int row = row0 + 4 * g + r;
-            if (row < a.M) a.kpart[((size_t)blockIdx.z * a.M + row) * a.N + col] = sum[r];
+            if (row < a.M) a.kpart[((size_t)kc * a.M + row) * a.N + col] = sum[r];
         }
     } else if (EM == kEStore) {
 #pragma unroll
@@ -435,8 +437,24 @@ __global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
     // runs on XCD b % 8; give the M tiles of one column block consecutive slots on the
     // same XCD, so its weight tiles are fetched from HBM once and then hit that XCD's L2.
     const int mb = (a.M + MT * 16 - 1) / (MT * 16);
-    const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
-    const int nblk = (idx / mb) * 8 + xcd;
+    const int KB = a.K >> 8;
+    constexpr bool KXCD = EM == kEPartial && !FULLK;
+    int nblk, rb, kbx = 0;
+    if constexpr (KXCD) {
+        // one k-block chain per block: XCD x takes k-blocks x, x + 8, ... of every tile, so each
+        // slice of A and W is fetched from HBM by one XCD only (the column-block order below
+        // fetches A once per XCD); the grid is 8 x tiles x ceil(KB / 8) blocks
+        const int nb = (a.N / 16 + NW - 1) / NW, ntiles = nb * mb;
+        const int xcd = blockIdx.x & 7, i = blockIdx.x >> 3;
+        kbx = xcd + 8 * (i / ntiles);
+        if (kbx >= KB) return;
+        nblk = (i % ntiles) / mb;
+        rb = (i % ntiles) % mb;
+    } else {
+        const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
+        nblk = (idx / mb) * 8 + xcd;
+        rb = idx % mb;
+    }
     // kESiluMul: waves 0 .. NW/2-1 take gate tiles j, waves NW/2 .. take the up tiles j
     constexpr int HW = NW / 2;
     const int half = a.N / 32;                                  // gate tiles
@@ -444,12 +462,11 @@ __global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
     if (EM == kESiluMul ? nblk * HW >= half : nblk * NW >= a.N / 16) return;
     const int nt = EM == kESiluMul ? (wv < HW ? jg : half + jg) : nblk * NW + wv;
     const bool nvalid = EM == kESiluMul ? jg < half : nt < a.N / 16;
-    const int row0 = (idx % mb) * MT * 16;
-    const int KB = a.K >> 8;
-    // kEPartial: one k-block chain per block (grid z = KB), or -- FULLK, enough row blocks to
-    // fill the chip -- every chain summed in order in the block and stored as chain 0
-    const int kb0 = EM == kEPartial && !FULLK ? blockIdx.z : 0;
-    const int kb1 = EM == kEPartial && !FULLK ? blockIdx.z + 1 : KB;
+    const int row0 = rb * MT * 16;
+    // kEPartial: one k-block chain per block, or -- FULLK, enough row blocks to fill the
+    // chip -- every chain summed in order in the block and stored as chain 0
+    const int kb0 = KXCD ? kbx : 0;
+    const int kb1 = KXCD ? kbx + 1 : KB;
     q35_f32x4 sum[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) sum[i] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
@@ -524,7 +541,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_large_m(GemmArgs a) {
     }
     if (!nvalid) return;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) epilogue<EM>(a, sum[mt], nt, row0 + mt * 16, lane);
+    for (int mt = 0; mt < MT; ++mt) epilogue<EM>(a, sum[mt], nt, row0 + mt * 16, lane, KXCD ? kbx : 0);
 }
 
 // ---------------------------------------------------------------- K = 1024, batched lanes
@@ -1043,8 +1060,10 @@ static void launch_large(const GemmArgs& a, hipStream_t st) {
     }
     if (EM == kEPartial && gz == 1)
         hipLaunchKernelGGL((gemm_large_m<EM, 4, 4, true>), dim3((nb + 7) / 8 * 8 * mb, 1, 1), dim3(256), 0, st, a);
+    else if (EM == kEPartial)      // k-blocks by XCD: 8 x tiles x ceil(KB / 8) blocks
+        hipLaunchKernelGGL((gemm_large_m<EM, 4, 4>), dim3(8 * nb * mb * ((gz + 7) / 8)), dim3(256), 0, st, a);
     else
-        hipLaunchKernelGGL((gemm_large_m<EM, 4, 4>), dim3((nb + 7) / 8 * 8 * mb, 1, gz), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((gemm_large_m<EM, 4, 4>), dim3((nb + 7) / 8 * 8 * mb, 1, 1), dim3(256), 0, st, a);
 }
 
 template <int AM, int EM>
