@@ -135,6 +135,15 @@ int q35_mtp_round(q35_engine* e, q35_state* s, const int32_t* lanes, int n, cons
 int q35_mtp_round_stop(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* cur,
                        int k, int32_t stop, int32_t* emit, int32_t* n_emit, int64_t* stats);
 
+/* The verify half of a round on drafts the caller made (mtpaccept::accept_round with its
+ * candidates, engine/mtp_accept.h:248): drafts [n][k] (draft step j of lane i at i * k + j, as
+ * q35_mtp_draft steps 0 .. k-1 made them, whose MTP K/V entries are then kept on a full accept);
+ * the (k+1)-row verify body over [cur, drafts], accept, rollback, emit, n_emit, stop and stats as
+ * in q35_mtp_round_stop. Drafts from elsewhere verify the same way (greedy verification is
+ * lossless whatever the drafts); only the drafter's own cache assumes they came from it. */
+int q35_mtp_verify(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* cur, int k,
+                   const int32_t* drafts, int32_t stop, int32_t* emit, int32_t* n_emit, int64_t* stats);
+
 /* Adaptive speculation depth (mtpadapt::Tracker, engine/mtp_adaptive.h:1-254): one policy per
  * request decides the depth of its next round -- 2, 1, or 0 (plain steps for the rest of the
  * request) -- from the tokens its own rounds emitted: the window estimate is emitted tokens per

@@ -1452,6 +1452,52 @@ int q35_mtp_round(q35_engine* e, q35_state* s, const int32_t* lanes, int n, cons
 // stop >= 0: an accepted draft equal to `stop` ends the accepted prefix (the target row before
 // it chose the same token, so it is emitted as the bonus and left pending, never fed): the
 // session driver's stop cut, engine/mtp_accept.cpp:585-600
+// The verify body of a speculative round and its greedy accept / rollback (speccheck/mtp.py:
+// 150-177; mtpaccept::accept_round, engine/mtp_accept.h:248): per lane, the (k+1)-row body
+// over [cur, d1..dk] with per-row GDN factors, accept of the longest prefix the target rows
+// confirm (the stop cut applied), then the state, window and MTP cache kept for rows 0..a.
+static void mtp_verify_accept(q35_engine* e, q35_state* s, const std::vector<int>& ls, const std::vector<int>& P,
+                   const int32_t* cur, int k, const std::vector<std::vector<int>>& drafts, int32_t stop,
+                   int32_t* emit, int32_t* n_emit, int64_t* stats) {
+    const int n = (int)ls.size();
+    // verify body over [cur, d1..dk] per lane with per-row GDN checkpoints
+    HCK(hipStreamSynchronize(e->st));
+    const int T = k + 1, R = n * T;
+    for (int i = 0; i < n; ++i)
+        for (int t = 0; t < T; ++t) {
+            int r = i * T + t;
+            e->h_tok[r] = t == 0 ? cur[i] : drafts[i][t - 1];
+            e->h_lane[r] = ls[i]; e->h_pos[r] = P[i] + t; e->h_slot[r] = P[i] + t;
+        }
+    body(e, s, R, T, true);
+    lm_head(e, 0, R, false, !body_final_normed(e, R, T, true) ? e->final_norm : nullptr);
+    HCK(hipMemcpyAsync(e->h_out, e->tok_dev, R * sizeof(int), hipMemcpyDeviceToHost, e->st));
+    HCK(hipStreamSynchronize(e->st));
+    std::vector<int> rows(n);
+    for (int i = 0; i < n; ++i) {
+        const int* tgt = e->h_out + i * T;
+        int a = 0;
+        while (a < k && drafts[i][a] == tgt[a] && drafts[i][a] != stop) ++a;
+        int m = 0;
+        for (int j = 0; j < a; ++j) emit[i * (k + 1) + m++] = drafts[i][j];
+        emit[i * (k + 1) + m++] = tgt[a];
+        n_emit[i] = m;
+        const int l = ls[i];
+        s->prefix[l] = P[i] + a + 1;
+        // the verify body recorded every row as factors on top of slot cur (after moving
+        // the lane's earlier pending rows into slot cur + 1): rows 0..a are now pending
+        if (s->pend[l] > 0) s->cur[l] = (s->cur[l] + 1) % s->nslots;
+        s->pend[l] = a + 1;
+        s->pset[l] ^= 1;
+        s->wcur[l] = (s->wcur[l] + 1 + a) % s->nslots;
+        if (a == k) s->mtp_len[l] += k;
+        rows[i] = i * T + a;
+        if (stats) { stats[0] += k; stats[1] += a; stats[2] += 1; stats[3] += T; }
+    }
+    save_hlast(e, s, rows, ls);
+    HCK(hipStreamSynchronize(e->st));
+}
+
 int q35_mtp_round_stop(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* cur,
                        int k, int32_t stop, int32_t* emit, int32_t* n_emit, int64_t* stats) {
     return guard([&] {
@@ -1475,42 +1521,35 @@ int q35_mtp_round_stop(q35_engine* e, q35_state* s, const int32_t* lanes, int n,
             if (rc) throw Q35Error(rc, g_err);
             for (int i = 0; i < n; ++i) { drafts[i][j] = dt[i]; y[i] = dt[i]; }
         }
-        // verify body over [cur, d1..dk] per lane with per-row GDN checkpoints
-        HCK(hipStreamSynchronize(e->st));
-        const int T = k + 1, R = n * T;
-        for (int i = 0; i < n; ++i)
-            for (int t = 0; t < T; ++t) {
-                int r = i * T + t;
-                e->h_tok[r] = t == 0 ? cur[i] : drafts[i][t - 1];
-                e->h_lane[r] = ls[i]; e->h_pos[r] = P[i] + t; e->h_slot[r] = P[i] + t;
-            }
-        body(e, s, R, T, true);
-        lm_head(e, 0, R, false, !body_final_normed(e, R, T, true) ? e->final_norm : nullptr);
-        HCK(hipMemcpyAsync(e->h_out, e->tok_dev, R * sizeof(int), hipMemcpyDeviceToHost, e->st));
-        HCK(hipStreamSynchronize(e->st));
-        std::vector<int> rows(n);
+        mtp_verify_accept(e, s, ls, P, cur, k, drafts, stop, emit, n_emit, stats);
+    });
+}
+
+// The verify half of a round on drafts the caller made (mtpaccept::accept_round's candidates,
+// engine/mtp_accept.h:248): draft step j of lane i in drafts[i * k + j].
+int q35_mtp_verify(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* cur, int k,
+                   const int32_t* drafts, int32_t stop, int32_t* emit, int32_t* n_emit, int64_t* stats) {
+    return guard([&] {
+        REQ(e && s && cur && drafts && emit && n_emit, Q35_ERR_ARG, "null argument");
+        REQ(k >= 1 && k <= s->mtp_k, Q35_ERR_STATE, "k exceeds the state's MTP slots");
+        REQ(n > 0 && n * (k + 1) <= e->R, Q35_ERR_CAP, "rows exceed max_rows");
+        ++e->meta_epoch;
+        std::vector<int> ls(n), P(n);
+        std::vector<std::vector<int>> dr(n, std::vector<int>(k));
         for (int i = 0; i < n; ++i) {
-            const int* tgt = e->h_out + i * T;
-            int a = 0;
-            while (a < k && drafts[i][a] == tgt[a] && drafts[i][a] != stop) ++a;
-            int m = 0;
-            for (int j = 0; j < a; ++j) emit[i * (k + 1) + m++] = drafts[i][j];
-            emit[i * (k + 1) + m++] = tgt[a];
-            n_emit[i] = m;
-            const int l = ls[i];
-            s->prefix[l] = P[i] + a + 1;
-            // the verify body recorded every row as factors on top of slot cur (after moving
-            // the lane's earlier pending rows into slot cur + 1): rows 0..a are now pending
-            if (s->pend[l] > 0) s->cur[l] = (s->cur[l] + 1) % s->nslots;
-            s->pend[l] = a + 1;
-            s->pset[l] ^= 1;
-            s->wcur[l] = (s->wcur[l] + 1 + a) % s->nslots;
-            if (a == k) s->mtp_len[l] += k;
-            rows[i] = i * T + a;
-            if (stats) { stats[0] += k; stats[1] += a; stats[2] += 1; stats[3] += T; }
+            ls[i] = lanes ? lanes[i] : i;
+            check_lane(s, ls[i]);
+            check_tok(cur[i]);
+            for (int j = 0; j < i; ++j) REQ(ls[j] != ls[i], Q35_ERR_ARG, "duplicate lane in one round");
+            P[i] = s->prefix[ls[i]];
+            REQ(P[i] + k + 1 <= s->cap, Q35_ERR_CAP, "lane cache is full");
+            REQ(s->mtp_len[ls[i]] + k <= s->mtp_cap, Q35_ERR_CAP, "MTP cache is full");
+            for (int j = 0; j < k; ++j) {
+                check_tok(drafts[i * k + j]);
+                dr[i][j] = drafts[i * k + j];
+            }
         }
-        save_hlast(e, s, rows, ls);
-        HCK(hipStreamSynchronize(e->st));
+        mtp_verify_accept(e, s, ls, P, cur, k, dr, stop, emit, n_emit, stats);
     });
 }
 

@@ -73,6 +73,8 @@ _SIGS = {
     "q35_op_gdn_step_norm": ([C.c_void_p] * 10 + [C.c_int, C.c_int], C.c_int),
     "q35_op_gemm_a": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
                        C.c_int, C.c_void_p, C.c_int, C.c_void_p], C.c_int),
+    "q35_mtp_verify": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int32,
+                        C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "q35_op_attn_decode": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
                            + [C.c_void_p] * 4 + [C.c_int], C.c_int),
     "q35_op_lm_head_argmax": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p], C.c_int),
@@ -393,6 +395,20 @@ class State:
         _ck(load_library().q35_mtp_draft(self.eng.h, self.h, _p(ln) if ln is not None else None, n, _p(y),
                                          _p(pos), step, _p(out), _p(xd), _p(lg) if logits else None))
         return out, xd, lg
+
+    def mtp_verify(self, cur, drafts, lanes=None, stats: np.ndarray | None = None, stop: int = -1):
+        """The verify half of a round on the caller's drafts [n][k] (mtpaccept::accept_round's
+        candidates); returns each lane's emitted tokens."""
+        c = _i32(cur)
+        d = np.ascontiguousarray(np.asarray(drafts, np.int32).reshape(c.size, -1))
+        n, k = d.shape
+        ln = _i32(lanes) if lanes is not None else None
+        emit = np.zeros((n, k + 1), np.int32)
+        ne = np.zeros(n, np.int32)
+        st = stats if stats is not None else np.zeros(4, np.int64)
+        _ck(load_library().q35_mtp_verify(self.eng.h, self.h, _p(ln) if ln is not None else None, n, _p(c), k,
+                                          _p(d), stop, _p(emit), _p(ne), _p(st)))
+        return [list(emit[i, :ne[i]]) for i in range(n)]
 
     def mtp_round(self, cur, k: int, lanes=None, stats: np.ndarray | None = None, stop: int = -1):
         """One speculative round per lane; stop >= 0 applies the session's stop cut (an

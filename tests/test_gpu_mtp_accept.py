@@ -126,3 +126,58 @@ def test_adaptive_step_mixed_depths_lossless():
         plain.close()
     finally:
         eng.close()
+
+
+def test_draft_then_verify_equals_round():
+    """The reference's two-call round (mtpdraft::draft_round twice, then mtpaccept::accept_round
+    with the candidates) through q35_mtp_draft + q35_mtp_verify gives q35_mtp_round's emits and
+    leaves the same state (S, window, K/V, MTP K/V, prefix) bit for bit, over rounds that accept
+    no draft and both drafts (the reshaped-norm setting of the test above, factor -4)."""
+    from oracle.weights import lane_prompt_ids
+    from qwen35 import Engine, State
+    eng = Engine(max_rows=64, max_ctx=512, seed=0)
+    try:
+        emb = "model.language_model.embed_tokens.weight"
+        E = eng.read_tensor(emb, 248320 * 1024).reshape(248320, 1024)
+        E[STOP, D] = 0x4100
+        E[1000, D] = 0xC100
+        eng.load_tensor(emb, E.reshape(-1))
+        del E
+        eng.load_tensor("model.language_model.norm.weight", _norm_w(0xC0A0))
+        eng.load_tensor("mtp.norm.weight", _norm_w(0xC0A0))
+        lanes = 4
+        a = State(eng, lanes, 256, mtp_k=2, mtp_cap=256)
+        b = State(eng, lanes, 256, mtp_k=2, mtp_cap=256)
+        cur = []
+        for i in range(lanes):
+            ids = lane_prompt_ids(40 + i, 0, 6 + 2 * i)
+            y = a.prefill(i, ids)
+            assert b.prefill(i, ids) == y
+            cur.append(int(y))
+        ca, cb, seen = list(cur), list(cur), set()
+        for r in range(6):
+            print(f"draft + verify: round {r}", flush=True)
+            ea = a.mtp_round(ca, 2)
+            P = [b.prefix_len(i) for i in range(lanes)]
+            d1, _, _ = b.mtp_draft(cb, [p + 1 for p in P], 0)
+            d2, _, _ = b.mtp_draft(d1, [p + 2 for p in P], 1)
+            eb = b.mtp_verify(cb, np.stack([d1, d2], 1))
+            assert [list(map(int, x)) for x in ea] == [list(map(int, x)) for x in eb], r
+            seen |= {len(x) - 1 for x in ea}
+            ca = [int(x[-1]) for x in ea]
+            cb = [int(x[-1]) for x in eb]
+        for i in range(lanes):
+            n = a.prefix_len(i)
+            assert n == b.prefix_len(i)
+            for w in ("S", "win"):
+                assert np.array_equal(a.read(i, w), b.read(i, w)), (i, w)
+            for w in ("k", "v"):
+                assert np.array_equal(a.read(i, w, n), b.read(i, w, n)), (i, w)
+            for w in ("mk", "mv"):
+                assert np.array_equal(a.read(i, w, 8), b.read(i, w, 8)), (i, w)
+        print("accepted drafts per round seen:", sorted(seen), flush=True)
+        assert {0, 2} <= seen
+        a.close()
+        b.close()
+    finally:
+        eng.close()
