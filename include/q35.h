@@ -96,6 +96,16 @@ int q35_state_restore(q35_engine* e, q35_state* s, int lane, const void* host, s
 int q35_prefill(q35_engine* e, q35_state* s, int lane, const int32_t* ids, int n, int32_t* y0,
                 float* logits);
 
+/* Prompts of n lanes at once (the batched form of prefill_wave, engine/prefill.cpp:63, which takes
+ * one request): lane lanes[i] (i when NULL) consumes ids[off_i .. off_i + lens[i]) with off_i the
+ * sum of the lens before it; rows of different lanes share each body pass (rounds of at most
+ * max_rows rows, the same row count for every lane of a round); y0[i] = greedy id after lane i's
+ * last prompt token; logits (nullable) [n][248320] that row's logits. Each lane ends as after
+ * q35_prefill of its own prompt (the same kernels for prompts under 64 tokens: bit-identical;
+ * a single lane takes q35_prefill's waves). */
+int q35_prefill_lanes(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* ids,
+                      const int32_t* lens, int32_t* y0, float* logits);
+
 /* The same prompt with every row priced (prefill_wave with PrefillLogits::kAll,
  * engine/prefill.h:46-58,116-118, the reference's byte-identity gate mode): sampled[i] = greedy
  * id (lowest id on ties) of prompt row i, top_logit[i] (nullable) = that id's bf16-valued

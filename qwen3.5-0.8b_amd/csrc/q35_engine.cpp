@@ -730,9 +730,10 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt, int defe
 // batched body the normed rows are in e->nrm; after a batch-1 body (`normw` given) the
 // final RMSNorm of the residual rows is applied first.
 void lm_head(q35_engine* e, int row0, int M, bool want_logits, const uint16_t* normw = nullptr,
-             float* top_val = nullptr) {
+             float* top_val = nullptr, const uint16_t* rows = nullptr) {
     GemmArgs a{};
-    a.W = e->E; a.N = kVocab; a.K = kHidden; a.M = M; a.X = e->nrm + (size_t)row0 * kHidden; a.ldx = kHidden;
+    a.W = e->E; a.N = kVocab; a.K = kHidden; a.M = M; a.ldx = kHidden;
+    a.X = (rows ? rows : e->nrm) + (size_t)row0 * kHidden;   // rows: final-normed rows given by the caller
     a.forms = e->forms;
     const int amode = kAPlain;
     if (normw)   // one small norm launch: cheaper than normalising in each of the 15,520 blocks
@@ -1318,6 +1319,89 @@ void prefill_waves(q35_engine* e, q35_state* s, int lane, const int32_t* ids, in
         *sampled = e->h_out[0];
     }
     HCK(hipStreamSynchronize(e->st));
+}
+
+// Prompts of several lanes in shared body passes (the batched form of prefill_wave,
+// engine/prefill.cpp:63, one wave per request there): every round takes the lanes with prompt
+// tokens left, at most max_rows rows, T rows per lane (the fewest any of them has left), so rows
+// of different lanes share each GEMM; a lane whose prompt ends in the round gets its greedy id
+// from its last row. A single lane takes the one-lane waves of q35_prefill (chunked GDN, flash
+// attention for >= 64 rows).
+static void prefill_lanes(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* ids,
+                          const int32_t* lens, int32_t* y0, float* logits) {
+    REQ(e && s && ids && lens && y0 && n > 0, Q35_ERR_ARG, "null argument");
+    std::vector<int> ls(n), off(n), left(n);
+    long long tot = 0;
+    for (int i = 0; i < n; ++i) {
+        ls[i] = lanes ? lanes[i] : i;
+        check_lane(s, ls[i]);
+        for (int j = 0; j < i; ++j) REQ(ls[j] != ls[i], Q35_ERR_ARG, "duplicate lane in one prefill");
+        REQ(lens[i] > 0, Q35_ERR_ARG, "empty prompt");
+        REQ(s->prefix[ls[i]] + lens[i] <= s->cap, Q35_ERR_CAP, "prompt exceeds the lane's cache capacity");
+        off[i] = (int)tot;
+        left[i] = lens[i];
+        tot += lens[i];
+    }
+    for (long long t = 0; t < tot; ++t) check_tok(ids[t]);
+    REQ(e->weights_ready, Q35_ERR_STATE, "weights not initialised");
+    if (n == 1) {
+        prefill_waves(e, s, ls[0], ids, lens[0], false, y0, nullptr, logits);
+        return;
+    }
+    for (;;) {
+        std::vector<int> act;
+        for (int i = 0; i < n; ++i) if (left[i] > 0) act.push_back(i);
+        if (act.empty()) break;
+        for (size_t g0 = 0; g0 < act.size(); g0 += (size_t)e->R) {
+            const std::vector<int> grp(act.begin() + g0, act.begin() + std::min(act.size(), g0 + (size_t)e->R));
+            const int nl = (int)grp.size();
+            int T = e->R / nl;
+            for (int i : grp) T = std::min(T, left[i]);
+            HCK(hipStreamSynchronize(e->st));
+            for (int k = 0; k < nl; ++k) {
+                const int i = grp[k], l = ls[i], done = lens[i] - left[i];
+                for (int t = 0; t < T; ++t) {
+                    const int r = k * T + t;
+                    e->h_tok[r] = ids[off[i] + done + t];
+                    e->h_lane[r] = l; e->h_pos[r] = s->prefix[l] + t; e->h_slot[r] = s->prefix[l] + t;
+                }
+            }
+            const int R = nl * T;
+            body(e, s, R, T, false);
+            if (!body_final_normed(e, R, T, false))
+                HCK(launch_addnorm(2, nullptr, nullptr, e->x, nullptr, nullptr, 0, e->final_norm, e->nrm, R, e->st));
+            std::vector<int> fin, src, fl;
+            for (int k = 0; k < nl; ++k) {
+                const int i = grp[k], l = ls[i];
+                s->prefix[l] += T;
+                advance_lane(s, l);
+                left[i] -= T;
+                if (left[i] == 0) { fin.push_back(i); src.push_back(k * T + T - 1); fl.push_back(l); }
+            }
+            if (fin.empty()) continue;
+            const int m = (int)fin.size();
+            save_hlast(e, s, src, fl);
+            // the finishing lanes' last rows, gathered contiguously for one lm_head pass
+            HCK(hipStreamSynchronize(e->st));
+            for (int k = 0; k < m; ++k) { e->h_src[k] = src[k]; e->h_dst[k] = k; }
+            upload_idx(e, m);
+            HCK(launch_copy_rows(e->nrm, e->ridx_src, e->h, e->ridx_dst, m, kHidden, e->st));
+            lm_head(e, 0, m, logits != nullptr, nullptr, nullptr, e->h);
+            HCK(hipMemcpyAsync(e->h_out, e->tok_dev, m * sizeof(int), hipMemcpyDeviceToHost, e->st));
+            if (logits)
+                for (int k = 0; k < m; ++k)
+                    HCK(hipMemcpyAsync(logits + (size_t)fin[k] * kVocab, e->logits_dev + (size_t)k * kVocab,
+                                       (size_t)kVocab * 4, hipMemcpyDeviceToHost, e->st));
+            HCK(hipStreamSynchronize(e->st));
+            for (int k = 0; k < m; ++k) y0[fin[k]] = e->h_out[k];
+        }
+    }
+    ++e->meta_epoch;
+}
+
+int q35_prefill_lanes(q35_engine* e, q35_state* s, const int32_t* lanes, int n, const int32_t* ids,
+                      const int32_t* lens, int32_t* y0, float* logits) {
+    return guard([&] { prefill_lanes(e, s, lanes, n, ids, lens, y0, logits); });
 }
 
 int q35_prefill(q35_engine* e, q35_state* s, int lane, const int32_t* ids, int n, int32_t* y0, float* logits) {

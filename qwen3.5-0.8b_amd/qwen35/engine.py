@@ -73,6 +73,8 @@ _SIGS = {
     "q35_op_gdn_step_norm": ([C.c_void_p] * 10 + [C.c_int, C.c_int], C.c_int),
     "q35_op_gemm_a": ([C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
                        C.c_int, C.c_void_p, C.c_int, C.c_void_p], C.c_int),
+    "q35_prefill_lanes": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
+                           C.c_void_p], C.c_int),
     "q35_mtp_verify": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int32,
                         C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "q35_op_attn_decode": ([C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
@@ -362,6 +364,19 @@ class State:
         _ck(load_library().q35_prefill(self.eng.h, self.h, lane, _p(ids), ids.size, C.byref(y0),
                                        _p(lg) if logits else None))
         return (y0.value, lg) if logits else y0.value
+
+    def prefill_lanes(self, prompts, lanes=None, logits: bool = False):
+        """Prompts of several lanes in shared body passes (q35_prefill_lanes): prompts[i] goes to
+        lane lanes[i] (i when None); returns the greedy ids after each prompt (and their logits)."""
+        ids = _i32(np.concatenate([np.asarray(p, np.int32) for p in prompts]))
+        lens = _i32([len(p) for p in prompts])
+        n = lens.size
+        ln = _i32(lanes) if lanes is not None else None
+        y0 = np.zeros(n, np.int32)
+        lg = np.empty((n, VOCAB), np.float32) if logits else None
+        _ck(load_library().q35_prefill_lanes(self.eng.h, self.h, _p(ln) if ln is not None else None, n, _p(ids),
+                                             _p(lens), _p(y0), _p(lg) if logits else None))
+        return (y0, lg) if logits else y0
 
     def prefill_all(self, lane: int, ids, logits: bool = False):
         """The prompt with every row priced (PrefillLogits::kAll, engine/prefill.h:46-58): per-row

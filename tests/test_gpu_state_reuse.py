@@ -102,3 +102,45 @@ def test_fork_with_mtp_cache(eng):
         assert np.array_equal(o[1], outs[0][1]) and np.array_equal(o[2], outs[0][2])
     for s in (a, b, c):
         s.close()
+
+
+@pytest.mark.parametrize("exact", [0, 1])
+def test_prefill_lanes_equals_one_lane_prefills(exact):
+    """q35_prefill_lanes (prompts of several lanes sharing body passes, ragged lengths, more
+    rows than max_rows so rounds split) against q35_prefill of each lane alone: greedy ids and
+    logits rows equal, and every lane's state (S, window, K/V, prefix) bit-identical. Prompts
+    under 64 tokens take the same kernels both ways; with prompt_exact the long prompt's waves
+    do too, so then the long lane is bit-identical as well (else within the engine tolerance)."""
+    from oracle.weights import lane_prompt_ids
+    from qwen35 import Engine, State
+    e = Engine(max_rows=64, max_ctx=512, seed=0)
+    try:
+        e.set_option("prompt_exact", exact)
+        lens = [5, 17, 1, 40, 9, 90]
+        prompts = [lane_prompt_ids(60 + i, 0, L) for i, L in enumerate(lens)]
+        lanes = [3, 0, 5, 1, 4, 2]
+        a = State(e, 6, 256)
+        y, lg = a.prefill_lanes(prompts, lanes, logits=True)
+        b = State(e, 6, 256)
+        for i, (p, ln) in enumerate(zip(prompts, lanes)):
+            yb, lb = b.prefill(ln, p, logits=True)
+            same = exact or len(p) < 64
+            if same:
+                assert int(y[i]) == int(yb) and np.array_equal(lg[i], lb), i
+            else:
+                assert np.abs(lg[i] - lb).max() <= 0.375, i
+            assert a.prefix_len(ln) == b.prefix_len(ln) == len(p)
+            if same:
+                for w in ("S", "win"):
+                    assert np.array_equal(a.read(ln, w), b.read(ln, w)), (i, w)
+                for w in ("k", "v"):
+                    assert np.array_equal(a.read(ln, w, len(p)), b.read(ln, w, len(p))), (i, w)
+        # and the lanes decode on from there as the one-lane states do
+        t = a.decode_step([int(v) for v in y], lanes)
+        tb = b.decode_step([int(v) for v in y], lanes)
+        short = [i for i, p in enumerate(prompts) if exact or len(p) < 64]
+        assert all(int(t[i]) == int(tb[i]) for i in short)
+        a.close()
+        b.close()
+    finally:
+        e.close()
