@@ -37,9 +37,13 @@ KERNEL_NAMES = {"attn": "attn_fused", "gdn": "gdn_persist", "lm_head": "gemm_lmh
 # the calibration are in the file named by TRAFFIC_SOURCE.
 TRAFFIC_SOURCE = "profiles/hbm_traffic_decode_b256_ctx4096.md"
 MEASURED_TRAFFIC = {
-    ("attn", 256, 4096): (1058666.2 * 2.0 + 1024.0 * 1.0) * 1024,                        # attn_fused
-    ("gdn", 256, 4096): (146571.6 * 2.0 + 90239.4 * 1.0) * 1024,    # gdn_persist, gdn_defer 3 (4-step average)
-    ("lm_head", 256, 4096): (250422.2 * 2.0 + 2048.0 * 1.0) * 1024,                       # gemm_lmhead3
+    ("attn", 256, 4096): (1057689.8 * 2.0 + 1024.0 * 1.0) * 1024,                        # attn_fused
+    ("gdn", 256, 4096): (146562.7 * 2.0 + 90237.5 * 1.0) * 1024,    # gdn_persist, gdn_defer 3 (4-step average)
+    ("lm_head", 256, 4096): (250422.1 * 2.0 + 2048.0 * 1.0) * 1024,                       # gemm_lmhead3
+    # projection / MLP family, the average launch of a step: 24 gate|up, 18 in_proj, 6 qkv, 24 down,
+    # 24 out/o (FETCH x2 + WRITE per launch of each, KiB)
+    ("gemm", 256, 4096): (24 * (9331.1 * 2 + 1792.0) + 18 * (10336.3 * 2 + 4116.2) + 6 * (7227.2 * 2 + 2560.0)
+                          + 24 * (4521.0 * 2 + 14336.0) + 24 * (2601.0 * 2 + 8192.0)) / 96 * 1024,
 }
 
 
@@ -129,6 +133,29 @@ def run_prefill(eng, n: int, reps: int = 2):
         best = dt if best is None else min(best, dt)
     st.close()
     return {"tokens": n, "ms": round(best * 1e3, 2), "tok_s": round(n / best, 1), "wave_rows": eng.max_rows}
+
+
+def run_prefill_lanes(eng, B: int, n: int, reps: int = 2):
+    """Prompts of n random ids into each of B lanes through shared body passes
+    (q35_prefill_lanes). Returns the best of `reps` timed passes."""
+    import numpy as np
+    from qwen35 import State
+    rng = np.random.default_rng(0)
+    prompts = [rng.integers(0, 248320, n).astype(np.int32) for _ in range(B)]
+    st = State(eng, B, n + 64)
+    st.prefill_lanes([p[:4] for p in prompts])     # warm
+    best = None
+    for _ in range(reps):
+        st.reset()
+        eng.sync()
+        t0 = time.perf_counter()
+        st.prefill_lanes(prompts)
+        eng.sync()
+        dt = time.perf_counter() - t0
+        best = dt if best is None else min(best, dt)
+    st.close()
+    return {"lanes": B, "tokens_per_lane": n, "ms": round(best * 1e3, 2), "tok_s": round(B * n / best, 1),
+            "max_rows": eng.max_rows}
 
 
 def run_mtp(eng, B: int, ctx: int, rounds: int, warmup: int, seed: int = 1, k: int = 2):
@@ -368,6 +395,7 @@ def main():
         eng.set_option("prompt_exact", 1)
         pre["exact"] = run_prefill(eng, args.prefill_len, reps=1)
         eng.set_option("prompt_exact", 0)
+        pre["lanes"] = run_prefill_lanes(eng, B, 64)
     cpu = None
     if not args.no_cpu:
         tps, thr, n, rates = cpu_baseline(L)
