@@ -210,7 +210,11 @@ int q35_op_gdn_step_norm(q35_engine* e, const uint16_t* proj, const uint16_t* co
 /* Y[M][N] = A . W^T with A made by one of the GEMM's A producers from X (and X2): amode 0 A = X
  * (bf16 [M][K]); 1 SwiGLU A = bf16(bf16(silu(X)) * X2) (X, X2 bf16 [M][K]); 2 gated RMSNorm
  * A = bf16(aux_w * (X * rsqrt(mean_head(X^2) + 1e-6)) * silu(X2)) (X f32 [M][K], X2 bf16 z,
- * aux_w [128]). M <= 16 uses the one-row GEMM's in-register producer, M > 16 the batched one. */
+ * aux_w [128]); 3 A = X through the many-row kernel (K = 1024, 17 <= M <= max_rows: X is tiled into
+ * the engine's staging, then the GEMM prompt waves of >= 512 rows use); 5 A = X with the batched
+ * SwiGLU epilogue, Y [M][N/2] = bf16(bf16(silu(bf16(X.Wg^T))) * bf16(X.Wu^T)) for W = [gate; up];
+ * 6 the same through the many-row kernel. M <= 16 uses the one-row GEMM's in-register producer,
+ * M > 16 the batched one. */
 int q35_op_gemm_a(q35_engine* e, const uint16_t* w_tiled_dev, int N, int K, int amode, const void* x_dev, int ldx,
                   const void* x2_dev, int ldx2, const uint16_t* aux_dev, int M, uint16_t* y_dev);
 /* One gated GQA attention layer of the decode path on a state's K/V cache (attn_decode_layer,

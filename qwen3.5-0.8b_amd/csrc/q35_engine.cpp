@@ -394,7 +394,7 @@ void resolve_plain(q35_engine* e) {
 void alloc_scratch(q35_engine* e) {
     const size_t R = e->R;
     e->x = dalloc<uint16_t>(R * kHidden);
-    e->h = dalloc<uint16_t>(R * kHidden);
+    e->h = dalloc<uint16_t>((R + 15) / 16 * 16 * kHidden);   // whole 16-row tiles (tiled layout)
     e->delta = dalloc<uint16_t>(R * kHidden);
     e->nrm = dalloc<uint16_t>(R * kHidden);
     e->proj = dalloc<uint16_t>(R * kGdnInRows);
@@ -521,9 +521,9 @@ void materialize(q35_engine* e, q35_state* s, const std::vector<int>& lanes) {
 // add+norm); emode kEResidual: x <- bf16(x + bf16(sum)) (batch-1 path).
 void gemm(q35_engine* e, const uint16_t* W, int N, int K, int M, const void* X, int ldx,
           uint16_t* Y, int ldy, int amode = kAPlain, const void* X2 = nullptr, int ldx2 = 0,
-          const uint16_t* aux = nullptr, int emode = -1, uint16_t* xres = nullptr) {
+          const uint16_t* aux = nullptr, int emode = -1, uint16_t* xres = nullptr, bool x_tiled = false) {
     GemmArgs a{};
-    a.W = W; a.N = N; a.K = K; a.M = M; a.X = X; a.ldx = ldx; a.X2 = X2; a.ldx2 = ldx2;
+    a.W = W; a.N = N; a.K = K; a.M = M; a.X = X; a.ldx = ldx; a.X2 = X2; a.ldx2 = ldx2; a.x_tiled = x_tiled ? 1 : 0;
     a.aux_w = aux; a.Y = Y; a.ldy = ldy;
     a.kpart = e->kpart; a.prod = e->prod; a.xres = xres; a.forms = e->forms;
     KTimer kt(e, kFamGemm);
@@ -533,6 +533,9 @@ void gemm(q35_engine* e, const uint16_t* W, int N, int K, int M, const void* X, 
 // Batch-1 path (<= 16 rows): the residual add lives in the producing GEMM's epilogue and the
 // RMSNorm in the consuming GEMM's A operand, so no add+norm launches remain.
 inline bool small_rows(int R) { return R <= 16; }
+// Bodies of >= 512 rows (prompt waves, MTP verify at many lanes): the normed rows e->h go out in
+// the weights' tiled fragment layout and the K = 1024 GEMMs that read them run gemm_wide.
+inline bool wide_rows(const q35_engine* e, int R) { return e->forms.gemm_wide && R >= 512; }
 
 // One-row bodies (a batch-1 decode step, a one-token prompt): the 1024-wide GEMVs (out_proj,
 // o_proj, down) run one wave per (column tile, k-block) and leave their k-block chains in
@@ -603,7 +606,8 @@ void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16
     if (small_rows(R))
         norm_gemm(e, rr, w.W_in, kAttnInRows, R, e->proj, kAttnInRows, w.norm_in);
     else
-        gemm(e, w.W_in, kAttnInRows, kHidden, R, e->h, kHidden, e->proj, kAttnInRows);
+        gemm(e, w.W_in, kAttnInRows, kHidden, R, e->h, kHidden, e->proj, kAttnInRows, kAPlain, nullptr, 0, nullptr, -1,
+             nullptr, wide_rows(e, R));
     AttnArgs a{};
     a.proj = e->proj; a.q_norm = w.q_norm; a.k_norm = w.k_norm;
     a.kc = kc; a.vc = vc; a.kv_lane = kv_lane; a.kv_layer_off = layer_off; a.cap = cap;
@@ -630,16 +634,19 @@ void mlp_layer(q35_engine* e, const LayerW& w, int R, B1Res* rr = nullptr) {
         resid_gemm(e, rr, w.W_down, kFF, R, e->gu, kGuRows, kASiluMul, e->gu + kFF, kGuRows);
         return;
     }
-    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(R, 2048, e->forms), w.norm_post, e->h, R, e->st));
+    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(R, 2048, e->forms), w.norm_post, e->h, R, e->st,
+                       wide_rows(e, R)));
     // gate|up GEMM with the SwiGLU product in its epilogue: act [R][3584] -> plain down GEMM
-    gemm(e, w.W_gu, kGuRows, kHidden, R, e->h, kHidden, e->gu, kFF, kAPlain, nullptr, 0, nullptr, kESiluMul);
+    gemm(e, w.W_gu, kGuRows, kHidden, R, e->h, kHidden, e->gu, kFF, kAPlain, nullptr, 0, nullptr, kESiluMul, nullptr,
+         wide_rows(e, R));
     gemm(e, w.W_down, kHidden, kFF, R, e->gu, kFF, nullptr, 0);
 }
 
 // Batched path: fold the down-projection chains into x and normalise for the next consumer.
 void finish_norm(q35_engine* e, int R, const uint16_t* nw, uint16_t* out) {
     if (small_rows(R)) return;
-    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(R, kFF, e->forms), nw, out, R, e->st));
+    HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(R, kFF, e->forms), nw, out, R, e->st,
+                       out == e->h && wide_rows(e, R)));
 }
 
 // Runs the 24-layer body over R = nl * T rows (rows of one lane consecutive) and leaves the
@@ -674,14 +681,15 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt, int defe
     res.mid = mid_partials(e, R);   // 2 .. 16 rows: e->x folded in place, e->h the normed rows
     B1Res* rr = b1_partials(e, R, T, ckpt) || res.mid ? &res : nullptr;
     HCK(launch_addnorm(0, e->tok_dev, e->E, e->x, nullptr, nullptr, 0, e->L[0].norm_in, small ? nullptr : e->h,
-                       R, e->st));
+                       R, e->st, !small && wide_rows(e, R)));
     for (int l = 0; l < e->n_layers; ++l) {
         const LayerW& w = e->L[l];
         if (!is_attn_layer(l)) {
             if (small)
                 norm_gemm(e, rr, w.W_in, kGdnInRows, R, e->proj, kGdnInRows, w.norm_in);
             else
-                gemm(e, w.W_in, kGdnInRows, kHidden, R, e->h, kHidden, e->proj, kGdnInRows);
+                gemm(e, w.W_in, kGdnInRows, kHidden, R, e->h, kHidden, e->proj, kGdnInRows, kAPlain, nullptr, 0, nullptr,
+                     -1, nullptr, wide_rows(e, R));
             GdnArgs g{};
             g.proj = e->proj; g.o = e->o; g.conv_w = w.conv_w; g.A_log = w.A_log; g.dt_bias = w.dt_bias;
             g.S = s->S; g.S_lane = s->S_lane(); g.S_slot = (long long)kGdnLayers * kSLayer;
@@ -769,7 +777,8 @@ void mtp_draft_pass(q35_engine* e, q35_state* s, int n, const uint16_t* hsrc) {
         gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, e->x, kHidden);
     } else {
         gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, nullptr, 0);
-        HCK(launch_addnorm(4, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(n, 2048, e->forms), e->M.norm_in, e->h, n, e->st));
+        HCK(launch_addnorm(4, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(n, 2048, e->forms), e->M.norm_in, e->h, n, e->st,
+                           wide_rows(e, n)));
     }
     attention_layer(e, e->M, n, s->mkc, s->mvc, s->mkv_lane(), 0, s->mtp_capT);
     mlp_layer(e, e->M, n);
@@ -1791,7 +1800,20 @@ int q35_op_gemm_a(q35_engine* e, const uint16_t* wt, int N, int K, int amode, co
                   const void* x2, int ldx2, const uint16_t* aux, int M, uint16_t* y) {
     return guard([&] {
         REQ(e && wt && x && y && M > 0 && N % 16 == 0 && K % 256 == 0 && K <= 4096, Q35_ERR_ARG, "bad gemm shape");
-        REQ(amode == kAPlain || amode == kASiluMul || amode == kAGatedNorm, Q35_ERR_ARG, "amode is 0, 1 or 2");
+        REQ(amode == kAPlain || amode == kASiluMul || amode == kAGatedNorm || amode == 3 || amode == 5 || amode == 6,
+            Q35_ERR_ARG, "amode is 0 .. 3, 5, 6");
+        if (amode == 3 || amode == 5 || amode == 6) {
+            // plain A through the batched GEMMs with the SwiGLU epilogue (5: Y [M][N/2] =
+            // bf16(bf16(silu(X.Wg^T)) * bf16(X.Wu^T)), W = gate rows then up rows), and through the
+            // many-row kernel (3: stored, 6: SwiGLU), X tiled into the engine's h staging first
+            REQ(K == kHidden && M >= 17 && M <= e->R && ldx == K, Q35_ERR_ARG, "amode 3/5/6: K = 1024, 17 <= M <= max_rows");
+            const bool wide = amode != 5;
+            const int em = amode == 3 ? kEStore : kESiluMul;
+            if (wide) HCK(launch_tile((const uint16_t*)x, M, K, e->h, 0, 0, e->st));
+            gemm(e, wt, N, K, M, wide ? e->h : x, K, y, em == kESiluMul ? N / 2 : N, kAPlain, nullptr, 0, nullptr, em,
+                 nullptr, wide);
+            return;
+        }
         REQ(amode == kAPlain || x2, Q35_ERR_ARG, "this producer needs x2");
         REQ(amode != kAGatedNorm || (aux && K % 128 == 0), Q35_ERR_ARG, "gated norm needs its weight");
         REQ(M <= 16 || amode == kAPlain || ((size_t)M * K <= (size_t)e->R * kFF), Q35_ERR_CAP,
@@ -1874,7 +1896,7 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             e->gdn_chunked = value ? 0 : 1;
             e->forms.attn_prompt = value ? 0 : 1;
         } else if (n == "b1_partials" || n == "attn_prompt" || n == "partial_rows" || n == "gemv_tpb" ||
-                   n == "gemm_pre" || n == "lmhead_persist" || n == "attn_split4" || n == "attn_pair" || n == "attn_rows" || n == "gdn_rows" ||
+                   n == "gemm_pre" || n == "lmhead_persist" || n == "attn_split4" || n == "gemm_wide" || n == "attn_pair" || n == "attn_rows" || n == "gdn_rows" ||
                    n == "gdn_defer" || n == "mid_partials") {
             // kernel-form switches of this engine: captured steps hold the old forms
             REQ(n != "partial_rows" || value >= 17, Q35_ERR_ARG, "partial_rows must exceed the 16-row batch-1 path");
@@ -1887,6 +1909,7 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             else if (n == "gemv_tpb") e->forms.gemv_tpb = value;
             else if (n == "gemm_pre") e->forms.gemm_pre = value;
             else if (n == "attn_split4") e->forms.attn_split4 = value ? 1 : 0;
+            else if (n == "gemm_wide") e->forms.gemm_wide = value ? 1 : 0;
             else if (n == "attn_pair") e->forms.attn_pair = value ? 1 : 0;
             else if (n == "attn_rows") e->forms.attn_rows = value ? 1 : 0;
             else if (n == "gdn_rows") e->forms.gdn_rows = value ? 1 : 0;

@@ -702,6 +702,152 @@ __global__ void __launch_bounds__(64 * NW) gemm_pre(GemmArgs a) {
     for (int mt = 0; mt < MT; ++mt) epilogue<EM>(a, sum[mt], nt, row0 + mt * 16, lane);
 }
 
+// ---------------------------------------------------------------- K = 1024, many rows
+// Prompt waves and MTP verify bodies (M >= 512 rows): 256-row x 128-column block tiles, the
+// K = 1024 stream through a three-stage LDS ring of two MFMA steps each (48 KiB per stage:
+// 16 row tiles and 8 column tiles x 2 steps x 1 KiB), one barrier per stage, two stages in
+// flight while one is consumed. A comes in the weights' tiled fragment layout (tiled_offset
+// with rows as n: the producing add+norm writes it so), so every DMA instruction moves one
+// contiguous KiB that is already a fragment: ds_read_b128 at lane * 16 bytes, no swizzle.
+// 8 waves, wave (wm, wn) owns rows 64 wm .. +64 (4 row tiles) x columns 64 wn .. +64 (4 column
+// tiles): 16 MFMAs per 8 fragment reads per step. kESiluMul: waves wn = 0 take gate tiles j,
+// wn = 1 the matching up tiles (64 output columns per block). Reduction: the canonical one
+// (per k-block an MFMA chain over its 8 steps from zero, chains summed in k-block order), so
+// rows equal the other GEMM forms bit for bit.
+constexpr int kWideStage = 48 * 1024;
+constexpr int kWideLds = 3 * kWideStage;
+
+template <int EM>
+__global__ void __launch_bounds__(512) gemm_wide(GemmArgs a) {
+    extern __shared__ q35_u32x4 dyn_lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wv >> 1, wn = wv & 1;
+    const int mb = (a.M + 255) / 256;
+    const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
+    const int nblk = (idx / mb) * 8 + xcd, rb = idx % mb;
+    const int ntiles = a.N / 16, mtiles = (a.M + 15) / 16;
+    const int half = a.N / 32;                                   // kESiluMul: gate tiles
+    if (EM == kESiluMul ? nblk * 4 >= half : nblk * 8 >= ntiles) return;
+    // the 8 column tiles of this block (kESiluMul: 4 gate tiles, then the matching 4 up tiles)
+    auto col_tile = [&](int c) {
+        if (EM == kESiluMul) return c < 4 ? nblk * 4 + c : half + nblk * 4 + (c - 4);
+        return nblk * 8 + c;
+    };
+    const int tr0 = rb * 16;                                      // first row tile
+    // DMA pieces of a stage: 32 A pieces (row tile t, step u), 16 W pieces (column tile c, step
+    // u); wave wv issues pieces 6 wv .. 6 wv + 5 (pieces of tiles past the end re-read the last
+    // valid tile: unconditional, so the wait counts stay exact)
+    const char* pbase[6];
+    unsigned ploff[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        const int pc = 6 * wv + i;
+        if (pc < 32) {
+            const int t = min(tr0 + (pc >> 1), mtiles - 1), u = pc & 1;
+            pbase[i] = (const char*)((const uint16_t*)a.X + ((size_t)t * 4 * 8 + u) * 512);
+        } else {
+            const int c = (pc - 32) >> 1, u = pc & 1;
+            const int nt = min(col_tile(c), ntiles - 1);
+            pbase[i] = (const char*)(a.W + ((size_t)nt * 4 * 8 + u) * 512);
+        }
+        ploff[i] = (unsigned)pc * 1024u;
+    }
+    auto issue = [&](int j) {          // stage j: k-block j / 4, steps 2 (j % 4) .. +1
+        const unsigned koff = (unsigned)((j >> 2) * 8 + (j & 3) * 2) * 1024u;   // bytes within a tile's kb rows
+        char* lds = (char*)dyn_lds + (j % 3) * kWideStage;
+#pragma unroll
+        for (int i = 0; i < 6; ++i)
+            __builtin_amdgcn_global_load_lds((const void*)(uniform_ptr(pbase[i] + koff) + lane * 16),
+                                             (__attribute__((address_space(3))) void*)(lds + ploff[i]), 16, 0, 0);
+    };
+    q35_f32x4 c[4][4], sum[4][4];
+    issue(0);
+    issue(1);
+    // this wave's fragment bases: its 4 row tiles' pieces (2 wm * 4 + i, step u) and its 4 column
+    // tiles' pieces (32 + 2 (4 wn + i) + u), 1 KiB each; the lane's 16 bytes at lane * 16
+    const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) const void*)dyn_lds + lane * 16;
+    const unsigned abase = lds0 + (unsigned)(wm * 8) * 1024u, bbase = lds0 + (unsigned)(32 + wn * 8) * 1024u;
+    for (int j = 0; j < 16; ++j) {
+        if (j < 15) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();      // stage j landed for every wave; stage j - 1 consumed
+        asm volatile("" ::: "memory");
+        if (j + 2 < 16) issue(j + 2);
+        const unsigned so = (unsigned)((j % 3) * kWideStage);
+        const unsigned sa = abase + so, sbb = bbase + so;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            q35_u32x4 af[4], bw[4];
+#define Q35_WRD(dst, base, off) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "n"(off) : "memory")
+            if (u == 0) {
+                Q35_WRD(af[0], sa, 0); Q35_WRD(af[1], sa, 2048); Q35_WRD(af[2], sa, 4096); Q35_WRD(af[3], sa, 6144);
+                Q35_WRD(bw[0], sbb, 0); Q35_WRD(bw[1], sbb, 2048); Q35_WRD(bw[2], sbb, 4096); Q35_WRD(bw[3], sbb, 6144);
+            } else {
+                Q35_WRD(af[0], sa, 1024); Q35_WRD(af[1], sa, 3072); Q35_WRD(af[2], sa, 5120); Q35_WRD(af[3], sa, 7168);
+                Q35_WRD(bw[0], sbb, 1024); Q35_WRD(bw[1], sbb, 3072); Q35_WRD(bw[2], sbb, 5120); Q35_WRD(bw[3], sbb, 7168);
+            }
+#undef Q35_WRD
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(af[0]), "+v"(af[1]), "+v"(af[2]), "+v"(af[3]), "+v"(bw[0]), "+v"(bw[1]), "+v"(bw[2]), "+v"(bw[3]));
+            const bool first = (j & 3) == 0 && u == 0;     // a k-block's chain starts from zero
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int jn = 0; jn < 4; ++jn)
+                    c[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(af[i]), as_bf(bw[jn]),
+                                                                        first ? (q35_f32x4){0.f, 0.f, 0.f, 0.f} : c[i][jn], 0, 0, 0);
+        }
+        if ((j & 3) == 3) {                // k-block j / 4 done: ((c0 + c1) + c2) + c3
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int jn = 0; jn < 4; ++jn)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sum[i][jn][r] = j == 3 ? c[i][jn][r] : sum[i][jn][r] + c[i][jn][r];
+        }
+    }
+    const int row0 = (tr0 + wm * 4) * 16;
+    if (EM == kESiluMul) {
+        // up waves (wn = 1) hand bf16(u) to the gate waves through the (now free) ring:
+        // 4 x 4 x 4 x 4 x 64 bf16 = 128 KiB of the 144 KiB
+        uint16_t* ub = (uint16_t*)dyn_lds;                         // [wm][i][jn][4][64]
+        __syncthreads();
+        if (wn == 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int jn = 0; jn < 4; ++jn)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ub[((((wm * 4 + i) * 4 + jn) * 4 + r) * 64) + lane] = f2bf(sum[i][jn][r]);
+        }
+        __syncthreads();
+        if (wn == 1) return;
+#pragma unroll
+        for (int jn = 0; jn < 4; ++jn) {
+            const int jt = nblk * 4 + jn;
+            if (jt >= half) continue;
+            const int col = jt * 16 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = row0 + i * 16 + 4 * (lane >> 4) + r;
+                    const float uu = bf2f(ub[((((wm * 4 + i) * 4 + jn) * 4 + r) * 64) + lane]);
+                    if (row < a.M) a.Y[(size_t)row * a.ldy + col] = f2bf(__fmul_rn(rbf(silu_f(rbf(sum[i][jn][r]))), uu));
+                }
+        }
+        return;
+    }
+#pragma unroll
+    for (int jn = 0; jn < 4; ++jn) {
+        const int nt = nblk * 8 + wn * 4 + jn;
+        if (nt >= ntiles) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) epilogue<EM>(a, sum[i][jn], nt, row0 + i * 16, lane);
+    }
+}
+
 // ---------------------------------------------------------------- tied lm_head, batched lanes
 // K = 1024 (the hidden size), argmax epilogue, launches of M <= 512. Persistent blocks of NW waves,
 // about one per CU: a block stages its 64 A rows (64 x 1024 bf16 = 128 KiB) in LDS once, in
@@ -1004,6 +1150,16 @@ __global__ void __launch_bounds__(1024) argmax_rows(const float* pv, const int* 
 // (one chain left for the add+norm) instead of one block per chain
 int gemm_partial_chains(int M, int K, const KernelForms& f) { return M > 16 && M >= f.partial_rows ? 1 : K / 256; }
 
+// many rows, A in the tiled layout: K = 1024, stored or SwiGLU outputs only
+static hipError_t launch_wide(const GemmArgs& a, int em, hipStream_t st) {
+    if (a.K != kHidden || a.M <= 16 || (em != kEStore && em != kESiluMul) || !a.Y || (em == kESiluMul && a.N % 32))
+        return hipErrorInvalidValue;
+    const int nb = em == kESiluMul ? (a.N / 32 + 3) / 4 : (a.N / 16 + 7) / 8, mb = (a.M + 255) / 256;
+    if (em == kESiluMul) hipLaunchKernelGGL(gemm_wide<kESiluMul>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
+    else hipLaunchKernelGGL(gemm_wide<kEStore>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
+    return hipGetLastError();
+}
+
 template <int EM>
 static void launch_large(const GemmArgs& a, hipStream_t st) {
     const int KB = a.K / 256;
@@ -1085,6 +1241,10 @@ static hipError_t launch_am_em(const GemmArgs& a, hipStream_t st) {
         return hipGetLastError();
     }
     if (EM == kEResidual || AM == kANormX || AM == kANormXP) return hipErrorInvalidValue;   // batch-1 forms only
+    if (a.x_tiled) {
+        if (AM != kAPlain) return hipErrorInvalidValue;
+        return launch_wide(a, EM, st);
+    }
     if (AM != kAPlain) {
         // produce A once into a.prod (bf16 [M][K]), then the plain batched GEMM
         if (!a.prod) return hipErrorInvalidValue;
@@ -1116,7 +1276,9 @@ hipError_t gemm_init() {
         hipFuncSetAttribute((const void*)gemm_pre<kEStore, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<2>()) != hipSuccess ||
         hipFuncSetAttribute((const void*)gemm_pre<kESiluMul, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<2>()) != hipSuccess ||
         hipFuncSetAttribute((const void*)gemm_pre<kEStore, 4, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<4>()) != hipSuccess ||
-        hipFuncSetAttribute((const void*)gemm_pre<kESiluMul, 4, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<4>()) != hipSuccess)
+        hipFuncSetAttribute((const void*)gemm_pre<kESiluMul, 4, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<4>()) != hipSuccess ||
+        hipFuncSetAttribute((const void*)gemm_wide<kEStore>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess ||
+        hipFuncSetAttribute((const void*)gemm_wide<kESiluMul>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess)
         return hipGetLastError();
     return hipSuccess;
 }
@@ -1143,6 +1305,7 @@ hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st) 
     if (emode == kEResidual) { Q35_AM(kEResidual) }
     if (emode == kESiluMul) {       // batched lanes only: a plain A operand, Y = act [M][N/2]
         if (amode != kAPlain || a.M <= 16 || a.N % 32 || !a.Y) return hipErrorInvalidValue;
+        if (a.x_tiled) return launch_wide(a, kESiluMul, st);
         launch_large<kESiluMul>(a, st);
         return hipGetLastError();
     }

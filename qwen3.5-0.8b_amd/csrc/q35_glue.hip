@@ -20,7 +20,9 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 // One row per block, 256 threads x 4 elements.
 // The mode is a template argument: with a run-time mode the compiler waited for the residual
 // row's load at the mode branch, before issuing the chain loads (two round trips instead of one).
-template <int mode>
+// TILED: h in the weights' tiled fragment layout (tiled_offset with the row as n), the A operand
+// of the many-row K = 1024 GEMM; a thread's 4 elements stay contiguous there.
+template <int mode, bool TILED = false>
 __global__ void __launch_bounds__(256) addnorm_kernel(const int* tok, const uint16_t* E,
                                                       uint16_t* x, const uint16_t* delta,
                                                       const float* kpart, int kblocks,
@@ -85,7 +87,7 @@ __global__ void __launch_bounds__(256) addnorm_kernel(const int* tok, const uint
     uint2 st;
     st.x = o[0] | ((uint32_t)o[1] << 16);
     st.y = o[2] | ((uint32_t)o[3] << 16);
-    *(uint2*)(h + (size_t)r * kHidden + k) = st;
+    *(uint2*)(h + (TILED ? tiled_offset(r, k, kHidden) : (size_t)r * kHidden + k)) = st;
 }
 
 // MTP fc input (speccheck/mtp.py:64-69): [rmsnorm_zc(E[y], w_e) | rmsnorm_zc(h, w_h)].
@@ -121,8 +123,20 @@ __global__ void __launch_bounds__(256) mtp_concat_kernel(const int* tok, const u
 
 hipError_t launch_addnorm(int mode, const int* tok, const uint16_t* E, uint16_t* x,
                           const uint16_t* delta, const float* kpart, int kblocks,
-                          const uint16_t* w, uint16_t* h, int rows, hipStream_t st) {
+                          const uint16_t* w, uint16_t* h, int rows, hipStream_t st, int h_tiled) {
     if (rows <= 0) return hipErrorInvalidValue;
+    if (h_tiled) {
+        if (!h) return hipErrorInvalidValue;
+#define Q35_ADDNORM_T(M) hipLaunchKernelGGL((addnorm_kernel<M, true>), dim3(rows), dim3(256), 0, st, tok, E, x, delta, kpart, kblocks, w, h)
+        switch (mode) {
+            case 0: Q35_ADDNORM_T(0); break;
+            case 3: Q35_ADDNORM_T(3); break;
+            case 4: Q35_ADDNORM_T(4); break;
+            default: return hipErrorInvalidValue;
+        }
+#undef Q35_ADDNORM_T
+        return hipGetLastError();
+    }
 #define Q35_ADDNORM(M) hipLaunchKernelGGL(addnorm_kernel<M>, dim3(rows), dim3(256), 0, st, tok, E, x, delta, kpart, kblocks, w, h)
     switch (mode) {
         case 0: Q35_ADDNORM(0); break;

@@ -27,6 +27,7 @@ struct KernelForms {
     int attn_prompt = 1;       // prompt waves of >= 64 rows: flash-form MFMA kernel (1) or one-row kernels (0)
     int mid_partials = 1;      // bodies of 2 .. 16 rows: k-block chains + add+norm (0: residual-epilogue GEMMs)
     int gdn_rows = 1;          // MTP verify (2-3 rows per lane, whole-head blocks): the persistent GDN kernel
+    int gemm_wide = 1;         // K = 1024 GEMMs of >= 512 rows: 256 x 128 tiles through an LDS ring, A tiled
     int gdn_defer = 3;         // decode steps: a lane's GDN state update is kept as pending factors for up
                                // to this many steps, the state written on the next (0: every step)
 };
@@ -51,6 +52,8 @@ struct GemmArgs {
     uint16_t* xres;        // kEResidual: residual rows [M][1024], x <- bf16(x + bf16(sum))
     uint16_t* hout;        // kANormX (optional): the normalised rows [M][1024] are written here
     int kpb;               // kANormXP: k-block chains of the producing GEMM pending in kpart
+    int x_tiled;           // X in the weights' tiled fragment layout (tiled_offset, rows as n): the
+                           // many-row K = 1024 GEMM (gemm_wide); M rows padded to whole 16-row tiles
     KernelForms forms;
 };
 // One-time kernel attribute setup (dynamic LDS above 64 KiB for the batch-1 producers).
@@ -80,7 +83,8 @@ struct RowMeta {
 //   then h = rmsnorm_zc(x, w) (skipped when h == nullptr)
 hipError_t launch_addnorm(int mode, const int* tok, const uint16_t* E, uint16_t* x,
                           const uint16_t* delta, const float* kpart, int kblocks,
-                          const uint16_t* w, uint16_t* h, int rows, hipStream_t st);
+                          const uint16_t* w, uint16_t* h, int rows, hipStream_t st,
+                          int h_tiled = 0);
 // MTP fc input: cat[rmsnorm_zc(E[tok], we) | rmsnorm_zc(hin, wh)] -> out [rows][2048]
 hipError_t launch_mtp_concat(const int* tok, const uint16_t* E, const uint16_t* hin, int ldh,
                              const uint16_t* we, const uint16_t* wh, uint16_t* out, int rows,
