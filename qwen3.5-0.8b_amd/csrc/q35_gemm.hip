@@ -768,7 +768,10 @@ __global__ void __launch_bounds__(512) gemm_wide(GemmArgs a) {
     // tiles' pieces (32 + 2 (4 wn + i) + u), 1 KiB each; the lane's 16 bytes at lane * 16
     const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) const void*)dyn_lds + lane * 16;
     const unsigned abase = lds0 + (unsigned)(wm * 8) * 1024u, bbase = lds0 + (unsigned)(32 + wn * 8) * 1024u;
-    for (int j = 0; j < 16; ++j) {
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {           // unrolled: a chain's first step is known statically
+        const int j = kb * 4 + jj;
         if (j < 15) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();      // stage j landed for every wave; stage j - 1 consumed
@@ -776,29 +779,33 @@ __global__ void __launch_bounds__(512) gemm_wide(GemmArgs a) {
         if (j + 2 < 16) issue(j + 2);
         const unsigned so = (unsigned)((j % 3) * kWideStage);
         const unsigned sa = abase + so, sbb = bbase + so;
+        // both steps' fragments requested at once; step 0's MFMAs run while step 1's reads land
+        q35_u32x4 af[2][4], bw[2][4];
+#define Q35_WRD(dst, base, off) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "n"(off) : "memory")
+        Q35_WRD(af[0][0], sa, 0); Q35_WRD(af[0][1], sa, 2048); Q35_WRD(af[0][2], sa, 4096); Q35_WRD(af[0][3], sa, 6144);
+        Q35_WRD(bw[0][0], sbb, 0); Q35_WRD(bw[0][1], sbb, 2048); Q35_WRD(bw[0][2], sbb, 4096); Q35_WRD(bw[0][3], sbb, 6144);
+        Q35_WRD(af[1][0], sa, 1024); Q35_WRD(af[1][1], sa, 3072); Q35_WRD(af[1][2], sa, 5120); Q35_WRD(af[1][3], sa, 7168);
+        Q35_WRD(bw[1][0], sbb, 1024); Q35_WRD(bw[1][1], sbb, 3072); Q35_WRD(bw[1][2], sbb, 5120); Q35_WRD(bw[1][3], sbb, 7168);
+#undef Q35_WRD
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            q35_u32x4 af[4], bw[4];
-#define Q35_WRD(dst, base, off) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "n"(off) : "memory")
-            if (u == 0) {
-                Q35_WRD(af[0], sa, 0); Q35_WRD(af[1], sa, 2048); Q35_WRD(af[2], sa, 4096); Q35_WRD(af[3], sa, 6144);
-                Q35_WRD(bw[0], sbb, 0); Q35_WRD(bw[1], sbb, 2048); Q35_WRD(bw[2], sbb, 4096); Q35_WRD(bw[3], sbb, 6144);
-            } else {
-                Q35_WRD(af[0], sa, 1024); Q35_WRD(af[1], sa, 3072); Q35_WRD(af[2], sa, 5120); Q35_WRD(af[3], sa, 7168);
-                Q35_WRD(bw[0], sbb, 1024); Q35_WRD(bw[1], sbb, 3072); Q35_WRD(bw[2], sbb, 5120); Q35_WRD(bw[3], sbb, 7168);
-            }
-#undef Q35_WRD
-            asm volatile("s_waitcnt lgkmcnt(0)"
-                         : "+v"(af[0]), "+v"(af[1]), "+v"(af[2]), "+v"(af[3]), "+v"(bw[0]), "+v"(bw[1]), "+v"(bw[2]), "+v"(bw[3]));
-            const bool first = (j & 3) == 0 && u == 0;     // a k-block's chain starts from zero
+            if (u == 0)
+                asm volatile("s_waitcnt lgkmcnt(8)"
+                             : "+v"(af[0][0]), "+v"(af[0][1]), "+v"(af[0][2]), "+v"(af[0][3]),
+                               "+v"(bw[0][0]), "+v"(bw[0][1]), "+v"(bw[0][2]), "+v"(bw[0][3]));
+            else
+                asm volatile("s_waitcnt lgkmcnt(0)"
+                             : "+v"(af[1][0]), "+v"(af[1][1]), "+v"(af[1][2]), "+v"(af[1][3]),
+                               "+v"(bw[1][0]), "+v"(bw[1][1]), "+v"(bw[1][2]), "+v"(bw[1][3]));
+            const bool first = jj == 0 && u == 0;     // a k-block's chain starts from zero
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int jn = 0; jn < 4; ++jn)
-                    c[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(af[i]), as_bf(bw[jn]),
+                    c[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(af[u][i]), as_bf(bw[u][jn]),
                                                                         first ? (q35_f32x4){0.f, 0.f, 0.f, 0.f} : c[i][jn], 0, 0, 0);
         }
-        if ((j & 3) == 3) {                // k-block j / 4 done: ((c0 + c1) + c2) + c3
+        if (jj == 3) {                     // k-block kb done: ((c0 + c1) + c2) + c3
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
