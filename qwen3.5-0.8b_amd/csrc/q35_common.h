@@ -79,13 +79,17 @@ __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(((uin
 
 // Round-to-nearest-even f32 -> bf16 bits (NaN stays a quiet NaN).
 // Branchless (selects, no divergent branch per element).
-__device__ __forceinline__ uint16_t f2bf(float f) {
-    const uint32_t u = __float_as_uint(f);
-    const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-    const uint32_t nan = (u >> 16) | 0x40u;
-    return (uint16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? nan : rne);
+// f32 -> bf16, round to nearest even (NaN: the high half with the quiet bit set), by gfx950's
+// v_cvt_pk_bf16_f32: one instruction for two values instead of six for one. Checked on MI355X
+// against the integer form (u + 0x7fff + ((u >> 16) & 1)) >> 16, NaN -> (u >> 16) | 0x40, for all
+// 2^32 inputs: identical bits.
+__device__ __forceinline__ uint32_t f2bf2(float lo, float hi) {
+    uint32_t r;
+    asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+    return r;
 }
-__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ uint16_t f2bf(float f) { return (uint16_t)f2bf2(f, 0.f); }
+__device__ __forceinline__ float rbf(float f) { return __uint_as_float(f2bf2(0.f, f) & 0xffff0000u); }
 
 // A block barrier for LDS traffic only: __syncthreads() also orders global memory, for which
 // the compiler makes every wave wait for all of its outstanding loads first, including loads

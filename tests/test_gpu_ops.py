@@ -76,3 +76,39 @@ def test_lm_head_argmax(eng, oracle_weights):
         m = row.max()
         assert tok[r].item() == int(torch.nonzero(row == m)[0])
     assert tok[2].item() == tok[3].item()
+
+
+@pytest.mark.parametrize("mode", [2, 3])
+@pytest.mark.parametrize("N,M", [(8224, 600), (5120, 1024), (7168, 768), (1024, 513)])
+def test_wide_gemm_forms_bit_identical(mode, N, M):
+    """The many-row K = 1024 GEMM (q35_op_gemm_a amodes 3 / 6: A staged in the fragment layout,
+    128-row blocks two per CU (gemm_wide 2) or 256-row blocks (3)) equals the batched GEMMs
+    (amodes 0 / 5) bit for bit: stored outputs, and the SwiGLU epilogue on [gate; up] weights,
+    including ragged last row blocks; the stored form also against float64 (1 bf16 ulp)."""
+    import torch
+    from qwen35 import Engine
+    print(f"wide gemm mode={mode} N={N} M={M}", flush=True)
+    e = Engine(max_rows=1024, max_ctx=64, seed=0)
+    try:
+        e.set_option("gemm_wide", mode)
+        g = torch.Generator().manual_seed(N + M + mode)
+        W = (0.02 * torch.randn(N, 1024, generator=g)).to(torch.bfloat16).cuda()
+        X = torch.randn(M, 1024, generator=g).to(torch.bfloat16).cuda()
+        Wt = torch.empty_like(W)
+        ys = [torch.zeros(M, N, dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+        ss = [torch.zeros(M, N // 2, dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+        torch.cuda.synchronize()   # torch-stream inputs complete before the engine stream reads them
+        e.op_tile_weight(W.data_ptr(), N, 1024, Wt.data_ptr())
+        for am, y in zip((0, 3), ys):
+            e.op_gemm_a(Wt.data_ptr(), N, 1024, am, X.data_ptr(), 1024, 0, 0, 0, M, y.data_ptr())
+        for am, y in zip((5, 6), ss):
+            e.op_gemm_a(Wt.data_ptr(), N, 1024, am, X.data_ptr(), 1024, 0, 0, 0, M, y.data_ptr())
+        e.sync()
+        assert torch.equal(ys[0].view(torch.int16), ys[1].view(torch.int16))
+        assert torch.equal(ss[0].view(torch.int16), ss[1].view(torch.int16))
+        ref = X.double() @ W.double().t()
+        got = ys[1].double()
+        ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(1e-30))) - 7)
+        assert ((got - ref).abs() <= ulp + 1e-6).all()
+    finally:
+        e.close()
