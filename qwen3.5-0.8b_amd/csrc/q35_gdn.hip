@@ -330,8 +330,9 @@ __global__ void __launch_bounds__(256, 2) gdn_persist(GdnArgs a, int nitems) {
     float* fbuf = (float*)(sbuf + 4096);
     __shared__ float qs[128], ks[128], vs[VC];
     __shared__ float red[NG][VC];            // r partials, then o partials
-    __shared__ float wred[4];
-    __shared__ float gate_s[2][2];           // (decay, beta) of items with even / odd k
+    __shared__ float wred[TR][4];            // per row: the waves' q / k square sums
+    __shared__ float gate_s[TR > 2 ? TR : 2][2];   // (decay, beta): one row, of items with even / odd k;
+                                             // verify rows: of rows 0 .. TR-1
     __shared__ float qq[32];                 // the item's 32 quads of o^2, in column order
     // item k's row metadata: lane | cur << 16 | wcur << 20 | pend code << 24
     __shared__ int meta[kPersistMaxItems];
@@ -495,40 +496,56 @@ __global__ void __launch_bounds__(256, 2) gdn_persist(GdnArgs a, int nitems) {
         cw[2] = __uint_as_float(op.cpk.y << 16); cw[3] = __uint_as_float(op.cpk.y & 0xffff0000u);
         cvw[0] = __uint_as_float(op.dpk.x << 16); cvw[1] = __uint_as_float(op.dpk.x & 0xffff0000u);
         cvw[2] = __uint_as_float(op.dpk.y << 16); cvw[3] = __uint_as_float(op.dpk.y & 0xffff0000u);
+        // causal conv of every row first (taps over [w0, w1, w2, raw] in order, f32, one rounding,
+        // bf16 SiLU), with the rows' square sums and gates: none of it reads the state, so the rows'
+        // latencies overlap instead of each row waiting for its own before the state passes
+        float uqr[TR], uvr[TR];
 #pragma unroll
         for (int t = 0; t < TR; ++t) {
-        const int r = gi * TR + t;              // this row
-        const float ox = bf2f(op.x[t]), oxv = bf2f(op.xv[t]);
-        // causal conv: taps over [w0, w1, w2, raw] in order, f32, one rounding, bf16 SiLU
-        {
+            const float ox = bf2f(op.x[t]), oxv = bf2f(op.xv[t]);
             float u = 0.f;
             u = u + w0 * cw[0]; u = u + w1 * cw[1]; u = u + w2 * cw[2]; u = u + ox * cw[3];
-            float uq = rbf(silu_f(rbf(u)));
+            uqr[t] = rbf(silu_f(rbf(u)));
             w0 = w1; w1 = w2; w2 = ox;
-            if (tid < 128) qs[tid] = uq; else ks[tid - 128] = uq;
+            uvr[t] = 0.f;
             if (hasv) {
                 float uv = 0.f;
                 uv = uv + v0 * cvw[0]; uv = uv + v1 * cvw[1]; uv = uv + v2 * cvw[2]; uv = uv + oxv * cvw[3];
-                vs[tid] = rbf(silu_f(rbf(uv)));
+                uvr[t] = rbf(silu_f(rbf(uv)));
                 v0 = v1; v1 = v2; v2 = oxv;
             }
-            float ss = wave_sum(uq * uq);
-            if ((tid & 63) == 0) wred[tid >> 6] = ss;
-            if (TR == 1 && tid == 0 && k == 0) gates(op, 0, gate_s[0]);
-            if (TR > 1 && tid == 0) gates(op, t, gate_s[0]);       // read after this row's first barrier
+            // the conv window after this row: its values are final now (verify rows: slot wcur + 1 + t)
+            float* Wo = Wbase + ((wcur + 1 + t) % a.nslots) * a.W_slot;
+            Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2;
+            if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
         }
-        // the conv window after this row: its values are final now (verify rows: slot wcur + 1 + t)
-        float* Wo = Wbase + ((wcur + 1 + t) % a.nslots) * a.W_slot;
-        Wo[cqk] = w0; Wo[6144 + cqk] = w1; Wo[12288 + cqk] = w2;
-        if (hasv) { Wo[cv] = v0; Wo[6144 + cv] = v1; Wo[12288 + cv] = v2; }
+        {
+            float ss[TR];
+#pragma unroll
+            for (int t = 0; t < TR; ++t) ss[t] = wave_sum(uqr[t] * uqr[t]);
+            if ((tid & 63) == 0) {
+#pragma unroll
+                for (int t = 0; t < TR; ++t) wred[t][tid >> 6] = ss[t];
+            }
+            if (TR == 1 && tid == 0 && k == 0) gates(op, 0, gate_s[0]);
+            if (TR > 1 && tid == 0) {
+#pragma unroll
+                for (int t = 0; t < TR; ++t) gates(op, t, gate_s[t]);   // read after row 0's first barrier
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TR; ++t) {
+        const int r = gi * TR + t;              // this row
+        if (tid < 128) qs[tid] = uqr[t]; else ks[tid - 128] = uqr[t];
+        if (hasv) vs[tid] = uvr[t];
         lds_barrier();
         if (more && t == 0) { fetch_fac(k + 1); fetch_rows(1); }   // fbuf's rows were read before this barrier
         if (TR > 1 && more && t == 1) fetch_rows(3);
         // q~ and k~ of this thread's 16 rows, normalised where they are read (the same two
         // rounded products as a normalisation pass, without its barrier)
-        const float rq = rsqrtf((wred[0] + wred[1]) + 1e-6f);
-        const float rk = rsqrtf((wred[2] + wred[3]) + 1e-6f);
-        const float gam = gate_s[TR == 1 ? (k & 1) : 0][0], beta = gate_s[TR == 1 ? (k & 1) : 0][1];
+        const float rq = rsqrtf((wred[t][0] + wred[t][1]) + 1e-6f);
+        const float rk = rsqrtf((wred[t][2] + wred[t][3]) + 1e-6f);
+        const float gam = gate_s[TR == 1 ? (k & 1) : t][0], beta = gate_s[TR == 1 ? (k & 1) : t][1];
         float kn[KR], qn[KR];
 #pragma unroll
         for (int i = 0; i < KR; ++i) {
