@@ -1909,10 +1909,7 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             else if (n == "gemv_tpb") e->forms.gemv_tpb = value;
             else if (n == "gemm_pre") e->forms.gemm_pre = value;
             else if (n == "attn_split4") e->forms.attn_split4 = value ? 1 : 0;
-            else if (n == "gemm_wide") {
-                REQ(value >= 0 && value <= 3, Q35_ERR_ARG, "gemm_wide is 0 (off), 1 (auto), 2 (128-row blocks) or 3 (256-row blocks)");
-                e->forms.gemm_wide = value;
-            }
+            else if (n == "gemm_wide") e->forms.gemm_wide = value ? 1 : 0;
             else if (n == "attn_pair") e->forms.attn_pair = value ? 1 : 0;
             else if (n == "attn_rows") e->forms.attn_rows = value ? 1 : 0;
             else if (n == "gdn_rows") e->forms.gdn_rows = value ? 1 : 0;

@@ -703,43 +703,30 @@ __global__ void __launch_bounds__(64 * NW) gemm_pre(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------- K = 1024, many rows
-// Prompt waves and MTP verify bodies (M >= 512 rows): RT x 16-row x 128-column block tiles and
-// the K = 1024 stream through an LDS ring, one barrier per stage. A comes in the weights' tiled
-// fragment layout (tiled_offset with rows as n: the producing add+norm writes it so), so every
-// DMA instruction moves one contiguous KiB that is already a fragment: ds_read_b128 at lane *
-// 16 bytes, no swizzle. Wave (wm, wn) owns rows 64 wm .. +64 (4 row tiles) x columns 64 wn ..
-// +64 (4 column tiles): 16 MFMAs per 8 fragment reads per step. Two shapes:
-//  RT = 16: 256-row blocks of 8 waves, one per CU; stages of two MFMA steps (48 KiB: 16 row
-//           tiles and 8 column tiles x 2 steps x 1 KiB), a three-stage ring (144 KiB), two
-//           stages in flight while one is consumed; both steps' fragment reads issued before
-//           the first step's MFMAs;
-//  RT = 8:  128-row blocks of 4 waves, two per CU; stages of one step (16 KiB), a four-stage
-//           ring (64 KiB), three in flight. The two blocks of a CU meet at no common barrier,
-//           so one block's MFMAs run while the other waits for its stage.
-// kESiluMul: waves wn = 0 take gate tiles j, wn = 1 the matching up tiles (64 output columns
-// per block). The stages of a k-block are unrolled, so a chain's first MFMA starts from a
-// literal zero. Reduction: the canonical one (per k-block an MFMA chain over its 8 steps from
-// zero, chains summed in k-block order), so rows equal the other GEMM forms bit for bit.
-template <int RT> struct WideShape {
-    static constexpr int NW = RT / 2;                     // waves
-    static constexpr int SPS = RT == 16 ? 2 : 1;          // MFMA steps per stage
-    static constexpr int RING = RT == 16 ? 3 : 4;         // stages in the ring
-    static constexpr int PIECES = (RT + 8) * SPS;         // 1 KiB DMA pieces per stage
-    static constexpr int DPW = PIECES / NW;               // DMA instructions per wave per stage
-    static constexpr int STAGE = PIECES * 1024;
-    static constexpr int LDS = RING * STAGE;
-    static constexpr int SPK = 8 / SPS;                   // stages per k-block
-    static constexpr int NS = 4 * SPK;                    // stages
-};
+// Prompt waves and MTP verify bodies (M >= 512 rows): 256-row x 128-column block tiles of 8 waves
+// (one block per CU) and the K = 1024 stream through a six-stage LDS ring of one MFMA step each
+// (24 KiB: 16 row tiles and 8 column tiles x 1 KiB), one barrier per stage. A comes in the weights'
+// tiled fragment layout (tiled_offset with rows as n: the producing add+norm writes it so), so
+// every DMA instruction moves one contiguous KiB that is already a fragment: ds_read_b128 at lane
+// * 16 bytes, no swizzle. Wave (wm, wn) owns rows 64 wm .. +64 (4 row tiles) x columns 64 wn ..
+// +64 (4 column tiles): 16 MFMAs per 8 fragment reads per step. Software pipelined: while a wave
+// issues step j's MFMAs it reads step j + 1's fragments into its other register set (the LDS
+// latency hides behind its own matrix work instead of adding to it), and the DMA runs four steps
+// ahead of the reads. kESiluMul: wave wn takes gate tiles 2 wn, 2 wn + 1 and the matching up tiles,
+// so the SwiGLU is lane-local (64 output columns per block). The steps of a k-block are unrolled, so a chain's first MFMA starts
+// from a literal zero. Reduction: the canonical one (per k-block an MFMA chain over its 8 steps
+// from zero, chains summed in k-block order), so rows equal the other GEMM forms bit for bit.
+constexpr int kWideRing = 6;                        // stages (one MFMA step, 24 KiB each)
+constexpr int kWideStage = 24 * 1024;
+constexpr int kWideLds = kWideRing * kWideStage;    // 144 KiB
 
-template <int EM, int RT>
-__global__ void __launch_bounds__(32 * RT, RT == 8 ? 2 : 1) gemm_wide(GemmArgs a) {
-    using S = WideShape<RT>;
+template <int EM>
+__global__ void __launch_bounds__(512) gemm_wide(GemmArgs a) {
     extern __shared__ q35_u32x4 dyn_lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wv >> 1, wn = wv & 1;
-    const int mb = (a.M + 16 * RT - 1) / (16 * RT);
+    const int mb = (a.M + 255) / 256;
     const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
     const int nblk = (idx / mb) * 8 + xcd, rb = idx % mb;
     const int ntiles = a.N / 16, mtiles = (a.M + 15) / 16;
@@ -750,95 +737,83 @@ __global__ void __launch_bounds__(32 * RT, RT == 8 ? 2 : 1) gemm_wide(GemmArgs a
         if (EM == kESiluMul) return c < 4 ? nblk * 4 + c : half + nblk * 4 + (c - 4);
         return nblk * 8 + c;
     };
-    const int tr0 = rb * RT;                                      // first row tile
-    // DMA pieces of a stage: RT x SPS A pieces (row tile t, step u), 8 x SPS W pieces (column
-    // tile c, step u), piece pc at pc KiB; wave wv issues pieces DPW wv .. DPW wv + DPW - 1
-    // (pieces of tiles past the end re-read the last valid tile: unconditional, so the wait
-    // counts stay exact)
-    const char* pbase[S::DPW];
-    unsigned ploff[S::DPW];
+    const int tr0 = rb * 16;                                      // first row tile
+    // DMA pieces of a stage: 16 A pieces (row tile t), 8 W pieces (column tile c), piece pc at pc
+    // KiB; wave wv issues pieces 3 wv .. 3 wv + 2 (pieces of tiles past the end re-read the last
+    // valid tile: unconditional, so the wait counts stay exact)
+    const char* pbase[3];
+    unsigned ploff[3];
 #pragma unroll
-    for (int i = 0; i < S::DPW; ++i) {
-        const int pc = S::DPW * wv + i;
-        if (pc < RT * S::SPS) {
-            const int t = min(tr0 + pc / S::SPS, mtiles - 1), u = pc % S::SPS;
-            pbase[i] = (const char*)((const uint16_t*)a.X + ((size_t)t * 4 * 8 + u) * 512);
+    for (int i = 0; i < 3; ++i) {
+        const int pc = 3 * wv + i;
+        if (pc < 16) {
+            const int t = min(tr0 + pc, mtiles - 1);
+            pbase[i] = (const char*)((const uint16_t*)a.X + (size_t)t * 4 * 8 * 512);
         } else {
-            const int c = (pc - RT * S::SPS) / S::SPS, u = (pc - RT * S::SPS) % S::SPS;
-            const int nt = min(col_tile(c), ntiles - 1);
-            pbase[i] = (const char*)(a.W + ((size_t)nt * 4 * 8 + u) * 512);
+            const int nt = min(col_tile(pc - 16), ntiles - 1);
+            pbase[i] = (const char*)(a.W + (size_t)nt * 4 * 8 * 512);
         }
         ploff[i] = (unsigned)pc * 1024u;
     }
-    auto issue = [&](int j) {          // stage j: k-block j / SPK, steps SPS (j % SPK) ..
-        const unsigned koff = (unsigned)((j / S::SPK) * 8 + (j % S::SPK) * S::SPS) * 1024u;
-        char* lds = (char*)dyn_lds + (j % S::RING) * S::STAGE;
+    // stage j = k-block j / 8, step j % 8: the j-th KiB of every tile's 32 KiB
+    auto issue = [&](int j) {
+        const unsigned koff = (unsigned)j * 1024u;
+        char* lds = (char*)dyn_lds + (j % kWideRing) * kWideStage;
 #pragma unroll
-        for (int i = 0; i < S::DPW; ++i)
+        for (int i = 0; i < 3; ++i)
             __builtin_amdgcn_global_load_lds((const void*)(uniform_ptr(pbase[i] + koff) + lane * 16),
                                              (__attribute__((address_space(3))) void*)(lds + ploff[i]), 16, 0, 0);
     };
+    // this wave's fragments of a stage: its 4 row tiles' pieces (4 wm + i) and its 4 column
+    // tiles' pieces (16 + 4 wn + i), 1 KiB each; the lane's 16 bytes at lane * 16
+    const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) const void*)dyn_lds + lane * 16;
+    // kESiluMul: wave wn takes gate tiles 2 wn, 2 wn + 1 (pieces 16 + 2 wn + h) and the matching up
+    // tiles (pieces 20 + 2 wn + h), so each lane holds both operands of its outputs
+    const unsigned abase = lds0 + (unsigned)(wm * 4) * 1024u;
+    const unsigned bbase = lds0 + (unsigned)(16 + (EM == kESiluMul ? 2 : 4) * wn) * 1024u;
+    constexpr int B2 = EM == kESiluMul ? 4096 : 2048, B3 = B2 + 1024;   // offsets of B tiles 2, 3
+    q35_u32x4 fa[2][4], fb[2][4];                                 // two register sets: [set][tile]
+    auto rd = [&](int j, q35_u32x4 (&af)[4], q35_u32x4 (&bw)[4]) {
+        const unsigned so = (unsigned)((j % kWideRing) * kWideStage);
+        const unsigned sa = abase + so, sbb = bbase + so;
+#define Q35_WRD(dst, base, off) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "n"(off) : "memory")
+        Q35_WRD(af[0], sa, 0); Q35_WRD(af[1], sa, 1024); Q35_WRD(af[2], sa, 2048); Q35_WRD(af[3], sa, 3072);
+        Q35_WRD(bw[0], sbb, 0); Q35_WRD(bw[1], sbb, 1024); Q35_WRD(bw[2], sbb, B2); Q35_WRD(bw[3], sbb, B3);
+#undef Q35_WRD
+    };
     q35_f32x4 c[4][4], sum[4][4];
 #pragma unroll
-    for (int j = 0; j < S::RING - 1; ++j) issue(j);
-    // this wave's fragment bases: its 4 row tiles' pieces (SPS (4 wm + i) + u) and its 4 column
-    // tiles' pieces (RT SPS + SPS (4 wn + i) + u), 1 KiB each; the lane's 16 bytes at lane * 16
-    const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) const void*)dyn_lds + lane * 16;
-    const unsigned abase = lds0 + (unsigned)(wm * 4 * S::SPS) * 1024u;
-    const unsigned bbase = lds0 + (unsigned)(RT * S::SPS + wn * 4 * S::SPS) * 1024u;
+    for (int j = 0; j < kWideRing - 1; ++j) issue(j);
+    asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");      // stage 0 landed
+    rd(0, fa[0], fb[0]);
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-    for (int jj = 0; jj < S::SPK; ++jj) {
-        const int j = kb * S::SPK + jj;
-        // stage j landed for every wave (the later stages already issued may be in flight);
-        // every wave is done with stage j - 1
-        if (RT == 16) {
-            if (j < S::NS - 1) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        } else {
-            if (j < S::NS - 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-            else if (j == S::NS - 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        }
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        if (j + S::RING - 1 < S::NS) issue(j + S::RING - 1);
-        const unsigned so = (unsigned)((j % S::RING) * S::STAGE);
-        const unsigned sa = abase + so, sbb = bbase + so;
-        q35_u32x4 af[S::SPS][4], bw[S::SPS][4];
-        constexpr int PS = S::SPS * 1024;                 // bytes between a wave's tiles
-#define Q35_WRD(dst, base, off) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "n"(off) : "memory")
-        Q35_WRD(af[0][0], sa, 0); Q35_WRD(af[0][1], sa, PS); Q35_WRD(af[0][2], sa, 2 * PS); Q35_WRD(af[0][3], sa, 3 * PS);
-        Q35_WRD(bw[0][0], sbb, 0); Q35_WRD(bw[0][1], sbb, PS); Q35_WRD(bw[0][2], sbb, 2 * PS); Q35_WRD(bw[0][3], sbb, 3 * PS);
-        if constexpr (S::SPS == 2) {
-            Q35_WRD(af[S::SPS - 1][0], sa, 1024); Q35_WRD(af[S::SPS - 1][1], sa, 3072);
-            Q35_WRD(af[S::SPS - 1][2], sa, 5120); Q35_WRD(af[S::SPS - 1][3], sa, 7168);
-            Q35_WRD(bw[S::SPS - 1][0], sbb, 1024); Q35_WRD(bw[S::SPS - 1][1], sbb, 3072);
-            Q35_WRD(bw[S::SPS - 1][2], sbb, 5120); Q35_WRD(bw[S::SPS - 1][3], sbb, 7168);
-        }
-#undef Q35_WRD
+    for (int jj = 0; jj < 8; ++jj) {
+        const int j = kb * 8 + jj, cur = jj & 1;
+        // stage j + 1 landed for every wave (stages j + 2 .. j + 4 may still be in flight), stage
+        // j's fragments are in registers set cur; every wave is done with stage j's slot reads,
+        // so the slot of stage j - 1 takes stage j + 5
+        // (the last stages issue no DMA, so the count of later stages in flight shrinks to 0). The
+        // vector-memory waits carry no register operands: a branch between asm statements that
+        // name the fragment registers would let the compiler copy them before the LDS wait.
+        if (kb < 3 || jj < 4) asm volatile("s_waitcnt vmcnt(9)" ::: "memory");   // stages j + 2 .. j + 4 out, j <= 27
+        else if (jj == 4) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");       // j = 28: stages 30, 31
+        else if (jj == 5) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");       // j = 29: stage 31
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier"
+                     : "+v"(fa[cur][0]), "+v"(fa[cur][1]), "+v"(fa[cur][2]), "+v"(fa[cur][3]),
+                       "+v"(fb[cur][0]), "+v"(fb[cur][1]), "+v"(fb[cur][2]), "+v"(fb[cur][3])
+                     :: "memory");
+        if (kb < 3 || jj < 3) issue(j + kWideRing - 1);     // stages 5 .. 31
+        if (j + 1 < 32) rd(j + 1, fa[cur ^ 1], fb[cur ^ 1]);
 #pragma unroll
-        for (int u = 0; u < S::SPS; ++u) {
-            if (u == 0 && S::SPS == 2)
-                asm volatile("s_waitcnt lgkmcnt(8)"
-                             : "+v"(af[0][0]), "+v"(af[0][1]), "+v"(af[0][2]), "+v"(af[0][3]),
-                               "+v"(bw[0][0]), "+v"(bw[0][1]), "+v"(bw[0][2]), "+v"(bw[0][3]));
-            else
-                asm volatile("s_waitcnt lgkmcnt(0)"
-                             : "+v"(af[u][0]), "+v"(af[u][1]), "+v"(af[u][2]), "+v"(af[u][3]),
-                               "+v"(bw[u][0]), "+v"(bw[u][1]), "+v"(bw[u][2]), "+v"(bw[u][3]));
-            const bool first = jj == 0 && u == 0;     // a k-block's chain starts from zero
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int jn = 0; jn < 4; ++jn)
-                    c[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(af[u][i]), as_bf(bw[u][jn]),
-                                                                        first ? (q35_f32x4){0.f, 0.f, 0.f, 0.f} : c[i][jn], 0, 0, 0);
-            // keep the step's MFMAs here: the compiler would otherwise sink them past the next
-            // waits and barrier, so that no LDS read overlaps any matrix work
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (jj == S::SPK - 1) {            // k-block kb done: ((c0 + c1) + c2) + c3
+            for (int jn = 0; jn < 4; ++jn)
+                c[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(fa[cur][i]), as_bf(fb[cur][jn]),
+                                                                    jj == 0 ? (q35_f32x4){0.f, 0.f, 0.f, 0.f} : c[i][jn], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (jj == 7) {                     // k-block kb done: ((c0 + c1) + c2) + c3
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -848,51 +823,29 @@ __global__ void __launch_bounds__(32 * RT, RT == 8 ? 2 : 1) gemm_wide(GemmArgs a
         }
     }
     const int row0 = (tr0 + wm * 4) * 16;
-    // Epilogue through the drained ring: each wave leaves its bf16 outputs in LDS in row order and
-    // stores them back as 16-byte row pieces (the MFMA layout would store 2 bytes per lane).
+    // Epilogue through the drained ring (no DMA is in flight): each wave leaves its bf16 outputs
+    // in its own LDS region in row order and stores them back as 16-byte row pieces (the MFMA
+    // layout would store 2 bytes per lane); a wave reads only what it wrote, so one block barrier
+    // (the ring is drained by every wave) is all the epilogue needs.
     __syncthreads();
     uint16_t* wl = (uint16_t*)dyn_lds;
     if (EM == kESiluMul) {
-        // the pair (wm, gate wave wn = 0) / (wm, up wave wn = 1) swaps halves: the gate wave makes
-        // the outputs of tiles jn = 0, 1 (needs bf16 u of them), the up wave those of jn = 2, 3
-        // (needs bf16 g of them), so both waves share the SiLU work
-        uint16_t* xb = wl + (size_t)(wm * 2 + wn) * 2048;          // [i][2][r][64] bf16 sent by this wave
-        const uint16_t* rb = wl + (size_t)(wm * 2 + (wn ^ 1)) * 2048;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    xb[((i * 2 + h) * 4 + r) * 64 + lane] = f2bf(sum[i][wn == 0 ? 2 + h : h][r]);
-        __syncthreads();
-        // outputs of tiles jn0 + h, h = 0, 1 into this wave's 64 x 32 staging (row stride 64 B)
-        const int jn0 = wn == 0 ? 0 : 2;
-        uint16_t ov[4][2][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float other = bf2f(rb[((i * 2 + h) * 4 + r) * 64 + lane]);
-                    const float own = sum[i][jn0 + h][r];
-                    const float g = wn == 0 ? rbf(own) : other, u = wn == 0 ? other : rbf(own);
-                    ov[i][h][r] = f2bf(__fmul_rn(rbf(silu_f(g)), u));
-                }
-        __syncthreads();
+        // lane holds gate (tiles h) and up (tiles 2 + h) of the same outputs: output tile
+        // nblk * 4 + 2 wn + h = bf16(bf16(silu(bf16(g))) * bf16(u))
         uint16_t* ob = wl + (size_t)wv * 2048;                    // [64 rows][32 cols]
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) ob[(i * 16 + 4 * (lane >> 4) + r) * 32 + h * 16 + (lane & 15)] = ov[i][h][r];
-        __syncthreads();
+                for (int r = 0; r < 4; ++r)
+                    ob[(i * 16 + 4 * (lane >> 4) + r) * 32 + h * 16 + (lane & 15)] =
+                        f2bf(__fmul_rn(rbf(silu_f(rbf(sum[i][h][r]))), rbf(sum[i][2 + h][r])));
+        wave_sync();
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int ch = lane + 64 * q, row = ch >> 2, piece = ch & 3;   // 4 pieces of 16 B per row
-            const int jt = nblk * 4 + jn0 + (piece >> 1);
+            const int jt = nblk * 4 + 2 * wn + (piece >> 1);
             const int grow = row0 + row;
             if (grow < a.M && jt < half)
                 *(q35_u32x4*)(a.Y + (size_t)grow * a.ldy + jt * 16 + (piece & 1) * 8) = *(const q35_u32x4*)(ob + row * 32 + piece * 8);
@@ -906,7 +859,7 @@ __global__ void __launch_bounds__(32 * RT, RT == 8 ? 2 : 1) gemm_wide(GemmArgs a
         for (int jn = 0; jn < 4; ++jn)
 #pragma unroll
             for (int r = 0; r < 4; ++r) ob[(i * 16 + 4 * (lane >> 4) + r) * 64 + jn * 16 + (lane & 15)] = f2bf(sum[i][jn][r]);
-    __syncthreads();
+    wave_sync();
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
         const int ch = lane + 64 * q, row = ch >> 3, piece = ch & 7;       // 8 pieces of 16 B per row
@@ -1224,21 +1177,9 @@ static hipError_t launch_wide(const GemmArgs& a, int em, hipStream_t st) {
     if (a.K != kHidden || a.M <= 16 || (em != kEStore && em != kESiluMul) || !a.Y || (em == kESiluMul && a.N % 32) ||
         a.ldy % 8 || ((uintptr_t)a.Y & 15))         // 16-byte row pieces in the epilogue
         return hipErrorInvalidValue;
-    const int nb = em == kESiluMul ? (a.N / 32 + 3) / 4 : (a.N / 16 + 7) / 8;
-    // 256-row blocks, or 128-row blocks (two per CU) when 256-row blocks would leave more than
-    // half of the CUs idle (at 768 rows the 256-row form measured 31 against 32.5 us for gate|up)
-    const int mb8 = (a.M + 127) / 128, g8 = (nb + 7) / 8 * 8 * mb8;
-    const int g16 = (nb + 7) / 8 * 8 * ((a.M + 255) / 256);
-    if (a.forms.gemm_wide == 2 || (a.forms.gemm_wide == 1 && g16 < 128)) {
-        using S = WideShape<8>;
-        if (em == kESiluMul) hipLaunchKernelGGL((gemm_wide<kESiluMul, 8>), dim3(g8), dim3(256), S::LDS, st, a);
-        else hipLaunchKernelGGL((gemm_wide<kEStore, 8>), dim3(g8), dim3(256), S::LDS, st, a);
-    } else {
-        using S = WideShape<16>;
-        const int mb = (a.M + 255) / 256, g = (nb + 7) / 8 * 8 * mb;
-        if (em == kESiluMul) hipLaunchKernelGGL((gemm_wide<kESiluMul, 16>), dim3(g), dim3(512), S::LDS, st, a);
-        else hipLaunchKernelGGL((gemm_wide<kEStore, 16>), dim3(g), dim3(512), S::LDS, st, a);
-    }
+    const int nb = em == kESiluMul ? (a.N / 32 + 3) / 4 : (a.N / 16 + 7) / 8, mb = (a.M + 255) / 256;
+    if (em == kESiluMul) hipLaunchKernelGGL(gemm_wide<kESiluMul>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
+    else hipLaunchKernelGGL(gemm_wide<kEStore>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
     return hipGetLastError();
 }
 
@@ -1359,10 +1300,8 @@ hipError_t gemm_init() {
         hipFuncSetAttribute((const void*)gemm_pre<kESiluMul, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<2>()) != hipSuccess ||
         hipFuncSetAttribute((const void*)gemm_pre<kEStore, 4, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<4>()) != hipSuccess ||
         hipFuncSetAttribute((const void*)gemm_pre<kESiluMul, 4, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<4>()) != hipSuccess ||
-        hipFuncSetAttribute((const void*)gemm_wide<kEStore, 16>, hipFuncAttributeMaxDynamicSharedMemorySize, WideShape<16>::LDS) != hipSuccess ||
-        hipFuncSetAttribute((const void*)gemm_wide<kESiluMul, 16>, hipFuncAttributeMaxDynamicSharedMemorySize, WideShape<16>::LDS) != hipSuccess ||
-        hipFuncSetAttribute((const void*)gemm_wide<kEStore, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, WideShape<8>::LDS) != hipSuccess ||
-        hipFuncSetAttribute((const void*)gemm_wide<kESiluMul, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, WideShape<8>::LDS) != hipSuccess)
+        hipFuncSetAttribute((const void*)gemm_wide<kEStore>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess ||
+        hipFuncSetAttribute((const void*)gemm_wide<kESiluMul>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess)
         return hipGetLastError();
     return hipSuccess;
 }

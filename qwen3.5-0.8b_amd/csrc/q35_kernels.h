@@ -27,9 +27,7 @@ struct KernelForms {
     int attn_prompt = 1;       // prompt waves of >= 64 rows: flash-form MFMA kernel (1) or one-row kernels (0)
     int mid_partials = 1;      // bodies of 2 .. 16 rows: k-block chains + add+norm (0: residual-epilogue GEMMs)
     int gdn_rows = 1;          // MTP verify (2-3 rows per lane, whole-head blocks): the persistent GDN kernel
-    int gemm_wide = 1;         // K = 1024 GEMMs of >= 512 rows through an LDS ring, A tiled: 256 x 128 tiles,
-                               // or 128 x 128 two per CU when 256-row blocks would fill under half the CUs
-                               // (1); forced 128-row (2) or 256-row (3) blocks; off (0)
+    int gemm_wide = 1;         // K = 1024 GEMMs of >= 512 rows: 256 x 128 tiles through an LDS ring, A tiled
     int gdn_defer = 3;         // decode steps: a lane's GDN state update is kept as pending factors for up
                                // to this many steps, the state written on the next (0: every step)
 };

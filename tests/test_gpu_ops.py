@@ -78,17 +78,17 @@ def test_lm_head_argmax(eng, oracle_weights):
     assert tok[2].item() == tok[3].item()
 
 
-@pytest.mark.parametrize("mode", [2, 3])
-@pytest.mark.parametrize("N,M", [(8224, 600), (5120, 1024), (7168, 768), (1024, 513)])
-def test_wide_gemm_forms_bit_identical(mode, N, M):
+@pytest.mark.parametrize("N,M", [(8224, 600), (5120, 1024), (7168, 768), (1024, 513), (7168, 2048)])
+def test_wide_gemm_forms_bit_identical(N, M):
     """The many-row K = 1024 GEMM (q35_op_gemm_a amodes 3 / 6: A staged in the fragment layout,
-    128-row blocks two per CU (gemm_wide 2) or 256-row blocks (3)) equals the batched GEMMs
-    (amodes 0 / 5) bit for bit: stored outputs, and the SwiGLU epilogue on [gate; up] weights,
-    including ragged last row blocks; the stored form also against float64 (1 bf16 ulp)."""
+    256-row blocks, a software-pipelined LDS ring) equals the batched GEMMs (amodes 0 / 5) bit for
+    bit: stored outputs, and the SwiGLU epilogue on [gate; up] weights, including ragged last row
+    blocks; the stored form also against float64 (1 bf16 ulp)."""
+    mode = 1
     import torch
     from qwen35 import Engine
     print(f"wide gemm mode={mode} N={N} M={M}", flush=True)
-    e = Engine(max_rows=1024, max_ctx=64, seed=0)
+    e = Engine(max_rows=2048, max_ctx=64, seed=0)
     try:
         e.set_option("gemm_wide", mode)
         g = torch.Generator().manual_seed(N + M + mode)
