@@ -533,9 +533,15 @@ void gemm(q35_engine* e, const uint16_t* W, int N, int K, int M, const void* X, 
 // Batch-1 path (<= 16 rows): the residual add lives in the producing GEMM's epilogue and the
 // RMSNorm in the consuming GEMM's A operand, so no add+norm launches remain.
 inline bool small_rows(int R) { return R <= 16; }
-// Bodies of >= 512 rows (prompt waves, MTP verify at many lanes): the normed rows e->h go out in
-// the weights' tiled fragment layout and the K = 1024 GEMMs that read them run gemm_wide.
-inline bool wide_rows(const q35_engine* e, int R) { return e->forms.gemm_wide && R >= 512; }
+// Whether the K = 1024 GEMM of width N over R normed rows takes them in the weights' tiled
+// fragment layout (the producing add+norm writes e->h so) and runs gemm_wide: bodies of >= 512
+// rows (prompt waves, MTP verify at many lanes, 256-row tiles) and batched lanes of 17 .. 511
+// rows (64-row tiles) except the GDN in_proj, whose 65 column blocks x 4 row blocks at 256 rows
+// would not fit the 256 CUs in one round (gemm_pre instead: 13.9 against 13.7 us in two rounds).
+inline bool wide_for(const q35_engine* e, int R, int N) {
+    return e->forms.gemm_wide && R > 16 && (R >= 512 || N != kGdnInRows);
+}
+inline int in_rows(int l) { return is_attn_layer(l) ? kAttnInRows : kGdnInRows; }
 
 // One-row bodies (a batch-1 decode step, a one-token prompt): the 1024-wide GEMVs (out_proj,
 // o_proj, down) run one wave per (column tile, k-block) and leave their k-block chains in
@@ -607,7 +613,7 @@ void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16
         norm_gemm(e, rr, w.W_in, kAttnInRows, R, e->proj, kAttnInRows, w.norm_in);
     else
         gemm(e, w.W_in, kAttnInRows, kHidden, R, e->h, kHidden, e->proj, kAttnInRows, kAPlain, nullptr, 0, nullptr, -1,
-             nullptr, wide_rows(e, R));
+             nullptr, wide_for(e, R, kAttnInRows));
     AttnArgs a{};
     a.proj = e->proj; a.q_norm = w.q_norm; a.k_norm = w.k_norm;
     a.kc = kc; a.vc = vc; a.kv_lane = kv_lane; a.kv_layer_off = layer_off; a.cap = cap;
@@ -635,18 +641,19 @@ void mlp_layer(q35_engine* e, const LayerW& w, int R, B1Res* rr = nullptr) {
         return;
     }
     HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(R, 2048, e->forms), w.norm_post, e->h, R, e->st,
-                       wide_rows(e, R)));
+                       wide_for(e, R, kGuRows)));
     // gate|up GEMM with the SwiGLU product in its epilogue: act [R][3584] -> plain down GEMM
     gemm(e, w.W_gu, kGuRows, kHidden, R, e->h, kHidden, e->gu, kFF, kAPlain, nullptr, 0, nullptr, kESiluMul, nullptr,
-         wide_rows(e, R));
+         wide_for(e, R, kGuRows));
     gemm(e, w.W_down, kHidden, kFF, R, e->gu, kFF, nullptr, 0);
 }
 
-// Batched path: fold the down-projection chains into x and normalise for the next consumer.
-void finish_norm(q35_engine* e, int R, const uint16_t* nw, uint16_t* out) {
+// Batched path: fold the down-projection chains into x and normalise for the next consumer (a
+// K = 1024 GEMM of width next_n when out is e->h).
+void finish_norm(q35_engine* e, int R, const uint16_t* nw, uint16_t* out, int next_n = 0) {
     if (small_rows(R)) return;
     HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(R, kFF, e->forms), nw, out, R, e->st,
-                       out == e->h && wide_rows(e, R)));
+                       out == e->h && wide_for(e, R, next_n)));
 }
 
 // Runs the 24-layer body over R = nl * T rows (rows of one lane consecutive) and leaves the
@@ -681,7 +688,7 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt, int defe
     res.mid = mid_partials(e, R);   // 2 .. 16 rows: e->x folded in place, e->h the normed rows
     B1Res* rr = b1_partials(e, R, T, ckpt) || res.mid ? &res : nullptr;
     HCK(launch_addnorm(0, e->tok_dev, e->E, e->x, nullptr, nullptr, 0, e->L[0].norm_in, small ? nullptr : e->h,
-                       R, e->st, !small && wide_rows(e, R)));
+                       R, e->st, !small && wide_for(e, R, in_rows(0))));
     for (int l = 0; l < e->n_layers; ++l) {
         const LayerW& w = e->L[l];
         if (!is_attn_layer(l)) {
@@ -689,7 +696,7 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt, int defe
                 norm_gemm(e, rr, w.W_in, kGdnInRows, R, e->proj, kGdnInRows, w.norm_in);
             else
                 gemm(e, w.W_in, kGdnInRows, kHidden, R, e->h, kHidden, e->proj, kGdnInRows, kAPlain, nullptr, 0, nullptr,
-                     -1, nullptr, wide_rows(e, R));
+                     -1, nullptr, wide_for(e, R, kGdnInRows));
             GdnArgs g{};
             g.proj = e->proj; g.o = e->o; g.conv_w = w.conv_w; g.A_log = w.A_log; g.dt_bias = w.dt_bias;
             g.S = s->S; g.S_lane = s->S_lane(); g.S_slot = (long long)kGdnLayers * kSLayer;
@@ -726,7 +733,7 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt, int defe
         mlp_layer(e, w, R, rr);
         const bool lastl = l + 1 == e->n_layers;
         const uint16_t* nw = lastl ? e->final_norm : e->L[l + 1].norm_in;
-        finish_norm(e, R, nw, lastl ? e->nrm : e->h);
+        finish_norm(e, R, nw, lastl ? e->nrm : e->h, lastl ? 0 : in_rows(l + 1));
     }
     // one-row body: the last layer's chains and the final norm in one add+norm launch; the
     // normed row is in e->nrm, so the caller's lm_head takes no norm weight
@@ -778,7 +785,7 @@ void mtp_draft_pass(q35_engine* e, q35_state* s, int n, const uint16_t* hsrc) {
     } else {
         gemm(e, e->mtp_fc, kHidden, 2048, n, e->cat, 2048, nullptr, 0);
         HCK(launch_addnorm(4, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(n, 2048, e->forms), e->M.norm_in, e->h, n, e->st,
-                           wide_rows(e, n)));
+                           wide_for(e, n, kAttnInRows)));
     }
     attention_layer(e, e->M, n, s->mkc, s->mvc, s->mkv_lane(), 0, s->mtp_capT);
     mlp_layer(e, e->M, n);

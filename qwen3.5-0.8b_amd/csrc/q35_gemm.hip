@@ -870,6 +870,140 @@ __global__ void __launch_bounds__(512) gemm_wide(GemmArgs a) {
     }
 }
 
+// K = 1024 at batched lanes (M <= 511 rows, decode): gemm_wide's ring and pipeline with 64-row x
+// 128-column block tiles (224 blocks for gate|up at 256 rows). 8 waves of 32 x 32 (wave (wm, wn):
+// row tiles 2 wm, 2 wm + 1; kEStore: column tiles 2 wn, 2 wn + 1; kESiluMul: gate tile wn and
+// the matching up tile, so the SwiGLU is lane-local); stages of two MFMA steps (24 KiB: 4 row
+// tiles and 8 column tiles x 2 steps x 1 KiB), a six-stage ring, DMA four stages ahead, the next
+// stage's fragments read during the current stage's MFMAs. A in the tiled fragment layout, as
+// for gemm_wide. Canonical reduction, bit-identical to the other forms.
+template <int EM>
+__global__ void __launch_bounds__(512) gemm_wide64(GemmArgs a) {
+    extern __shared__ q35_u32x4 dyn_lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wv >> 2, wn = wv & 3;
+    const int mb = (a.M + 63) / 64;
+    const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
+    const int nblk = (idx / mb) * 8 + xcd, rb = idx % mb;
+    const int ntiles = a.N / 16, mtiles = (a.M + 15) / 16;
+    const int half = a.N / 32;
+    if (EM == kESiluMul ? nblk * 4 >= half : nblk * 8 >= ntiles) return;
+    auto col_tile = [&](int c) {
+        if (EM == kESiluMul) return c < 4 ? nblk * 4 + c : half + nblk * 4 + (c - 4);
+        return nblk * 8 + c;
+    };
+    const int tr0 = rb * 4;
+    // DMA pieces of a stage: 8 A pieces (row tile pc / 2, step pc % 2), 16 W pieces (column tile
+    // (pc - 8) / 2, step pc % 2); wave wv issues pieces 3 wv .. 3 wv + 2
+    const char* pbase[3];
+    unsigned ploff[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int pc = 3 * wv + i;
+        if (pc < 8) {
+            const int t = min(tr0 + (pc >> 1), mtiles - 1);
+            pbase[i] = (const char*)((const uint16_t*)a.X + ((size_t)t * 4 * 8 + (pc & 1)) * 512);
+        } else {
+            const int nt = min(col_tile((pc - 8) >> 1), ntiles - 1);
+            pbase[i] = (const char*)(a.W + ((size_t)nt * 4 * 8 + (pc & 1)) * 512);
+        }
+        ploff[i] = (unsigned)pc * 1024u;
+    }
+    auto issue = [&](int j) {          // stage j: k-block j / 4, steps 2 (j % 4), + 1
+        const unsigned koff = (unsigned)((j >> 2) * 8 + (j & 3) * 2) * 1024u;
+        char* lds = (char*)dyn_lds + (j % kWideRing) * kWideStage;
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+            __builtin_amdgcn_global_load_lds((const void*)(uniform_ptr(pbase[i] + koff) + lane * 16),
+                                             (__attribute__((address_space(3))) void*)(lds + ploff[i]), 16, 0, 0);
+    };
+    const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) const void*)dyn_lds + lane * 16;
+    const unsigned abase = lds0 + (unsigned)(wm * 4) * 1024u;        // pieces 2 (2 wm + i) + u
+    const unsigned bbase = lds0 + (unsigned)(8 + (EM == kESiluMul ? 2 : 4) * wn) * 1024u;
+    constexpr int B1 = EM == kESiluMul ? 8192 : 2048;                 // offset of the second B tile
+    q35_u32x4 fa[2][2][2], fb[2][2][2];                               // [set][step][tile]
+    auto rd = [&](int j, q35_u32x4 (&af)[2][2], q35_u32x4 (&bw)[2][2]) {
+        const unsigned so = (unsigned)((j % kWideRing) * kWideStage);
+        const unsigned sa = abase + so, sbb = bbase + so;
+#define Q35_WRD(dst, base, off) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "n"(off) : "memory")
+        Q35_WRD(af[0][0], sa, 0); Q35_WRD(af[0][1], sa, 2048); Q35_WRD(bw[0][0], sbb, 0); Q35_WRD(bw[0][1], sbb, B1);
+        Q35_WRD(af[1][0], sa, 1024); Q35_WRD(af[1][1], sa, 3072); Q35_WRD(bw[1][0], sbb, 1024); Q35_WRD(bw[1][1], sbb, B1 + 1024);
+#undef Q35_WRD
+    };
+    q35_f32x4 c[2][2], sum[2][2];
+#pragma unroll
+    for (int j = 0; j < kWideRing - 1; ++j) issue(j);
+    asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");      // stage 0 landed
+    rd(0, fa[0], fb[0]);
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+        const int j = kb * 4 + jj, cur = jj & 1;
+        // stage j + 1 landed for every wave (stages j + 2 .. j + 4 may be in flight; none is
+        // issued past stage 15); the vector-memory waits name no registers (see gemm_wide)
+        if (kb < 3) asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
+        else if (jj == 0) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");  // j = 12: stages 14, 15
+        else if (jj == 1) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");  // j = 13: stage 15
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier"
+                     : "+v"(fa[cur][0][0]), "+v"(fa[cur][0][1]), "+v"(fa[cur][1][0]), "+v"(fa[cur][1][1]),
+                       "+v"(fb[cur][0][0]), "+v"(fb[cur][0][1]), "+v"(fb[cur][1][0]), "+v"(fb[cur][1][1])
+                     :: "memory");
+        if (kb < 2 || (kb == 2 && jj < 3)) issue(j + kWideRing - 1);   // stages 5 .. 15
+        if (j + 1 < 16) rd(j + 1, fa[cur ^ 1], fb[cur ^ 1]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int jn = 0; jn < 2; ++jn)
+                    c[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(fa[cur][u][i]), as_bf(fb[cur][u][jn]),
+                                                                        jj == 0 && u == 0 ? (q35_f32x4){0.f, 0.f, 0.f, 0.f} : c[i][jn], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (jj == 3) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int jn = 0; jn < 2; ++jn)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sum[i][jn][r] = kb == 0 ? c[i][jn][r] : sum[i][jn][r] + c[i][jn][r];
+        }
+    }
+    const int row0 = (tr0 + wm * 2) * 16;
+    __syncthreads();                   // the ring is drained by every wave: wave-private staging
+    uint16_t* wl = (uint16_t*)dyn_lds;
+    if (EM == kESiluMul) {
+        uint16_t* ob = wl + (size_t)wv * 512;                        // [32 rows][16 cols]
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                ob[(i * 16 + 4 * (lane >> 4) + r) * 16 + (lane & 15)] =
+                    f2bf(__fmul_rn(rbf(silu_f(rbf(sum[i][0][r]))), rbf(sum[i][1][r])));
+        wave_sync();
+        const int row = lane >> 1, piece = lane & 1, jt = nblk * 4 + wn, grow = row0 + row;
+        if (grow < a.M && jt < half)
+            *(q35_u32x4*)(a.Y + (size_t)grow * a.ldy + jt * 16 + piece * 8) = *(const q35_u32x4*)(ob + row * 16 + piece * 8);
+        return;
+    }
+    uint16_t* ob = wl + (size_t)wv * 1024;                           // [32 rows][32 cols]
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int jn = 0; jn < 2; ++jn)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ob[(i * 16 + 4 * (lane >> 4) + r) * 32 + jn * 16 + (lane & 15)] = f2bf(sum[i][jn][r]);
+    wave_sync();
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int ch = lane + 64 * q, row = ch >> 2, piece = ch & 3;
+        const int nt = nblk * 8 + wn * 2 + (piece >> 1), grow = row0 + row;
+        if (grow < a.M && nt < ntiles)
+            *(q35_u32x4*)(a.Y + (size_t)grow * a.ldy + nt * 16 + (piece & 1) * 8) = *(const q35_u32x4*)(ob + row * 32 + piece * 8);
+    }
+}
+
 // ---------------------------------------------------------------- tied lm_head, batched lanes
 // K = 1024 (the hidden size), argmax epilogue, launches of M <= 512. Persistent blocks of NW waves,
 // about one per CU: a block stages its 64 A rows (64 x 1024 bf16 = 128 KiB) in LDS once, in
@@ -1177,7 +1311,14 @@ static hipError_t launch_wide(const GemmArgs& a, int em, hipStream_t st) {
     if (a.K != kHidden || a.M <= 16 || (em != kEStore && em != kESiluMul) || !a.Y || (em == kESiluMul && a.N % 32) ||
         a.ldy % 8 || ((uintptr_t)a.Y & 15))         // 16-byte row pieces in the epilogue
         return hipErrorInvalidValue;
-    const int nb = em == kESiluMul ? (a.N / 32 + 3) / 4 : (a.N / 16 + 7) / 8, mb = (a.M + 255) / 256;
+    const int nb = em == kESiluMul ? (a.N / 32 + 3) / 4 : (a.N / 16 + 7) / 8;
+    if (a.M < 512) {                   // batched lanes: 64-row blocks
+        const int mb = (a.M + 63) / 64;
+        if (em == kESiluMul) hipLaunchKernelGGL(gemm_wide64<kESiluMul>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
+        else hipLaunchKernelGGL(gemm_wide64<kEStore>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
+        return hipGetLastError();
+    }
+    const int mb = (a.M + 255) / 256;
     if (em == kESiluMul) hipLaunchKernelGGL(gemm_wide<kESiluMul>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
     else hipLaunchKernelGGL(gemm_wide<kEStore>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
     return hipGetLastError();
@@ -1301,7 +1442,9 @@ hipError_t gemm_init() {
         hipFuncSetAttribute((const void*)gemm_pre<kEStore, 4, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<4>()) != hipSuccess ||
         hipFuncSetAttribute((const void*)gemm_pre<kESiluMul, 4, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, pre_lds_bytes<4>()) != hipSuccess ||
         hipFuncSetAttribute((const void*)gemm_wide<kEStore>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess ||
-        hipFuncSetAttribute((const void*)gemm_wide<kESiluMul>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess)
+        hipFuncSetAttribute((const void*)gemm_wide<kESiluMul>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess ||
+        hipFuncSetAttribute((const void*)gemm_wide64<kEStore>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess ||
+        hipFuncSetAttribute((const void*)gemm_wide64<kESiluMul>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess)
         return hipGetLastError();
     return hipSuccess;
 }
