@@ -78,12 +78,13 @@ def test_lm_head_argmax(eng, oracle_weights):
     assert tok[2].item() == tok[3].item()
 
 
-@pytest.mark.parametrize("N,M", [(8224, 600), (5120, 1024), (7168, 768), (1024, 513), (7168, 2048)])
+@pytest.mark.parametrize("N,M", [(8224, 600), (5120, 1024), (7168, 768), (1024, 513), (7168, 2048),
+                                 (7168, 256), (5120, 256), (8224, 100), (7168, 17), (1024, 300)])
 def test_wide_gemm_forms_bit_identical(N, M):
-    """The many-row K = 1024 GEMM (q35_op_gemm_a amodes 3 / 6: A staged in the fragment layout,
-    256-row blocks, a software-pipelined LDS ring) equals the batched GEMMs (amodes 0 / 5) bit for
-    bit: stored outputs, and the SwiGLU epilogue on [gate; up] weights, including ragged last row
-    blocks; the stored form also against float64 (1 bf16 ulp)."""
+    """The pipelined K = 1024 GEMMs with A in the fragment layout (q35_op_gemm_a amodes 3 / 6:
+    256-row blocks at >= 512 rows, 64-row blocks below) equal the batched GEMMs (amodes 0 / 5)
+    bit for bit: stored outputs, and the SwiGLU epilogue on [gate; up] weights, including ragged
+    last row blocks; the stored form also against float64 (1 bf16 ulp)."""
     mode = 1
     import torch
     from qwen35 import Engine
