@@ -37,12 +37,12 @@ KERNEL_NAMES = {"attn": "attn_fused", "gdn": "gdn_persist", "lm_head": "gemm_lmh
 # the calibration are in the file named by TRAFFIC_SOURCE.
 TRAFFIC_SOURCE = "profiles/hbm_traffic_decode_b256_ctx4096.md"
 MEASURED_TRAFFIC = {
-    ("attn", 256, 4096): (1057689.8 * 2.0 + 1024.0 * 1.0) * 1024,                        # attn_fused
-    ("gdn", 256, 4096): (146562.7 * 2.0 + 90237.5 * 1.0) * 1024,    # gdn_persist, gdn_defer 3 (4-step average)
-    ("lm_head", 256, 4096): (250422.1 * 2.0 + 2048.0 * 1.0) * 1024,                       # gemm_lmhead3
-    # projection / MLP family, the average launch of a step: 24 gate|up, 18 in_proj, 6 qkv, 24 down,
-    # 24 out/o (FETCH x2 + WRITE per launch of each, KiB)
-    ("gemm", 256, 4096): (24 * (9331.1 * 2 + 1792.0) + 18 * (10336.3 * 2 + 4116.2) + 6 * (7227.2 * 2 + 2560.0)
+    ("attn", 256, 4096): (1057685.1 * 2.0 + 1024.0 * 1.0) * 1024,                        # attn_fused
+    ("gdn", 256, 4096): (146563.0 * 2.0 + 90236.8 * 1.0) * 1024,    # gdn_persist, gdn_defer 3 (4-step average)
+    ("lm_head", 256, 4096): (250420.7 * 2.0 + 2048.0 * 1.0) * 1024,                       # gemm_lmhead3
+    # projection / MLP family, the average launch of a step: 24 gate|up (gemm_wide64), 18 in_proj
+    # (gemm_pre), 6 qkv (gemm_wide64), 24 down, 24 out/o (FETCH x2 + WRITE per launch of each, KiB)
+    ("gemm", 256, 4096): (24 * (9271.0 * 2 + 1792.0) + 18 * (10334.5 * 2 + 4116.2) + 6 * (7220.0 * 2 + 2560.0)
                           + 24 * (4521.0 * 2 + 14336.0) + 24 * (2601.0 * 2 + 8192.0)) / 96 * 1024,
 }
 
