@@ -846,16 +846,22 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
                 if (st < 2) load_k_sub<true>(a, lrow, j, q, st + 2, slot, kf[st & 1]);
                 else load_k_sub<true>(a, lrow, j, qnext, st - 2, slot, kf[st & 1]);
 #pragma unroll
-                for (int u = 0; u < NU; ++u)
+                for (int u = 0; u < NU; ++u) {
+                    // the lane's 4 consecutive slots go out as one 16-byte store (slots past the
+                    // row's last are never read: the P.V pass gives them zero weight)
+                    q35_f32x4 scv;
+                    const int t = 2 * u + tr, tt0 = t0 + st * 16 + 4 * g;
 #pragma unroll
                     for (int rr = 0; rr < 4; ++rr) {
                         const float lo = row_down4(acc[u][rr]);   // lanes with n % 8 < 4 add the q_lo column
                         const float sc = (acc[u][rr] + lo) * 0.0625f;
-                        const int t = 2 * u + tr, tt = t0 + st * 16 + 4 * g + rr;
-                        const bool ok = (n & 7) < 4 && tt <= lslot[u];
+                        const bool ok = (n & 7) < 4 && tt0 + rr <= lslot[u];
                         sv[u][st][rr] = ok ? sc : -INFINITY;
-                        if (ok) a.sc[((size_t)(r0 + t) * kNq + 4 * j + (n & 3)) * a.sc_ld + tt] = sc;
+                        scv[rr] = sc;
                     }
+                    if ((n & 7) < 4 && tt0 <= lslot[u])
+                        *(q35_f32x4*)(a.sc + ((size_t)(r0 + t) * kNq + 4 * j + (n & 3)) * a.sc_ld + tt0) = scv;
+                }
             }
 #pragma unroll
             for (int u = 0; u < NU; ++u) {
