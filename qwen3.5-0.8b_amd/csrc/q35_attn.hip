@@ -26,6 +26,14 @@
 namespace q35 {
 
 constexpr int kChunk = 256;
+// attn_rows: at most kRowsLdsParts parts (128 slots) keep their scores in LDS, as many as fit
+// beside the slice stats in the dynamic LDS of a block that still runs two per CU (80 KiB less
+// the static q staging and ml); the tail's row stride is kRowsLdsSlots either way
+constexpr int kRowsLdsParts = 8, kRowsLdsSlots = kRowsLdsParts * 128;
+__host__ __device__ constexpr int rows_lds_parts(int T, int max_chunks) {
+    return (65440 - T * 4 * 8 * max_chunks * 4) / (T * 4 * kRowsLdsSlots * 4) > 0
+               ? kRowsLdsParts : 0;
+}
 // attn_fused<*, 2>: dynamic LDS of its two items, the CU's 160 KiB less both halves' static
 // arrays (ubuf, ml, nparts)
 constexpr int kFused2MaxLds = 160 * 1024 - 16464;
@@ -111,7 +119,7 @@ template <bool NT = true>
 __device__ __forceinline__ void load_k_sub(const AttnArgs& a, int lrow, int j, int q, int st, int slot,
                                            q35_u32x4* kf) {
     const int lane = threadIdx.x & 63;
-    const int tile = min(q * 4 + st, slot >> 4);
+    const int tile = max(min(q * 4 + st, slot >> 4), 0);
     const uint16_t* kp = a.kc + lrow * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256 + (size_t)tile * 4096 + lane * 8;
 #pragma unroll
     for (int s = 0; s < 8; ++s)
@@ -771,12 +779,14 @@ __global__ void __launch_bounds__(256 * NI) attn_fused(AttnArgs a, int lds_slots
 // rows: B tile u holds rows 2u and 2u + 1 as columns 8 (t % 2) + h (q hi) and + 4 (q lo), and
 // an MFMA output column depends only on its own B column, so a row's scores and slice stats
 // are the one-row kernel's bits. Each V part, loaded once into registers, feeds the P.V of
-// every row at once (the rows' weights are rows of P). The scores go to the global scratch
-// (T rows x 4 heads x cap f32 do not fit LDS beside two blocks per CU); the block reads back
-// only what it wrote, after a block barrier.
+// every row at once (the rows' weights are rows of P). T rows x 4 heads x cap f32 scores do
+// not fit LDS beside two blocks per CU: the last kRowsLdsParts parts' scores stay in LDS (the
+// first written, the last read), the rest go to the global scratch; the block reads back only
+// what it wrote, after a block barrier.
 template <int T>
 __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
-    extern __shared__ float stl_all[];                  // [T][4][8 * max_chunks] slice stats
+    extern __shared__ float stl_all[];                  // [T][4][8 * max_chunks] slice stats, then
+                                                        // the LDS tail [T][4][kRowsLdsSlots]
     __shared__ uint16_t qbuf[2][16][256];               // q staging (tiles), then the part's weights
     __shared__ float ml_all[T][4][2];
     constexpr int NU = (T + 1) / 2;                     // q tiles
@@ -790,6 +800,9 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
     for (int t = 1; t < T; ++t) slot = max(slot, slot_t[t]);
     const int lrow = a.rm.lane[r0];
     const size_t sst = (size_t)a.max_chunks * 8;
+    float* tl = stl_all + (size_t)T * 4 * sst;
+    const int lpn = rows_lds_parts(T, a.max_chunks);
+    const int p0 = max(slot / kPart + 1 - lpn, 0);     // first part in the LDS tail
     // q fragments: tile u, column 8 (t % 2) + h = bf16(q) of row t = 2u + t % 2, head h, and
     // + 4 its low part (zero columns for a missing row), as load_q_frags makes them
     {
@@ -820,9 +833,16 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
 #pragma unroll
             for (int s = 0; s < 8; ++s) qf[u][s] = *(const q35_u32x4*)&qbuf[u][n][s * 32 + g * 8];
         q35_u32x4 kf[2][8];
-        load_k_sub<true>(a, lrow, j, wv, 0, slot, kf[0]);
-        load_k_sub<true>(a, lrow, j, wv, 1, slot, kf[1]);
+        // the first slice's sub-tile 0 strictly before its sub-tile 1: the loop head's wait for
+        // sub-tile 0 must hold on entry too, and with sub-tile 0 loaded last it would drain the
+        // whole prefetch (and the previous slice's score stores) at every slice
         const int nch = slot / kChunk + 1;
+        load_k_sub<true>(a, lrow, j, 4 * (nch - 1) + wv, 0, slot, kf[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        load_k_sub<true>(a, lrow, j, 4 * (nch - 1) + wv, 1, slot, kf[1]);
+        // this block's rows of the score scratch as a buffer resource (byte offsets)
+        const __amdgpu_buffer_rsrc_t scres = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(a.sc + (size_t)r0 * kNq * a.sc_ld), 0, T * kNq * a.sc_ld * 4, 0x00020000);
         const int tr = n >> 3;                           // this lane's row within a tile: 2u + tr
         int lslot[NU];                                   // that row's slot (-1: no such row)
 #pragma unroll
@@ -830,8 +850,12 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
             const int ta = 2 * u, tb = 2 * u + 1 < T ? 2 * u + 1 : 2 * u;
             lslot[u] = tr == 0 ? slot_t[ta] : 2 * u + 1 < T ? slot_t[tb] : -1;
         }
-        for (int c = 0; c < nch; ++c) {
-            const int q = 4 * c + wv, qnext = 4 * (c + 1) + wv, t0 = q * 64;
+        // chunks from the last down (a slice's scores and stats do not depend on the order):
+        // the top parts, written first, stay in the LDS tail, and the P.V pass starts on the
+        // scores written last, still in L2
+        for (int c = nch - 1; c >= 0; --c) {
+            const int q = 4 * c + wv, qnext = 4 * (c - 1) + wv, t0 = q * 64;
+            const bool inl = q >= 2 * p0;                // this slice's scores go to the LDS tail
             float sv[NU][4][4];
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
@@ -859,9 +883,20 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
                         sv[u][st][rr] = ok ? sc : -INFINITY;
                         scv[rr] = sc;
                     }
-                    if ((n & 7) < 4 && tt0 <= lslot[u])
-                        *(q35_f32x4*)(a.sc + ((size_t)(r0 + t) * kNq + 4 * j + (n & 3)) * a.sc_ld + tt0) = scv;
+                    // slices below the LDS tail: an unconditional buffer store (lanes without a
+                    // score get an offset past the range, which the hardware drops; a store
+                    // under a branch would make the compiler drain outstanding loads at the join)
+                    const bool okst = (n & 7) < 4 && tt0 <= lslot[u] && !inl;
+                    const int off = okst ? ((t * kNq + 4 * j + (n & 3)) * a.sc_ld + tt0) * 4 : 0x7ffffff0;
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        (q35_u32x4){__float_as_uint(scv[0]), __float_as_uint(scv[1]), __float_as_uint(scv[2]), __float_as_uint(scv[3])},
+                        scres, off, 0, 0);
+                    if (inl && (n & 7) < 4 && tt0 <= lslot[u])
+                        *(q35_f32x4*)(tl + (t * 4 + (n & 3)) * kRowsLdsSlots + (tt0 - 128 * p0)) = scv;
                 }
+                // sub-tiles stay in order: with the next sub-tile's MFMAs hoisted into this one
+                // their K wait also drained this slice's earlier score stores
+                __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
             for (int u = 0; u < NU; ++u) {
@@ -897,29 +932,45 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
     uint16_t* pl = &qbuf[0][0][0];
     // V two parts ahead (the K and q registers of the score pass are free here): parts
     // alternate between vfa and vfb, each refilled with the part after next once used
-    q35_u32x4 vfa[4][4], vfb[4][4];
-    load_vf<true>(a, lrow, j, 0, slot, 4 * wv, vfa);
-    load_vf<true>(a, lrow, j, 1, slot, 4 * wv, vfb);
     q35_f32x4 acc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
     const int np = slot / kPart + 1;
     // the thread's two scores (head i = idx / 128, slot idx % 128 of the part, idx = tid,
-    // tid + 256) of every row, loaded one part ahead (clamped to the last slot: unconditional)
-    float sr[T][2];
-    auto load_scores = [&](int pc) {
+    // tid + 256) of every row, loaded two parts ahead like V and issued just before that part's
+    // V (clamped to the last slot: unconditional). The vector-memory counter completes in
+    // order, so waiting for a part's scores then never waits for V loads issued later.
+    auto load_scores = [&](int pc, float (&sr)[T][2]) {
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 const int idx = tid + q * 256, i = idx >> 7, tt = idx & 127;
-                sr[t][q] = a.sc[((size_t)(r0 + t) * kNq + 4 * j + i) * a.sc_ld + min(pc * kPart + tt, slot)];
+                // both sources without a branch: a part in the LDS tail reads slot 0 of the
+                // scratch (one line for every lane) and takes the LDS value
+                const int ts = min(pc * kPart + tt, slot);
+                const bool lp = pc >= p0 && lpn > 0;
+                const float gv = a.sc[((size_t)(r0 + t) * kNq + 4 * j + i) * a.sc_ld + (lp ? 0 : ts)];
+                const float lv = *(lp ? tl + (t * 4 + i) * kRowsLdsSlots + max(ts - 128 * p0, 0) : stl_all);
+                sr[t][q] = lp ? lv : gv;
             }
     };
+    q35_u32x4 vfa[4][4], vfb[4][4];
+    float sra[T][2], srb[T][2];
+    // in this order (the loop's waits must hold on entry as well: with a part's scores issued
+    // after its V, the first wait of every part would drain the whole V prefetch)
+    load_scores(0, sra);
+    __builtin_amdgcn_sched_barrier(0);
+    load_vf<true>(a, lrow, j, 0, slot, 4 * wv, vfa);
+    __builtin_amdgcn_sched_barrier(0);
+    load_scores(1, srb);
+    __builtin_amdgcn_sched_barrier(0);
+    load_vf<true>(a, lrow, j, 1, slot, 4 * wv, vfb);
+    __builtin_amdgcn_sched_barrier(0);
     const int tg = lane >> 4;
     const int myslot = tg == 0 ? slot_t[0] : tg == 1 ? slot_t[T > 1 ? 1 : 0] : slot_t[T > 2 ? 2 : 0];
     // one part (a part at np, when np is odd, is idle: zero weights, its sum not added)
-    auto part = [&](int pc, q35_u32x4 (&vf)[4][4]) {
+    auto part = [&](int pc, q35_u32x4 (&vf)[4][4], float (&sr)[T][2]) {
         lds_barrier();          // ml is in; every wave is done with the previous part's weights
         // part_weights' arithmetic, from the scores in registers
 #pragma unroll
@@ -931,11 +982,11 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
                 pl[(4 * t + i) * kPlStride + tt] = tt < nn ? f2bf(expf(sr[t][q] - ml_all[t][i][0]) / ml_all[t][i][1]) : (uint16_t)0;
             }
         }
-        load_scores(pc + 1);
         lds_barrier();
         if (pc == np - 1) mask_vf(pc, slot, vf);
         q35_f32x4 out[4];
         pv_mfma(pl, 4 * T, vf, out);
+        load_scores(pc + 2, sr);
         load_vf<true>(a, lrow, j, pc + 2, slot, 4 * wv, vf);
         // lane (n, g) holds row g's heads: add this part where it is one of that row's parts
         if (tg < T && pc < myslot / kPart + 1) {
@@ -943,10 +994,9 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
             for (int i = 0; i < 4; ++i) acc[i] += out[i];
         }
     };
-    load_scores(0);
     for (int pc = 0; pc < np; pc += 2) {
-        part(pc, vfa);
-        part(pc + 1, vfb);
+        part(pc, vfa, sra);
+        part(pc + 1, vfb, srb);
     }
     if (tg < T) {
 #pragma unroll
@@ -1285,7 +1335,7 @@ hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
         const int ngrp = (a.T + kPrRows - 1) / kPrRows;
         hipLaunchKernelGGL(attn_prompt, dim3((ngrp + 3) / 4 * 8), dim3(256), kPrLds, st, a);
     } else if (use_rows(a)) {
-        const size_t lds = (size_t)a.T * 4 * 8 * a.max_chunks * 4;
+        const size_t lds = (size_t)a.T * 4 * (8 * a.max_chunks + (rows_lds_parts(a.T, a.max_chunks) ? kRowsLdsSlots : 0)) * 4;
         if (a.T == 2) hipLaunchKernelGGL(attn_rows<2>, dim3(a.R / 2 * kNkv), dim3(256), lds, st, a);
         else hipLaunchKernelGGL(attn_rows<3>, dim3(a.R / 3 * kNkv), dim3(256), lds, st, a);
     } else if (use_fused(a)) {
