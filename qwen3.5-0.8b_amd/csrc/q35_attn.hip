@@ -1260,7 +1260,9 @@ __global__ void __launch_bounds__(256) attn_prompt(AttnArgs a) {
             for (int dt = 0; dt < 16; ++dt) {
                 const float ov = rbf(o[dt][r] / lr[r]);
                 const float gt = rbf(sigmoid_f(bf2f(gv[r][dt])));
-                po[r * 256 + 16 * dt] = f2bf(ov * gt);
+                const int col = (4 * j + r) * 256 + 16 * dt + n;
+                if (a.out_tiled) a.out[tiled_offset(row, col, 2048)] = f2bf(ov * gt);
+                else po[r * 256 + 16 * dt] = f2bf(ov * gt);
             }
         }
     }
@@ -1305,6 +1307,8 @@ static bool use_prompt(const AttnArgs& a) {
     if (a.force != kAttnAuto) return false;
     return a.prompt_flash && shape;
 }
+
+bool attn_prompt_form(const AttnArgs& a) { return use_prompt(a); }
 
 // Whether the forced form can run this shape (kAttnAuto always can).
 bool attn_form_ok(const AttnArgs& a) {

@@ -521,9 +521,11 @@ void materialize(q35_engine* e, q35_state* s, const std::vector<int>& lanes) {
 // add+norm); emode kEResidual: x <- bf16(x + bf16(sum)) (batch-1 path).
 void gemm(q35_engine* e, const uint16_t* W, int N, int K, int M, const void* X, int ldx,
           uint16_t* Y, int ldy, int amode = kAPlain, const void* X2 = nullptr, int ldx2 = 0,
-          const uint16_t* aux = nullptr, int emode = -1, uint16_t* xres = nullptr, bool x_tiled = false) {
+          const uint16_t* aux = nullptr, int emode = -1, uint16_t* xres = nullptr, bool x_tiled = false,
+          bool y_tiled = false) {
     GemmArgs a{};
     a.W = W; a.N = N; a.K = K; a.M = M; a.X = X; a.ldx = ldx; a.X2 = X2; a.ldx2 = ldx2; a.x_tiled = x_tiled ? 1 : 0;
+    a.y_tiled = y_tiled ? 1 : 0;
     a.aux_w = aux; a.Y = Y; a.ldy = ldy;
     a.kpart = e->kpart; a.prod = e->prod; a.xres = xres; a.forms = e->forms;
     KTimer kt(e, kFamGemm);
@@ -597,13 +599,15 @@ void norm_gemm(q35_engine* e, B1Res* rr, const uint16_t* W, int N, int R, uint16
 // A 1024-wide output projection feeding the residual: epilogue add (<= 16 rows), k-block
 // chains for the next fold (one-row bodies) or chains for the add+norm kernel (batched).
 void resid_gemm(q35_engine* e, B1Res* rr, const uint16_t* W, int K, int R, const void* X, int ldx,
-                int amode = kAPlain, const void* X2 = nullptr, int ldx2 = 0, const uint16_t* aux = nullptr) {
+                int amode = kAPlain, const void* X2 = nullptr, int ldx2 = 0, const uint16_t* aux = nullptr,
+                bool x_tiled = false) {
     if (rr) {
         REQ(rr->pend == 0, Q35_ERR_STATE, "unfolded k-block chains");
         gemm(e, W, kHidden, K, R, X, ldx, nullptr, 0, amode, X2, ldx2, aux, kEPartial);
         rr->pend = K / 256;
     } else {
-        gemm(e, W, kHidden, K, R, X, ldx, nullptr, 0, amode, X2, ldx2, aux, small_rows(R) ? kEResidual : -1, e->x);
+        gemm(e, W, kHidden, K, R, X, ldx, nullptr, 0, amode, X2, ldx2, aux, small_rows(R) ? kEResidual : -1, e->x,
+             x_tiled);
     }
 }
 
@@ -625,12 +629,15 @@ void attention_layer(q35_engine* e, const LayerW& w, int R, uint16_t* kc, uint16
     a.split4 = e->forms.attn_split4;
     a.fused_pair = e->forms.attn_pair;
     a.rows_form = e->forms.attn_rows;
+    // a prompt wave's o_proj in the many-row full-K form: attn_prompt writes its output tiled
+    const bool tiled = !rr && wide_fullk(e->forms, R) && attn_prompt_form(a);
+    a.out_tiled = tiled ? 1 : 0;
     HCK(launch_attn_prep(a, e->st));
     {
         KTimer kt(e, kFamAttn);      // the attention core alone (scores, softmax, P.V, gate)
         HCK(launch_attn_core(a, e->st));
     }
-    resid_gemm(e, rr, w.W_out, 2048, R, e->aout, 2048);
+    resid_gemm(e, rr, w.W_out, 2048, R, e->aout, 2048, kAPlain, nullptr, 0, nullptr, tiled);
 }
 
 // MLP sub-block; on the batched path it leaves chains that `finish_norm` folds in.
@@ -642,10 +649,12 @@ void mlp_layer(q35_engine* e, const LayerW& w, int R, B1Res* rr = nullptr) {
     }
     HCK(launch_addnorm(3, nullptr, nullptr, e->x, nullptr, e->kpart, gemm_partial_chains(R, 2048, e->forms), w.norm_post, e->h, R, e->st,
                        wide_for(e, R, kGuRows)));
-    // gate|up GEMM with the SwiGLU product in its epilogue: act [R][3584] -> plain down GEMM
+    // gate|up GEMM with the SwiGLU product in its epilogue: act [R][3584] -> plain down GEMM;
+    // prompt waves of >= partial_rows rows: act in the tiled layout for the many-row full-K down
+    const bool tiled = wide_fullk(e->forms, R);
     gemm(e, w.W_gu, kGuRows, kHidden, R, e->h, kHidden, e->gu, kFF, kAPlain, nullptr, 0, nullptr, kESiluMul, nullptr,
-         wide_for(e, R, kGuRows));
-    gemm(e, w.W_down, kHidden, kFF, R, e->gu, kFF, nullptr, 0);
+         wide_for(e, R, kGuRows), tiled);
+    gemm(e, w.W_down, kHidden, kFF, R, e->gu, kFF, nullptr, 0, kAPlain, nullptr, 0, nullptr, -1, nullptr, tiled);
 }
 
 // Batched path: fold the down-projection chains into x and normalise for the next consumer (a

@@ -416,6 +416,31 @@ __global__ void __launch_bounds__(256) produce_kernel(GemmArgs a) {
     }
 }
 
+// The same producer writing Y in the tiled fragment layout (K = a.K): block (16-row tile, 16
+// chunks of 8 k), the row fastest across threads, so the 16 rows' pieces of one (k-block, step,
+// quarter) -- one contiguous 256-byte run of the layout -- are written together (one row per
+// block would leave each 16-byte piece alone in its line).
+// Made row-major (16 threads per row share its reads) and transposed through LDS.
+template <int AM>
+__global__ void __launch_bounds__(256) produce_tiled_kernel(GemmArgs a) {
+    __shared__ q35_u32x4 t[16][16];                     // [chunk][row]
+    const int tid = threadIdx.x;
+    {
+        const int r = tid >> 4, c = tid & 15, m = min(blockIdx.x * 16 + r, a.M - 1);
+        const int k0 = (blockIdx.y * 16 + c) * 8;
+        float rs = 0.f;
+        if (AM == kAGatedNorm) {
+            const int hq = (k0 / 128) * 128;    // head start
+            const float* po = (const float*)a.X + (size_t)m * a.ldx;
+            rs = head_rsqrt(half_head_ss(po + hq), half_head_ss(po + hq + 64));
+        }
+        t[c][r] = produce_a<AM>(a, m, k0, rs);
+    }
+    __syncthreads();
+    const int r = tid & 15, c = tid >> 4, m = blockIdx.x * 16 + r;
+    if (m < a.M) *(q35_u32x4*)(a.Y + tiled_offset(m, (blockIdx.y * 16 + c) * 8, a.K)) = t[c][r];
+}
+
 // ---------------------------------------------------------------- large M
 // Plain bf16 A. grid (8 * ceil(N/(16*NW) / 8) * ceil(M/(16*MT)), 1, kEPartial ? KB : 1); NW waves,
 // wave w -> column tile NW*(column block) + w; the block's A rows of one k-block are staged in LDS in
@@ -847,8 +872,10 @@ __global__ void __launch_bounds__(512) gemm_wide(GemmArgs a) {
             const int ch = lane + 64 * q, row = ch >> 2, piece = ch & 3;   // 4 pieces of 16 B per row
             const int jt = nblk * 4 + 2 * wn + (piece >> 1);
             const int grow = row0 + row;
-            if (grow < a.M && jt < half)
-                *(q35_u32x4*)(a.Y + (size_t)grow * a.ldy + jt * 16 + (piece & 1) * 8) = *(const q35_u32x4*)(ob + row * 32 + piece * 8);
+            const int col = jt * 16 + (piece & 1) * 8;          // 8 consecutive k: one 16-byte piece
+            if (grow < a.M && jt < half)                           // in either layout
+                *(q35_u32x4*)(a.Y + (a.y_tiled ? tiled_offset(grow, col, a.ldy) : (size_t)grow * a.ldy + col)) =
+                    *(const q35_u32x4*)(ob + row * 32 + piece * 8);
         }
         return;
     }
@@ -871,7 +898,10 @@ __global__ void __launch_bounds__(512) gemm_wide(GemmArgs a) {
 }
 
 // K = 1024 at batched lanes (M <= 511 rows, decode): gemm_wide's ring and pipeline with 64-row x
-// 128-column block tiles (224 blocks for gate|up at 256 rows). 8 waves of 32 x 32 (wave (wm, wn):
+// 128-column block tiles (224 blocks for gate|up at 256 rows). kEPartial: any K (a multiple of
+// 512), all of K in the block and the k-block chains summed in order into chain 0 -- the
+// residual projections of prompt waves of >= partial_rows rows (256 blocks at 2,048 rows and
+// N = 1024), bit-identical to gemm_large_m's full-K form. 8 waves of 32 x 32 (wave (wm, wn):
 // row tiles 2 wm, 2 wm + 1; kEStore: column tiles 2 wn, 2 wn + 1; kESiluMul: gate tile wn and
 // the matching up tile, so the SwiGLU is lane-local); stages of two MFMA steps (24 KiB: 4 row
 // tiles and 8 column tiles x 2 steps x 1 KiB), a six-stage ring, DMA four stages ahead, the next
@@ -885,15 +915,27 @@ __global__ void __launch_bounds__(512) gemm_wide64(GemmArgs a) {
     const int wm = wv >> 2, wn = wv & 3;
     const int mb = (a.M + 63) / 64;
     const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
-    const int nblk = (idx / mb) * 8 + xcd, rb = idx % mb;
     const int ntiles = a.N / 16, mtiles = (a.M + 15) / 16;
     const int half = a.N / 32;
+    // column blocks by XCD (a weight slab stays in one XCD's L2); kEPartial (N = 1024: 8 column
+    // blocks) row blocks by XCD instead, so an XCD fetches its quarter of the long A rows
+    // once, not all of A
+    const int ncb = (ntiles + 7) / 8;
+#ifdef Q35_COLMAP
+    const int nblk = EM == kEPartial ? (idx % ncb + 8 * 0) * 0 + (idx / ((mb + 7) / 8 * 8)) * 8 + xcd : (idx / mb) * 8 + xcd;
+    const int rb = EM == kEPartial ? idx % ((mb + 7) / 8 * 8) : idx % mb;
+#else
+    const int nblk = EM == kEPartial ? idx % ncb : (idx / mb) * 8 + xcd;
+    const int rb = EM == kEPartial ? (idx / ncb) * 8 + xcd : idx % mb;
+#endif
+    if (EM == kEPartial && rb >= mb) return;
     if (EM == kESiluMul ? nblk * 4 >= half : nblk * 8 >= ntiles) return;
     auto col_tile = [&](int c) {
         if (EM == kESiluMul) return c < 4 ? nblk * 4 + c : half + nblk * 4 + (c - 4);
         return nblk * 8 + c;
     };
     const int tr0 = rb * 4;
+    const int KB = a.K >> 8, NS = 4 * KB;                             // k-blocks, stages
     // DMA pieces of a stage: 8 A pieces (row tile pc / 2, step pc % 2), 16 W pieces (column tile
     // (pc - 8) / 2, step pc % 2); wave wv issues pieces 3 wv .. 3 wv + 2
     const char* pbase[3];
@@ -903,10 +945,10 @@ __global__ void __launch_bounds__(512) gemm_wide64(GemmArgs a) {
         const int pc = 3 * wv + i;
         if (pc < 8) {
             const int t = min(tr0 + (pc >> 1), mtiles - 1);
-            pbase[i] = (const char*)((const uint16_t*)a.X + ((size_t)t * 4 * 8 + (pc & 1)) * 512);
+            pbase[i] = (const char*)((const uint16_t*)a.X + ((size_t)t * KB * 8 + (pc & 1)) * 512);
         } else {
             const int nt = min(col_tile((pc - 8) >> 1), ntiles - 1);
-            pbase[i] = (const char*)(a.W + ((size_t)nt * 4 * 8 + (pc & 1)) * 512);
+            pbase[i] = (const char*)(a.W + ((size_t)nt * KB * 8 + (pc & 1)) * 512);
         }
         ploff[i] = (unsigned)pc * 1024u;
     }
@@ -936,22 +978,22 @@ __global__ void __launch_bounds__(512) gemm_wide64(GemmArgs a) {
     for (int j = 0; j < kWideRing - 1; ++j) issue(j);
     asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");      // stage 0 landed
     rd(0, fa[0], fb[0]);
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-        const int j = kb * 4 + jj, cur = jj & 1;
+        const int j = kb * 4 + jj, cur = jj & 1, left = NS - 2 - j;    // stages issued after j + 1
         // stage j + 1 landed for every wave (stages j + 2 .. j + 4 may be in flight; none is
-        // issued past stage 15); the vector-memory waits name no registers (see gemm_wide)
-        if (kb < 3) asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
-        else if (jj == 0) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");  // j = 12: stages 14, 15
-        else if (jj == 1) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");  // j = 13: stage 15
+        // issued past the last stage); the vector-memory waits name no registers (see gemm_wide)
+        if (left >= 3) asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
+        else if (left == 2) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        else if (left == 1) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier"
                      : "+v"(fa[cur][0][0]), "+v"(fa[cur][0][1]), "+v"(fa[cur][1][0]), "+v"(fa[cur][1][1]),
                        "+v"(fb[cur][0][0]), "+v"(fb[cur][0][1]), "+v"(fb[cur][1][0]), "+v"(fb[cur][1][1])
                      :: "memory");
-        if (kb < 2 || (kb == 2 && jj < 3)) issue(j + kWideRing - 1);   // stages 5 .. 15
-        if (j + 1 < 16) rd(j + 1, fa[cur ^ 1], fb[cur ^ 1]);
+        if (j + kWideRing - 1 < NS) issue(j + kWideRing - 1);          // stages 5 .. NS - 1
+        if (j + 1 < NS) rd(j + 1, fa[cur ^ 1], fb[cur ^ 1]);
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -971,6 +1013,16 @@ __global__ void __launch_bounds__(512) gemm_wide64(GemmArgs a) {
         }
     }
     const int row0 = (tr0 + wm * 2) * 16;
+    if (EM == kEPartial) {             // full K: the summed chains as chain 0
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int jn = 0; jn < 2; ++jn) {
+                const int nt = nblk * 8 + wn * 2 + jn;
+                if (nt < ntiles) epilogue<kEPartial>(a, sum[i][jn], nt, row0 + i * 16, lane, 0);
+            }
+        return;
+    }
     __syncthreads();                   // the ring is drained by every wave: wave-private staging
     uint16_t* wl = (uint16_t*)dyn_lds;
     if (EM == kESiluMul) {
@@ -1305,12 +1357,18 @@ __global__ void __launch_bounds__(1024) argmax_rows(const float* pv, const int* 
 // kEPartial GEMMs with at least forms.partial_rows rows sum all k-block chains in the block
 // (one chain left for the add+norm) instead of one block per chain
 int gemm_partial_chains(int M, int K, const KernelForms& f) { return M > 16 && M >= f.partial_rows ? 1 : K / 256; }
+bool wide_fullk(const KernelForms& f, int M) { return f.gemm_wide && M >= 512 && M >= f.partial_rows; }
 
 // many rows, A in the tiled layout: K = 1024, stored or SwiGLU outputs only
 static hipError_t launch_wide(const GemmArgs& a, int em, hipStream_t st) {
+    if (em == kEPartial) {             // full K into chain 0 (64 x 128 blocks)
+        if (a.M < a.forms.partial_rows || a.M <= 16 || a.K % 512 || !a.kpart || a.N % 16) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(gemm_wide64<kEPartial>, dim3(((a.N / 16 + 7) / 8) * (((a.M + 63) / 64 + 7) / 8 * 8)), dim3(512), kWideLds, st, a);
+        return hipGetLastError();
+    }
     if (a.K != kHidden || a.M <= 16 || (em != kEStore && em != kESiluMul) || !a.Y || (em == kESiluMul && a.N % 32) ||
-        a.ldy % 8 || ((uintptr_t)a.Y & 15))         // 16-byte row pieces in the epilogue
-        return hipErrorInvalidValue;
+        a.ldy % 8 || ((uintptr_t)a.Y & 15) || (a.y_tiled && (em != kESiluMul || a.M < 512 || a.ldy % 256)))
+        return hipErrorInvalidValue;        // 16-byte row pieces in the epilogue
     const int nb = em == kESiluMul ? (a.N / 32 + 3) / 4 : (a.N / 16 + 7) / 8;
     if (a.M < 512) {                   // batched lanes: 64-row blocks
         const int mb = (a.M + 63) / 64;
@@ -1410,11 +1468,20 @@ static hipError_t launch_am_em(const GemmArgs& a, hipStream_t st) {
         return launch_wide(a, EM, st);
     }
     if (AM != kAPlain) {
-        // produce A once into a.prod (bf16 [M][K]), then the plain batched GEMM
+        // produce A once into a.prod (bf16 [M][K]), then the plain batched GEMM (the many-row
+        // full-K residual projection: A produced in the tiled layout)
         if (!a.prod) return hipErrorInvalidValue;
         GemmArgs p = a;
         p.Y = a.prod;
         p.ldy = a.K;
+        if (EM == kEPartial && wide_fullk(a.forms, a.M) && a.K % 512 == 0) {
+            hipLaunchKernelGGL((produce_tiled_kernel<AM>), dim3((a.M + 15) / 16, a.K / 128), dim3(256), 0, st, p);
+            GemmArgs g = a;
+            g.X = a.prod;
+            g.ldx = a.K;
+            g.x_tiled = 1;
+            return launch_wide(g, kEPartial, st);
+        }
         hipLaunchKernelGGL((produce_kernel<AM>), dim3(a.M), dim3(256), 0, st, p);
         GemmArgs g = a;
         g.X = a.prod;
@@ -1444,7 +1511,8 @@ hipError_t gemm_init() {
         hipFuncSetAttribute((const void*)gemm_wide<kEStore>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess ||
         hipFuncSetAttribute((const void*)gemm_wide<kESiluMul>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess ||
         hipFuncSetAttribute((const void*)gemm_wide64<kEStore>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess ||
-        hipFuncSetAttribute((const void*)gemm_wide64<kESiluMul>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess)
+        hipFuncSetAttribute((const void*)gemm_wide64<kESiluMul>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess ||
+        hipFuncSetAttribute((const void*)gemm_wide64<kEPartial>, hipFuncAttributeMaxDynamicSharedMemorySize, kWideLds) != hipSuccess)
         return hipGetLastError();
     return hipSuccess;
 }

@@ -54,6 +54,8 @@ struct GemmArgs {
     int kpb;               // kANormXP: k-block chains of the producing GEMM pending in kpart
     int x_tiled;           // X in the weights' tiled fragment layout (tiled_offset, rows as n): the
                            // many-row K = 1024 GEMM (gemm_wide); M rows padded to whole 16-row tiles
+    int y_tiled;           // gemm_wide's SwiGLU epilogue: Y in that tiled layout (K = ldy) for a
+                           // consumer that reads it as x_tiled (the many-row full-K down projection)
     KernelForms forms;
 };
 // One-time kernel attribute setup (dynamic LDS above 64 KiB for the batch-1 producers).
@@ -61,6 +63,8 @@ hipError_t gemm_init();
 // k-block chains a batched kEPartial GEMM leaves in kpart
 int gemm_partial_chains(int M, int K, const KernelForms& f);
 hipError_t launch_gemm(const GemmArgs& a, int amode, int emode, hipStream_t st);
+// the many-row full-K residual projection (gemm_wide64<kEPartial>, A tiled) takes an M-row GEMM
+bool wide_fullk(const KernelForms& f, int M);
 // kEArgmax: how many (max, index) partials per row the launch for `a` writes (launch_argmax's n)
 int gemm_argmax_partials(const GemmArgs& a);
 // The batched A producer alone: a.prod [M][K] bf16 = the producer's A operand (kASiluMul or
@@ -172,6 +176,7 @@ struct AttnArgs {
     float* part;           // scratch [R][2 * max_chunks][8][256] (128-slot parts)
     int max_chunks;
     uint16_t* out;         // [R][2048] gated attention output (input of o_proj)
+    int out_tiled;         // attn_prompt only: out in the GEMMs' tiled fragment layout (K = 2048)
     int R;
     int T;                 // rows per lane (a lane's rows are consecutive; MTP verify: k + 1)
     const float* inv_freq; // [32] f32 rope inverse frequencies
@@ -187,6 +192,7 @@ enum AttnForce { kAttnAuto = 0, kAttnSplit = 1, kAttnSplit4 = 2, kAttnFused = 3,
 hipError_t launch_attn_prep(const AttnArgs& a, hipStream_t st);   // q/k norm + rope, cache append
 hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st);   // scores, softmax, P.V, gate
 bool attn_form_ok(const AttnArgs& a);     // the forced form (AttnArgs::force) can run this shape
+bool attn_prompt_form(const AttnArgs& a); // launch_attn_core runs attn_prompt (honours out_tiled)
 hipError_t attn_init();   // one-time kernel attribute setup
 
 // Synthetic init (portable stream, see q35_init.hip).

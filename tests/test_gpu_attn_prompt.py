@@ -100,6 +100,19 @@ def test_prompt_attention_vs_float64(eng, pre, n):
         assert (d <= 2 * ulp + REL_W * mag).all() and d.mean() <= MEAN_D, (mode, d.max(), d.mean())
 
 
+def _untile(buf, rows, K):
+    """Rows [rows][K] of a buffer in the GEMMs' tiled fragment layout (16-row tiles; within a
+    tile and 256-wide k-block, step s = (k % 256) / 8 % 8, lane = 16 (k % 256 / 64) + row % 16,
+    8 consecutive k per lane): the layout a prompt wave of >= 1,024 rows leaves its attention
+    output in for the many-row o_proj."""
+    r = np.arange(rows)[:, None]
+    k = np.arange(K)[None, :]
+    kk = k & 255
+    lane = (kk >> 6) * 16 + (r & 15)
+    off = ((((r >> 4) * (K >> 8) + (k >> 8)) * 8 + ((kk >> 3) & 7)) * 64 + lane) * 8 + (kk & 7)
+    return buf.reshape(-1)[off]
+
+
 def test_prompt_attention_long_context_sampled_rows():
     """A 2,048-row wave after a 2,000-slot prefix (contexts up to 4,048 slots: 64 K/V tiles,
     the online softmax rescaling across many tiles), checked on 48 sampled rows (every head)
@@ -113,7 +126,8 @@ def test_prompt_attention_long_context_sampled_rows():
         st.prefill(0, lane_prompt_ids(9, 0, pre))
         st.prefill(0, lane_prompt_ids(9, 1, n))
         q = eng.read_scratch("q", (n, 8, 256), np.float32)
-        aout = _u16f(eng.read_scratch("aout", (n, 2048), np.uint16)).reshape(n, 8, 256)
+        # the 2,048-row wave's o_proj runs in the many-row full-K form: aout is tiled
+        aout = _u16f(_untile(eng.read_scratch("aout", (n, 2048), np.uint16), n, 2048)).reshape(n, 8, 256)
         proj = eng.read_scratch("proj", (n, 5120), np.uint16)
         K = _u16f(st.read(0, "k", pre + n)[5])
         V = _u16f(st.read(0, "v", pre + n)[5])
