@@ -34,8 +34,10 @@ constexpr int kCWs = 4 * kC * 128 + kC * kC; // workspace floats per (chunk, hea
 // order so that every scan wave reads its operands as contiguous 16-byte vectors
 // (lane = 16 kq + mr, see mfma4):
 //   kcd  [wave 4][lane 64][ks 32]  A[m = 16w + mr][k = 4ks + kq]      (phase 1)
-//   q'   [wave 4][lane 64][ks 32]  A[m = 16w + mr][k = 4ks + kq]      (phase 2)
-//   intra[wave 4][lane 64][ks 16]  A[m = 16w + mr][j = 4ks + kq]      (phase 2)
+//   q'   [wave 4][kb 4][part 2][lane 64] x 8 bf16  A[m = 16w + lane % 16][k = 32kb + 8(lane / 16) + e]
+//   intra[wave 4][kb 2][part 2][lane 64] x 8 bf16  A[m = 16w + lane % 16][j = 32kb + 8(lane / 16) + e]
+//        (phase 2 on v_mfma_f32_16x16x32_bf16: each f32 value as a bf16 hi / lo pair, x = hi +
+//        lo within 2^-18 |x|, and each product as hi.hi + hi.lo + lo.hi)
 //   k'^T [wave 4][half 2][lane 64][ks 16]  A[m = 32w + 16half + mr][i = 4ks + kq] = k'[i][m]  (phase 3)
 //   nv   [slice 8][wave 4][lane 64][r 4]   nv[16w + 4kq + r][16 slice + mr]   (phase 1, C layout)
 constexpr int kWsKcd = 0, kWsQ = 8192, kWsIntra = 16384, kWsK = 20480, kWsNv = 28672;
@@ -44,6 +46,20 @@ constexpr int kWsKcd = 0, kWsQ = 8192, kWsIntra = 16384, kWsK = 20480, kWsNv = 2
 // D[4 (l/16) + r][l%16], r = 0..3.
 __device__ __forceinline__ q35_f32x4 mfma4(float av, float bv, q35_f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, c, 0, 0, 0);
+}
+
+// 8 f32 values as bf16: part 0 the rounded values (hi), part 1 the rounded remainders x - hi (lo)
+__device__ __forceinline__ q35_u32x4 bf16_part8(const float (&x)[8], int part) {
+    q35_u32x4 r;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t hi = f2bf2(x[2 * w], x[2 * w + 1]);
+        r[w] = part ? f2bf2(x[2 * w] - __uint_as_float(hi << 16), x[2 * w + 1] - __uint_as_float(hi & 0xffff0000u)) : hi;
+    }
+    return r;
+}
+__device__ __forceinline__ q35_f32x4 mfma_bf16(q35_u32x4 av, q35_u32x4 bv, q35_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(q35_bf16x8*)&av, *(q35_bf16x8*)&bv, c, 0, 0, 0);
 }
 
 constexpr int kConvRows = 16;
@@ -90,7 +106,7 @@ __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
     const int nrow = min(kC, a.T - t0);
 
     __shared__ float qn[kC][129], kn[kC][129], vv[kC][129];
-    __shared__ float ut[kC][kC + 1];
+    __shared__ float ut[kC][kC + 1], intra_s[kC][kC + 1];
     __shared__ float gl[kC], bl[kC], cum[kC], ecum[kC];
 
     // ---- post-conv SiLU values (gdn_chunk_conv) of the head's q, k and v channels as 16-byte
@@ -173,8 +189,7 @@ __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
                 const int i = wv * 16 + 4 * kq + r, j = nt * 16 + mr;
                 const float pair = j <= i ? expf(cum[i] - cum[j]) : 0.f;
                 ut[i][j] = j < i ? (au[r] * bl[i]) * pair : 0.f;     // (beta_i k~_i) . k~_j, decayed
-                // intra in the scan's operand order: [w][lane (j % 4, i % 16)][j / 4]
-                ws[kWsIntra + ((wv * 64 + (j & 3) * 16 + (i & 15)) * 16 + (j >> 2))] = ai[r] * pair;
+                intra_s[i][j] = ai[r] * pair;
             }
         }
         for (int nt = wv + 1; nt < 4; ++nt)       // upper tiles: zero
@@ -182,7 +197,7 @@ __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
             for (int r = 0; r < 4; ++r) {
                 const int i = wv * 16 + 4 * kq + r, j = nt * 16 + mr;
                 ut[i][j] = 0.f;
-                ws[kWsIntra + ((wv * 64 + (j & 3) * 16 + (i & 15)) * 16 + (j >> 2))] = 0.f;
+                intra_s[i][j] = 0.f;
             }
     }
     __syncthreads();
@@ -195,15 +210,14 @@ __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int u = tid + 256 * k;
-            // q': A[m = i][k = d] -> [i / 16][lane (d % 4, i % 16)][d / 4]; vector u = (lane slot, d/4 quad)
+            // q' = q~ e^cum as bf16 hi / lo: vector u = (w, kb, part, lane)
             {
-                const int q = u & 7, ln = (u >> 3) & 63, i = (u >> 9) * 16 + (ln & 15), dq = ln >> 4;
-                float4 v;
-                v.x = qn[i][16 * q + dq] * ecum[i];
-                v.y = qn[i][16 * q + 4 + dq] * ecum[i];
-                v.z = qn[i][16 * q + 8 + dq] * ecum[i];
-                v.w = qn[i][16 * q + 12 + dq] * ecum[i];
-                *(float4*)&ws[kWsQ + 4 * u] = v;
+                const int ln = u & 63, part = (u >> 6) & 1, kb = (u >> 7) & 3, w = u >> 9;
+                const int i = 16 * w + (ln & 15), k0 = 32 * kb + 8 * (ln >> 4);
+                float x[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = qn[i][k0 + e] * ecum[i];
+                *(q35_u32x4*)((uint16_t*)(ws + kWsQ) + 8 * u) = bf16_part8(x, part);
             }
             // k'^T: A[m = d][kk = i] -> [d / 16][lane (i % 4, d % 16)][i / 4]; vector u = (lane slot, i/4 quad)
             {
@@ -216,6 +230,17 @@ __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
                 v.w = kn[i0 + 12][d] * ut[i0 + 12][kC];
                 *(float4*)&ws[kWsK + 4 * u] = v;
             }
+        }
+        // intra as bf16 hi / lo: vector u = (w, kb, part, lane)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int u = tid + 256 * k;
+            const int ln = u & 63, part = (u >> 6) & 1, kb = (u >> 7) & 1, w = u >> 8;
+            const int i = 16 * w + (ln & 15), j0 = 32 * kb + 8 * (ln >> 4);
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = intra_s[i][j0 + e];
+            *(q35_u32x4*)((uint16_t*)(ws + kWsIntra) + 8 * u) = bf16_part8(x, part);
         }
         if (tid == 0) a.chunk_cdec[c * kHv + h] = expf(cum[kC - 1]);
     }
@@ -305,20 +330,20 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
     // this wave's A operands of one chunk, in registers: kcd and q' rows 16w + mr (k = 4ks + kq),
     // intra row 16w + mr (j = 4ks + kq), k'^T rows 32w + 16 half + mr (i = 4ks + kq), and nv
     // (16-byte vectors loaded straight into the set: no copy waits for the data before its use)
-    struct Ops { q35_f32x4 kcd[8], qp[8], in[4], kp[2][4], nv; float cd; };
+    struct Ops { q35_f32x4 kcd[8]; q35_u32x4 qp[8], in[4]; q35_f32x4 kp[2][4], nv; float cd; };
     auto load_ops = [&](int c, Ops& o) {
         const float* ws = a.chunk_ws + ((size_t)c * kHv + h) * kCWs;
         o.cd = a.chunk_cdec[c * kHv + h];
         const q35_f32x4* pk = (const q35_f32x4*)(ws + kWsKcd + (wv * 64 + ln) * 32);
-        const q35_f32x4* pq = (const q35_f32x4*)(ws + kWsQ + (wv * 64 + ln) * 32);
-        const q35_f32x4* pi = (const q35_f32x4*)(ws + kWsIntra + (wv * 64 + ln) * 16);
+        const q35_u32x4* pq = (const q35_u32x4*)(ws + kWsQ) + wv * 512 + ln;        // [kb][part] x 64 lanes
+        const q35_u32x4* pi = (const q35_u32x4*)(ws + kWsIntra) + wv * 256 + ln;
         const q35_f32x4* pp0 = (const q35_f32x4*)(ws + kWsK + ((wv * 2 + 0) * 64 + ln) * 16);
         const q35_f32x4* pp1 = (const q35_f32x4*)(ws + kWsK + ((wv * 2 + 1) * 64 + ln) * 16);
         o.nv = *(const q35_f32x4*)(ws + kWsNv + ((blockIdx.y * 4 + wv) * 64 + ln) * 4);
 #pragma unroll
-        for (int v = 0; v < 8; ++v) { o.kcd[v] = pk[v]; o.qp[v] = pq[v]; }
+        for (int v = 0; v < 8; ++v) { o.kcd[v] = pk[v]; o.qp[v] = pq[64 * v]; }
 #pragma unroll
-        for (int v = 0; v < 4; ++v) { o.in[v] = pi[v]; o.kp[0][v] = pp0[v]; o.kp[1][v] = pp1[v]; }
+        for (int v = 0; v < 4; ++v) { o.in[v] = pi[64 * v]; o.kp[0][v] = pp0[v]; o.kp[1][v] = pp1[v]; }
     };
     // a ring of three operand sets: chunk c's loads are issued two chunks ahead (one chunk of
     // compute does not cover the workspace's load latency); the ring index is static (the
@@ -336,6 +361,17 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
         float sf[32];
 #pragma unroll
         for (int ks = 0; ks < 32; ++ks) sf[ks] = S[ks * 4 + kq][mr];
+        // phase 2's B fragments of S (16x16x32 layout: k = 32 kb + 8 kq + e, column mr), as bf16
+        // hi / lo pairs, read before the barrier (phase 3 rewrites S)
+        q35_u32x4 sb[4][2];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = S[32 * kb + 8 * kq + e][mr];
+            sb[kb][0] = bf16_part8(x, 0);
+            sb[kb][1] = bf16_part8(x, 1);
+        }
         // phase 1: v_new = nv - kcd S   (wave w: rows 16w .. 16w+15)
         {
             q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -350,11 +386,28 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
         for (int ks = 0; ks < 16; ++ks) vf[ks] = vn[ks * 4 + kq][mr];
         // phase 2: o = q' S + intra v_new
         {
+            q35_u32x4 vb[2][2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                float x[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = vn[32 * kb + 8 * kq + e][mr];
+                vb[kb][0] = bf16_part8(x, 0);
+                vb[kb][1] = bf16_part8(x, 1);
+            }
             q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 32; ++ks) acc = mfma4(cur_ops.qp[ks >> 2][ks & 3], sf[ks], acc);
+            for (int kb = 0; kb < 4; ++kb) {
+                acc = mfma_bf16(cur_ops.qp[2 * kb], sb[kb][0], acc);
+                acc = mfma_bf16(cur_ops.qp[2 * kb], sb[kb][1], acc);
+                acc = mfma_bf16(cur_ops.qp[2 * kb + 1], sb[kb][0], acc);
+            }
 #pragma unroll
-            for (int ks = 0; ks < 16; ++ks) acc = mfma4(cur_ops.in[ks >> 2][ks & 3], vf[ks], acc);
+            for (int kb = 0; kb < 2; ++kb) {
+                acc = mfma_bf16(cur_ops.in[2 * kb], vb[kb][0], acc);
+                acc = mfma_bf16(cur_ops.in[2 * kb], vb[kb][1], acc);
+                acc = mfma_bf16(cur_ops.in[2 * kb + 1], vb[kb][0], acc);
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = wv * 16 + 4 * kq + r;
