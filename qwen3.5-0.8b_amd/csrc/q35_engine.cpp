@@ -722,6 +722,10 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt, int defe
             const bool chunked = e->gdn_chunked && !small && nl == 1 && T >= 64 && !ckpt;
             const bool fused_norm = !small && cs == 1 && !chunked;   // whole-head blocks: norm in the GDN kernel
             if (fused_norm) { g.y = e->prod; g.gnorm = w.gnorm; }
+            // the chunked form's output kernel applies the gated norm too (tiled for the many-row
+            // full-K out_proj)
+            const bool tiled = chunked && wide_fullk(e->forms, R);
+            if (chunked) { g.y = e->prod; g.gnorm = w.gnorm; g.y_tiled = tiled ? 1 : 0; }
             g.chunk_ws = e->gchunk; g.chunk_cdec = e->gcdec; g.conv_u = e->gu;   // gu is free until the MLP
             {
                 KTimer kt(e, kFamGdn);
@@ -733,6 +737,8 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt, int defe
             }
             if (fused_norm)
                 gemm(e, w.W_out, kHidden, 2048, R, e->prod, 2048, nullptr, 0);
+            else if (chunked)
+                resid_gemm(e, rr, w.W_out, 2048, R, e->prod, 2048, kAPlain, nullptr, 0, nullptr, tiled);
             else
                 resid_gemm(e, rr, w.W_out, 2048, R, e->o, 2048, kAGatedNorm, e->proj + kGdnZOff, kGdnInRows, w.gnorm);
         } else {

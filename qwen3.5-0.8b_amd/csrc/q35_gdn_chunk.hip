@@ -1,6 +1,6 @@
 // GatedDeltaNet over a prompt wave of one lane in the chunked (UT-transform) form, chunk 64
 // (speccheck/specimpl.py:187-235; the reference engine's gdn_chunk_prefill,
-// engine/kernels_gdn.cpp:488). Three kernels:
+// engine/kernels_gdn.cpp:488). Four kernels:
 //
 //   gdn_chunk_conv  grid (16-row run, 256 channels): causal conv + bf16 SiLU of every (row,
 //                   channel) of the wave with the recurrent kernel's arithmetic -> conv_u, and
@@ -14,9 +14,15 @@
 //                   Rows past the wave are zero with g = beta = 0, as the reference pads.
 //   gdn_chunk_scan  grid (head, 16-column slice): the chunk recurrence, sequential over chunks
 //                   with the slice S[:, n0 .. n0+16) of the f32 state in LDS:
-//                     v_new = nv - kcd S;  o = q' S + intra v_new;  S = e^cum_63 S + k'^T v_new
+//                     v_new = nv - kcd S;  S = e^cum_63 S + k'^T v_new
 //                   on v_mfma_f32_16x16x4_f32 (f32 products, f32 accumulate). The value columns
-//                   of the delta rule never mix, so 8 slices per head run independently.
+//                   of the delta rule never mix, so 8 slices per head run independently. Each
+//                   chunk's S (before its update) and v_new go to the workspace as bf16 hi / lo
+//                   MFMA fragments for
+//   gdn_chunk_out   grid (chunk, head): o = q' S + intra v_new of every chunk at once (off the
+//                   recurrence's sequential path) on v_mfma_f32_16x16x32_bf16, each operand a
+//                   bf16 hi / lo pair (x = hi + lo within 2^-18 |x|) and each product hi.hi +
+//                   hi.lo + lo.hi, f32 accumulate.
 //
 // The state is read from slot cur and written to slot (cur + 1) % nslots (no rows pending:
 // the engine applies them first), the conv window, from slot wcur to (wcur + 1) % nslots,
@@ -29,18 +35,21 @@
 namespace q35 {
 
 constexpr int kC = 64;                      // chunk rows
-constexpr int kCWs = 4 * kC * 128 + kC * kC; // workspace floats per (chunk, head)
+constexpr int kCWs = 4 * kC * 128 + kC * kC + 8 * 3072;   // workspace floats per (chunk, head)
 // Workspace per (chunk, head), written by the prep kernel directly in the scan's MFMA operand
 // order so that every scan wave reads its operands as contiguous 16-byte vectors
 // (lane = 16 kq + mr, see mfma4):
 //   kcd  [wave 4][lane 64][ks 32]  A[m = 16w + mr][k = 4ks + kq]      (phase 1)
 //   q'   [wave 4][kb 4][part 2][lane 64] x 8 bf16  A[m = 16w + lane % 16][k = 32kb + 8(lane / 16) + e]
 //   intra[wave 4][kb 2][part 2][lane 64] x 8 bf16  A[m = 16w + lane % 16][j = 32kb + 8(lane / 16) + e]
-//        (phase 2 on v_mfma_f32_16x16x32_bf16: each f32 value as a bf16 hi / lo pair, x = hi +
-//        lo within 2^-18 |x|, and each product as hi.hi + hi.lo + lo.hi)
+//        (gdn_chunk_out: part 0 = bf16(x), part 1 = bf16(x - part 0))
 //   k'^T [wave 4][half 2][lane 64][ks 16]  A[m = 32w + 16half + mr][i = 4ks + kq] = k'[i][m]  (phase 3)
 //   nv   [slice 8][wave 4][lane 64][r 4]   nv[16w + 4kq + r][16 slice + mr]   (phase 1, C layout)
-constexpr int kWsKcd = 0, kWsQ = 8192, kWsIntra = 16384, kWsK = 20480, kWsNv = 28672;
+//   Sb   [slice 8][kb 4][part 2][lane 64] x 8 bf16  S[32kb + 8(lane / 16) + e][16 slice + lane % 16]
+//        (the chunk's state before its update; written by the scan)
+//   Vb   [slice 8][kb 2][part 2][lane 64] x 8 bf16  v_new[32kb + 8(lane / 16) + e][16 slice + lane % 16]
+constexpr int kWsKcd = 0, kWsQ = 8192, kWsIntra = 16384, kWsK = 20480, kWsNv = 28672, kWsSb = 36864,
+              kWsVb = 53248;
 
 // MFMA f32 16x16x4: lane l supplies A[l%16][l/16] and B[l/16][l%16] and holds
 // D[4 (l/16) + r][l%16], r = 0..3.
@@ -327,23 +336,21 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
     __syncthreads();
 
     const int mr = ln & 15, kq = ln >> 4;          // A row / k-quad of this lane
-    // this wave's A operands of one chunk, in registers: kcd and q' rows 16w + mr (k = 4ks + kq),
-    // intra row 16w + mr (j = 4ks + kq), k'^T rows 32w + 16 half + mr (i = 4ks + kq), and nv
-    // (16-byte vectors loaded straight into the set: no copy waits for the data before its use)
-    struct Ops { q35_f32x4 kcd[8]; q35_u32x4 qp[8], in[4]; q35_f32x4 kp[2][4], nv; float cd; };
+    // this wave's A operands of one chunk, in registers: kcd rows 16w + mr (k = 4ks + kq), k'^T
+    // rows 32w + 16 half + mr (i = 4ks + kq), and nv (16-byte vectors loaded straight into the
+    // set: no copy waits for the data before its use)
+    struct Ops { q35_f32x4 kcd[8], kp[2][4], nv; float cd; };
     auto load_ops = [&](int c, Ops& o) {
         const float* ws = a.chunk_ws + ((size_t)c * kHv + h) * kCWs;
         o.cd = a.chunk_cdec[c * kHv + h];
         const q35_f32x4* pk = (const q35_f32x4*)(ws + kWsKcd + (wv * 64 + ln) * 32);
-        const q35_u32x4* pq = (const q35_u32x4*)(ws + kWsQ) + wv * 512 + ln;        // [kb][part] x 64 lanes
-        const q35_u32x4* pi = (const q35_u32x4*)(ws + kWsIntra) + wv * 256 + ln;
         const q35_f32x4* pp0 = (const q35_f32x4*)(ws + kWsK + ((wv * 2 + 0) * 64 + ln) * 16);
         const q35_f32x4* pp1 = (const q35_f32x4*)(ws + kWsK + ((wv * 2 + 1) * 64 + ln) * 16);
         o.nv = *(const q35_f32x4*)(ws + kWsNv + ((blockIdx.y * 4 + wv) * 64 + ln) * 4);
 #pragma unroll
-        for (int v = 0; v < 8; ++v) { o.kcd[v] = pk[v]; o.qp[v] = pq[64 * v]; }
+        for (int v = 0; v < 8; ++v) o.kcd[v] = pk[v];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) { o.in[v] = pi[64 * v]; o.kp[0][v] = pp0[v]; o.kp[1][v] = pp1[v]; }
+        for (int v = 0; v < 4; ++v) { o.kp[0][v] = pp0[v]; o.kp[1][v] = pp1[v]; }
     };
     // a ring of three operand sets: chunk c's loads are issued two chunks ahead (one chunk of
     // compute does not cover the workspace's load latency); the ring index is static (the
@@ -354,23 +361,21 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
     auto step = [&](int c, auto par) {
         constexpr int P = decltype(par)::value;
         Ops& cur_ops = ops[P];
-        const int t0 = c * kC;
         // operands two chunks ahead (unconditional, clamped: no branch splits the wait counts)
         load_ops(min(c + 2, nchunks - 1), ops[(P + 2) % 3]);
-        // B fragments of S, shared by phases 1 and 2 (all waves read S before the barrier)
+        // B fragments of S for phase 1 (all waves read S before the barrier)
         float sf[32];
 #pragma unroll
         for (int ks = 0; ks < 32; ++ks) sf[ks] = S[ks * 4 + kq][mr];
-        // phase 2's B fragments of S (16x16x32 layout: k = 32 kb + 8 kq + e, column mr), as bf16
-        // hi / lo pairs, read before the barrier (phase 3 rewrites S)
-        q35_u32x4 sb[4][2];
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
+        // this chunk's S as gdn_chunk_out's B fragments (16x16x32 layout: k = 32 kb + 8 kq + e,
+        // column mr; wave w writes k-block w), bf16 hi / lo pairs
+        q35_u32x4* wsc = (q35_u32x4*)(a.chunk_ws + ((size_t)c * kHv + h) * kCWs);
+        {
             float x[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] = S[32 * kb + 8 * kq + e][mr];
-            sb[kb][0] = bf16_part8(x, 0);
-            sb[kb][1] = bf16_part8(x, 1);
+            for (int e = 0; e < 8; ++e) x[e] = S[32 * wv + 8 * kq + e][mr];
+            wsc[kWsSb / 4 + ((blockIdx.y * 4 + wv) * 2 + 0) * 64 + ln] = bf16_part8(x, 0);
+            wsc[kWsSb / 4 + ((blockIdx.y * 4 + wv) * 2 + 1) * 64 + ln] = bf16_part8(x, 1);
         }
         // phase 1: v_new = nv - kcd S   (wave w: rows 16w .. 16w+15)
         {
@@ -381,38 +386,16 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
             for (int r = 0; r < 4; ++r) vn[wv * 16 + 4 * kq + r][mr] = cur_ops.nv[r] - acc[r];
         }
         __syncthreads();
-        float vf[16];       // B fragments of v_new, shared by phases 2 and 3
+        float vf[16];       // B fragments of v_new for phase 3
 #pragma unroll
         for (int ks = 0; ks < 16; ++ks) vf[ks] = vn[ks * 4 + kq][mr];
-        // phase 2: o = q' S + intra v_new
-        {
-            q35_u32x4 vb[2][2];
+        // v_new as gdn_chunk_out's B fragments (waves 0, 1: k-block w), bf16 hi / lo pairs
+        if (wv < 2) {
+            float x[8];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                float x[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] = vn[32 * kb + 8 * kq + e][mr];
-                vb[kb][0] = bf16_part8(x, 0);
-                vb[kb][1] = bf16_part8(x, 1);
-            }
-            q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                acc = mfma_bf16(cur_ops.qp[2 * kb], sb[kb][0], acc);
-                acc = mfma_bf16(cur_ops.qp[2 * kb], sb[kb][1], acc);
-                acc = mfma_bf16(cur_ops.qp[2 * kb + 1], sb[kb][0], acc);
-            }
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                acc = mfma_bf16(cur_ops.in[2 * kb], vb[kb][0], acc);
-                acc = mfma_bf16(cur_ops.in[2 * kb], vb[kb][1], acc);
-                acc = mfma_bf16(cur_ops.in[2 * kb + 1], vb[kb][0], acc);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = wv * 16 + 4 * kq + r;
-                if (t0 + row < a.T) a.o[(size_t)(t0 + row) * 2048 + h * 128 + n0 + mr] = acc[r];
-            }
+            for (int e = 0; e < 8; ++e) x[e] = vn[32 * wv + 8 * kq + e][mr];
+            wsc[kWsVb / 4 + ((blockIdx.y * 2 + wv) * 2 + 0) * 64 + ln] = bf16_part8(x, 0);
+            wsc[kWsVb / 4 + ((blockIdx.y * 2 + wv) * 2 + 1) * 64 + ln] = bf16_part8(x, 1);
         }
         // phase 3: S = e^cum_63 S + k'^T v_new   (wave w: its own state rows 32w .. 32w+31;
         // no other wave reads S after the barrier above)
@@ -437,6 +420,86 @@ __global__ void __launch_bounds__(256) gdn_chunk_scan(GdnArgs a, int nchunks) {
     for (int e = tid; e < 128 * 16; e += 256) Sout[(e >> 4) * 128 + n0 + (e & 15)] = S[e >> 4][e & 15];
 }
 
+// o = q' S + intra v_new of chunk blockIdx.x, head blockIdx.y: wave w takes row tile w (rows 16w
+// .. 16w + 15) over the 8 column slices; its A fragments (q' and intra hi / lo) are loaded once,
+// the slices' B fragments one slice ahead. With a.y the block holds the head's whole rows, so it
+// applies the gated RMSNorm itself and stores y (bf16, tiled with a.y_tiled) instead of o.
+__global__ void __launch_bounds__(256) gdn_chunk_out(GdnArgs a) {
+    __shared__ float ot[kC][129];                // with y: the chunk's o of this head
+    __shared__ float ssl[kC][2];                 // and its rows' half-head sums of squares
+    const int c = blockIdx.x, h = blockIdx.y;
+    const int tid = threadIdx.x, ln = tid & 63, wv = tid >> 6, mr = ln & 15, kq = ln >> 4;
+    const q35_u32x4* ws = (const q35_u32x4*)(a.chunk_ws + ((size_t)c * kHv + h) * kCWs);
+    q35_u32x4 aq[8], ai[4];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) aq[v] = ws[kWsQ / 4 + (wv * 8 + v) * 64 + ln];      // [kb][part]
+#pragma unroll
+    for (int v = 0; v < 4; ++v) ai[v] = ws[kWsIntra / 4 + (wv * 4 + v) * 64 + ln];
+    q35_u32x4 sb[2][8], vb[2][4];                // [slice parity][kb][part]
+    auto load_b = [&](int sl, q35_u32x4 (&s8)[8], q35_u32x4 (&v4)[4]) {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) s8[v] = ws[kWsSb / 4 + (sl * 8 + v) * 64 + ln];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) v4[v] = ws[kWsVb / 4 + (sl * 4 + v) * 64 + ln];
+    };
+    load_b(0, sb[0], vb[0]);
+    const int t0 = c * kC;
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) {
+        const int b = sl & 1;
+        if (sl + 1 < 8) load_b(sl + 1, sb[b ^ 1], vb[b ^ 1]);
+        q35_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            acc = mfma_bf16(aq[2 * kb], sb[b][2 * kb], acc);
+            acc = mfma_bf16(aq[2 * kb], sb[b][2 * kb + 1], acc);
+            acc = mfma_bf16(aq[2 * kb + 1], sb[b][2 * kb], acc);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            acc = mfma_bf16(ai[2 * kb], vb[b][2 * kb], acc);
+            acc = mfma_bf16(ai[2 * kb], vb[b][2 * kb + 1], acc);
+            acc = mfma_bf16(ai[2 * kb + 1], vb[b][2 * kb], acc);
+        }
+        if (a.y) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ot[wv * 16 + 4 * kq + r][sl * 16 + mr] = acc[r];
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = wv * 16 + 4 * kq + r;
+                if (t0 + row < a.T) a.o[(size_t)(t0 + row) * 2048 + h * 128 + sl * 16 + mr] = acc[r];
+            }
+        }
+    }
+    if (!a.y) return;
+    // the gated RMSNorm of the out_proj producer (same reduction order and arithmetic): thread
+    // (row, half) sums the half head's 64 squares, then 8-column pieces are gated and stored
+    __syncthreads();
+    if (tid < 128) {
+        float v[64];
+#pragma unroll
+        for (int i = 0; i < 64; ++i) v[i] = ot[tid >> 1][(tid & 1) * 64 + i];
+        ssl[tid >> 1][tid & 1] = half_head_ss_regs(v);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int u = tid + 256 * k;
+        const int row = (u >> 8) * 16 + (u & 15), ch = (u >> 4) & 15;    // the tile's 16 rows adjacent
+        const int m = t0 + row;
+        if (m >= a.T) continue;
+        const float rs = head_rsqrt(ssl[row][0], ssl[row][1]);
+        float ov[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ov[e] = ot[row][ch * 8 + e];
+        const q35_u32x4 zz = *(const q35_u32x4*)(a.proj + (size_t)m * kGdnInRows + kGdnZOff + h * 128 + ch * 8);
+        const q35_u32x4 ww = *(const q35_u32x4*)(a.gnorm + ch * 8);
+        const int col = h * 128 + ch * 8;
+        *(q35_u32x4*)(a.y + (a.y_tiled ? tiled_offset(m, col, 2048) : (size_t)m * 2048 + col)) = gated8(ov, zz, ww, rs);
+    }
+}
+
 hipError_t launch_gdn_chunked(const GdnArgs& a, hipStream_t st) {
     if (a.nlanes != 1 || a.T < 1 || a.ckpt || !a.chunk_ws || !a.chunk_cdec) return hipErrorInvalidValue;
     const int nchunks = (a.T + kC - 1) / kC;
@@ -444,6 +507,7 @@ hipError_t launch_gdn_chunked(const GdnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(gdn_chunk_conv, dim3((a.T + kConvRows - 1) / kConvRows, 6144 / 256), dim3(256), 0, st, a);
     hipLaunchKernelGGL(gdn_chunk_prep, dim3(nchunks, kHv), dim3(256), 0, st, a);
     hipLaunchKernelGGL(gdn_chunk_scan, dim3(kHv, 8), dim3(256), 0, st, a, nchunks);
+    hipLaunchKernelGGL(gdn_chunk_out, dim3(nchunks, kHv), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

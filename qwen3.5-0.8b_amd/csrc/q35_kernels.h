@@ -131,10 +131,11 @@ struct GdnArgs {
     const int* lane;           // [R] state lane of each row
     int T;                     // rows per lane (rows of one lane are consecutive)
     int nlanes;
-    // Optional fused gated RMSNorm (whole-head blocks only, col_slices == 1):
+    // Optional fused gated RMSNorm (whole-head blocks and the chunked form's output kernel):
     // y[r][h*128 + j] = bf16(w[j] * (o * rsqrt(mean_head(o^2) + eps)) * silu(z)), bf16 [R][2048]
     uint16_t* y;
     const uint16_t* gnorm;     // [128]
+    int y_tiled;               // chunked form: y in the GEMMs' tiled fragment layout (K = 2048)
     // Chunked prompt form (one lane, no checkpoints): per-(chunk, head) workspace and decays,
     // and the wave's post-conv SiLU values [T][6144] bf16
     float* chunk_ws;
