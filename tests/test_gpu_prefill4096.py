@@ -97,22 +97,26 @@ def test_prefill_all_rows_equal_token_by_token(max_rows, n):
         e.close()
 
 
-def test_wide_gemm_prompt_waves_bit_identical():
+@pytest.mark.parametrize("max_rows,n", [(1024, 1100), (2048, 1500)])
+def test_wide_gemm_prompt_waves_bit_identical(max_rows, n):
     """Prompt waves of >= 512 rows run their K = 1024 GEMMs (input projections, gate|up) in the
-    many-row kernel on A in the tiled layout (engine option gemm_wide); a 1,100-token prompt in
-    waves of 1,024 and 76 rows gives the same sampled ids, logits and GDN states bit for bit as
-    the 32 x 64 block kernels (prefill_all: every row priced)."""
+    many-row kernel on A in the tiled layout, and waves of >= partial_rows (1,024) rows their
+    residual projections (down, out_proj, o_proj) in the many-row full-K form with A tiled by its
+    producer (engine option gemm_wide); a 1,100-token prompt in waves of 1,024 and 76 rows, and
+    a 1,500-row wave (a ragged last 64-row block and chunk), give the same sampled ids, logits and
+    GDN states bit for bit as the 32 x 64 block kernels (prefill_all: every row priced)."""
     from oracle.weights import lane_prompt_ids
     from qwen35 import Engine, State
-    ids = lane_prompt_ids(88, 0, 1100)
-    e = Engine(max_rows=1024, max_ctx=1200, seed=0)
+    print(f"wide GEMM forms, max_rows {max_rows}, prompt {n}", flush=True)
+    ids = lane_prompt_ids(88, 0, n)
+    e = Engine(max_rows=max_rows, max_ctx=n + 100, seed=0)
     try:
         res = []
         for wide in (1, 0):
             e.set_option("gemm_wide", wide)
-            st = State(e, 1, 1152)
+            st = State(e, 1, n + 52)
             samp, top = st.prefill_all(0, ids)
-            res.append((samp, top, st.read(0, "S"), st.read(0, "k", 1100), st.read(0, "v", 1100)))
+            res.append((samp, top, st.read(0, "S"), st.read(0, "k", n), st.read(0, "v", n)))
             st.close()
         for x, y in zip(*res):
             assert np.array_equal(x, y)
