@@ -26,13 +26,16 @@
 namespace q35 {
 
 constexpr int kChunk = 256;
-// attn_rows: at most kRowsLdsParts parts (128 slots) keep their scores in LDS, as many as fit
-// beside the slice stats in the dynamic LDS of a block that still runs two per CU (80 KiB less
-// the static q staging and ml); the tail's row stride is kRowsLdsSlots either way
-constexpr int kRowsLdsParts = 8, kRowsLdsSlots = kRowsLdsParts * 128;
-__host__ __device__ constexpr int rows_lds_parts(int T, int max_chunks) {
-    return (65440 - T * 4 * 8 * max_chunks * 4) / (T * 4 * kRowsLdsSlots * 4) > 0
-               ? kRowsLdsParts : 0;
+// attn_rows<T, W>: the top parts (128 slots) whose scores fit the block's dynamic LDS beside
+// the slice stats keep them there -- W = 4: two blocks per CU (80 KiB each, less the static q
+// staging and ml), at most 8 parts; W = 8: one block per CU, at most 24 parts
+constexpr int kRowsLdsDyn4 = 80 * 1024 - 16480, kRowsLdsDyn8 = 160 * 1024 - 16480;
+__host__ __device__ constexpr int rows_lds_parts(int T, int max_chunks, int W) {
+    return max(0, min(W == 8 ? 24 : 8, ((W == 8 ? kRowsLdsDyn8 : kRowsLdsDyn4) - T * 4 * 8 * max_chunks * 4) /
+                                           (T * 4 * 128 * 4)));
+}
+__host__ __device__ constexpr size_t rows_lds_bytes(int T, int max_chunks, int W) {
+    return (size_t)T * 4 * (8 * max_chunks + 128 * rows_lds_parts(T, max_chunks, W)) * 4;
 }
 // attn_fused<*, 2>: dynamic LDS of its two items, the CU's 160 KiB less both halves' static
 // arrays (ubuf, ml, nparts)
@@ -334,20 +337,20 @@ __device__ __forceinline__ void softmax_ml(const float* stats, size_t stats_stri
     }
 }
 
-// V fragments of part pc for dim tiles dt0 .. dt0 + 3: vf[ks][i] = slots pc*128 + 32 ks + 8 g
-// .. +8 of dim 16 (dt0 + i) + n. Unconditional loads with the 8-slot group clamped to slot's
+// V fragments of part pc for dim tiles dt0 .. dt0 + NTL - 1: vf[ks][i] = slots pc*128 + 32 ks +
+// 8 g .. +8 of dim 16 (dt0 + i) + n. Unconditional loads with the 8-slot group clamped to slot's
 // (past the end every lane re-reads that group, so the wait counts stay exact); slots past
 // `slot` are zeroed by mask_vf before use.
-template <bool NT = true>
+template <bool NT = true, int NTL = 4>
 __device__ __forceinline__ void load_vf(const AttnArgs& a, int lrow, int j, int pc, int slot, int dt0,
-                                        q35_u32x4 (*vf)[4]) {
+                                        q35_u32x4 (*vf)[NTL]) {
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     const uint16_t* vb = a.vc + lrow * a.kv_lane + a.kv_layer_off + (size_t)j * a.cap * 256;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
         const int sg = min(pc * 16 + 4 * ks + g, slot >> 3);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NTL; ++i) {
             const q35_u32x4* p = (const q35_u32x4*)(vb + (size_t)sg * 2048 + (16 * (dt0 + i) + n) * 8);
             vf[ks][i] = NT ? __builtin_nontemporal_load(p) : *p;
         }
@@ -356,7 +359,8 @@ __device__ __forceinline__ void load_vf(const AttnArgs& a, int lrow, int j, int 
 
 // Zero the V values of slots past `slot` in part pc's fragments (its last part only: V memory
 // past the written slots is not initialised, and a zero weight times a NaN would be NaN).
-__device__ __forceinline__ void mask_vf(int pc, int slot, q35_u32x4 (*vf)[4]) {
+template <int NTL = 4>
+__device__ __forceinline__ void mask_vf(int pc, int slot, q35_u32x4 (*vf)[NTL]) {
     const int g = (threadIdx.x & 63) >> 4;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -366,14 +370,15 @@ __device__ __forceinline__ void mask_vf(int pc, int slot, q35_u32x4 (*vf)[4]) {
         for (int w = 0; w < 4; ++w)
             mk[w] = (cnt > 2 * w ? 0xffffu : 0u) | (cnt > 2 * w + 1 ? 0xffff0000u : 0u);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NTL; ++i)
             vf[ks][i] = (q35_u32x4){vf[ks][i][0] & mk[0], vf[ks][i][1] & mk[1], vf[ks][i][2] & mk[2], vf[ks][i][3] & mk[3]};
     }
 }
 
-// The part's four 32-slot steps for the wave's 4 dim tiles: out[i] = D of tile dt0 + i.
+// The part's four 32-slot steps for the wave's NTL dim tiles: out[i] = D of tile dt0 + i.
 // pl: P in LDS, [16][kPlStride] bf16 (query column rows); rows >= nq are taken as zero.
-__device__ __forceinline__ void pv_mfma(const uint16_t* pl, int nq, q35_u32x4 (*vf)[4], q35_f32x4* out) {
+template <int NTL = 4>
+__device__ __forceinline__ void pv_mfma(const uint16_t* pl, int nq, q35_u32x4 (*vf)[NTL], q35_f32x4* out) {
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     q35_u32x4 af[4];
 #pragma unroll
@@ -382,7 +387,7 @@ __device__ __forceinline__ void pv_mfma(const uint16_t* pl, int nq, q35_u32x4 (*
         af[ks] = n < nq ? v : (q35_u32x4){0u, 0u, 0u, 0u};
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NTL; ++i) {
         q35_f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
@@ -783,13 +788,17 @@ __global__ void __launch_bounds__(256 * NI) attn_fused(AttnArgs a, int lds_slots
 // not fit LDS beside two blocks per CU: the last kRowsLdsParts parts' scores stay in LDS (the
 // first written, the last read), the rest go to the global scratch; the block reads back only
 // what it wrote, after a block barrier.
-template <int T>
-__global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
+// W = 8 (engine option attn_rows 2): one block of 8 waves per CU -- the memory parallelism of
+// two 4-wave blocks, and three times the LDS tail; P.V then takes 2 dim tiles per wave.
+template <int T, int W = 4>
+__global__ void __launch_bounds__(64 * W) attn_rows(AttnArgs a) {
     extern __shared__ float stl_all[];                  // [T][4][8 * max_chunks] slice stats, then
-                                                        // the LDS tail [T][4][kRowsLdsSlots]
+                                                        // the LDS tail [T][4][lpn * 128]
     __shared__ uint16_t qbuf[2][16][256];               // q staging (tiles), then the part's weights
     __shared__ float ml_all[T][4][2];
     constexpr int NU = (T + 1) / 2;                     // q tiles
+    constexpr int NTL = 16 / W;                         // P.V dim tiles per wave
+    constexpr int WPT = 8 / W;                          // weights per thread and row of a part
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, n = lane & 15, g = lane >> 4;
     const int pr = blockIdx.x, j = pr % kNkv, r0 = (pr / kNkv) * T;
     int slot_t[T];
@@ -801,11 +810,11 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
     const int lrow = a.rm.lane[r0];
     const size_t sst = (size_t)a.max_chunks * 8;
     float* tl = stl_all + (size_t)T * 4 * sst;
-    const int lpn = rows_lds_parts(T, a.max_chunks);
+    const int lpn = rows_lds_parts(T, a.max_chunks, W), lsl = 128 * lpn;
     const int p0 = max(slot / kPart + 1 - lpn, 0);     // first part in the LDS tail
     // q fragments: tile u, column 8 (t % 2) + h = bf16(q) of row t = 2u + t % 2, head h, and
     // + 4 its low part (zero columns for a missing row), as load_q_frags makes them
-    {
+    if (tid < 256) {
 #pragma unroll
         for (int t = 0; t < 2 * NU; ++t)
 #pragma unroll
@@ -821,9 +830,9 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
                     qbuf[t >> 1][c + 4][tid] = 0;
                 }
             }
-        __syncthreads();
     }
-    // scores: wave wv takes slices 4c + wv (score_slice's arithmetic, one MFMA chain per tile)
+    __syncthreads();
+    // scores: wave wv takes slices W c + wv (score_slice's arithmetic, one MFMA chain per tile)
     {
         // q fragments in registers, K two sub-tiles ahead (kf[st % 2] holds sub-tile st; the
         // registers of sub-tile st are refilled with sub-tile st + 2, then the next slice's)
@@ -836,10 +845,10 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
         // the first slice's sub-tile 0 strictly before its sub-tile 1: the loop head's wait for
         // sub-tile 0 must hold on entry too, and with sub-tile 0 loaded last it would drain the
         // whole prefetch (and the previous slice's score stores) at every slice
-        const int nch = slot / kChunk + 1;
-        load_k_sub<true>(a, lrow, j, 4 * (nch - 1) + wv, 0, slot, kf[0]);
+        const int nch = (slot / 64 + W) / W;             // rounds of W slices
+        load_k_sub<true>(a, lrow, j, W * (nch - 1) + wv, 0, slot, kf[0]);
         __builtin_amdgcn_sched_barrier(0);
-        load_k_sub<true>(a, lrow, j, 4 * (nch - 1) + wv, 1, slot, kf[1]);
+        load_k_sub<true>(a, lrow, j, W * (nch - 1) + wv, 1, slot, kf[1]);
         // this block's rows of the score scratch as a buffer resource (byte offsets)
         const __amdgpu_buffer_rsrc_t scres = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(a.sc + (size_t)r0 * kNq * a.sc_ld), 0, T * kNq * a.sc_ld * 4, 0x00020000);
@@ -854,7 +863,7 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
         // the top parts, written first, stay in the LDS tail, and the P.V pass starts on the
         // scores written last, still in L2
         for (int c = nch - 1; c >= 0; --c) {
-            const int q = 4 * c + wv, qnext = 4 * (c - 1) + wv, t0 = q * 64;
+            const int q = W * c + wv, qnext = W * (c - 1) + wv, t0 = q * 64;
             const bool inl = q >= 2 * p0;                // this slice's scores go to the LDS tail
             float sv[NU][4][4];
 #pragma unroll
@@ -892,7 +901,7 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
                         (q35_u32x4){__float_as_uint(scv[0]), __float_as_uint(scv[1]), __float_as_uint(scv[2]), __float_as_uint(scv[3])},
                         scres, off, 0, 0);
                     if (inl && (n & 7) < 4 && tt0 <= lslot[u])
-                        *(q35_f32x4*)(tl + (t * 4 + (n & 3)) * kRowsLdsSlots + (tt0 - 128 * p0)) = scv;
+                        *(q35_f32x4*)(tl + (t * 4 + (n & 3)) * lsl + (tt0 - 128 * p0)) = scv;
                 }
                 // sub-tiles stay in order: with the next sub-tile's MFMAs hoisted into this one
                 // their K wait also drained this slice's earlier score stores
@@ -932,66 +941,66 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
     uint16_t* pl = &qbuf[0][0][0];
     // V two parts ahead (the K and q registers of the score pass are free here): parts
     // alternate between vfa and vfb, each refilled with the part after next once used
-    q35_f32x4 acc[4];
+    q35_f32x4 acc[NTL];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < NTL; ++i) acc[i] = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
     const int np = slot / kPart + 1;
-    // the thread's two scores (head i = idx / 128, slot idx % 128 of the part, idx = tid,
-    // tid + 256) of every row, loaded two parts ahead like V and issued just before that part's
-    // V (clamped to the last slot: unconditional). The vector-memory counter completes in
+    // the thread's scores (head i = idx / 128, slot idx % 128 of the part, idx = tid + 64 W q)
+    // of every row, loaded two parts ahead like V and issued just before that part's V
+    // (clamped to the last slot: unconditional). The vector-memory counter completes in
     // order, so waiting for a part's scores then never waits for V loads issued later.
-    auto load_scores = [&](int pc, float (&sr)[T][2]) {
+    auto load_scores = [&](int pc, float (&sr)[T][WPT]) {
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const int idx = tid + q * 256, i = idx >> 7, tt = idx & 127;
+            for (int q = 0; q < WPT; ++q) {
+                const int idx = tid + q * 64 * W, i = idx >> 7, tt = idx & 127;
                 // both sources without a branch: a part in the LDS tail reads slot 0 of the
                 // scratch (one line for every lane) and takes the LDS value
                 const int ts = min(pc * kPart + tt, slot);
                 const bool lp = pc >= p0 && lpn > 0;
                 const float gv = a.sc[((size_t)(r0 + t) * kNq + 4 * j + i) * a.sc_ld + (lp ? 0 : ts)];
-                const float lv = *(lp ? tl + (t * 4 + i) * kRowsLdsSlots + max(ts - 128 * p0, 0) : stl_all);
+                const float lv = *(lp ? tl + (t * 4 + i) * lsl + max(ts - 128 * p0, 0) : stl_all);
                 sr[t][q] = lp ? lv : gv;
             }
     };
-    q35_u32x4 vfa[4][4], vfb[4][4];
-    float sra[T][2], srb[T][2];
+    q35_u32x4 vfa[4][NTL], vfb[4][NTL];
+    float sra[T][WPT], srb[T][WPT];
     // in this order (the loop's waits must hold on entry as well: with a part's scores issued
     // after its V, the first wait of every part would drain the whole V prefetch)
     load_scores(0, sra);
     __builtin_amdgcn_sched_barrier(0);
-    load_vf<true>(a, lrow, j, 0, slot, 4 * wv, vfa);
+    load_vf<true, NTL>(a, lrow, j, 0, slot, NTL * wv, vfa);
     __builtin_amdgcn_sched_barrier(0);
     load_scores(1, srb);
     __builtin_amdgcn_sched_barrier(0);
-    load_vf<true>(a, lrow, j, 1, slot, 4 * wv, vfb);
+    load_vf<true, NTL>(a, lrow, j, 1, slot, NTL * wv, vfb);
     __builtin_amdgcn_sched_barrier(0);
     const int tg = lane >> 4;
     const int myslot = tg == 0 ? slot_t[0] : tg == 1 ? slot_t[T > 1 ? 1 : 0] : slot_t[T > 2 ? 2 : 0];
     // one part (a part at np, when np is odd, is idle: zero weights, its sum not added)
-    auto part = [&](int pc, q35_u32x4 (&vf)[4][4], float (&sr)[T][2]) {
+    auto part = [&](int pc, q35_u32x4 (&vf)[4][NTL], float (&sr)[T][WPT]) {
         lds_barrier();          // ml is in; every wave is done with the previous part's weights
         // part_weights' arithmetic, from the scores in registers
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int nn = min(kPart, slot_t[t] + 1 - pc * kPart);
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const int idx = tid + q * 256, i = idx >> 7, tt = idx & 127;
+            for (int q = 0; q < WPT; ++q) {
+                const int idx = tid + q * 64 * W, i = idx >> 7, tt = idx & 127;
                 pl[(4 * t + i) * kPlStride + tt] = tt < nn ? f2bf(expf(sr[t][q] - ml_all[t][i][0]) / ml_all[t][i][1]) : (uint16_t)0;
             }
         }
         lds_barrier();
-        if (pc == np - 1) mask_vf(pc, slot, vf);
-        q35_f32x4 out[4];
-        pv_mfma(pl, 4 * T, vf, out);
+        if (pc == np - 1) mask_vf<NTL>(pc, slot, vf);
+        q35_f32x4 out[NTL];
+        pv_mfma<NTL>(pl, 4 * T, vf, out);
         load_scores(pc + 2, sr);
-        load_vf<true>(a, lrow, j, pc + 2, slot, 4 * wv, vf);
+        load_vf<true, NTL>(a, lrow, j, pc + 2, slot, NTL * wv, vf);
         // lane (n, g) holds row g's heads: add this part where it is one of that row's parts
         if (tg < T && pc < myslot / kPart + 1) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] += out[i];
+            for (int i = 0; i < NTL; ++i) acc[i] += out[i];
         }
     };
     for (int pc = 0; pc < np; pc += 2) {
@@ -1000,10 +1009,10 @@ __global__ void __launch_bounds__(256) attn_rows(AttnArgs a) {
     }
     if (tg < T) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NTL; ++i)
 #pragma unroll
             for (int h = 0; h < 4; ++h) {
-                const int d = 64 * wv + 16 * i + (lane & 15);
+                const int d = 16 * (NTL * wv + i) + (lane & 15);
                 a.out[(size_t)(r0 + tg) * 2048 + (4 * j + h) * 256 + d] = gated_out(a, r0 + tg, 4 * j + h, d, acc[i][h]);
             }
     }
@@ -1275,6 +1284,10 @@ hipError_t attn_init() {
     if (e != hipSuccess) return e;
     e = hipFuncSetAttribute((const void*)attn_fused<true, 2>, hipFuncAttributeMaxDynamicSharedMemorySize, kFused2MaxLds);
     if (e != hipSuccess) return e;
+    e = hipFuncSetAttribute((const void*)attn_rows<2, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, kRowsLdsDyn8);
+    if (e != hipSuccess) return e;
+    e = hipFuncSetAttribute((const void*)attn_rows<3, 8>, hipFuncAttributeMaxDynamicSharedMemorySize, kRowsLdsDyn8);
+    if (e != hipSuccess) return e;
     return hipFuncSetAttribute((const void*)attn_prompt, hipFuncAttributeMaxDynamicSharedMemorySize, kPrLds);
 }
 
@@ -1295,8 +1308,11 @@ static bool use_fused2(const AttnArgs& a) {
 // one row per lane on the split path: the prep runs inside the slice score kernel
 static bool prep_in_scores(const AttnArgs& a) { return !use_fused(a) && a.T == 1; }
 // a lane's 2-3 verify rows in one block when the (lane, kv head) blocks fill the CUs
+static int rows_w(const AttnArgs& a) { return a.rows_form == 2 ? 8 : 4; }
 static bool use_rows(const AttnArgs& a) {
-    const bool shape = (a.T == 2 || a.T == 3) && a.R % a.T == 0;
+    // the slice stats (and the tail) fit the block's dynamic LDS
+    const bool shape = (a.T == 2 || a.T == 3) && a.R % a.T == 0 &&
+                       rows_lds_bytes(a.T, a.max_chunks, rows_w(a)) <= (rows_w(a) == 8 ? (size_t)kRowsLdsDyn8 : 65536);
     if (a.force == kAttnRows) return shape;
     if (a.force != kAttnAuto) return false;
     return a.rows_form && shape && a.R / a.T * kNkv >= 256;
@@ -1339,9 +1355,13 @@ hipError_t launch_attn_core(const AttnArgs& a, hipStream_t st) {
         const int ngrp = (a.T + kPrRows - 1) / kPrRows;
         hipLaunchKernelGGL(attn_prompt, dim3((ngrp + 3) / 4 * 8), dim3(256), kPrLds, st, a);
     } else if (use_rows(a)) {
-        const size_t lds = (size_t)a.T * 4 * (8 * a.max_chunks + (rows_lds_parts(a.T, a.max_chunks) ? kRowsLdsSlots : 0)) * 4;
-        if (a.T == 2) hipLaunchKernelGGL(attn_rows<2>, dim3(a.R / 2 * kNkv), dim3(256), lds, st, a);
-        else hipLaunchKernelGGL(attn_rows<3>, dim3(a.R / 3 * kNkv), dim3(256), lds, st, a);
+        const int W = rows_w(a);
+        const size_t lds = rows_lds_bytes(a.T, a.max_chunks, W);
+        if (W == 8) {
+            if (a.T == 2) hipLaunchKernelGGL((attn_rows<2, 8>), dim3(a.R / 2 * kNkv), dim3(512), lds, st, a);
+            else hipLaunchKernelGGL((attn_rows<3, 8>), dim3(a.R / 3 * kNkv), dim3(512), lds, st, a);
+        } else if (a.T == 2) hipLaunchKernelGGL((attn_rows<2, 4>), dim3(a.R / 2 * kNkv), dim3(256), lds, st, a);
+        else hipLaunchKernelGGL((attn_rows<3, 4>), dim3(a.R / 3 * kNkv), dim3(256), lds, st, a);
     } else if (use_fused(a)) {
         if (a.T < 1 || a.R % a.T) return hipErrorInvalidValue;
         const int pairs = a.R / a.T * kNkv;

@@ -1924,6 +1924,7 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             REQ(n != "partial_rows" || value >= 17, Q35_ERR_ARG, "partial_rows must exceed the 16-row batch-1 path");
             REQ(n != "gemv_tpb" || value == 1 || value == 2, Q35_ERR_ARG, "gemv_tpb is 1 or 2");
             REQ(n != "gdn_defer" || (value >= 0 && value <= kMaxDefer), Q35_ERR_ARG, "gdn_defer is 0 .. 4");
+            REQ(n != "attn_rows" || (value >= 0 && value <= 2), Q35_ERR_ARG, "attn_rows is 0, 1 or 2");
             HCK(hipStreamSynchronize(e->st));
             if (n == "b1_partials") e->b1_partials = value ? 1 : 0;
             else if (n == "attn_prompt") e->forms.attn_prompt = value ? 1 : 0;
@@ -1933,7 +1934,7 @@ int q35_set_option(q35_engine* e, const char* name, int value) {
             else if (n == "attn_split4") e->forms.attn_split4 = value ? 1 : 0;
             else if (n == "gemm_wide") e->forms.gemm_wide = value ? 1 : 0;
             else if (n == "attn_pair") e->forms.attn_pair = value ? 1 : 0;
-            else if (n == "attn_rows") e->forms.attn_rows = value ? 1 : 0;
+            else if (n == "attn_rows") e->forms.attn_rows = value;
             else if (n == "gdn_rows") e->forms.gdn_rows = value ? 1 : 0;
             else if (n == "gdn_defer") e->forms.gdn_defer = value;
             else if (n == "mid_partials") e->forms.mid_partials = value ? 1 : 0;

@@ -23,7 +23,8 @@ struct KernelForms {
     int partial_rows = 1024;   // batched kEPartial GEMMs with M >= this leave one (summed) chain
     int attn_split4 = 1;       // split attention path: 4-wave score blocks, P.V split over dim quarters
     int attn_pair = 1;         // fused attention, one row per lane: two (row, kv head) items per block
-    int attn_rows = 1;         // MTP verify (2-3 rows per lane) at >= 128 lanes: one block per (lane, kv head)
+    int attn_rows = 2;         // MTP verify (2-3 rows per lane) at >= 128 lanes: one block per (lane, kv head)
+                               // (1: 4 waves, two blocks per CU; 2: 8 waves, one per CU, a larger LDS tail)
     int attn_prompt = 1;       // prompt waves of >= 64 rows: flash-form MFMA kernel (1) or one-row kernels (0)
     int mid_partials = 1;      // bodies of 2 .. 16 rows: k-block chains + add+norm (0: residual-epilogue GEMMs)
     int gdn_rows = 1;          // MTP verify (2-3 rows per lane, whole-head blocks): the persistent GDN kernel

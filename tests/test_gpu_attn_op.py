@@ -212,7 +212,8 @@ def test_attention_op_config3_grid(L):
 @pytest.mark.parametrize("L", [1024, 8192])
 def test_attention_op_ragged_and_verify_rows(L):
     """Ragged contexts (each lane its own position, from 5 to L - 1) at 32 and 256 lanes, and a
-    lane's 3 MTP verify rows (causal inside the block of rows) at 256 lanes (the rows form)."""
+    lane's 3 MTP verify rows (causal inside the block of rows) at 256 lanes (the rows form, in
+    its 4-wave and 8-wave blocks: engine option attn_rows 1 and 2)."""
     print(f"attention op ragged / verify rows L={L}", flush=True)
     h = Harness(L, 768)
     try:
@@ -222,8 +223,11 @@ def test_attention_op_ragged_and_verify_rows(L):
             pos[0], pos[-1] = 5, L - 1
             run_grid(h, B, 1, pos, [0, B // 3, B - 1])
         pos = [int(p) for p in rng.integers(5, L - 2, 256)]
-        run_grid(h, 256, 3, pos, [0, 255])
-        run_grid(h, 64, 2, pos[:64], [7])
+        for rows in (1, 2):          # the rows form with 4-wave blocks, then with 8-wave blocks
+            h.e.set_option("attn_rows", rows)
+            run_grid(h, 256, 3, pos, [0, 255])
+            run_grid(h, 64, 2, pos[:64], [7])
+        h.e.set_option("attn_rows", 2)
     finally:
         h.s.close()
         h.e.close()

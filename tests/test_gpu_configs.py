@@ -277,9 +277,9 @@ def test_verify_rows_attention_bit_identical():
     try:
         toks = [int(t) for t in np.random.default_rng(6).integers(0, 248320, B)]
         outs = []
-        for rows in (1, 0):
+        for rows in (2, 1, 0):       # 8-wave and 4-wave rows blocks, then one block per row
             e.set_option("attn_rows", rows)
-            e.set_option("gdn_rows", rows)
+            e.set_option("gdn_rows", min(rows, 1))
             short, long_ = State(e, B, 1000, mtp_k=2, mtp_cap=64), State(e, B, 1000, mtp_k=2, mtp_cap=64)
             short.seed(3, 300)
             long_.seed(4, 900)
@@ -297,12 +297,13 @@ def test_verify_rows_attention_bit_identical():
             res.append(short.decode_step([x[-1] for x in em1], logits=True))
             short.close()
             outs.append(res)
-        a, b = outs
-        assert a[0] == b[0] and a[2] == b[2]
-        assert np.array_equal(a[1], b[1]) and np.array_equal(a[3], b[3])
-        assert np.array_equal(a[4][0], b[4][0])
-        assert np.array_equal(a[4][1].view(np.uint32), b[4][1].view(np.uint32))
+        b = outs[-1]
+        for a in outs[:-1]:
+            assert a[0] == b[0] and a[2] == b[2]
+            assert np.array_equal(a[1], b[1]) and np.array_equal(a[3], b[3])
+            assert np.array_equal(a[4][0], b[4][0])
+            assert np.array_equal(a[4][1].view(np.uint32), b[4][1].view(np.uint32))
     finally:
-        e.set_option("attn_rows", 1)
+        e.set_option("attn_rows", 2)
         e.set_option("gdn_rows", 1)
         e.close()
