@@ -1370,7 +1370,7 @@ static hipError_t launch_wide(const GemmArgs& a, int em, hipStream_t st) {
         a.ldy % 8 || ((uintptr_t)a.Y & 15) || (a.y_tiled && (em != kESiluMul || a.M < 512 || a.ldy % 256)))
         return hipErrorInvalidValue;        // 16-byte row pieces in the epilogue
     const int nb = em == kESiluMul ? (a.N / 32 + 3) / 4 : (a.N / 16 + 7) / 8;
-    if (a.M < 512) {                   // batched lanes: 64-row blocks
+    if (a.M < 512 || a.N <= 64) {      // batched lanes, or a few columns: 64-row blocks
         const int mb = (a.M + 63) / 64;
         if (em == kESiluMul) hipLaunchKernelGGL(gemm_wide64<kESiluMul>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
         else hipLaunchKernelGGL(gemm_wide64<kEStore>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
