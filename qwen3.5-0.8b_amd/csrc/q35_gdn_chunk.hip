@@ -180,22 +180,25 @@ __global__ void __launch_bounds__(256) gdn_chunk_prep(GdnArgs a) {
     }
     __syncthreads();
     if (tid < kC) ecum[tid] = expf(cum[tid]);
-    // ---- ut (strictly lower) and intra (lower) on MFMA: wave w takes row tile w against the
-    // column tiles nt <= w; A = k~ (ut) or q~ (intra) rows, B = k~^T
+    // ---- ut (strictly lower) and intra (lower) on MFMA: the 10 (row tile, column tile <= row
+    // tile) pairs dealt round-robin to the 4 waves (3, 3, 2, 2 each: row tile w against its
+    // w + 1 column tiles would give wave 3 four); A = k~ (ut) or q~ (intra) rows, B = k~^T
     float* ws = a.chunk_ws + ((size_t)c * kHv + h) * kCWs;
     {
         const int wv = tid >> 6, ln = tid & 63, mr = ln & 15, kq = ln >> 4;
-        for (int nt = 0; nt <= wv; ++nt) {
+        for (int pi = wv; pi < 10; pi += 4) {
+            const int rt = pi < 1 ? 0 : pi < 3 ? 1 : pi < 6 ? 2 : 3;        // pair pi = (rt, nt)
+            const int nt = pi - rt * (rt + 1) / 2;
             q35_f32x4 au = {0.f, 0.f, 0.f, 0.f}, ai = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
             for (int ks = 0; ks < 32; ++ks) {
                 const float bk = kn[nt * 16 + mr][ks * 4 + kq];
-                au = mfma4(kn[wv * 16 + mr][ks * 4 + kq], bk, au);
-                ai = mfma4(qn[wv * 16 + mr][ks * 4 + kq], bk, ai);
+                au = mfma4(kn[rt * 16 + mr][ks * 4 + kq], bk, au);
+                ai = mfma4(qn[rt * 16 + mr][ks * 4 + kq], bk, ai);
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int i = wv * 16 + 4 * kq + r, j = nt * 16 + mr;
+                const int i = rt * 16 + 4 * kq + r, j = nt * 16 + mr;
                 const float pair = j <= i ? expf(cum[i] - cum[j]) : 0.f;
                 ut[i][j] = j < i ? (au[r] * bl[i]) * pair : 0.f;     // (beta_i k~_i) . k~_j, decayed
                 intra_s[i][j] = ai[r] * pair;
