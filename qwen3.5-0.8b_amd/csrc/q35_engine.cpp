@@ -701,19 +701,11 @@ void body_kernels(q35_engine* e, q35_state* s, int R, int T, bool ckpt, int defe
     for (int l = 0; l < e->n_layers; ++l) {
         const LayerW& w = e->L[l];
         if (!is_attn_layer(l)) {
-            if (small) {
+            if (small)
                 norm_gemm(e, rr, w.W_in, kGdnInRows, R, e->proj, kGdnInRows, w.norm_in);
-            } else if (wide_for(e, R, kGdnInRows)) {
-                // many-row launches in whole rounds of blocks: the first 8,192 columns (64 column
-                // blocks), then the 32 gate columns as a small launch of their own (a 65th column
-                // block of 2 tiles would add a round of full-length blocks); the same bits
-                gemm(e, w.W_in, kGdnBOff, kHidden, R, e->h, kHidden, e->proj, kGdnInRows, kAPlain, nullptr, 0, nullptr,
-                     -1, nullptr, true);
-                gemm(e, w.W_in + (size_t)(kGdnBOff / 16) * (kHidden / 256) * 4096, kGdnInRows - kGdnBOff, kHidden, R,
-                     e->h, kHidden, e->proj + kGdnBOff, kGdnInRows, kAPlain, nullptr, 0, nullptr, -1, nullptr, true);
-            } else {
-                gemm(e, w.W_in, kGdnInRows, kHidden, R, e->h, kHidden, e->proj, kGdnInRows, kAPlain, nullptr, 0, nullptr);
-            }
+            else
+                gemm(e, w.W_in, kGdnInRows, kHidden, R, e->h, kHidden, e->proj, kGdnInRows, kAPlain, nullptr, 0, nullptr,
+                     -1, nullptr, wide_for(e, R, kGdnInRows));
             GdnArgs g{};
             g.proj = e->proj; g.o = e->o; g.conv_w = w.conv_w; g.A_log = w.A_log; g.dt_bias = w.dt_bias;
             g.S = s->S; g.S_lane = s->S_lane(); g.S_slot = (long long)kGdnLayers * kSLayer;

@@ -1370,13 +1370,28 @@ static hipError_t launch_wide(const GemmArgs& a, int em, hipStream_t st) {
         a.ldy % 8 || ((uintptr_t)a.Y & 15) || (a.y_tiled && (em != kESiluMul || a.M < 512 || a.ldy % 256)))
         return hipErrorInvalidValue;        // 16-byte row pieces in the epilogue
     const int nb = em == kESiluMul ? (a.N / 32 + 3) / 4 : (a.N / 16 + 7) / 8;
-    if (a.M < 512 || a.N <= 64) {      // batched lanes, or a few columns: 64-row blocks
+    if (a.M < 512) {                   // batched lanes: 64-row blocks
         const int mb = (a.M + 63) / 64;
         if (em == kESiluMul) hipLaunchKernelGGL(gemm_wide64<kESiluMul>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
         else hipLaunchKernelGGL(gemm_wide64<kEStore>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
         return hipGetLastError();
     }
     const int mb = (a.M + 255) / 256;
+    if (em == kEStore && nb * mb > 256 && (nb * mb) % 256 <= 64 && (nb * mb) % 256 % mb == 0) {
+        // a last round of at most a quarter of the CUs (the GDN in_proj's 65th column block of 2
+        // tiles, the attention qkv's last 8 at 2,048 rows): whole rounds of 256 x 128 blocks, the
+        // remaining columns as 64-row blocks (16 stages) in a launch of their own; the same bits
+        const int nbm = (nb * mb - (nb * mb) % 256) / mb;
+        GemmArgs h = a, t = a;
+        h.N = nbm * 128;
+        t.N = a.N - h.N;
+        t.W = a.W + (size_t)(h.N / 16) * (a.K / 256) * 4096;
+        t.Y = a.Y + h.N;
+        hipLaunchKernelGGL(gemm_wide<kEStore>, dim3((nbm + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, h);
+        const int nbt = (t.N / 16 + 7) / 8;
+        hipLaunchKernelGGL(gemm_wide64<kEStore>, dim3((nbt + 7) / 8 * 8 * ((a.M + 63) / 64)), dim3(512), kWideLds, st, t);
+        return hipGetLastError();
+    }
     if (em == kESiluMul) hipLaunchKernelGGL(gemm_wide<kESiluMul>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
     else hipLaunchKernelGGL(gemm_wide<kEStore>, dim3((nb + 7) / 8 * 8 * mb), dim3(512), kWideLds, st, a);
     return hipGetLastError();
