@@ -163,9 +163,14 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, q35_f32x4 sum, int n
 // wave runs TPB MFMA chains on the same A fragments. Used with TPB = 2 for N >= 4096
 // (batch 1: 1,171 -> 1,209 tok/s; TPB = 4, a quarter of the blocks: 1,168).
 // KP: chain loads of the kANormXP fold (16, or 8 when the producing GEMM left at most 8)
-template <int AM, int EM, int TPB = 1, int KP = 16>
+// XT (TPB = 2): the grid covers the first 2 x gridDim.x column tiles and block b also takes
+// tile 2 x gridDim.x + b if it exists, so a width of 514 tiles (the GDN in_proj) runs as 256
+// blocks instead of a 257th one doubling up on a CU
+template <int AM, int EM, int TPB = 1, int KP = 16, bool XT = false>
 __global__ void __launch_bounds__(TPB > 1 ? 256 : 1024) gemm_small_m(GemmArgs a) {   // TPB > 1: K = 1024, 4 waves
     const int nt = blockIdx.x * TPB;
+    const int ntx = TPB * gridDim.x + blockIdx.x;       // XT: the extra tile
+    const bool hx = XT && ntx < a.N / 16;              // block-uniform
     const int mt = blockIdx.y;
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
@@ -176,12 +181,17 @@ __global__ void __launch_bounds__(TPB > 1 ? 256 : 1024) gemm_small_m(GemmArgs a)
     const bool mvalid = m < a.M;
 
     const q35_bf16x8* wp = (const q35_bf16x8*)(a.W + ((size_t)nt * KB + kb) * 4096) + lane;
-    q35_bf16x8 wf[TPB][8];
+    q35_bf16x8 wf[TPB][8], wx[8];
     auto load_w = [&] {
 #pragma unroll
         for (int t = 0; t < TPB; ++t)
 #pragma unroll
             for (int s = 0; s < 8; ++s) wf[t][s] = __builtin_nontemporal_load(wp + (size_t)t * KB * 512 + s * 64);
+        if (hx) {
+            const q35_bf16x8* wq = (const q35_bf16x8*)(a.W + ((size_t)ntx * KB + kb) * 4096) + lane;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) wx[s] = __builtin_nontemporal_load(wq + s * 64);
+        }
     };
     // batch 1 with a producer: the producer's own loads go first (the vector-memory counter
     // completes in order, so its arithmetic then overlaps the weight stream instead of
@@ -377,11 +387,17 @@ __global__ void __launch_bounds__(TPB > 1 ? 256 : 1024) gemm_small_m(GemmArgs a)
         epilogue<EM>(a, acc[0], nt, mt * 16, lane);
         return;
     }
-    __shared__ q35_f32x4 part[TPB][16][64];
+    __shared__ q35_f32x4 part[TPB + XT][16][64];
 #pragma unroll
     for (int t = 0; t < TPB; ++t) part[t][wv][lane] = acc[t];
+    if (hx) {
+        q35_f32x4 ax = (q35_f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) ax = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(af[s]), wx[s], ax, 0, 0, 0);
+        part[TPB][wv][lane] = ax;
+    }
     __syncthreads();
-    if (wv >= TPB) return;                 // wave t sums tile t's k-block chains in order
+    if (wv >= TPB + (hx ? 1 : 0)) return;  // wave t sums tile t's k-block chains in order
     q35_f32x4 sum = part[wv][0][lane];
     for (int w = 1; w < KB; ++w) {
         q35_f32x4 p = part[wv][w][lane];
@@ -396,7 +412,7 @@ __global__ void __launch_bounds__(TPB > 1 ? 256 : 1024) gemm_small_m(GemmArgs a)
         }
         return;
     }
-    epilogue<EM>(a, sum, nt + wv, mt * 16, lane);
+    epilogue<EM>(a, sum, wv < TPB ? nt + wv : ntx, mt * 16, lane);
 }
 
 // Elementwise A producer for batched launches: Y[m][k] = produce_a(m, k) (bf16), so the
@@ -1471,6 +1487,8 @@ static hipError_t launch_am_em(const GemmArgs& a, hipStream_t st) {
                  a.N % 32 == 0 && a.N >= 4096 && KB == 4) {
             if (AM == kANormXP && a.kpb <= 8)      // after out_proj / o_proj (8 chains)
                 hipLaunchKernelGGL((gemm_small_m<AM, EM, 2, 8>), dim3(a.N / 32, 1, 1), dim3(64 * KB), 0, st, a);
+            else if (a.N / 32 > 256 && a.N / 16 - 512 <= 256)   // GDN in_proj: 256 blocks, 2 of them 3 tiles
+                hipLaunchKernelGGL((gemm_small_m<AM, EM, 2, 16, true>), dim3(256, 1, 1), dim3(64 * KB), 0, st, a);
             else
                 hipLaunchKernelGGL((gemm_small_m<AM, EM, 2>), dim3(a.N / 32, 1, 1), dim3(64 * KB), 0, st, a);
         } else
