@@ -276,7 +276,7 @@ def run_mtp_accepting(eng, B: int, ctx: int, rounds: int, d: int = 7):
 def cpu_baseline(ctx: int, budget_s: float = 6.0, runs: int = 3):
     """The torch-CPU oracle (restatement of the reference's specimpl.py path) decoding lane 0
     of the same seeded workload on the host cores: the median tok/s of `runs` timed runs of
-    about budget_s each (median of 3), continuing one greedy sequence."""
+    about budget_s each (the baseline protocol: median of 3), continuing one greedy sequence."""
     import statistics
     import torch
     from oracle.seeded import seeded_forward

@@ -246,10 +246,10 @@ class Engine:
 
 
 # Round cost in plain decode steps of an MTP round at depth k, measured on one MI355X at batch 1,
-# ctx 4,096 (bench.py `mtp_k2.b1_k1` / `mtp_k2.b1` round_cost_steps: a k = 1 round 1.498 steps, a
-# k = 2 round 1.857). The reference bills its own gfx1151 rounds at 1.58 / 1.90
+# ctx 4,096 (bench.py `mtp_k2.b1_k1` / `mtp_k2.b1` round_cost_steps: a k = 1 round 1.552 steps, a
+# k = 2 round 1.920). The reference bills its own gfx1151 rounds at 1.58 / 1.90
 # (engine/mtp_adaptive.h:54-68); a policy on this engine uses these instead.
-MI355X_ROUND_COST = {1: 1.498, 2: 1.857}
+MI355X_ROUND_COST = {1: 1.552, 2: 1.920}
 
 
 class MtpPolicy:

@@ -182,8 +182,8 @@ def test_session_mtp_rounds_match_plain(tmp_path, monkeypatch):
 def test_session_adaptive_depth_abandons_and_matches_plain(tmp_path):
     """Random-init weights: the drafter never agrees, so each round emits one token; the
     session's adaptive tracker (engine/mtp_adaptive.h) demotes 2 -> 1 after 16 rounds and abandons
-    after 24 more, its estimates billed at this engine's measured round costs (1 / 1.857 and
-    1 / 1.498, not the reference's gfx1151 1.90 / 1.58), and the transcript is the plain session's.
+    after 24 more, its estimates billed at this engine's measured round costs (1 / 1.920 and
+    1 / 1.552, not the reference's gfx1151 1.90 / 1.58), and the transcript is the plain session's.
     A feed starts a fresh tracker: the next turn speculates at k = 2 again."""
     from oracle.weights import lane_prompt_ids
     from qwen35 import Engine
@@ -207,7 +207,7 @@ def test_session_adaptive_depth_abandons_and_matches_plain(tmp_path):
         assert "k=1 " in ad[0] and "window_rounds=16 " in ad[0] and "prev_k=2 " in ad[0]
         assert "k=0 " in ad[1] and "window_rounds=24 " in ad[1] and ad[1].endswith("plain=1")
         assert "k=1 " in ad[2] and "k=0 " in ad[3]
-        assert f"est={1 / 1.857:.4f} " in ad[0] and f"est={1 / 1.498:.4f} " in ad[1]
+        assert f"est={1 / 1.920:.4f} " in ad[0] and f"est={1 / 1.552:.4f} " in ad[1]
         acc = [l for l in logs[2] if l.startswith("ACCEPT ")]
         assert sum(" k=2 " in l for l in acc) == 32 and sum(" k=1 " in l for l in acc) == 48
     finally:
