@@ -937,13 +937,8 @@ __global__ void __launch_bounds__(512) gemm_wide64(GemmArgs a) {
     // blocks) row blocks by XCD instead, so an XCD fetches its quarter of the long A rows
     // once, not all of A
     const int ncb = (ntiles + 7) / 8;
-#ifdef Q35_COLMAP
-    const int nblk = EM == kEPartial ? (idx % ncb + 8 * 0) * 0 + (idx / ((mb + 7) / 8 * 8)) * 8 + xcd : (idx / mb) * 8 + xcd;
-    const int rb = EM == kEPartial ? idx % ((mb + 7) / 8 * 8) : idx % mb;
-#else
     const int nblk = EM == kEPartial ? idx % ncb : (idx / mb) * 8 + xcd;
     const int rb = EM == kEPartial ? (idx / ncb) * 8 + xcd : idx % mb;
-#endif
     if (EM == kEPartial && rb >= mb) return;
     if (EM == kESiluMul ? nblk * 4 >= half : nblk * 8 >= ntiles) return;
     auto col_tile = [&](int c) {
