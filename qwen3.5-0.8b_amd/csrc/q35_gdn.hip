@@ -55,7 +55,11 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
     // trip with the row metadata, instead of one more after the state): the first row's
     // projection inputs, the conv taps and the gate parameters, as raw bits
     const uint16_t* pr0 = a.proj + (size_t)(gi * a.T) * kGdnInRows;
-    uint16_t xr = pr0[cqk], xvr = pr0[cvc], bbr = pr0[kGdnBOff + h], aar = pr0[kGdnAOff + h];
+    uint16_t xr = pr0[cqk], xvr = pr0[cvc];
+    // raw b, a of row (tid mod 64) of the first 64-row chunk (the gates of a chunk's rows are made
+    // at its start, one row per thread of wave 0)
+    const uint16_t* pg = pr0 + (size_t)min(tid & 63, a.T - 1) * kGdnInRows;
+    uint16_t gbr = pg[kGdnBOff + h], gar = pg[kGdnAOff + h];
     const uint2 cpk = *(const uint2*)(a.conv_w + (size_t)cqk * 4);
     const uint2 dpk = *(const uint2*)(a.conv_w + (size_t)cvc * 4);
     const uint16_t alogr = a.A_log[h], dtbr = a.dt_bias[h];
@@ -68,7 +72,7 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
 
     __shared__ float qs[2][128], ks[2][128], vs[2][VC];   // by row parity
     __shared__ float wred[2][4];
-    __shared__ float gate_s[2][2];
+    __shared__ float gate_c[2][64][2];               // (decay, beta) of a 64-row chunk's rows, by chunk parity
     constexpr int NG = 16;            // fixed reduction groups of 8 k-rows, for every CS
     constexpr int GPT = KR / 8;       // groups per lane
     __shared__ float red_r[NG][VC], red_o[NG][VC];
@@ -138,10 +142,26 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
         const int r = gi * a.T + t;
         const int pb = t & 1;
         const uint16_t* pr = a.proj + (size_t)r * kGdnInRows;
-        const uint16_t xcur = xr, xvcur = xvr, bbcur = bbr, aacur = aar;
+        const uint16_t xcur = xr, xvcur = xvr;
         if (t + 1 < a.T) {      // the next row's inputs load while this row computes
             const uint16_t* pn = pr + kGdnInRows;
-            xr = pn[cqk]; xvr = pn[cvc]; bbr = pn[kGdnBOff + h]; aar = pn[kGdnAOff + h];
+            xr = pn[cqk]; xvr = pn[cvc];
+        }
+        if ((t & 63) == 0) {
+            // the gates (decay e^g, g = -e^A_log softplus(a + dt_bias); beta = sigmoid(b)) of rows
+            // t .. t+63, one row per thread: off the rows' sequential path (one thread's chain of
+            // transcendentals per row would sit before every row's barrier)
+            if (tid < 64) {
+                float bb = bf2f(gbr);
+                float aa = bf2f(gar) + dtb;
+                float sp = aa > 20.f ? aa : log1pf(expf(aa));
+                float g = A * sp;
+                gate_c[(t >> 6) & 1][tid][0] = expf(g);
+                gate_c[(t >> 6) & 1][tid][1] = sigmoid_f(bb);
+            }
+            const uint16_t* pgn = a.proj + (size_t)(gi * a.T + min(t + 64 + (tid & 63), a.T - 1)) * kGdnInRows;
+            gbr = pgn[kGdnBOff + h];           // the next chunk's
+            gar = pgn[kGdnAOff + h];
         }
         // causal conv: taps over [w0, w1, w2, raw] in order, f32, one rounding, bf16 SiLU
         {
@@ -161,21 +181,13 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a) {
             // squared norms: waves 0-1 hold q, waves 2-3 hold k
             float ss = wave_sum(uq * uq);
             if ((tid & 63) == 0) wred[pb][tid >> 6] = ss;
-            if (tid == 0) {
-                float bb = bf2f(bbcur);
-                float aa = bf2f(aacur) + dtb;
-                float sp = aa > 20.f ? aa : log1pf(expf(aa));
-                float g = A * sp;
-                gate_s[pb][0] = expf(g);
-                gate_s[pb][1] = sigmoid_f(bb);
-            }
         }
         lds_barrier();
         // q~ and k~ of this lane's rows, normalised where they are read (the same two rounded
         // products as a normalisation pass)
         const float rq = rsqrtf((wred[pb][0] + wred[pb][1]) + 1e-6f);
         const float rk = rsqrtf((wred[pb][2] + wred[pb][3]) + 1e-6f);
-        const float gam = gate_s[pb][0], beta = gate_s[pb][1];
+        const float gam = gate_c[(t >> 6) & 1][t & 63][0], beta = gate_c[(t >> 6) & 1][t & 63][1];
         float kn[KR], qn[KR];
 #pragma unroll
         for (int i = 0; i < KR; ++i) {
