@@ -540,9 +540,10 @@ __global__ void __launch_bounds__(256, 2) gdn_persist(GdnArgs a, int nitems) {
                 for (int t = 0; t < TR; ++t) wred[t][tid >> 6] = ss[t];
             }
             if (TR == 1 && tid == 0 && k == 0) gates(op, 0, gate_s[0]);
-            if (TR > 1 && tid == 0) {
+            if (TR > 1) {       // row t's by the first thread of wave t: the rows' chains in parallel
 #pragma unroll
-                for (int t = 0; t < TR; ++t) gates(op, t, gate_s[t]);   // read after row 0's first barrier
+                for (int t = 0; t < TR; ++t)
+                    if (tid == 64 * t) gates(op, t, gate_s[t]);   // read after row 0's first barrier
             }
         }
 #pragma unroll
